@@ -1,0 +1,133 @@
+/*
+ * thorn_amd.h - C ABI of the MI355X (gfx950) THORN optimizer step.
+ *
+ * The reference (pykeio/THORN, thorn/thorn.py) is a pure-Python PyTorch optimizer with no FFI.
+ * Its drop-in boundary is the Python API `THORN(...).step()`; this library is what the build's
+ * `thorn_amd.THORN` drives underneath, and each entry point below replaces a stretch of the
+ * reference's step named in its comment.
+ *
+ * Conventions
+ *   - All tensor pointers are device pointers to contiguous row-major fp32 data.
+ *   - Streams are hipStream_t passed as void*; every launch is asynchronous on that stream.
+ *   - Functions return 0 on success or a THORN_ERR_* code; thorn_last_error() describes the
+ *     last failure on the calling thread.
+ *   - The library allocates no device memory. Workspaces and tables come from the caller.
+ *   - Tables: the caller gets their size from *_table_bytes, lets *_fill_table write the bytes
+ *     into host memory (device addresses inside refer to `table_dev`), copies those bytes to
+ *     `table_dev` on the same stream, then calls the *_step function.
+ */
+#ifndef THORN_AMD_H
+#define THORN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THORN_ABI_VERSION 1
+
+enum {
+    THORN_OK = 0,
+    THORN_ERR_INVALID = 1,     /* bad argument (shape, null pointer, alignment) */
+    THORN_ERR_HIP = 2,         /* a HIP runtime call or kernel launch failed */
+    THORN_ERR_UNSUPPORTED = 3, /* valid request this build does not implement */
+};
+
+/* Per-matrix option flags (ThornOrthoMatDesc.flags). */
+#define THORN_MAT_PER_ROW_NORM 1   /* per-row normalization (thorn.py:704-707, 709-766) */
+#define THORN_MAT_MD 2             /* decouple_md with row and column gains (thorn.py:1603-1608) */
+#define THORN_MAT_MD_SCALAR 4      /* decouple_md with one scalar gain (thorn.py:1609-1612) */
+
+/* Per-step flags (ThornOrthoMatStep.step_flags). */
+#define THORN_STEP_KEEP_GRAD 8     /* write g *= gain back to the gradient (none_grad=False) */
+#define THORN_STEP_APPLY 16        /* update the parameter this step (thorn.py:1395-1396) */
+
+int thorn_abi_version(void);
+const char* thorn_last_error(void);
+/* sizeof of the ABI structs, so bindings can verify their layout:
+ * 0 = ThornOrthoMatDesc, 1 = ThornOrthoMatStep, 2 = ThornAdamTensorStep; 0 for anything else. */
+size_t thorn_abi_struct_size(int which);
+
+/* ------------------------------------------------------------------------------------------
+ * Orthogonalized group: momentum, Newton-Schulz, per-row normalization, cautious weight decay,
+ * decouple_md. Replaces THORN._batched_ortho_step (thorn.py:1427-1457) with _ortho_pre
+ * (thorn.py:1383-1397), _polar_decomp (thorn.py:626-667, including thorn::sym_addmm
+ * thorn.py:298-377) and _ortho_post (thorn.py:1399-1425).
+ * ------------------------------------------------------------------------------------------ */
+
+typedef struct ThornOrthoMatDesc {
+    int64_t rows, cols;   /* one matrix; a parameter with ndim > 2 is one desc per matrix */
+    int32_t flags;        /* THORN_MAT_* */
+    int32_t reserved;
+} ThornOrthoMatDesc;
+
+typedef struct ThornOrthoMatStep {
+    float* p;             /* parameter (rows x cols) */
+    float* g;             /* gradient */
+    float* m;             /* state['moment'] */
+    float* row_gain;      /* decouple_md: state['row_gain'] (rows) or state['gain'] (scalar) */
+    float* col_gain;      /* state['col_gain'] (cols) */
+    float* row_gain_moment;
+    float* row_gain_variance;
+    float* col_gain_moment;
+    float* col_gain_variance;
+    const float* target_norm;  /* state['target_norm'], 0-d */
+    float eta;            /* group lr * _lr_scale_ortho (thorn.py:1405) */
+    float weight_decay;
+    float beta1;
+    float gain_lr, gain_beta2, gain_w1, gain_w2, gain_eps;  /* w1 = 1 - beta1, w2 = 1 - beta2 */
+    float gain_bc1, gain_bc2;  /* 1/(1 - beta1^step), 1/(1 - beta2^step) of the gain Adam */
+    int32_t step_flags;   /* THORN_STEP_* */
+    int32_t reserved;
+} ThornOrthoMatStep;
+
+typedef struct thorn_ortho_plan* thorn_ortho_plan_t;
+
+int thorn_ortho_plan_create(const ThornOrthoMatDesc* mats, int n, thorn_ortho_plan_t* out);
+void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan);
+/* Device workspace; must be zero-filled once when allocated and kept for every later step. */
+size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
+size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
+int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
+                           void* table_dev, void* table_host);
+/* Runs the whole step for the group: coeffs holds iters (a, b, c) triples (thorn.py:425-480). */
+int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+                     void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Non-orthogonalized group: Adam / Adam-atan2 / rectified Adam with cautious weight decay, all
+ * tensors of all such groups in one launch. Replaces the per-parameter loop of _step_params
+ * (thorn.py:1659-1727) around _adam_update (thorn.py:838-888).
+ * ------------------------------------------------------------------------------------------ */
+
+typedef struct ThornAdamTensorStep {
+    float* p;
+    const float* g;
+    float* m;             /* state['moment'] */
+    float* v;             /* state['variance'] */
+    float lr;             /* group lr * rect * magma (thorn.py:1712) */
+    float weight_decay;
+    float beta2;
+    float w1, w2;         /* 1 - beta1, 1 - beta2 */
+    float bc1, bc2;       /* 1/(1 - beta1^step), 1/(1 - beta2^step) */
+    float eps;            /* 0 selects Adam-atan2 (thorn.py:879-880) */
+    int32_t apply;        /* update p (thorn.py:1707) */
+    int32_t degenerate;   /* rect == 0: u = m (thorn.py:883-885) */
+} ThornAdamTensorStep;
+
+typedef struct thorn_adam_plan* thorn_adam_plan_t;
+
+int thorn_adam_plan_create(const int64_t* numel, int n, thorn_adam_plan_t* out);
+void thorn_adam_plan_destroy(thorn_adam_plan_t plan);
+size_t thorn_adam_table_bytes(thorn_adam_plan_t plan);
+int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* table_dev,
+                          void* table_host);
+int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THORN_AMD_H */

@@ -1,0 +1,89 @@
+"""Small deterministic workloads shared by the golden-vector script and the parity tests.
+
+Each builder returns (params, groups, grad_fn): CPU fp32 leaf tensors, THORN parameter groups over
+them, and grad_fn(step, index, param) giving that step's gradient (pre-drawn, so the values do not
+depend on call order). Parity tests move everything to the GPU bit for bit.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def _leaf(t: torch.Tensor) -> torch.nn.Parameter:
+    return torch.nn.Parameter(t, requires_grad=True)
+
+
+def _grads(gen, shapes, steps, scale, outlier_rows=0.0):
+    out = {}
+    for s in range(1, steps + 1):
+        for i, shape in enumerate(shapes):
+            g = torch.randn(shape, generator=gen) * scale
+            if outlier_rows and len(shape) >= 2:
+                rows = shape[-2]
+                k = max(1, round(outlier_rows * rows))
+                idx = torch.randperm(rows, generator=gen)[:k]
+                g[..., idx, :] *= 10.0
+            out[(s, i)] = g
+    return out
+
+
+def config1(steps: int = 10):
+    """one 512x256 Linear weight, N(0, 0.02); gradients N(0, 1e-3^2), seed 3407."""
+    gen = torch.Generator().manual_seed(3407)
+    p = _leaf(torch.randn(512, 256, generator=gen) * 0.02)
+    grads = {}
+    for s in range(1, steps + 1):
+        grads[(s, 0)] = torch.randn(512, 256, generator=gen) * 1e-3
+    groups = [{'orthogonalize': True, 'params': [p], 'lr': 1e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.1,
+               'scaling_mode': 'moonlight', 'iters': 5}]
+    return [p], groups, lambda s, i, prm: grads[(s, i)]
+
+
+def mixed_small(steps: int = 20):
+    """Tall, wide, square, batched (3-D), odd-sized and tiny matrices plus Adam tensors."""
+    gen = torch.Generator().manual_seed(7)
+    ortho_a = [(96, 40), (40, 96), (64, 64), (3, 24, 40), (37, 13), (32, 5)]
+    ortho_b = [(33, 70), (70, 33)]
+    vec = [(50,), (7,)]
+    emb = [(200, 16)]
+    shapes = ortho_a + ortho_b + vec + emb
+    params = []
+    for sh in shapes:
+        init = torch.ones(sh) if len(sh) == 1 else torch.randn(sh, generator=gen) * 0.02
+        params.append(_leaf(init))
+    grads = _grads(gen, shapes, steps, 1e-3, outlier_rows=0.05)
+    na, nb, nv = len(ortho_a), len(ortho_b), len(vec)
+    groups = [
+        {'orthogonalize': True, 'params': params[:na], 'lr': 2e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.1},
+        {'orthogonalize': True, 'params': params[na:na + nb], 'lr': 1e-3, 'betas': (0.95, 0.95),
+         'weight_decay': 0.05, 'scaling_mode': 'jordan', 'force_per_neuron_norm': True},
+        {'orthogonalize': False, 'params': params[na + nb:na + nb + nv], 'lr': 1e-3, 'betas': (0.9, 0.95),
+         'weight_decay': 0.0, 'rectify': True},
+        {'orthogonalize': False, 'params': params[na + nb + nv:], 'lr': 1e-3, 'betas': (0.9, 0.99),
+         'weight_decay': 0.1, 'eps': 1e-8},
+    ]
+    return params, groups, lambda s, i, prm: grads[(s, i)]
+
+
+def md_small(steps: int = 20):
+    """decouple_md on the orthogonalized group (row/column gains and one scalar-gain group)."""
+    gen = torch.Generator().manual_seed(11)
+    md_split = [(48, 32), (32, 48), (40, 40), (2, 16, 24)]
+    md_scalar = [(24, 36)]
+    vec = [(64,)]
+    shapes = md_split + md_scalar + vec
+    params = []
+    for sh in shapes:
+        init = torch.ones(sh) if len(sh) == 1 else torch.randn(sh, generator=gen) * 0.02
+        params.append(_leaf(init))
+    grads = _grads(gen, shapes, steps, 1e-3, outlier_rows=0.05)
+    n1, n2 = len(md_split), len(md_scalar)
+    groups = [
+        {'orthogonalize': True, 'params': params[:n1], 'lr': 8e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.0,
+         'decouple_md': True},
+        {'orthogonalize': True, 'params': params[n1:n1 + n2], 'lr': 8e-3, 'betas': (0.9, 0.95),
+         'weight_decay': 0.05, 'decouple_md': True, 'split_gain': False, 'scaling_mode': 'moonlight'},
+        {'orthogonalize': False, 'params': params[n1 + n2:], 'lr': 1e-3, 'betas': (0.9, 0.95),
+         'weight_decay': 0.0},
+    ]
+    return params, groups, lambda s, i, prm: grads[(s, i)]

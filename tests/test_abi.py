@@ -1,0 +1,90 @@
+"""The C ABI library loads, exports every symbol of include/thorn_amd.h, and rejects bad input.
+
+CPU only: nothing here launches a kernel (error paths return before any HIP call).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from thorn_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / 'include' / 'thorn_amd.h'
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(thorn_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f'{n} has no ctypes signature in thorn_amd/_lib.py'
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_abi_version_and_struct_sizes():
+    lib = _lib.load()
+    assert lib.thorn_abi_version() == _lib.ABI_VERSION
+    assert lib.thorn_abi_struct_size(0) == _lib.ORTHO_MAT_DESC.itemsize
+    assert lib.thorn_abi_struct_size(1) == _lib.ORTHO_MAT_STEP.itemsize
+    assert lib.thorn_abi_struct_size(2) == _lib.ADAM_TENSOR_STEP.itemsize
+    assert lib.thorn_abi_struct_size(99) == 0
+
+
+def test_plan_rejects_bad_shapes():
+    with pytest.raises(_lib.ThornError, match='unsupported shape'):
+        _lib.OrthoPlan([0], [4], [0])
+    with pytest.raises(_lib.ThornError, match='exclusive'):
+        _lib.OrthoPlan([4], [4], [_lib.MAT_MD | _lib.MAT_MD_SCALAR])
+    with pytest.raises(_lib.ThornError, match='negative'):
+        _lib.AdamPlan([3, -1])
+
+
+def test_plan_sizes_and_empty_plans():
+    p = _lib.OrthoPlan([1024, 3072], [1024, 1024], [0, _lib.MAT_PER_ROW_NORM])
+    # three iterate copies per matrix (bf16 first iterate, f16 ping-pong) + two s x s buffers
+    want = 3 * 2 * (1024 * 1024 + 3072 * 1024) + 2 * 2 * 2 * 1024 * 1024
+    assert p.workspace_bytes >= want
+    assert p.table_bytes > 0
+    e = _lib.OrthoPlan([], [], [])
+    assert e.n == 0
+    a = _lib.AdamPlan([])
+    assert a.table_bytes > 0
+
+
+def test_fill_table_validates_pointers_without_gpu():
+    plan = _lib.OrthoPlan([8], [8], [_lib.MAT_MD])
+    steps = np.zeros(1, dtype=_lib.ORTHO_MAT_STEP)
+    host = np.zeros(plan.table_bytes, dtype=np.uint8)
+    with pytest.raises(_lib.ThornError, match='null p/g/m'):
+        plan.fill_table(steps, 256, 64, host.ctypes.data)
+    steps['p'] = 4096
+    steps['g'] = 8192
+    steps['m'] = 12288
+    with pytest.raises(_lib.ThornError, match='gain state'):
+        plan.fill_table(steps, 256, 64, host.ctypes.data)
+    with pytest.raises(_lib.ThornError, match='256-byte aligned'):
+        plan.fill_table(steps, 100, 64, host.ctypes.data)
+
+
+def test_step_rejects_zero_iterations():
+    plan = _lib.OrthoPlan([8], [8], [0])
+    with pytest.raises(_lib.ThornError, match='iters >= 1'):
+        plan.step(64, np.zeros((0, 3), dtype=np.float32), 0)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, '_lib', None)
+    monkeypatch.setattr(_lib, 'LIB_PATH', tmp_path / 'libthorn_amd.so')
+    with pytest.raises(ImportError, match='no non-HIP fallback'):
+        _lib.load()

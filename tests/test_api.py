@@ -1,0 +1,87 @@
+"""Host-side API parity with the reference (CPU only): constructor, groups, defaults, errors."""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn as nn
+
+import thorn_amd
+from oracle import thorn_oracle as O
+
+
+class Tiny(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.embed = nn.Embedding(10, 4)
+        self.proj = nn.Linear(4, 6)
+        self.conv = nn.Conv1d(2, 3, 5)
+        self.lm_head = nn.Linear(6, 10, bias=False)
+        self.norm = nn.LayerNorm(6)
+
+
+def test_auto_assign_matches_reference_rules():
+    m = Tiny()
+    opt = thorn_amd.THORN(m, lr=1e-3)
+    ref = O.OracleTHORN(m, lr=1e-3)
+    ids = lambda groups: [[id(p) for p in g['params']] for g in groups]
+    assert ids(opt.param_groups) == ids(ref.param_groups)
+    ortho = {id(p) for p in opt.param_groups[0]['params']}
+    assert id(m.proj.weight) in ortho and id(m.conv.weight) in ortho
+    assert id(m.embed.weight) not in ortho and id(m.lm_head.weight) not in ortho
+
+
+def test_group_defaults_match_reference():
+    p = nn.Parameter(torch.zeros(3, 3))
+    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3}])
+    ref = O.OracleTHORN([{'orthogonalize': True, 'params': [nn.Parameter(torch.zeros(3, 3))], 'lr': 1e-3}])
+    a = {k: v for k, v in opt.param_groups[0].items() if k != 'params'}
+    b = {k: v for k, v in ref.param_groups[0].items() if k != 'params'}
+    assert a == b
+    assert list(a) == list(b)
+
+
+def test_ortho_group_rejects_vectors():
+    with pytest.raises(AssertionError, match='ndim >= 2'):
+        thorn_amd.THORN([{'orthogonalize': True, 'params': [nn.Parameter(torch.zeros(3))], 'lr': 1e-3}])
+
+
+@pytest.mark.parametrize('bad,msg', [({'lr': -1.0}, 'learning rate'), ({'betas': (1.0, 0.9)}, 'beta1'),
+                                     ({'betas': (0.9, 1.5)}, 'beta2')])
+def test_invalid_hyperparameters_raise_value_error_at_step(bad, msg):
+    p = nn.Parameter(torch.zeros(3, 3))
+    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3, **bad}])
+    p.grad = torch.zeros(3, 3)
+    with pytest.raises(ValueError, match=msg):
+        opt.step()
+
+
+def test_unsupported_features_raise_not_implemented():
+    p = nn.Parameter(torch.zeros(3, 3))
+    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3, 'momentum_align': True}])
+    p.grad = torch.zeros(3, 3)
+    with pytest.raises(NotImplementedError, match='momentum_align'):
+        opt.step()
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    p = nn.Parameter(torch.zeros(3, 3))
+    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3}])
+    p.grad = torch.ones(3, 3)
+    with pytest.raises(RuntimeError, match='device tensors'):
+        opt.step()
+    assert torch.count_nonzero(p) == 0
+
+
+def test_coefficients_match_reference_goldens_exactly():
+    """The product's host solver reproduces the reference's coefficient tables bit for bit."""
+    from pathlib import Path
+    import numpy as np
+    from thorn_amd import _coeffs
+    z = np.load(Path(__file__).resolve().parent / 'golden' / 'coeffs.npz')
+    off = 0
+    for k, (l, it, sf, cu) in enumerate(z['settings']):
+        it = int(it)
+        a = np.asarray(_coeffs.ns_coefficients(float(l), it, float(sf), float(cu)))
+        np.testing.assert_array_equal(a, z['coeffs'][off:off + it])
+        off += it
+        assert list(_coeffs.gram_restarts(tuple(map(tuple, a)))) == [int(x) for x in z['restarts'][k] if x >= 0]

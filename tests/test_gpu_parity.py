@@ -1,0 +1,288 @@
+"""GPU parity: thorn_amd.THORN (HIP kernels on the MI355X) against the CPU oracle on identical inputs.
+
+Tolerances:
+  * fp32 optimizer state (moment, variance, gain moments): relative Frobenius <= 1e-5;
+  * the update delta p_new - p_old of orthogonalized matrices: relative Frobenius <= 2e-2 against
+    the oracle (the reference's float16 Gram Newton-Schulz; the HIP path runs the f16 plain
+    quintic on MFMA). Both are also compared with the exact update (the same step with the f64
+    closed-form polar map U phi(S) V^T), and the oracle-parity bound is widened by the
+    reference's own measured error against it. The widening only matters for tiny or skinny
+    matrices, where any float16 iteration with these coefficients is ~1-3e-2 off (a=8, b=-22,
+    c=15 cancel catastrophically near sigma=1; e.g. 2x2, 32x5); at the benchmark shapes the
+    reference's own error is ~1e-3;
+  * Adam-only tensors: delta p relative Frobenius <= 1e-4 (elementwise fp32 arithmetic).
+Inputs are generated on the CPU and copied bit for bit to the GPU.
+"""
+from __future__ import annotations
+
+import copy
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+from oracle import thorn_oracle as O  # noqa: E402
+from tests.golden import workloads  # noqa: E402
+
+DEV = 'cuda:0'
+
+
+def _thorn():
+    import thorn_amd
+    return thorn_amd
+
+
+def rel(a, b) -> float:
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    d = (a - b).norm().item()
+    n = b.norm().item()
+    return d / n if n > 0 else d
+
+
+def _clone_groups(groups, params_new):
+    """The same group dicts over another parameter list (params matched by position)."""
+    index = {}
+    flat = []
+    for g in groups:
+        for p in g['params']:
+            index[id(p)] = len(flat)
+            flat.append(p)
+    out = []
+    for g in groups:
+        d = {k: v for k, v in g.items() if k != 'params'}
+        d['params'] = [params_new[index[id(p)]] for p in g['params']]
+        out.append(d)
+    return out
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _copy_state_to(gpu_opt, gpu_params, cpu_opt, cpu_params):
+    """Teacher forcing: overwrite the GPU parameters and state with the oracle's."""
+    with torch.no_grad():
+        for pg, pc in zip(gpu_params, cpu_params):
+            pg.copy_(pc.to(DEV))
+            st = cpu_opt.state[pc]
+            gst = gpu_opt.state[pg]
+            for k, v in st.items():
+                if torch.is_tensor(v):
+                    gst[k].copy_(v.to(DEV))
+                else:
+                    gst[k] = v
+
+
+def exact_dp(p_old, g, m_prev, group: dict):
+    """The reference's step for one non-md orthogonalized matrix in float64 with the exact polar
+    map (thorn.py:1376-1381, 626-662 closed form, 704-766, 669-702)."""
+    grp = O.Group.from_dict(dict(group, params=[]))
+    b1 = grp.betas[0]
+    g64, m64, p64 = g.double(), m_prev.double(), p_old.double().clone()
+    m64 = m64 * b1 + g64
+    u = g64 + b1 * m64
+    coeffs = grp.coeffs[:grp.iters]
+    up = O.polar_closed_form(u, coeffs)
+    lr = grp.lr * O.lr_scale_ortho(up, grp)
+    if O.needs_neuron_norm(p_old, grp):
+        eps = float(torch.finfo(torch.float32).eps)
+        v_norm = up.norm(dim=(-2, -1), keepdim=True)
+        up = up * up.square().mean(dim=-1, keepdim=True).clamp_min(eps).rsqrt()
+        up = up * (v_norm / up.norm(dim=(-2, -1), keepdim=True).clamp_min(eps))
+    O.weight_decay_update(p64, up, weight_decay=grp.weight_decay, lr=lr)
+    return p64 - p_old.double()
+
+
+def check_ortho_dp(dpg, dpc, dpe, worst: dict, where: str) -> None:
+    """dpg: HIP update, dpc: oracle update, dpe: exact update (see the module docstring)."""
+    r, r_ex, ref_ex = rel(dpg, dpc), rel(dpg, dpe), rel(dpc, dpe)
+    worst['dp'] = max(worst.get('dp', 0.0), r)
+    worst['dp_exact'] = max(worst.get('dp_exact', 0.0), r_ex)
+    worst['ref_exact'] = max(worst.get('ref_exact', 0.0), ref_ex)
+    if r > 2e-2:
+        worst['widened'] = worst.get('widened', 0) + 1
+        _log(f'[gpu]   {where}: vs oracle {r:.2e}, vs exact {r_ex:.2e}, oracle vs exact {ref_ex:.2e}')
+    assert r <= 2e-2 + ref_ex, (where, r, r_ex, ref_ex)
+
+
+def _run_pair(build, steps, teacher_forced):
+    thorn_amd = _thorn()
+    torch.manual_seed(0)
+    params, groups, grads = build()
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    ggroups = _clone_groups(groups, gparams)
+    cpu = O.OracleTHORN(groups)
+    gpu = thorn_amd.THORN(ggroups)
+    worst = {'state': 0.0, 'dp': 0.0, 'dp_adam': 0.0, 'dp_exact': 0.0, 'ref_exact': 0.0, 'widened': 0}
+    group_of = {id(p): g for g in groups for p in g['params']}
+    for s in range(1, steps + 1):
+        if teacher_forced and s > 1:
+            _copy_state_to(gpu, gparams, cpu, params)
+        before_c = [p.detach().clone() for p in params]
+        before_g = [p.detach().clone() for p in gparams]
+        m_prev = [cpu.state[p]['moment'].clone() if 'moment' in cpu.state[p] else torch.zeros_like(p)
+                  for p in params]
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            g = grads(s, i, pc)
+            pc.grad = g.clone()
+            pg.grad = g.clone().to(DEV)
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            dpc = pc.detach() - before_c[i]
+            dpg = pg.detach().cpu() - before_g[i].cpu()
+            r = rel(dpg, dpc)
+            grp = group_of[id(pc)]
+            if not grp['orthogonalize']:
+                worst['dp_adam'] = max(worst['dp_adam'], r)
+            elif grp.get('decouple_md'):
+                worst['dp'] = max(worst['dp'], r)
+                assert r <= 2e-2, (s, i, r)
+            else:
+                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp)
+                check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
+            for k, v in cpu.state[pc].items():
+                if torch.is_tensor(v) and k != 'target_norm':
+                    worst['state'] = max(worst['state'], rel(gpu.state[pg][k], v))
+                elif not torch.is_tensor(v):
+                    assert gpu.state[pg][k] == v, (k, gpu.state[pg][k], v)
+            assert list(gpu.state[pg].keys()) == list(cpu.state[pc].keys())
+    return worst
+
+
+@pytest.mark.parametrize('name', ['config1', 'mixed_small'])
+def test_trajectory_free_running(name):
+    _log(f'[gpu] free-running trajectory {name}')
+    build = getattr(workloads, name)
+    w = _run_pair(build, 10, teacher_forced=False)
+    _log(f'[gpu] {name}: {w}')
+    assert w['state'] <= 1e-5, w
+    assert w['dp_adam'] <= 1e-4, w
+
+
+@pytest.mark.parametrize('name', ['config1', 'mixed_small', 'md_small'])
+def test_trajectory_teacher_forced(name):
+    _log(f'[gpu] teacher-forced trajectory {name}')
+    build = getattr(workloads, name)
+    w = _run_pair(build, 6, teacher_forced=True)
+    _log(f'[gpu] {name}: {w}')
+    assert w['state'] <= 1e-5, w
+    assert w['dp_adam'] <= 1e-4, w
+
+
+SHAPES = [(1, 17), (17, 1), (2, 2), (5, 3), (3, 5), (129, 130), (130, 129), (300, 7), (8, 520),
+          (256, 256), (1024, 64), (64, 1000), (257, 255), (4, 33, 17)]
+
+
+@pytest.mark.parametrize('shape', SHAPES)
+@pytest.mark.parametrize('wd', [0.0, 0.1])
+def test_single_matrix_update(shape, wd):
+    """One step on one matrix against the oracle; covers every tile-edge and transpose case."""
+    _log(f'[gpu] single matrix {shape} wd={wd}')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(sum(shape) * 7 + int(wd * 10))
+    p0 = torch.randn(shape, generator=g) * 0.02
+    grad = torch.randn(shape, generator=g) * 1e-3
+    pc = torch.nn.Parameter(p0.clone())
+    pg = torch.nn.Parameter(p0.clone().to(DEV))
+    grp = dict(orthogonalize=True, lr=1e-2, weight_decay=wd)
+    cpu = O.OracleTHORN([dict(grp, params=[pc])])
+    gpu = thorn_amd.THORN([dict(grp, params=[pg])])
+    pc.grad = grad.clone()
+    pg.grad = grad.clone().to(DEV)
+    cpu.step()
+    gpu.step()
+    torch.cuda.synchronize()
+    assert rel(gpu.state[pg]['moment'], cpu.state[pc]['moment']) <= 1e-6
+    dpg = pg.detach().cpu() - p0
+    dpc = pc.detach() - p0
+    dpe = exact_dp(p0, grad, torch.zeros_like(p0), grp)
+    w = {}
+    check_ortho_dp(dpg, dpc, dpe, w, f'{shape} wd={wd}')
+    _log(f'[gpu]   {w}')
+
+
+def test_ns_against_closed_form():
+    """lr=1, wd=0, square matrix: delta p = -scale * u', compared with U phi(S) V^T in f64."""
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(21)
+    for shape in [(256, 256), (512, 128)]:
+        _log(f'[gpu] closed form {shape}')
+        p0 = torch.zeros(shape)
+        grad = torch.randn(shape, generator=g)
+        pg = torch.nn.Parameter(p0.clone().to(DEV))
+        grp = dict(orthogonalize=True, lr=1.0, weight_decay=0.0, betas=(0.0, 0.0), scaling_mode='jordan')
+        gpu = thorn_amd.THORN([dict(grp, params=[pg])])
+        pg.grad = grad.clone().to(DEV)
+        gpu.step()
+        torch.cuda.synchronize()
+        scale = max(1, shape[0] / shape[1]) ** 0.5
+        u = -(pg.detach().cpu().double()) / scale
+        coeffs = O.optimal_composition(1e-3, 5, 0.03, 0.02)
+        ref = O.polar_closed_form(grad, coeffs)
+        r = rel(u, ref)
+        _log(f'[gpu]   rel vs closed form {r:.3e}')
+        assert r <= 1e-2
+
+
+def test_adam_only_group_matches_oracle_exactly_enough():
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(5)
+    shapes = [(1000,), (3, 7), (4099,), (1,), (64, 33)]
+    cps = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in shapes]
+    gps = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in cps]
+    for kw in [dict(eps=0.0, weight_decay=0.1), dict(eps=1e-8, weight_decay=0.0, rectify=True)]:
+        grp = dict(orthogonalize=False, lr=1e-3, **kw)
+        cpu = O.OracleTHORN([dict(grp, params=cps)])
+        gpu = thorn_amd.THORN([dict(grp, params=gps)])
+        for step in range(8):
+            p0 = [p.detach().clone() for p in cps]
+            for pc, pg in zip(cps, gps):
+                gr = torch.randn(pc.shape, generator=g) * 1e-3
+                pc.grad = gr.clone()
+                pg.grad = gr.clone().to(DEV)
+            cpu.step()
+            gpu.step()
+            torch.cuda.synchronize()
+            for k, (pc, pg) in enumerate(zip(cps, gps)):
+                for key in ('moment', 'variance'):
+                    assert rel(gpu.state[pg][key], cpu.state[pc][key]) <= 1e-6, (kw, step, key)
+                d = rel(pg.detach().cpu() - p0[k], pc.detach() - p0[k])
+                if step > 0 or not kw.get('rectify'):
+                    assert d <= 1e-4, (kw, step, k, d)
+            with torch.no_grad():
+                for pc, pg in zip(cps, gps):
+                    pg.copy_(pc.to(DEV))
+
+
+def test_state_dict_roundtrip_and_layout():
+    thorn_amd = _thorn()
+    params, groups, grads = workloads.md_small(2)
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    gpu = thorn_amd.THORN(_clone_groups(groups, gparams))
+    cpu = O.OracleTHORN(groups)
+    for i, (pc, pg) in enumerate(zip(params, gparams)):
+        pc.grad = grads(1, i, pc).clone()
+        pg.grad = grads(1, i, pc).clone().to(DEV)
+    cpu.step()
+    gpu.step()
+    sd_g, sd_c = gpu.state_dict(), cpu.state_dict()
+    assert sd_g['param_groups'] == sd_c['param_groups']
+    for k in sd_c['state']:
+        assert list(sd_g['state'][k].keys()) == list(sd_c['state'][k].keys())
+        for kk, v in sd_c['state'][k].items():
+            if torch.is_tensor(v):
+                assert sd_g['state'][k][kk].shape == v.shape and sd_g['state'][k][kk].dtype == v.dtype
+    gpu2 = thorn_amd.THORN(_clone_groups(groups, gparams))
+    gpu2.load_state_dict(copy.deepcopy(sd_g))
+    for i, (pc, pg) in enumerate(zip(params, gparams)):
+        pg.grad = grads(2, i, pc).clone().to(DEV)
+    gpu2.step()
+    torch.cuda.synchronize()
+    assert all(gpu2.state[p]['step'] == 3 for p in gparams)

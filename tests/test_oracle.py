@@ -1,0 +1,186 @@
+"""The CPU oracle (oracle/thorn_oracle.py) pinned against the reference's own outputs and closed forms.
+
+Golden vectors come from tests/golden/make_golden.py (the reference itself, run in the build
+container). With one CPU thread the restatement reproduces them bit for bit, which also pins the
+in-place op order of every step.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import thorn_oracle as O
+from tests.golden import workloads
+
+GOLD = Path(__file__).resolve().parent / 'golden'
+
+
+@pytest.fixture(autouse=True)
+def one_thread():
+    n = torch.get_num_threads()
+    torch.set_num_threads(1)
+    yield
+    torch.set_num_threads(n)
+
+
+def test_coefficients_match_reference():
+    z = np.load(GOLD / 'coeffs.npz')
+    off = 0
+    for k, (l, it, sf, cu) in enumerate(z['settings']):
+        it = int(it)
+        mine = np.asarray(O.optimal_composition(float(l), it, float(sf), float(cu)))
+        np.testing.assert_array_equal(mine, z['coeffs'][off:off + it])
+        off += it
+        ref_r = [int(x) for x in z['restarts'][k] if x >= 0]
+        assert O.gram_ns_restarts(*[tuple(c) for c in mine]) == ref_r
+
+
+def test_coefficients_closed_form_and_equioscillation():
+    # a degenerate interval returns the classic quintic (15/8, -10/8, 3/8)
+    a, b, c = O._optimal_quintic(1.0, 1.0)
+    assert (a, b, c) == (15 / 8, -10 / 8, 3 / 8)
+    # a Remez solution equioscillates: p - 1 reaches +-E at l, the two interior extrema and u
+    l, u = 0.1, 1.0
+    a, b, c = O._optimal_quintic(l, u)
+    xs = np.linspace(l, u, 200001)
+    p = a * xs + b * xs ** 3 + c * xs ** 5
+    err = np.abs(p - 1)
+    E = err.max()
+    assert abs(err[0] - E) < 1e-9 and abs(err[-1] - E) < 1e-9
+    # a perturbed quintic does worse (optimality)
+    p2 = (a * 1.001) * xs + b * xs ** 3 + c * xs ** 5
+    assert np.abs(p2 - 1).max() > E
+
+
+def test_polar_decomp_matches_reference():
+    z = np.load(GOLD / 'polar.npz')
+    coeffs = tuple(O.optimal_composition(1e-3, 5, 0.03, 0.02))
+    restarts = tuple(O.gram_ns_restarts(*coeffs))
+    k = 0
+    while f'in{k}' in z:
+        x = torch.from_numpy(z[f'in{k}'])
+        y = O.polar_decomp(x, coeffs, restarts)
+        np.testing.assert_array_equal(y.numpy(), z[f'out{k}'])
+        k += 1
+    assert k == 7
+
+
+@pytest.mark.parametrize('shape', [(32, 32), (24, 56), (56, 24), (3, 16, 40), (64, 192)])
+def test_polar_decomp_closed_form(shape):
+    """The f16 iteration equals U phi(S) V^T (f64 SVD) to f16 accuracy, for plain and Gram NS."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(shape, generator=g)
+    coeffs = tuple(O.optimal_composition(1e-3, 5, 0.03, 0.02))
+    restarts = tuple(O.gram_ns_restarts(*coeffs))
+    y = O.polar_decomp(x, coeffs, restarts).double()
+    ref = O.polar_closed_form(x, coeffs)
+    rel = ((y - ref).norm() / ref.norm()).item()
+    assert rel < 1e-2, rel
+    # a dropped iteration is caught
+    bad = O.polar_closed_form(x, coeffs[:-1])
+    assert ((y - bad).norm() / bad.norm()).item() > 3 * rel
+
+
+def test_pnn_matches_reference_and_invariants():
+    z = np.load(GOLD / 'pnn.npz')
+    u = torch.from_numpy(z['u_in'].copy())
+    p = torch.from_numpy(z['p_in'].copy())
+    O.per_neuron_norm_update(p, u, lr=3e-3, weight_decay=0.1)
+    np.testing.assert_array_equal(u.numpy(), z['u_out'])
+    np.testing.assert_array_equal(p.numpy(), z['p_out'])
+    # invariants (without the weight-decay term, which is added to u in place): Frobenius norm
+    # kept, row RMS equalized
+    u0 = torch.from_numpy(z['u_in']).double()
+    u1 = O.per_neuron_norm_update(None, torch.from_numpy(z['u_in'].copy())).double()
+    assert abs(u1.norm() / u0.norm() - 1) < 1e-6
+    rms = u1.square().mean(dim=-1).sqrt()
+    assert (rms.max() / rms.min() - 1) < 1e-5
+
+
+def test_adam_matches_reference():
+    z = np.load(GOLD / 'adam.npz')
+    cases = [dict(eps=0.0, weight_decay=0.1, degenerate=False), dict(eps=1e-8, weight_decay=0.0, degenerate=False),
+             dict(eps=0.0, weight_decay=0.05, degenerate=True)]
+    for k, case in enumerate(cases):
+        p = torch.from_numpy(z[f'p{k}'].copy())
+        m = torch.from_numpy(z[f'm{k}'].copy())
+        v = torch.from_numpy(z[f'v{k}'].copy())
+        for step in (1, 2, 7):
+            g = torch.from_numpy(z[f'g{k}_{step}'])
+            O.adam_update(p, g, m, v, step, beta1=0.9, beta2=0.95, lr=1e-3, **case)
+            np.testing.assert_array_equal(p.numpy(), z[f'p{k}_{step}'])
+            np.testing.assert_array_equal(m.numpy(), z[f'm{k}_{step}'])
+            np.testing.assert_array_equal(v.numpy(), z[f'v{k}_{step}'])
+
+
+def test_adam_special_case_equals_torch_adam():
+    """eps > 0, wd = 0, no rectification: THORN's Adam is torch.optim.Adam's update."""
+    g = torch.Generator().manual_seed(3)
+    p0 = torch.randn(500, generator=g)
+    grads = [torch.randn(500, generator=g) for _ in range(5)]
+    p = p0.clone()
+    m, v = torch.zeros(500), torch.zeros(500)
+    q = torch.nn.Parameter(p0.clone())
+    ta = torch.optim.Adam([q], lr=1e-2, betas=(0.9, 0.95), eps=1e-8)
+    for s, gr in enumerate(grads, start=1):
+        O.adam_update(p, gr, m, v, s, beta1=0.9, beta2=0.95, lr=1e-2, weight_decay=0.0, eps=1e-8)
+        q.grad = gr.clone()
+        ta.step()
+    torch.testing.assert_close(p, q.detach(), rtol=1e-5, atol=1e-7)
+
+
+def test_rect_equals_radam_term():
+    """compute_rect with rectify=True is RAdam's rectification (Liu et al. 2019, eq. in torch.optim.RAdam)."""
+    grp = O.Group(orthogonalize=False, params=[], lr=1e-3, rectify=True, betas=(0.9, 0.999))
+    b2 = 0.999
+    rho_inf = 2 / (1 - b2) - 1
+    for t in [1, 2, 5, 6, 10, 100, 1000]:
+        rho_t = rho_inf - 2 * t * b2 ** t / (1 - b2 ** t)
+        want = ((rho_t - 4) * (rho_t - 2) * rho_inf / ((rho_inf - 4) * (rho_inf - 2) * rho_t)) ** 0.5 if rho_t > 5 else None
+        got = O.compute_rect(grp, t)
+        if want is not None:
+            assert abs(got - want) < 1e-12
+        if rho_t <= 4:
+            assert got == 0.0
+    grp2 = O.Group(orthogonalize=False, params=[], lr=1e-3, rectify=False)
+    assert O.compute_rect(grp2, 1) == 1.0   # 0.0 ** 0.0
+
+
+def test_cautious_weight_decay_closed_form():
+    p = torch.tensor([1.0, -1.0, 2.0, -2.0, 0.0])
+    u = torch.tensor([0.5, 0.5, -0.5, -0.5, 1.0])
+    out = O.cautious_weight_decay(p, u.clone(), 0.1)
+    want = torch.tensor([0.5 + 0.1, 0.5, -0.5, -0.5 - 0.2, 1.0])
+    torch.testing.assert_close(out, want)
+
+
+def _run_oracle(build, steps, snap):
+    torch.manual_seed(0)
+    params, groups, grads = build()
+    opt = O.OracleTHORN(groups)
+    got = {}
+    for s in range(1, steps + 1):
+        for i, p in enumerate(params):
+            p.grad = grads(s, i, p).clone()
+        opt.step()
+        if s % snap == 0 or s == 1:
+            for i, p in enumerate(params):
+                got[f's{s}_p{i}'] = p.detach().clone().numpy()
+                for k, v in opt.state[p].items():
+                    got[f's{s}_{k}{i}'] = v.clone().numpy() if torch.is_tensor(v) else np.asarray(v)
+    return got
+
+
+@pytest.mark.parametrize('name,build,steps', [('traj_config1.npz', workloads.config1, 10),
+                                              ('traj_mixed.npz', workloads.mixed_small, 20),
+                                              ('traj_md.npz', workloads.md_small, 20)])
+def test_trajectories_match_reference(name, build, steps):
+    z = np.load(GOLD / name)
+    got = _run_oracle(build, steps, 10)
+    keys = [k for k in z.files if not k.startswith('init_')]
+    assert set(keys) == set(got), sorted(set(keys) ^ set(got))
+    for k in keys:
+        np.testing.assert_array_equal(got[k], z[k], err_msg=k)

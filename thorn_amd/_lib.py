@@ -1,0 +1,168 @@
+"""ctypes binding of libthorn_amd.so (the C ABI in include/thorn_amd.h).
+
+The library is loaded after ``torch`` so that both share one HIP runtime (the library's
+``libamdhip64.so.7`` dependency resolves to the copy torch already loaded). There is no fallback:
+if the library is missing or fails to load, importing the optimizer's step path raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+import torch  # noqa: F401  (loads the HIP runtime first)
+
+LIB_PATH = Path(__file__).resolve().parent / 'libthorn_amd.so'
+
+THORN_OK = 0
+THORN_ERR_INVALID = 1
+THORN_ERR_HIP = 2
+THORN_ERR_UNSUPPORTED = 3
+
+MAT_PER_ROW_NORM = 1
+MAT_MD = 2
+MAT_MD_SCALAR = 4
+STEP_KEEP_GRAD = 8
+STEP_APPLY = 16
+
+# numpy mirrors of the C structs (align=True reproduces the C layout on x86-64)
+ORTHO_MAT_DESC = np.dtype([('rows', np.int64), ('cols', np.int64), ('flags', np.int32),
+                           ('reserved', np.int32)], align=True)
+ORTHO_MAT_STEP = np.dtype([
+    ('p', np.uint64), ('g', np.uint64), ('m', np.uint64),
+    ('row_gain', np.uint64), ('col_gain', np.uint64),
+    ('row_gain_moment', np.uint64), ('row_gain_variance', np.uint64),
+    ('col_gain_moment', np.uint64), ('col_gain_variance', np.uint64),
+    ('target_norm', np.uint64),
+    ('eta', np.float32), ('weight_decay', np.float32), ('beta1', np.float32),
+    ('gain_lr', np.float32), ('gain_beta2', np.float32), ('gain_w1', np.float32),
+    ('gain_w2', np.float32), ('gain_eps', np.float32),
+    ('gain_bc1', np.float32), ('gain_bc2', np.float32),
+    ('step_flags', np.int32), ('reserved', np.int32),
+], align=True)
+ADAM_TENSOR_STEP = np.dtype([
+    ('p', np.uint64), ('g', np.uint64), ('m', np.uint64), ('v', np.uint64),
+    ('lr', np.float32), ('weight_decay', np.float32), ('beta2', np.float32),
+    ('w1', np.float32), ('w2', np.float32), ('bc1', np.float32), ('bc2', np.float32),
+    ('eps', np.float32), ('apply', np.int32), ('degenerate', np.int32),
+], align=True)
+
+# every exported symbol of include/thorn_amd.h: name -> (restype, argtypes)
+_vp, _sz, _i, _f, _cp = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
+SIGNATURES = {
+    'thorn_abi_version': (_i, []),
+    'thorn_last_error': (_cp, []),
+    'thorn_abi_struct_size': (_sz, [_i]),
+    'thorn_ortho_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
+    'thorn_ortho_plan_destroy': (None, [_vp]),
+    'thorn_ortho_workspace_bytes': (_sz, [_vp]),
+    'thorn_ortho_table_bytes': (_sz, [_vp]),
+    'thorn_ortho_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
+    'thorn_ortho_step': (_i, [_vp, _vp, _vp, _i, _vp]),
+    'thorn_adam_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
+    'thorn_adam_plan_destroy': (None, [_vp]),
+    'thorn_adam_table_bytes': (_sz, [_vp]),
+    'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp]),
+    'thorn_adam_step': (_i, [_vp, _vp, _vp]),
+}
+ABI_VERSION = 1
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads and checks the library once; raises ImportError when it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(f'{LIB_PATH} is missing: build it with `python -m thorn_amd.build` '
+                          '(hipcc, gfx950). THORN has no non-HIP fallback.')
+    lib = ctypes.CDLL(os.fspath(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.thorn_abi_version()
+    if ver != ABI_VERSION:
+        raise ImportError(f'{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it')
+    for which, dt in enumerate((ORTHO_MAT_DESC, ORTHO_MAT_STEP, ADAM_TENSOR_STEP)):
+        size = lib.thorn_abi_struct_size(which)
+        if size != dt.itemsize:
+            raise ImportError(f'ABI struct {which} is {size} bytes in the library but {dt.itemsize} '
+                              'in the binding; rebuild the library')
+    _lib = lib
+    return lib
+
+
+class ThornError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str) -> None:
+    if rc != THORN_OK:
+        msg = load().thorn_last_error().decode(errors='replace')
+        raise ThornError(f'{what} failed (code {rc}): {msg}')
+
+
+class OrthoPlan:
+    """Host plan of one orthogonalized matrix set (shapes and per-matrix options)."""
+
+    def __init__(self, rows, cols, flags):
+        lib = load()
+        self._lib = lib
+        descs = np.zeros(len(rows), dtype=ORTHO_MAT_DESC)
+        descs['rows'] = rows
+        descs['cols'] = cols
+        descs['flags'] = flags
+        h = ctypes.c_void_p()
+        check(lib.thorn_ortho_plan_create(descs.ctypes.data if len(rows) else None, len(rows),
+                                          ctypes.byref(h)), 'thorn_ortho_plan_create')
+        self.handle = h
+        self.n = len(rows)
+        self.workspace_bytes = lib.thorn_ortho_workspace_bytes(h)
+        self.table_bytes = lib.thorn_ortho_table_bytes(h)
+
+    def fill_table(self, steps: np.ndarray, workspace: int, table_dev: int, table_host: int) -> None:
+        check(self._lib.thorn_ortho_fill_table(self.handle, steps.ctypes.data, workspace, table_dev,
+                                               table_host), 'thorn_ortho_fill_table')
+
+    def step(self, table_dev: int, coeffs: np.ndarray, stream: int) -> None:
+        iters = coeffs.shape[0]
+        check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, stream),
+              'thorn_ortho_step')
+
+    def __del__(self):
+        h = getattr(self, 'handle', None)
+        if h is not None and h.value:
+            self._lib.thorn_ortho_plan_destroy(h)
+            self.handle = None
+
+
+class AdamPlan:
+    """Host plan of one multi-tensor Adam launch (element counts of every tensor)."""
+
+    def __init__(self, numels):
+        lib = load()
+        self._lib = lib
+        arr = np.asarray(numels, dtype=np.int64)
+        h = ctypes.c_void_p()
+        check(lib.thorn_adam_plan_create(arr.ctypes.data if len(arr) else None, len(arr), ctypes.byref(h)),
+              'thorn_adam_plan_create')
+        self.handle = h
+        self.n = len(arr)
+        self.table_bytes = lib.thorn_adam_table_bytes(h)
+
+    def fill_table(self, steps: np.ndarray, table_dev: int, table_host: int) -> None:
+        check(self._lib.thorn_adam_fill_table(self.handle, steps.ctypes.data, table_dev, table_host),
+              'thorn_adam_fill_table')
+
+    def step(self, table_dev: int, stream: int) -> None:
+        check(self._lib.thorn_adam_step(self.handle, table_dev, stream), 'thorn_adam_step')
+
+    def __del__(self):
+        h = getattr(self, 'handle', None)
+        if h is not None and h.value:
+            self._lib.thorn_adam_plan_destroy(h)
+            self.handle = None

@@ -1,0 +1,439 @@
+// C ABI of the THORN step (declared in include/thorn_amd.h): host-side plans, device tables and
+// the launch sequence. One translation unit: the kernel sources are included below.
+#include "../../include/thorn_amd.h"
+#include "ns_kernels.hip"
+#include "update_kernels.hip"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(THORN_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return THORN_OK;
+}
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Offsets of one matrix's workspace buffers (bytes from the workspace base; kNone = absent).
+constexpr size_t kNone = ~size_t(0);
+struct MatLayout {
+    int32_t rows, cols, s, l, ldx, lds, tall, flags;
+    int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
+    size_t x0, xa, xb, gram, poly, uout, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
+};
+
+struct TaskOffsets {
+    size_t order, starts;
+    int32_t n, total;
+};
+
+}  // namespace
+
+struct thorn_ortho_plan {
+    std::vector<MatLayout> mats;
+    size_t ws_bytes = 0;
+    size_t table_bytes = 0;
+    size_t mats_off = 0;
+    TaskOffsets pre{}, sym{}, g3{}, pnn{}, md{};
+    std::vector<int32_t> pre_order, sym_order, g3_order, pnn_order, md_order;
+};
+
+struct thorn_adam_plan {
+    std::vector<int64_t> numel;
+    std::vector<int32_t> order;
+    std::vector<int32_t> starts;
+    size_t table_bytes = 0;
+    size_t starts_off = 0, order_off = 0;
+    int32_t total = 0;
+};
+
+namespace {
+
+using thorn::NsCfg;
+
+// Appends a task list (order + block starts) to the table layout.
+TaskOffsets add_tasks(size_t& off, const std::vector<int32_t>& order, const std::vector<int64_t>& blocks_of) {
+    TaskOffsets t;
+    t.n = static_cast<int32_t>(order.size());
+    int64_t total = 0;
+    for (int32_t i : order) total += blocks_of[i];
+    t.total = static_cast<int32_t>(total);
+    t.order = off;
+    off = align_up(off + sizeof(int32_t) * std::max<size_t>(1, order.size()), 16);
+    t.starts = off;
+    off = align_up(off + sizeof(int32_t) * (order.size() + 1), 16);
+    return t;
+}
+
+void write_tasks(char* host, const TaskOffsets& t, const std::vector<int32_t>& order,
+                 const std::vector<int64_t>& blocks_of) {
+    int32_t* o = reinterpret_cast<int32_t*>(host + t.order);
+    int32_t* s = reinterpret_cast<int32_t*>(host + t.starts);
+    int32_t acc = 0;
+    for (size_t k = 0; k < order.size(); ++k) {
+        o[k] = order[k];
+        s[k] = acc;
+        acc += static_cast<int32_t>(blocks_of[order[k]]);
+    }
+    s[order.size()] = acc;
+}
+
+thorn::TaskList task_list(const char* dev, const TaskOffsets& t) {
+    thorn::TaskList tl;
+    tl.order = reinterpret_cast<const int32_t*>(dev + t.order);
+    tl.starts = reinterpret_cast<const int32_t*>(dev + t.starts);
+    tl.n = t.n;
+    tl.total = t.total;
+    return tl;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int thorn_abi_version(void) { return THORN_ABI_VERSION; }
+
+const char* thorn_last_error(void) { return g_last_error.c_str(); }
+
+size_t thorn_abi_struct_size(int which) {
+    switch (which) {
+        case 0: return sizeof(ThornOrthoMatDesc);
+        case 1: return sizeof(ThornOrthoMatStep);
+        case 2: return sizeof(ThornAdamTensorStep);
+        default: return 0;
+    }
+}
+
+int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_plan_t* out) {
+    if (!out) return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: out is null");
+    *out = nullptr;
+    if (n < 0 || (n > 0 && !descs)) return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: bad matrix list");
+    auto* plan = new thorn_ortho_plan();
+    size_t ws = 0;
+    auto take = [&ws](size_t bytes) {
+        if (bytes == 0) return kNone;
+        const size_t o = ws;
+        ws = align_up(ws + bytes, kAlign);
+        return o;
+    };
+    for (int i = 0; i < n; ++i) {
+        const ThornOrthoMatDesc& d = descs[i];
+        if (d.rows <= 0 || d.cols <= 0 || d.rows > (1 << 20) || d.cols > (1 << 20) ||
+            d.rows * d.cols > (int64_t(1) << 30)) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: matrix " + std::to_string(i) +
+                                               " has unsupported shape " + std::to_string(d.rows) + "x" +
+                                               std::to_string(d.cols));
+        }
+        if ((d.flags & THORN_MAT_MD) && (d.flags & THORN_MAT_MD_SCALAR)) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: MD and MD_SCALAR are exclusive");
+        }
+        MatLayout L{};
+        L.rows = static_cast<int32_t>(d.rows);
+        L.cols = static_cast<int32_t>(d.cols);
+        L.s = std::min(L.rows, L.cols);
+        L.l = std::max(L.rows, L.cols);
+        L.tall = L.rows > L.cols;
+        L.ldx = static_cast<int32_t>(align_up(L.cols, 8));
+        L.lds = static_cast<int32_t>(align_up(L.s, 8));
+        L.flags = d.flags & (THORN_MAT_PER_ROW_NORM | THORN_MAT_MD | THORN_MAT_MD_SCALAR);
+        L.mom_tiles_r = static_cast<int32_t>(cdiv(L.rows, thorn::kTileR));
+        L.mom_tiles_c = static_cast<int32_t>(cdiv(L.cols, thorn::kTileC));
+        L.g3_tiles_m = static_cast<int32_t>(cdiv(L.rows, NsCfg::BM));
+        L.g3_tiles_n = static_cast<int32_t>(cdiv(L.cols, NsCfg::BN));
+        const int32_t T = static_cast<int32_t>(cdiv(L.s, NsCfg::BM));
+        L.sym_tiles = T * (T + 1) / 2;
+        const bool pnn = L.flags & THORN_MAT_PER_ROW_NORM;
+        const bool md = L.flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR);
+        const int64_t mom_tiles = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
+        L.n_psq = md ? static_cast<int32_t>(pnn ? mom_tiles : int64_t(L.g3_tiles_m) * L.g3_tiles_n) : 0;
+        const size_t xbytes = size_t(L.rows) * L.ldx * 2;
+        const size_t sbytes = size_t(L.s) * L.lds * 2;
+        L.x0 = take(2 * xbytes);   // fp32
+        L.xa = take(xbytes);
+        L.xb = take(xbytes);
+        L.gram = take(sbytes);
+        L.poly = take(sbytes);
+        L.uout = pnn ? take(xbytes) : kNone;
+        L.normpart = take(sizeof(float) * mom_tiles);
+        L.rowpart = md ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
+        L.colpart = (L.flags & THORN_MAT_MD) ? take(sizeof(float) * size_t(L.mom_tiles_r) * L.cols) : kNone;
+        L.rowsqpart = pnn ? take(sizeof(float) * size_t(L.g3_tiles_n) * L.rows) : kNone;
+        L.rowscale = pnn ? take(sizeof(float) * L.rows) : kNone;
+        L.scal = take(sizeof(float) * 8);
+        L.psqpart = md ? take(sizeof(float) * L.n_psq) : kNone;
+        plan->mats.push_back(L);
+    }
+    plan->ws_bytes = std::max<size_t>(ws, kAlign);
+
+    // Task orders: symmetric phases longest contraction first, the rest in matrix order.
+    std::vector<int32_t> all(n);
+    for (int i = 0; i < n; ++i) all[i] = i;
+    plan->pre_order = all;
+    plan->sym_order = all;
+    std::stable_sort(plan->sym_order.begin(), plan->sym_order.end(),
+                     [&](int a, int b) { return plan->mats[a].l > plan->mats[b].l; });
+    plan->g3_order = plan->sym_order;
+    for (int i = 0; i < n; ++i) {
+        if (plan->mats[i].flags & THORN_MAT_PER_ROW_NORM) plan->pnn_order.push_back(i);
+        if (plan->mats[i].flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
+    }
+    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n);
+    for (int i = 0; i < n; ++i) {
+        const MatLayout& L = plan->mats[i];
+        mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
+        sym_blocks[i] = L.sym_tiles;
+        g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
+    }
+    size_t off = 0;
+    plan->mats_off = 0;
+    off = align_up(sizeof(thorn::OrthoMat) * std::max(1, n), 64);
+    plan->pre = add_tasks(off, plan->pre_order, mom_blocks);
+    plan->sym = add_tasks(off, plan->sym_order, sym_blocks);
+    plan->g3 = add_tasks(off, plan->g3_order, g3_blocks);
+    plan->pnn = add_tasks(off, plan->pnn_order, mom_blocks);
+    plan->md = add_tasks(off, plan->md_order, mom_blocks);
+    plan->table_bytes = off;
+    for (const TaskOffsets* t : {&plan->pre, &plan->sym, &plan->g3}) {
+        if (int64_t(t->total) >= (int64_t(1) << 31) - 1) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: grid too large");
+        }
+    }
+    *out = plan;
+    return THORN_OK;
+}
+
+void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan) { delete plan; }
+
+size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan) { return plan ? plan->ws_bytes : 0; }
+
+size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan) { return plan ? plan->table_bytes : 0; }
+
+int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
+                           void* table_dev, void* table_host) {
+    if (!plan || !table_dev || !table_host) return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: null argument");
+    const int n = static_cast<int>(plan->mats.size());
+    if (n > 0 && (!steps || !workspace)) return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: null steps/workspace");
+    if ((reinterpret_cast<uintptr_t>(workspace) % kAlign) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: workspace must be 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(table_dev) % 64) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: table_dev must be 64-byte aligned");
+    char* host = static_cast<char*>(table_host);
+    std::memset(host, 0, plan->table_bytes);
+    char* ws = static_cast<char*>(workspace);
+    auto at = [ws](size_t o) -> void* { return o == kNone ? nullptr : ws + o; };
+    auto* mats = reinterpret_cast<thorn::OrthoMat*>(host + plan->mats_off);
+    for (int i = 0; i < n; ++i) {
+        const MatLayout& L = plan->mats[i];
+        const ThornOrthoMatStep& S = steps[i];
+        const bool md = L.flags & THORN_MAT_MD, mds = L.flags & THORN_MAT_MD_SCALAR;
+        if (!S.p || !S.g || !S.m)
+            return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: matrix " + std::to_string(i) + " has a null p/g/m");
+        if ((md && (!S.row_gain || !S.col_gain || !S.row_gain_moment || !S.row_gain_variance ||
+                    !S.col_gain_moment || !S.col_gain_variance || !S.target_norm)) ||
+            (mds && (!S.row_gain || !S.row_gain_moment || !S.row_gain_variance || !S.target_norm)))
+            return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: matrix " + std::to_string(i) + " lacks gain state");
+        if (((reinterpret_cast<uintptr_t>(S.p) | reinterpret_cast<uintptr_t>(S.g) |
+              reinterpret_cast<uintptr_t>(S.m)) & 3u) != 0)
+            return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: fp32 tensors must be 4-byte aligned");
+        thorn::OrthoMat& M = mats[i];
+        M.p = S.p; M.g = S.g; M.m = S.m;
+        M.rg = S.row_gain; M.cg = S.col_gain;
+        M.rgm = S.row_gain_moment; M.rgv = S.row_gain_variance;
+        M.cgm = S.col_gain_moment; M.cgv = S.col_gain_variance;
+        M.target = S.target_norm;
+        M.x0 = static_cast<float*>(at(L.x0));
+        M.xa = static_cast<_Float16*>(at(L.xa));
+        M.xb = static_cast<_Float16*>(at(L.xb));
+        M.gram = static_cast<_Float16*>(at(L.gram));
+        M.poly = static_cast<_Float16*>(at(L.poly));
+        M.uout = static_cast<_Float16*>(at(L.uout));
+        M.normpart = static_cast<float*>(at(L.normpart));
+        M.rowpart = static_cast<float*>(at(L.rowpart));
+        M.colpart = static_cast<float*>(at(L.colpart));
+        M.rowsqpart = static_cast<float*>(at(L.rowsqpart));
+        M.rowscale = static_cast<float*>(at(L.rowscale));
+        M.scal = static_cast<float*>(at(L.scal));
+        M.psqpart = static_cast<float*>(at(L.psqpart));
+        M.rows = L.rows; M.cols = L.cols; M.s = L.s; M.l = L.l;
+        M.ldx = L.ldx; M.lds = L.lds; M.tall = L.tall;
+        int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
+        if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m)) flags |= thorn::kFlagVec4;
+        M.flags = flags;
+        M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
+        M.gain_lr = S.gain_lr; M.gain_beta2 = S.gain_beta2; M.gain_w1 = S.gain_w1; M.gain_w2 = S.gain_w2;
+        M.gain_eps = S.gain_eps; M.gain_bc1 = S.gain_bc1; M.gain_bc2 = S.gain_bc2;
+        M.mom_tiles_r = L.mom_tiles_r; M.mom_tiles_c = L.mom_tiles_c;
+        M.g3_tiles_m = L.g3_tiles_m; M.g3_tiles_n = L.g3_tiles_n;
+        M.n_psq = L.n_psq;
+        M.apply_tiles = L.mom_tiles_r * L.mom_tiles_c;
+    }
+    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n);
+    for (int i = 0; i < n; ++i) {
+        const MatLayout& L = plan->mats[i];
+        mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
+        sym_blocks[i] = L.sym_tiles;
+        g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
+    }
+    write_tasks(host, plan->pre, plan->pre_order, mom_blocks);
+    write_tasks(host, plan->sym, plan->sym_order, sym_blocks);
+    write_tasks(host, plan->g3, plan->g3_order, g3_blocks);
+    write_tasks(host, plan->pnn, plan->pnn_order, mom_blocks);
+    write_tasks(host, plan->md, plan->md_order, mom_blocks);
+    return THORN_OK;
+}
+
+int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+                     void* stream) {
+    if (!plan || !table_dev) return fail(THORN_ERR_INVALID, "thorn_ortho_step: null argument");
+    if (iters < 1 || !coeffs) return fail(THORN_ERR_INVALID, "thorn_ortho_step: need iters >= 1 and coefficients");
+    const int n = static_cast<int>(plan->mats.size());
+    if (n == 0) return THORN_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const char* dev = static_cast<const char*>(table_dev);
+    const auto* mats = reinterpret_cast<const thorn::OrthoMat*>(dev + plan->mats_off);
+    int rc;
+    hipLaunchKernelGGL(thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0, st, mats, task_list(dev, plan->pre));
+    if ((rc = check_launch("ortho_pre_kernel"))) return rc;
+    hipLaunchKernelGGL(thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
+    if ((rc = check_launch("ortho_norm_kernel"))) return rc;
+    const thorn::TaskList sym = task_list(dev, plan->sym), g3 = task_list(dev, plan->g3);
+    for (int it = 0; it < iters; ++it) {
+        if (it == 0)
+            hipLaunchKernelGGL(thorn::ns_gram_kernel<true>, dim3(sym.total), dim3(256), 0, st, mats, sym, it);
+        else
+            hipLaunchKernelGGL(thorn::ns_gram_kernel<false>, dim3(sym.total), dim3(256), 0, st, mats, sym, it);
+        if ((rc = check_launch("ns_gram_kernel"))) return rc;
+        hipLaunchKernelGGL(thorn::ns_poly_kernel, dim3(sym.total), dim3(256), 0, st, mats, sym,
+                           coeffs[3 * it], coeffs[3 * it + 1], coeffs[3 * it + 2]);
+        if ((rc = check_launch("ns_poly_kernel"))) return rc;
+        if (it == 0)
+            hipLaunchKernelGGL(thorn::ns_update_kernel<true>, dim3(g3.total), dim3(256), 0, st, mats, g3, it,
+                               it == iters - 1 ? 1 : 0);
+        else
+            hipLaunchKernelGGL(thorn::ns_update_kernel<false>, dim3(g3.total), dim3(256), 0, st, mats, g3, it,
+                               it == iters - 1 ? 1 : 0);
+        if ((rc = check_launch("ns_update_kernel"))) return rc;
+    }
+    if (plan->pnn.n > 0) {
+        const thorn::TaskList pnn = task_list(dev, plan->pnn);
+        hipLaunchKernelGGL(thorn::ortho_rowstats_kernel, dim3(pnn.n), dim3(256), 0, st, mats, pnn.order);
+        if ((rc = check_launch("ortho_rowstats_kernel"))) return rc;
+        hipLaunchKernelGGL(thorn::ortho_pnn_apply_kernel, dim3(pnn.total), dim3(256), 0, st, mats, pnn);
+        if ((rc = check_launch("ortho_pnn_apply_kernel"))) return rc;
+    }
+    if (plan->md.n > 0) {
+        const thorn::TaskList md = task_list(dev, plan->md);
+        hipLaunchKernelGGL(thorn::ortho_md_factor_kernel, dim3(md.n), dim3(256), 0, st, mats, md.order);
+        if ((rc = check_launch("ortho_md_factor_kernel"))) return rc;
+        hipLaunchKernelGGL(thorn::ortho_md_rescale_kernel, dim3(md.total), dim3(256), 0, st, mats, md);
+        if ((rc = check_launch("ortho_md_rescale_kernel"))) return rc;
+    }
+    return THORN_OK;
+}
+
+int thorn_adam_plan_create(const int64_t* numel, int n, thorn_adam_plan_t* out) {
+    if (!out) return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: out is null");
+    *out = nullptr;
+    if (n < 0 || (n > 0 && !numel)) return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: bad tensor list");
+    auto* plan = new thorn_adam_plan();
+    plan->numel.assign(numel, numel + n);
+    int64_t acc = 0;
+    for (int i = 0; i < n; ++i) {
+        if (numel[i] < 0) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: negative numel");
+        }
+        if (numel[i] == 0) continue;
+        plan->order.push_back(i);
+        plan->starts.push_back(static_cast<int32_t>(acc));
+        acc += cdiv(numel[i], thorn::kAdamChunk);
+        if (acc >= (int64_t(1) << 31) - 1) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: grid too large");
+        }
+    }
+    plan->starts.push_back(static_cast<int32_t>(acc));
+    plan->total = static_cast<int32_t>(acc);
+    size_t off = align_up(sizeof(thorn::AdamTensor) * std::max(1, n), 64);
+    plan->order_off = off;
+    off = align_up(off + sizeof(int32_t) * std::max<size_t>(1, plan->order.size()), 16);
+    plan->starts_off = off;
+    off = align_up(off + sizeof(int32_t) * plan->starts.size(), 16);
+    plan->table_bytes = off;
+    *out = plan;
+    return THORN_OK;
+}
+
+void thorn_adam_plan_destroy(thorn_adam_plan_t plan) { delete plan; }
+
+size_t thorn_adam_table_bytes(thorn_adam_plan_t plan) { return plan ? plan->table_bytes : 0; }
+
+int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* table_dev,
+                          void* table_host) {
+    if (!plan || !table_dev || !table_host) return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: null argument");
+    const int n = static_cast<int>(plan->numel.size());
+    if (n > 0 && !steps) return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: null steps");
+    if ((reinterpret_cast<uintptr_t>(table_dev) % 64) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: table_dev must be 64-byte aligned");
+    char* host = static_cast<char*>(table_host);
+    std::memset(host, 0, plan->table_bytes);
+    auto* ts = reinterpret_cast<thorn::AdamTensor*>(host);
+    for (int i = 0; i < n; ++i) {
+        const ThornAdamTensorStep& S = steps[i];
+        if (plan->numel[i] > 0 && (!S.g || !S.m || !S.v || (S.apply && !S.p)))
+            return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: tensor " + std::to_string(i) + " has a null pointer");
+        if (((reinterpret_cast<uintptr_t>(S.p) | reinterpret_cast<uintptr_t>(S.g) |
+              reinterpret_cast<uintptr_t>(S.m) | reinterpret_cast<uintptr_t>(S.v)) & 3u) != 0)
+            return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: fp32 tensors must be 4-byte aligned");
+        thorn::AdamTensor& T = ts[i];
+        T.p = S.p; T.g = S.g; T.m = S.m; T.v = S.v;
+        T.n = plan->numel[i];
+        T.lr = S.lr; T.wd = S.weight_decay; T.beta2 = S.beta2; T.w1 = S.w1; T.w2 = S.w2;
+        T.bc1 = S.bc1; T.bc2 = S.bc2; T.eps = S.eps;
+        int32_t f = 0;
+        if (S.apply) f |= thorn::kAdamApply;
+        if (S.degenerate) f |= thorn::kAdamDegenerate;
+        if (S.eps == 0.f) f |= thorn::kAdamAtan2;
+        if ((!S.apply || aligned16(S.p)) && aligned16(S.g) && aligned16(S.m) && aligned16(S.v)) f |= thorn::kAdamVec4;
+        T.flags = f;
+    }
+    std::memcpy(host + plan->order_off, plan->order.data(), sizeof(int32_t) * plan->order.size());
+    std::memcpy(host + plan->starts_off, plan->starts.data(), sizeof(int32_t) * plan->starts.size());
+    return THORN_OK;
+}
+
+int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream) {
+    if (!plan || !table_dev) return fail(THORN_ERR_INVALID, "thorn_adam_step: null argument");
+    if (plan->total == 0) return THORN_OK;
+    const char* dev = static_cast<const char*>(table_dev);
+    thorn::TaskList tl;
+    tl.order = reinterpret_cast<const int32_t*>(dev + plan->order_off);
+    tl.starts = reinterpret_cast<const int32_t*>(dev + plan->starts_off);
+    tl.n = static_cast<int32_t>(plan->order.size());
+    tl.total = plan->total;
+    hipLaunchKernelGGL(thorn::adam_kernel, dim3(plan->total), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<const thorn::AdamTensor*>(dev), tl);
+    return check_launch("adam_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,166 @@
+// Shared device helpers and table layouts for the THORN step on gfx950 (MI355X).
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, the f16 MFMA builtins and the
+// ds_read_tr16_b64 LDS transpose read. Lane layouts used below were checked on an MI355X:
+//   v_mfma_f32_32x32x16_f16: lane l feeds A[row l%32][k 8*(l/32)+e] and B[k 8*(l/32)+e][col l%32],
+//     and holds D[8*(r/4) + 4*(l/32) + r%4][l%32] in accumulator register r.
+//   ds_read_tr16_b64: in each 16-lane group, lane i (a=i/4, b=i%4) receives element b of the
+//     8-byte chunks addressed by lanes a, a+4, a+8, a+12.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace thorn {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((vector_size(8)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------------------
+// Numeric helpers
+// ---------------------------------------------------------------------------------------------
+
+// log(1 + exp(x)) with PyTorch's default threshold: x > 20 returns x (F.softplus, beta=1).
+__device__ __forceinline__ float softplus_f(float x) {
+    return x > 20.f ? x : log1pf(expf(x));
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) {
+    return 1.f / (1.f + expf(-x));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 reduced separately).
+__device__ __forceinline__ float halfwave_sum(float v) {
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Deterministic block reduction over blockDim.x threads (a multiple of 64, at most 1024).
+// Every thread returns the total. `scratch` holds at least blockDim.x / 64 floats.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wid] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += scratch[i];
+    return t;
+}
+
+// Finds the task k with starts[k] <= b < starts[k+1] (starts has n+1 entries, ascending).
+__device__ __forceinline__ int find_task(const int32_t* starts, int n, int b) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (starts[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Device tables (built on the host by the plan, copied to the device by the caller each step)
+// ---------------------------------------------------------------------------------------------
+
+enum OrthoFlags : int32_t {
+    kFlagPNN = 1,        // per-row normalization of the update (tall, or forced)
+    kFlagMD = 2,         // decoupled magnitude/direction with row and column gains
+    kFlagMDScalar = 4,   // decoupled magnitude/direction with one scalar gain
+    kFlagKeepGrad = 8,   // write g *= gain back into the user's gradient (none_grad=False)
+    kFlagApply = 16,     // the parameter is updated this step
+    kFlagVec4 = 32,      // p, g, m 16-byte aligned and cols % 4 == 0: float4 path
+};
+
+// One matrix of an orthogonalized group. All user tensors are fp32, row-major rows x cols,
+// contiguous; workspace buffers use padded leading dimensions (multiples of 8 elements).
+struct OrthoMat {
+    float* p;
+    float* g;
+    float* m;
+    float* rg;   // row gains (rows) or the scalar gain
+    float* cg;   // column gains (cols)
+    float* rgm;
+    float* rgv;
+    float* cgm;
+    float* cgv;
+    const float* target;   // decoupled-magnitude target norm (0-d)
+
+    float* x0;         // rows x ldx, u = g + beta1*m (fp32, unnormalized)
+    _Float16* xa;      // rows x ldx, Newton-Schulz iterate (ping)
+    _Float16* xb;      // rows x ldx, Newton-Schulz iterate (pong)
+    _Float16* gram;    // s x lds
+    _Float16* poly;    // s x lds
+    _Float16* uout;    // rows x ldx, final update (per-row-normalized matrices only)
+    float* normpart;   // [mom_tiles] partial sums of u^2
+    float* rowpart;    // [mom_tiles_c][rows] partial row sums of p*g*softplus(cg)
+    float* colpart;    // [mom_tiles_r][cols] partial column sums of p*g*softplus(rg)
+    float* rowsqpart;  // [g3_tiles_n][rows] partial row sums of u'^2
+    float* rowscale;   // [rows] per-row rsqrt(mean u'^2)
+    float* scal;       // [8] per-matrix scalars (see kScal*)
+    float* psqpart;    // [n_psq] partial sums of p^2 after the update
+
+    int32_t rows, cols, s, l;
+    int32_t ldx, lds;
+    int32_t tall;
+    int32_t flags;
+    float eta;        // lr * scaling for this matrix
+    float wd;
+    float beta1;
+    float gain_lr, gain_beta2, gain_w1, gain_w2, gain_eps;
+    float gain_bc1, gain_bc2;   // Adam bias corrections for the gains at this matrix's step
+    int32_t mom_tiles_r, mom_tiles_c;
+    int32_t g3_tiles_m, g3_tiles_n;
+    int32_t n_psq;
+    int32_t apply_tiles;   // elementwise tiles of the per-row-normalized apply kernel
+};
+
+enum ScalSlot : int {
+    kScalSigma = 0,    // 1 / (||u||_F + 1e-8)
+    kScalGamma = 1,    // per-row-normalization Frobenius rescale
+    kScalMDFactor = 2, // target / (||p||_F + 1e-8)
+};
+
+// A grouped launch: task k covers blocks [starts[k], starts[k+1]) and works on matrix order[k].
+struct TaskList {
+    const int32_t* order;
+    const int32_t* starts;
+    int32_t n;
+    int32_t total;
+};
+
+// One tensor of a non-orthogonalized (Adam) group, flattened.
+struct AdamTensor {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    int64_t n;
+    float lr;       // group lr * rect * magma
+    float wd;
+    float beta2;
+    float w1, w2;   // 1 - beta1, 1 - beta2 (rounded from double)
+    float bc1, bc2;
+    float eps;
+    int32_t flags;  // kAdam*
+};
+
+enum AdamFlags : int32_t {
+    kAdamApply = 1,       // write p (the reference skips p when it is not updated this step)
+    kAdamDegenerate = 2,  // rectification says rho <= 4: u = m, lr*rect == 0
+    kAdamAtan2 = 4,       // eps == 0: Adam-atan2
+    kAdamVec4 = 8,        // all four pointers 16-byte aligned: float4 path
+};
+
+}  // namespace thorn

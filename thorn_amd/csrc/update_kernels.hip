@@ -1,0 +1,361 @@
+// Bandwidth-bound THORN kernels (gfx950): momentum + first Newton-Schulz iterate, per-matrix
+// norms, decoupled-magnitude gains, per-row normalization apply, and the multi-tensor Adam.
+//
+// Elementwise kernels over a matrix use 16 x 256 tiles: 256 threads, wave w owns rows 4w..4w+3,
+// lane l owns columns 4l..4l+3 (float4 path) or l, l+64, l+128, l+192 (scalar path). Partial sums
+// are written per tile and reduced later in a fixed order, so every result is bitwise
+// reproducible run to run (no float atomics).
+#include "thorn_kernels.hpp"
+
+namespace thorn {
+
+constexpr int kTileR = 16, kTileC = 256;
+
+__device__ __forceinline__ int tile_col(int c0, int lane, int e, bool vec) {
+    return vec ? c0 + 4 * lane + e : c0 + lane + 64 * e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Momentum, decoupled-magnitude pre-step and the first iterate (thorn.py:1376-1397, 890-908)
+// ---------------------------------------------------------------------------------------------
+//   md:   G = softplus(rg_i) * softplus(cg_j); p /= G; pg = p * g; g *= G
+//         rowpart += pg * softplus(cg_j); colpart += pg * softplus(rg_i)
+//   m = m * beta1 + g;  u = g + beta1 * m;  x0 = u (fp32);  normpart += u^2
+__global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
+    __shared__ float colred[4][kTileC];
+    __shared__ float scratch[4];
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
+    const bool vec = M.flags & kFlagVec4;
+    const bool keep_grad = M.flags & kFlagKeepGrad;
+    const float beta1 = M.beta1;
+
+    float spc[4] = {1.f, 1.f, 1.f, 1.f};
+    bool cok[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int c = tile_col(c0, lane, e, vec);
+        cok[e] = c < M.cols;
+        if (md && cok[e]) spc[e] = softplus_f(M.cg[c]);
+    }
+    const float sp_scalar = mds ? softplus_f(M.rg[0]) : 1.f;
+    float colacc[4] = {0.f, 0.f, 0.f, 0.f};
+    float nrm = 0.f;
+
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = r0 + rr;
+        if (row >= M.rows) break;   // uniform over the wave
+        const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
+        const int64_t rbase = (int64_t)row * M.cols;
+        float gv[4], mv[4], pv[4];
+        if (vec) {
+            const int c = c0 + 4 * lane;
+            if (cok[0]) {
+                float4 t = *reinterpret_cast<const float4*>(M.g + rbase + c);
+                gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
+                t = *reinterpret_cast<const float4*>(M.m + rbase + c);
+                mv[0] = t.x; mv[1] = t.y; mv[2] = t.z; mv[3] = t.w;
+                if (md || mds) {
+                    t = *reinterpret_cast<const float4*>(M.p + rbase + c);
+                    pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (!cok[e]) continue;
+                const int c = tile_col(c0, lane, e, false);
+                gv[e] = M.g[rbase + c];
+                mv[e] = M.m[rbase + c];
+                if (md || mds) pv[e] = M.p[rbase + c];
+            }
+        }
+        float rowacc = 0.f;
+        float xv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!cok[e]) { xv[e] = 0.f; continue; }
+            float g = gv[e];
+            if (md || mds) {
+                const float G = md ? spr * spc[e] : sp_scalar;
+                const float p = pv[e] / G;
+                const float pg = p * g;
+                g = g * G;
+                pv[e] = p;
+                gv[e] = g;
+                rowacc += md ? pg * spc[e] : pg;
+                colacc[e] += pg * spr;
+            }
+            const float m = mv[e] * beta1 + g;
+            mv[e] = m;
+            const float u = fmaf(m, beta1, g);
+            xv[e] = u;
+            nrm += u * u;
+        }
+        if (md || mds) {
+            rowacc = wave_sum(rowacc);
+            if (lane == 0) M.rowpart[(int64_t)tc * M.rows + row] = rowacc;
+        }
+        float* xrow = M.x0 + (int64_t)row * M.ldx;
+        if (vec) {
+            if (cok[0]) {
+                const int c = c0 + 4 * lane;
+                *reinterpret_cast<float4*>(M.m + rbase + c) = make_float4(mv[0], mv[1], mv[2], mv[3]);
+                if (md || mds) {
+                    *reinterpret_cast<float4*>(M.p + rbase + c) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+                    if (keep_grad)
+                        *reinterpret_cast<float4*>(M.g + rbase + c) = make_float4(gv[0], gv[1], gv[2], gv[3]);
+                }
+                *reinterpret_cast<float4*>(xrow + c) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (!cok[e]) continue;
+                const int c = tile_col(c0, lane, e, false);
+                M.m[rbase + c] = mv[e];
+                if (md || mds) {
+                    M.p[rbase + c] = pv[e];
+                    if (keep_grad) M.g[rbase + c] = gv[e];
+                }
+                xrow[c] = xv[e];
+            }
+        }
+    }
+
+    if (md) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) colred[wave][tile_col(0, lane, e, vec)] = colacc[e];
+        __syncthreads();
+        const int c = c0 + threadIdx.x;
+        if (c < M.cols) {
+            const float t = colred[0][threadIdx.x] + colred[1][threadIdx.x] + colred[2][threadIdx.x] +
+                            colred[3][threadIdx.x];
+            M.colpart[(int64_t)tr * M.cols + c] = t;
+        }
+    }
+    const float total = block_sum(nrm, scratch);
+    if (threadIdx.x == 0) M.normpart[local] = total;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per matrix: sigma = 1 / (||u||_F + 1e-8) (thorn.py:633) and, with decouple_md, the Adam-atan2
+// steps of the gains from d softplus (thorn.py:910-967). The gains' updates only read p*g from
+// before the parameter update, so they run here, before Newton-Schulz.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats) {
+    __shared__ float scratch[4];
+    const OrthoMat& M = mats[blockIdx.x];
+    const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
+    float s = 0.f;
+    for (int t = threadIdx.x; t < ntiles; t += 256) s += M.normpart[t];
+    s = block_sum(s, scratch);
+    if (threadIdx.x == 0) M.scal[kScalSigma] = 1.f / (sqrtf(s) + 1e-8f);
+
+    const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
+    if (!(md || mds) || !(M.flags & kFlagApply)) return;
+    AdamScalars a;
+    a.lr = M.gain_lr; a.wd = 0.f; a.beta2 = M.gain_beta2; a.w1 = M.gain_w1; a.w2 = M.gain_w2;
+    a.bc1 = M.gain_bc1; a.bc2 = M.gain_bc2; a.eps = M.gain_eps;
+    a.apply = true; a.degenerate = false; a.atan2_mode = M.gain_eps == 0.f;
+    if (md) {
+        for (int i = threadIdx.x; i < M.rows; i += 256) {
+            float t = 0.f;
+            for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpart[(int64_t)c * M.rows + i];
+            float gain = M.rg[i], mo = M.rgm[i], va = M.rgv[i];
+            const float grad = t * sigmoid_f(gain);
+            adam_elem(gain, grad, mo, va, a);
+            M.rg[i] = gain; M.rgm[i] = mo; M.rgv[i] = va;
+        }
+        for (int j = threadIdx.x; j < M.cols; j += 256) {
+            float t = 0.f;
+            for (int r = 0; r < M.mom_tiles_r; ++r) t += M.colpart[(int64_t)r * M.cols + j];
+            float gain = M.cg[j], mo = M.cgm[j], va = M.cgv[j];
+            const float grad = t * sigmoid_f(gain);
+            adam_elem(gain, grad, mo, va, a);
+            M.cg[j] = gain; M.cgm[j] = mo; M.cgv[j] = va;
+        }
+    } else {
+        float t = 0.f;
+        for (int i = threadIdx.x; i < M.rows; i += 256)
+            for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpart[(int64_t)c * M.rows + i];
+        t = block_sum(t, scratch);
+        if (threadIdx.x == 0) {
+            float gain = M.rg[0], mo = M.rgm[0], va = M.rgv[0];
+            const float grad = t * sigmoid_f(gain);
+            adam_elem(gain, grad, mo, va, a);
+            M.rg[0] = gain; M.rgm[0] = mo; M.rgv[0] = va;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per-row normalization (thorn.py:709-766): s_i = rsqrt(max(mean_j u'_ij^2, eps)),
+// gamma = ||u'||_F / max(||s * u'||_F, eps); one block per matrix.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __restrict__ mats,
+                                                             const int32_t* __restrict__ idx) {
+    __shared__ float scratch[4];
+    const OrthoMat& M = mats[idx[blockIdx.x]];
+    const float eps = 1.1920928955078125e-07f;   // torch.finfo(torch.float32).eps
+    float tot = 0.f, nw = 0.f;
+    for (int i = threadIdx.x; i < M.rows; i += 256) {
+        float rs = 0.f;
+        for (int t = 0; t < M.g3_tiles_n; ++t) rs += M.rowsqpart[(int64_t)t * M.rows + i];
+        const float mean = rs / (float)M.cols;
+        const float s = 1.f / sqrtf(fmaxf(mean, eps));
+        M.rowscale[i] = s;
+        tot += rs;
+        nw += s * s * rs;
+    }
+    tot = block_sum(tot, scratch);
+    nw = block_sum(nw, scratch);
+    if (threadIdx.x == 0) M.scal[kScalGamma] = sqrtf(tot) / fmaxf(sqrtf(nw), eps);
+}
+
+// p <- p - eta * cwd((u' * s_i) * gamma) over per-row-normalized matrices, plus p^2 partials for md.
+__global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
+    __shared__ float scratch[4];
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    const float gamma = M.scal[kScalGamma];
+    const bool md = M.flags & (kFlagMD | kFlagMDScalar);
+    float psq = 0.f;
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = r0 + rr;
+        if (row >= M.rows) break;
+        const float s = M.rowscale[row];
+        const int64_t rbase = (int64_t)row * M.cols;
+        const _Float16* urow = M.uout + (int64_t)row * M.ldx;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + lane + 64 * e;
+            if (c >= M.cols) continue;
+            const float u = ((float)urow[c] * s) * gamma;
+            const float p = cautious_step(M.p[rbase + c], u, M.eta, M.wd);
+            M.p[rbase + c] = p;
+            psq += p * p;
+        }
+    }
+    if (md) {
+        const float t = block_sum(psq, scratch);
+        if (threadIdx.x == 0) M.psqpart[local] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// decouple_md tail (thorn.py:1414-1421, 969-977): p *= target / (||p||_F + 1e-8), then
+// p *= softplus(rg_i), p *= softplus(cg_j) with the gains already updated.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ortho_md_factor_kernel(const OrthoMat* __restrict__ mats,
+                                                              const int32_t* __restrict__ idx) {
+    __shared__ float scratch[4];
+    const OrthoMat& M = mats[idx[blockIdx.x]];
+    float s = 0.f;
+    for (int t = threadIdx.x; t < M.n_psq; t += 256) s += M.psqpart[t];
+    s = block_sum(s, scratch);
+    if (threadIdx.x == 0) M.scal[kScalMDFactor] = M.target[0] / (sqrtf(s) + 1e-8f);
+}
+
+__global__ __launch_bounds__(256) void ortho_md_rescale_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    const bool md = M.flags & kFlagMD;
+    const bool apply = M.flags & kFlagApply;
+    const float f = M.scal[kScalMDFactor];
+    float spc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int c = c0 + lane + 64 * e;
+        spc[e] = (md && c < M.cols) ? softplus_f(M.cg[c]) : 1.f;
+    }
+    const float sp_scalar = md ? 1.f : softplus_f(M.rg[0]);
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = r0 + rr;
+        if (row >= M.rows) break;
+        const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
+        const int64_t rbase = (int64_t)row * M.cols;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + lane + 64 * e;
+            if (c >= M.cols) continue;
+            float p = M.p[rbase + c];
+            if (apply) p = p * f;
+            p = p * spr;
+            if (md) p = p * spc[e];
+            M.p[rbase + c] = p;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Multi-tensor Adam / Adam-atan2 with cautious weight decay (thorn.py:838-888), 4096 elements
+// per block.
+// ---------------------------------------------------------------------------------------------
+constexpr int kAdamChunk = 4096;
+
+__global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict__ ts, TaskList tl) {
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const AdamTensor& T = ts[tl.order[k]];
+    const int64_t base = (int64_t)(b - tl.starts[k]) * kAdamChunk;
+    AdamScalars s;
+    s.lr = T.lr; s.wd = T.wd; s.beta2 = T.beta2; s.w1 = T.w1; s.w2 = T.w2;
+    s.bc1 = T.bc1; s.bc2 = T.bc2; s.eps = T.eps;
+    s.apply = T.flags & kAdamApply;
+    s.degenerate = T.flags & kAdamDegenerate;
+    s.atan2_mode = T.flags & kAdamAtan2;
+    if (T.flags & kAdamVec4) {
+#pragma unroll
+        for (int q = 0; q < kAdamChunk / 1024; ++q) {
+            const int64_t i = base + (int64_t)(q * 256 + threadIdx.x) * 4;
+            if (i + 3 < T.n) {
+                float4 p4 = s.apply ? *reinterpret_cast<const float4*>(T.p + i) : make_float4(0, 0, 0, 0);
+                const float4 g4 = *reinterpret_cast<const float4*>(T.g + i);
+                float4 m4 = *reinterpret_cast<const float4*>(T.m + i);
+                float4 v4 = *reinterpret_cast<const float4*>(T.v + i);
+                adam_elem(p4.x, g4.x, m4.x, v4.x, s);
+                adam_elem(p4.y, g4.y, m4.y, v4.y, s);
+                adam_elem(p4.z, g4.z, m4.z, v4.z, s);
+                adam_elem(p4.w, g4.w, m4.w, v4.w, s);
+                *reinterpret_cast<float4*>(T.m + i) = m4;
+                *reinterpret_cast<float4*>(T.v + i) = v4;
+                if (s.apply) *reinterpret_cast<float4*>(T.p + i) = p4;
+            } else {
+                for (int64_t j = i; j < T.n && j < i + 4; ++j) {
+                    float p = s.apply ? T.p[j] : 0.f, m = T.m[j], v = T.v[j];
+                    adam_elem(p, T.g[j], m, v, s);
+                    T.m[j] = m; T.v[j] = v;
+                    if (s.apply) T.p[j] = p;
+                }
+            }
+        }
+    } else {
+        for (int q = 0; q < kAdamChunk / 256; ++q) {
+            const int64_t j = base + q * 256 + threadIdx.x;
+            if (j >= T.n) break;
+            float p = s.apply ? T.p[j] : 0.f, m = T.m[j], v = T.v[j];
+            adam_elem(p, T.g[j], m, v, s);
+            T.m[j] = m; T.v[j] = v;
+            if (s.apply) T.p[j] = p;
+        }
+    }
+}
+
+}  // namespace thorn

@@ -1,0 +1,514 @@
+"""THORN optimizer on MI355X: the reference's Python API over the HIP library.
+
+Drop-in for ``thorn.THORN`` (pykeio/THORN, thorn/thorn.py:1229): the constructor overloads, the
+parameter-group keys and defaults, the validation errors, the per-parameter state keys (and so
+``state_dict``/``load_state_dict``) and ``step(closure=None, *, param=None)`` are the reference's.
+What runs underneath is different: every group's whole step is a handful of grouped HIP launches
+on the current stream (see ``thorn_amd.csrc``), driven through the C ABI in include/thorn_amd.h.
+
+Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
+behaviour): Magma ``momentum_align`` (thorn.py:800-836), sparse gradients (thorn.py:1667-1700),
+DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), ``decouple_md`` on non-orthogonalized
+groups, non-fp32 parameters, and gradient release with ``update_rate > 1``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field, fields, MISSING
+from functools import partial
+from typing import Any, Callable, Literal, Optional, Union, cast, overload
+
+import numpy as np
+import torch
+import torch.nn as nn
+from torch.nn import Parameter
+from torch.optim import Optimizer
+from typing_extensions import NotRequired, TypedDict
+
+from . import _coeffs
+from . import _lib
+
+__all__ = ['THORN', 'THORNOrthoGroup', 'THORNNonOrthoGroup', 'THORNGroup']
+
+# softplus(LN_E_SUB_1) == 1 (thorn.py:1602)
+LN_E_SUB_1 = 0.5413248546
+
+_TargetNorm = Union[Literal['init', 'min', 'max'], Callable[[torch.Tensor], Union[torch.Tensor, float]]]
+
+
+class THORNOrthoGroup(TypedDict, total=True):
+    """Keys of an orthogonalized group (thorn.py:1188-1209)."""
+    orthogonalize: Literal[True]
+    params: list
+    lr: NotRequired[float]
+    betas: NotRequired[tuple]
+    weight_decay: NotRequired[float]
+    none_grad: NotRequired[bool]
+    scaling_mode: NotRequired[Literal['md', 'moonlight', 'jordan']]
+    target_rms: NotRequired[float]
+    decouple_md: NotRequired[bool]
+    target_norm: NotRequired[_TargetNorm]
+    gain_lr: NotRequired[float]
+    gain_betas: NotRequired[tuple]
+    split_gain: NotRequired[bool]
+    momentum_align: NotRequired[bool]
+    force_per_neuron_norm: NotRequired[bool]
+    iters: NotRequired[int]
+    lower_bound: NotRequired[float]
+    cushion: NotRequired[float]
+    safety_factor: NotRequired[float]
+    coeffs: NotRequired[list]
+
+
+class THORNNonOrthoGroup(TypedDict, total=True):
+    """Keys of a non-orthogonalized group (thorn.py:1211-1225)."""
+    orthogonalize: Literal[False]
+    params: list
+    lr: NotRequired[float]
+    betas: NotRequired[tuple]
+    weight_decay: NotRequired[float]
+    none_grad: NotRequired[bool]
+    rectify: NotRequired[bool]
+    eps: NotRequired[float]
+    momentum_align: NotRequired[bool]
+    decouple_md: NotRequired[bool]
+    target_norm: NotRequired[_TargetNorm]
+    gain_lr: NotRequired[float]
+    gain_betas: NotRequired[tuple]
+    split_gain: NotRequired[bool]
+
+
+THORNGroup = Union[THORNOrthoGroup, THORNNonOrthoGroup]
+
+
+@dataclass
+class _Group:
+    """Per-step view of a parameter group: the reference's _THORNParameterGroup (thorn.py:535-612),
+    rebuilt from the group dict at every step so LR schedulers take effect."""
+    orthogonalize: bool
+    params: list
+    lr: float
+    base_lr: float = field(init=False)
+    none_grad: bool = field(default=True)
+    weight_decay: float = field(default=0.1)
+    betas: tuple = field(default_factory=lambda: (0.9, 0.95))
+    scaling_mode: Optional[str] = field(default=None)
+    target_rms: float = field(default=0.2)
+    target_norm: Any = field(default=None)
+    iters: int = field(default=5)
+    rectify: bool = field(default=False)
+    eps: float = field(default=0)
+    lower_bound: float = field(default=1e-3)
+    safety_factor: float = field(default=0.03)
+    cushion: float = field(default=0.02)
+    momentum_align: bool = field(default=False)
+    coeffs: list = field(init=False)
+    restarts: list = field(init=False)
+    decouple_md: bool = field(default=False)
+    gain_lr: float = field(default=1e-3)
+    gain_betas: tuple = field(default_factory=lambda: (0.9, 0.95))
+    norm_axis: Any = field(default=None)
+    split_gain: bool = field(default=True)
+    force_per_neuron_norm: bool = field(default=False)
+
+    @classmethod
+    def from_kwargs(cls, **kwargs) -> '_Group':
+        return cls(**{k: kwargs[k] for k in kwargs if k in cls.__dataclass_fields__})
+
+    def __post_init__(self):
+        if self.lr < 0.0:
+            raise ValueError(f'Invalid learning rate `{self.lr}`; should be >= 0')
+        if not (0.0 <= self.betas[0] < 1.0):
+            raise ValueError(f'Invalid beta1 `{self.betas[0]}`; should be in [0, 1)')
+        if not (0.0 <= self.betas[1] < 1.0):
+            raise ValueError(f'Invalid beta2 `{self.betas[1]}`; should be in [0, 1)')
+        self.base_lr = self.lr
+        c = _coeffs.ns_coefficients(self.lower_bound, self.iters, self.safety_factor, self.cushion)
+        self.coeffs = list(c)
+        self.restarts = list(_coeffs.gram_restarts(c))
+
+    @property
+    def scaling_mode_(self) -> str:
+        if self.scaling_mode is None:
+            return 'md' if self.decouple_md else 'moonlight'
+        return self.scaling_mode
+
+    @property
+    def gain_lr_(self) -> float:
+        return self.gain_lr * (float(self.lr) / self.base_lr)
+
+    def norm_axis_(self, p: torch.Tensor):
+        return self.norm_axis if self.norm_axis is not None else ((-2, -1) if p.ndim > 1 else -1)
+
+    def target_norm_(self, p: torch.Tensor) -> torch.Tensor:
+        tn = self.target_norm
+        if tn is None:
+            tn = 'max' if self.orthogonalize else 'init'
+        if callable(tn):
+            tn = tn(p)
+        elif tn == 'init':
+            tn = p.norm(dim=self.norm_axis_(p), keepdim=True)
+        elif tn == 'min':
+            tn = min(p.size(-2), p.size(-1)) ** 0.5
+        elif tn == 'max':
+            tn = max(p.size(-2), p.size(-1)) ** 0.5
+        if isinstance(tn, (float, int)):
+            return torch.full((), tn, dtype=p.dtype, device=p.device)
+        return tn.to(dtype=p.dtype, device=p.device)
+
+
+def _lr_scale_ortho(shape, group: _Group) -> float:
+    """thorn.py:768-780."""
+    rows, cols = shape[-2], shape[-1]
+    mode = group.scaling_mode_
+    if mode == 'md':
+        return max(rows / cols, cols / rows) ** 0.5
+    if mode == 'moonlight':
+        assert group.target_rms > 0
+        return group.target_rms * (max(1, rows, cols) ** 0.5)
+    if mode == 'jordan':
+        return max(1, rows / cols) ** 0.5
+    raise ValueError(f'Invalid scaling_mode `{mode}`')
+
+
+def _compute_rect(group: _Group, step) -> float:
+    """RAdam rectification term (thorn.py:782-798)."""
+    beta2 = group.betas[1]
+    if beta2 > 0.0:
+        rho_inf = 2 / (1 - beta2) - 1
+        rho = rho_inf - 2 * step * (beta2 ** step) / (1 - beta2 ** step)
+        return (
+            ((rho - 4) * (rho - 2) * rho_inf / ((rho_inf - 4) * (rho_inf - 2) * rho)) ** 0.5
+            if rho > 4.0 else 0.0
+        ) ** float(group.rectify)
+    return 1.0
+
+
+def _needs_neuron_norm(shape, group: _Group) -> bool:
+    """thorn.py:704-707."""
+    return group.betas[1] > 0 and (shape[-2] > shape[-1] or group.force_per_neuron_norm)
+
+
+def _check_tensor(t: torch.Tensor, what: str) -> None:
+    if t.dtype != torch.float32:
+        raise NotImplementedError(f'THORN on MI355X supports fp32 tensors only; {what} is {t.dtype}')
+    if not t.is_cuda:
+        raise RuntimeError(f'THORN on MI355X needs device tensors; {what} is on {t.device}')
+    if not t.is_contiguous():
+        raise NotImplementedError(f'THORN on MI355X needs contiguous tensors; {what} is not')
+
+
+class _OrthoRunner:
+    """One orthogonalized parameter set: plan, workspace and the per-step table."""
+
+    def __init__(self, params: list, group: _Group, device: torch.device):
+        self.params = params
+        self.device = device
+        rows, cols, flags, owner, sub = [], [], [], [], []
+        for i, p in enumerate(params):
+            r, c = p.shape[-2], p.shape[-1]
+            batch = math.prod(p.shape[:-2])
+            f = 0
+            if _needs_neuron_norm(p.shape, group):
+                f |= _lib.MAT_PER_ROW_NORM
+            if group.decouple_md:
+                f |= _lib.MAT_MD if group.split_gain else _lib.MAT_MD_SCALAR
+            for b in range(batch):
+                rows.append(r)
+                cols.append(c)
+                flags.append(f)
+                owner.append(i)
+                sub.append(b)
+        self.rows = np.asarray(rows, dtype=np.int64)
+        self.cols = np.asarray(cols, dtype=np.int64)
+        self.owner = owner
+        self.sub = np.asarray(sub, dtype=np.int64)
+        self.plan = _lib.OrthoPlan(rows, cols, flags)
+        self.workspace = torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
+        self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
+        self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
+        self.scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)
+        self.md = group.decouple_md
+        self.split_gain = group.split_gain
+
+    def run(self, opt: 'THORN', group: _Group) -> None:
+        params, steps = self.params, self.steps
+        n = len(self.owner)
+        elem = np.asarray([p.shape[-2] * p.shape[-1] for p in params], dtype=np.int64)[self.owner]
+        bytes_off = self.sub * elem * 4
+        own = self.owner
+        p_ptr = np.asarray([p.data_ptr() for p in params], dtype=np.uint64)[own]
+        g_ptr = np.asarray([p.grad.data_ptr() for p in params], dtype=np.uint64)[own]
+        states = [opt.state[p] for p in params]
+        m_ptr = np.asarray([s['moment'].data_ptr() for s in states], dtype=np.uint64)[own]
+        steps['p'] = p_ptr + bytes_off.astype(np.uint64)
+        steps['g'] = g_ptr + bytes_off.astype(np.uint64)
+        steps['m'] = m_ptr + bytes_off.astype(np.uint64)
+        steps['eta'] = (group.lr * self.scale)[own]
+        steps['weight_decay'] = group.weight_decay
+        steps['beta1'] = group.betas[0]
+        flags = _lib.STEP_APPLY | (0 if group.none_grad else _lib.STEP_KEEP_GRAD)
+        steps['step_flags'] = flags
+        if self.md:
+            gb1, gb2 = group.gain_betas
+            steps['gain_lr'] = group.gain_lr_
+            steps['gain_beta2'] = gb2
+            steps['gain_w1'] = 1 - gb1
+            steps['gain_w2'] = 1 - gb2
+            steps['gain_eps'] = group.eps
+            st = np.asarray([s['step'] for s in states], dtype=np.float64)[own]
+            steps['gain_bc1'] = 1 / (1 - gb1 ** st)
+            steps['gain_bc2'] = 1 / (1 - gb2 ** st)
+            rows = self.rows
+            cols = self.cols
+            sub = self.sub
+
+            def ptrs(key, per):
+                base = np.asarray([s[key].data_ptr() for s in states], dtype=np.uint64)[own]
+                return base + (sub * per * 4).astype(np.uint64)
+
+            if self.split_gain:
+                steps['row_gain'] = ptrs('row_gain', rows)
+                steps['row_gain_moment'] = ptrs('row_gain_moment', rows)
+                steps['row_gain_variance'] = ptrs('row_gain_variance', rows)
+                steps['col_gain'] = ptrs('col_gain', cols)
+                steps['col_gain_moment'] = ptrs('col_gain_moment', cols)
+                steps['col_gain_variance'] = ptrs('col_gain_variance', cols)
+            else:
+                steps['row_gain'] = ptrs('gain', 0)
+                steps['row_gain_moment'] = ptrs('gain_moment', 0)
+                steps['row_gain_variance'] = ptrs('gain_variance', 0)
+            tn = np.empty(n, dtype=np.uint64)
+            for k, (i, b) in enumerate(zip(own, sub)):
+                t = states[i]['target_norm']
+                tn[k] = t.data_ptr() + (int(b) * 4 if t.numel() > 1 else 0)
+            steps['target_norm'] = tn
+        host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
+        self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
+        self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
+        coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
+        self.plan.step(self.table.data_ptr(), coeffs, torch.cuda.current_stream(self.device).cuda_stream)
+
+
+class _AdamRunner:
+    """All tensors of the non-orthogonalized groups of one step: one multi-tensor launch."""
+
+    def __init__(self, params: list, device: torch.device):
+        self.params = params
+        self.device = device
+        self.plan = _lib.AdamPlan([p.numel() for p in params])
+        self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
+        self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
+
+    def run(self, entries: list) -> None:
+        """entries: (p, state, group) per tensor, in plan order."""
+        s = self.steps
+        for k, (p, state, group) in enumerate(entries):
+            step = state['step']
+            beta1, beta2 = group.betas
+            rect = _compute_rect(group, step)
+            s[k]['p'] = p.data_ptr()
+            s[k]['g'] = p.grad.data_ptr()
+            s[k]['m'] = state['moment'].data_ptr()
+            s[k]['v'] = state['variance'].data_ptr()
+            s[k]['lr'] = group.lr * rect * 1.0
+            s[k]['weight_decay'] = group.weight_decay
+            s[k]['beta2'] = beta2
+            s[k]['w1'] = 1 - beta1
+            s[k]['w2'] = 1 - beta2
+            s[k]['bc1'] = 1 / (1 - beta1 ** step)
+            s[k]['bc2'] = 1 / (1 - beta2 ** step)
+            s[k]['eps'] = group.eps
+            s[k]['apply'] = 1
+            s[k]['degenerate'] = 1 if rect == 0.0 else 0
+        host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
+        self.plan.fill_table(s, self.table.data_ptr(), host.data_ptr())
+        self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
+        self.plan.step(self.table.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
+
+
+class THORN(Optimizer):
+    """Drop-in for pykeio/THORN's ``THORN`` (thorn.py:1229-1776) on one MI355X."""
+
+    param_groups: list
+    polar_decomp_batch_size: int = 32 * 1024 * 1024   # accepted for compatibility (thorn.py:1237)
+
+    @overload
+    def __init__(self, params: nn.Module, *, lr: float, none_grad: bool = True, weight_decay: float = 0.1,
+                 betas: tuple = (0.9, 0.95), scaling_mode: Optional[str] = None, target_rms: float = 0.2,
+                 target_norm: Optional[_TargetNorm] = None, iters: int = 5, rectify: bool = False,
+                 eps: float = 0, lower_bound: float = 1e-3, safety_factor: float = 0.03,
+                 cushion: float = 0.02, momentum_align: bool = False, gradient_release: bool = False,
+                 decouple_md: bool = False, gain_lr: float = 1e-3, gain_betas: tuple = (0.9, 0.95),
+                 split_gain: bool = True, backend=torch.cuda): ...
+
+    @overload
+    def __init__(self, params: list): ...
+
+    def __init__(self, params, *, backend=torch.cuda, **conf):
+        _lib.load()   # fail at construction, not at the first step, when the library is missing
+        self._update_rate = 1
+        self.backend = backend
+        groups = THORN._auto_assign(params, **conf) if isinstance(params, nn.Module) else params
+        for group in groups:
+            assert 'orthogonalize' in group
+            if group['orthogonalize']:
+                assert all(map(lambda x: x.ndim >= 2, group['params'])), \
+                    'Only parameters with ndim >= 2 can be orthogonalized'
+        self.is_distributed = False
+        self.rank = None
+        defaults = dict()
+        for f in fields(_Group):
+            if f.default is not MISSING:
+                defaults[f.name] = f.default
+            elif f.default_factory is not MISSING:
+                defaults[f.name] = f.default_factory()
+        super().__init__(cast(list, groups), defaults)
+        self._param_to_group: dict = {}
+        for group in self.param_groups:
+            for p in group['params']:
+                self._param_to_group[id(p)] = group
+        self._runners: dict = {}
+        if isinstance(params, nn.Module) and conf.get('gradient_release', False):
+            self.setup_gradient_release(params)
+
+    @staticmethod
+    def _auto_assign(module: nn.Module, **keys) -> list:
+        """thorn.py:1302-1331: ndim >= 2, not an ``lm_head``, not an ``nn.Embedding`` weight."""
+        embedding_params = []
+
+        def filter_embeddings(m: nn.Module):
+            if isinstance(m, nn.Embedding):
+                embedding_params.append(id(m.weight))
+        module.apply(filter_embeddings)
+        ortho, regular = [], []
+        for name, prm in module.named_parameters():
+            if prm.ndim >= 2 and 'lm_head' not in name and id(prm) not in embedding_params:
+                ortho.append(prm)
+            else:
+                regular.append(prm)
+        return [{'orthogonalize': True, 'params': ortho, **keys},
+                {'orthogonalize': False, 'params': regular, **keys}]
+
+    # -- state initialisation (thorn.py:1591-1634) ---------------------------------------------
+    def _init_state(self, p: torch.Tensor, group: _Group) -> None:
+        state = self.state[p]
+        if 'step' in state:
+            return
+        state['step'] = 1
+        state['moment'] = torch.zeros_like(p)
+        if not group.orthogonalize:
+            state['variance'] = torch.zeros_like(p)
+        if group.decouple_md:
+            if p.ndim > 1 and group.split_gain:
+                state['row_gain'] = torch.full((*p.shape[:-1], 1), LN_E_SUB_1, dtype=p.dtype, device=p.device)
+                state['col_gain'] = torch.full((*p.shape[:-2], 1, *p.shape[-1:]), LN_E_SUB_1, dtype=p.dtype,
+                                               device=p.device)
+                for k in ['row_gain', 'col_gain']:
+                    state[f'{k}_moment'] = torch.zeros_like(state[k])
+                    state[f'{k}_variance'] = torch.zeros_like(state[k])
+            else:
+                state['gain'] = torch.full((), LN_E_SUB_1, dtype=p.dtype, device=p.device)
+                state['gain_moment'] = torch.zeros((), dtype=p.dtype, device=p.device)
+                state['gain_variance'] = torch.zeros((), dtype=p.dtype, device=p.device)
+            state['target_norm'] = group.target_norm_(p)
+
+    def _validate(self, p: torch.Tensor, group: _Group) -> None:
+        if group.momentum_align:
+            raise NotImplementedError('momentum_align (Magma) is not implemented on the MI355X path')
+        g = p.grad
+        if g.is_sparse:
+            raise NotImplementedError('sparse gradients are not implemented on the MI355X path')
+        if type(p.data).__name__ == 'DTensor' or type(g).__name__ == 'DTensor':
+            raise NotImplementedError('DTensor / FSDP2 parameters are not implemented on the MI355X path')
+        if g.shape != p.shape:
+            raise AssertionError(f'gradient shape {tuple(g.shape)} != parameter shape {tuple(p.shape)}')
+        _check_tensor(p, 'parameter')
+        _check_tensor(g, 'gradient')
+        if g.device != p.device:
+            raise RuntimeError('gradient and parameter are on different devices')
+        if not group.orthogonalize and group.decouple_md:
+            raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
+                                      'on the MI355X path')
+        if self._update_rate != 1:
+            raise NotImplementedError('gradient release with update_rate > 1 is not implemented '
+                                      'on the MI355X path')
+
+    def _runner(self, key, factory):
+        r = self._runners.get(key)
+        if r is None:
+            r = factory()
+            self._runners[key] = r
+        return r
+
+    # -- step (thorn.py:1583-1753) ---------------------------------------------------------------
+    def _step_params(self, params: list, group: _Group, gi: int) -> None:
+        live = []
+        for p in params:
+            if p is None or p.grad is None:
+                continue
+            self._validate(p, group)
+            self._init_state(p, group)
+            live.append(p)
+        if not live:
+            return
+        by_dev: dict = {}
+        for p in live:
+            by_dev.setdefault(p.device, []).append(p)
+        for dev, ps in by_dev.items():
+            with torch.cuda.device(dev):
+                if group.orthogonalize:
+                    key = ('ortho', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
+                           group.decouple_md, group.split_gain, group.force_per_neuron_norm,
+                           group.betas[1] > 0)
+                    runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev))
+                    runner.run(self, group)
+                else:
+                    key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
+                    runner = self._runner(key, lambda: _AdamRunner(ps, dev))
+                    runner.run([(p, self.state[p], group) for p in ps])
+        for p in live:
+            if group.none_grad:
+                p.grad = None
+            self.state[p]['step'] += 1
+
+    @overload
+    def step(self, closure: None = None, *, param: Optional[torch.nn.Parameter] = None) -> None: ...
+
+    @overload
+    def step(self, closure: Callable[[], float], *, param: Optional[torch.nn.Parameter] = None) -> float: ...
+
+    @torch.no_grad()
+    def step(self, closure: Optional[Callable[[], float]] = None, *, param: Optional[torch.nn.Parameter] = None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        if param is None:
+            for gi, group in enumerate(self.param_groups):
+                self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+        else:
+            group = self._param_to_group[id(param)]
+            gi = next(i for i, g in enumerate(self.param_groups) if g is group)
+            self._step_params([param], _Group.from_kwargs(**group), gi)
+        return loss
+
+    def setup_gradient_release(self, model: nn.Module, update_rate: int = 1, ignore_existing_hooks: bool = False):
+        """thorn.py:1755-1776: step each parameter from its post-accumulate-grad hook."""
+        def _hook(param: torch.Tensor, optimizer: 'THORN'):
+            optimizer.step(param=cast(Parameter, param))
+            param.grad = None
+
+        hooks = []
+        for p in model.parameters():
+            if p.requires_grad:
+                if p._post_accumulate_grad_hooks is not None and len(p._post_accumulate_grad_hooks) > 0 \
+                        and not ignore_existing_hooks:
+                    for h in hooks:
+                        if hasattr(h, 'remove'):
+                            h.remove()
+                    raise ValueError('Model already has post_accumulate_grad_hooks. If this is expected, '
+                                     'pass `ignore_existing_hooks=True`.')
+                hooks.append(p.register_post_accumulate_grad_hook(partial(_hook, optimizer=self)))
+        model._gradient_release_hooks = hooks
+        self._update_rate = update_rate
