@@ -126,6 +126,30 @@ int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* ste
                           void* table_host);
 int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Optional launch timing (measurement only; no counterpart in the reference). While enabled, the
+ * *_step functions record a hipEvent pair around every launch, up to `max_launches` launches;
+ * *_timing_read waits for them, writes the summed milliseconds and launch counts per kernel
+ * kind (THORN_KIND_*) and starts a new window. max_launches = 0 disables timing.
+ * ------------------------------------------------------------------------------------------ */
+enum {
+    THORN_KIND_PRE = 0,        /* momentum + first iterate (ortho_pre_kernel) */
+    THORN_KIND_NORM = 1,       /* per-matrix norm, decouple_md gains */
+    THORN_KIND_GRAM = 2,       /* Newton-Schulz Gram matrix */
+    THORN_KIND_POLY = 3,       /* Newton-Schulz polynomial a I + b A + c A^2 */
+    THORN_KIND_UPDATE = 4,     /* Newton-Schulz update P X / X P (and the fused apply) */
+    THORN_KIND_ROWSTATS = 5,   /* per-row normalization statistics */
+    THORN_KIND_PNN_APPLY = 6,  /* per-row normalized apply */
+    THORN_KIND_MD_FACTOR = 7,  /* decouple_md renormalization factor */
+    THORN_KIND_MD_RESCALE = 8, /* decouple_md reassembly */
+    THORN_KIND_ADAM = 9,       /* multi-tensor Adam */
+    THORN_KIND_COUNT = 10
+};
+int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
+int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);
+int thorn_adam_timing_enable(thorn_adam_plan_t plan, int max_launches);
+int thorn_adam_timing_read(thorn_adam_plan_t plan, double* ms, int* launches, int n_kinds);
+
 #ifdef __cplusplus
 }
 #endif

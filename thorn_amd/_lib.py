@@ -65,7 +65,12 @@ SIGNATURES = {
     'thorn_adam_table_bytes': (_sz, [_vp]),
     'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp]),
     'thorn_adam_step': (_i, [_vp, _vp, _vp]),
+    'thorn_ortho_timing_enable': (_i, [_vp, _i]),
+    'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
+    'thorn_adam_timing_enable': (_i, [_vp, _i]),
+    'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
+KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam']
 ABI_VERSION = 1
 
 _lib = None
@@ -106,6 +111,13 @@ def check(rc: int, what: str) -> None:
         raise ThornError(f'{what} failed (code {rc}): {msg}')
 
 
+def _timing_read(fn, handle) -> dict:
+    ms = np.zeros(len(KINDS), dtype=np.float64)
+    cnt = np.zeros(len(KINDS), dtype=np.int32)
+    check(fn(handle, ms.ctypes.data, cnt.ctypes.data, len(KINDS)), 'timing_read')
+    return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(KINDS) if cnt[i] > 0}
+
+
 class OrthoPlan:
     """Host plan of one orthogonalized matrix set (shapes and per-matrix options)."""
 
@@ -132,6 +144,12 @@ class OrthoPlan:
         iters = coeffs.shape[0]
         check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, stream),
               'thorn_ortho_step')
+
+    def timing_enable(self, max_launches: int) -> None:
+        check(self._lib.thorn_ortho_timing_enable(self.handle, max_launches), 'thorn_ortho_timing_enable')
+
+    def timing_read(self) -> dict:
+        return _timing_read(self._lib.thorn_ortho_timing_read, self.handle)
 
     def __del__(self):
         h = getattr(self, 'handle', None)
@@ -160,6 +178,12 @@ class AdamPlan:
 
     def step(self, table_dev: int, stream: int) -> None:
         check(self._lib.thorn_adam_step(self.handle, table_dev, stream), 'thorn_adam_step')
+
+    def timing_enable(self, max_launches: int) -> None:
+        check(self._lib.thorn_adam_timing_enable(self.handle, max_launches), 'thorn_adam_timing_enable')
+
+    def timing_read(self) -> dict:
+        return _timing_read(self._lib.thorn_adam_timing_read, self.handle)
 
     def __del__(self):
         h = getattr(self, 'handle', None)

@@ -42,6 +42,73 @@ struct TaskOffsets {
     int32_t n, total;
 };
 
+// Optional per-launch timing: a pool of hipEvent pairs recorded around each launch while enabled.
+struct LaunchTimer {
+    std::vector<hipEvent_t> ev;   // 2 per record
+    std::vector<int> kind;
+    int used = 0;
+    bool overflow = false;
+
+    ~LaunchTimer() { release(); }
+    void release() {
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+        ev.clear();
+        kind.clear();
+        used = 0;
+    }
+    bool enabled() const { return !ev.empty(); }
+    int begin(int k, hipStream_t st) {
+        if (!enabled()) return -1;
+        if (used >= static_cast<int>(kind.size())) {
+            overflow = true;
+            return -1;
+        }
+        kind[used] = k;
+        (void)hipEventRecord(ev[2 * used], st);
+        return used++;
+    }
+    void end(int slot, hipStream_t st) {
+        if (slot >= 0) (void)hipEventRecord(ev[2 * slot + 1], st);
+    }
+};
+
+int timer_enable(LaunchTimer& t, int max_launches) {
+    t.release();
+    if (max_launches <= 0) return THORN_OK;
+    t.ev.resize(2 * size_t(max_launches));
+    t.kind.assign(max_launches, -1);
+    for (auto& e : t.ev) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            t.release();
+            return THORN_ERR_HIP;
+        }
+    }
+    t.used = 0;
+    t.overflow = false;
+    return THORN_OK;
+}
+
+int timer_read(LaunchTimer& t, double* ms, int* count, int n_kinds) {
+    for (int k = 0; k < n_kinds; ++k) {
+        ms[k] = 0.0;
+        count[k] = 0;
+    }
+    for (int i = 0; i < t.used; ++i) {
+        if (hipEventSynchronize(t.ev[2 * i + 1]) != hipSuccess) return THORN_ERR_HIP;
+        float e = 0.f;
+        if (hipEventElapsedTime(&e, t.ev[2 * i], t.ev[2 * i + 1]) != hipSuccess) return THORN_ERR_HIP;
+        const int k = t.kind[i];
+        if (k >= 0 && k < n_kinds) {
+            ms[k] += e;
+            count[k] += 1;
+        }
+    }
+    const bool of = t.overflow;
+    t.used = 0;
+    t.overflow = false;
+    return of ? THORN_ERR_INVALID : THORN_OK;
+}
+
 }  // namespace
 
 struct thorn_ortho_plan {
@@ -51,6 +118,7 @@ struct thorn_ortho_plan {
     size_t mats_off = 0;
     TaskOffsets pre{}, sym{}, g3{}, pnn{}, md{};
     std::vector<int32_t> pre_order, sym_order, g3_order, pnn_order, md_order;
+    LaunchTimer timer;
 };
 
 struct thorn_adam_plan {
@@ -60,6 +128,7 @@ struct thorn_adam_plan {
     size_t table_bytes = 0;
     size_t starts_off = 0, order_off = 0;
     int32_t total = 0;
+    LaunchTimer timer;
 };
 
 namespace {
@@ -311,43 +380,66 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     hipStream_t st = static_cast<hipStream_t>(stream);
     const char* dev = static_cast<const char*>(table_dev);
     const auto* mats = reinterpret_cast<const thorn::OrthoMat*>(dev + plan->mats_off);
-    int rc;
-    hipLaunchKernelGGL(thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0, st, mats, task_list(dev, plan->pre));
-    if ((rc = check_launch("ortho_pre_kernel"))) return rc;
-    hipLaunchKernelGGL(thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
-    if ((rc = check_launch("ortho_norm_kernel"))) return rc;
+    LaunchTimer& tm = plan->timer;
+    int rc, slot;
+#define THORN_LAUNCH(kind, name, ...)                      \
+    slot = tm.begin(kind, st);                             \
+    hipLaunchKernelGGL(__VA_ARGS__);                       \
+    tm.end(slot, st);                                      \
+    if ((rc = check_launch(name))) return rc;
+
+    THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
+                 st, mats, task_list(dev, plan->pre));
+    THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
     const thorn::TaskList sym = task_list(dev, plan->sym), g3 = task_list(dev, plan->g3);
     for (int it = 0; it < iters; ++it) {
-        if (it == 0)
-            hipLaunchKernelGGL(thorn::ns_gram_kernel<true>, dim3(sym.total), dim3(256), 0, st, mats, sym, it);
-        else
-            hipLaunchKernelGGL(thorn::ns_gram_kernel<false>, dim3(sym.total), dim3(256), 0, st, mats, sym, it);
-        if ((rc = check_launch("ns_gram_kernel"))) return rc;
-        hipLaunchKernelGGL(thorn::ns_poly_kernel, dim3(sym.total), dim3(256), 0, st, mats, sym,
-                           coeffs[3 * it], coeffs[3 * it + 1], coeffs[3 * it + 2]);
-        if ((rc = check_launch("ns_poly_kernel"))) return rc;
-        if (it == 0)
-            hipLaunchKernelGGL(thorn::ns_update_kernel<true>, dim3(g3.total), dim3(256), 0, st, mats, g3, it,
-                               it == iters - 1 ? 1 : 0);
-        else
-            hipLaunchKernelGGL(thorn::ns_update_kernel<false>, dim3(g3.total), dim3(256), 0, st, mats, g3, it,
-                               it == iters - 1 ? 1 : 0);
-        if ((rc = check_launch("ns_update_kernel"))) return rc;
+        const int fin = it == iters - 1 ? 1 : 0;
+        if (it == 0) {
+            THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel<true>, dim3(sym.total), dim3(256),
+                         0, st, mats, sym, it);
+        } else {
+            THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel<false>, dim3(sym.total), dim3(256),
+                         0, st, mats, sym, it);
+        }
+        THORN_LAUNCH(THORN_KIND_POLY, "ns_poly_kernel", thorn::ns_poly_kernel, dim3(sym.total), dim3(256), 0, st,
+                     mats, sym, coeffs[3 * it], coeffs[3 * it + 1], coeffs[3 * it + 2]);
+        if (it == 0) {
+            THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel<true>, dim3(g3.total),
+                         dim3(256), 0, st, mats, g3, it, fin);
+        } else {
+            THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel<false>, dim3(g3.total),
+                         dim3(256), 0, st, mats, g3, it, fin);
+        }
     }
     if (plan->pnn.n > 0) {
         const thorn::TaskList pnn = task_list(dev, plan->pnn);
-        hipLaunchKernelGGL(thorn::ortho_rowstats_kernel, dim3(pnn.n), dim3(256), 0, st, mats, pnn.order);
-        if ((rc = check_launch("ortho_rowstats_kernel"))) return rc;
-        hipLaunchKernelGGL(thorn::ortho_pnn_apply_kernel, dim3(pnn.total), dim3(256), 0, st, mats, pnn);
-        if ((rc = check_launch("ortho_pnn_apply_kernel"))) return rc;
+        THORN_LAUNCH(THORN_KIND_ROWSTATS, "ortho_rowstats_kernel", thorn::ortho_rowstats_kernel, dim3(pnn.n),
+                     dim3(256), 0, st, mats, pnn.order);
+        THORN_LAUNCH(THORN_KIND_PNN_APPLY, "ortho_pnn_apply_kernel", thorn::ortho_pnn_apply_kernel, dim3(pnn.total),
+                     dim3(256), 0, st, mats, pnn);
     }
     if (plan->md.n > 0) {
         const thorn::TaskList md = task_list(dev, plan->md);
-        hipLaunchKernelGGL(thorn::ortho_md_factor_kernel, dim3(md.n), dim3(256), 0, st, mats, md.order);
-        if ((rc = check_launch("ortho_md_factor_kernel"))) return rc;
-        hipLaunchKernelGGL(thorn::ortho_md_rescale_kernel, dim3(md.total), dim3(256), 0, st, mats, md);
-        if ((rc = check_launch("ortho_md_rescale_kernel"))) return rc;
+        THORN_LAUNCH(THORN_KIND_MD_FACTOR, "ortho_md_factor_kernel", thorn::ortho_md_factor_kernel, dim3(md.n),
+                     dim3(256), 0, st, mats, md.order);
+        THORN_LAUNCH(THORN_KIND_MD_RESCALE, "ortho_md_rescale_kernel", thorn::ortho_md_rescale_kernel,
+                     dim3(md.total), dim3(256), 0, st, mats, md);
     }
+#undef THORN_LAUNCH
+    return THORN_OK;
+}
+
+int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches) {
+    if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_timing_enable: null plan");
+    if (timer_enable(plan->timer, max_launches)) return fail(THORN_ERR_HIP, "thorn_ortho_timing_enable: hipEventCreate failed");
+    return THORN_OK;
+}
+
+int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds) {
+    if (!plan || !ms || !launches || n_kinds < 0) return fail(THORN_ERR_INVALID, "thorn_ortho_timing_read: bad argument");
+    const int rc = timer_read(plan->timer, ms, launches, n_kinds);
+    if (rc == THORN_ERR_HIP) return fail(rc, "thorn_ortho_timing_read: event query failed");
+    if (rc) return fail(rc, "thorn_ortho_timing_read: more launches than the enabled capacity");
     return THORN_OK;
 }
 
@@ -431,9 +523,26 @@ int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream)
     tl.starts = reinterpret_cast<const int32_t*>(dev + plan->starts_off);
     tl.n = static_cast<int32_t>(plan->order.size());
     tl.total = plan->total;
-    hipLaunchKernelGGL(thorn::adam_kernel, dim3(plan->total), dim3(256), 0, static_cast<hipStream_t>(stream),
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int slot = plan->timer.begin(THORN_KIND_ADAM, st);
+    hipLaunchKernelGGL(thorn::adam_kernel, dim3(plan->total), dim3(256), 0, st,
                        reinterpret_cast<const thorn::AdamTensor*>(dev), tl);
+    plan->timer.end(slot, st);
     return check_launch("adam_kernel");
+}
+
+int thorn_adam_timing_enable(thorn_adam_plan_t plan, int max_launches) {
+    if (!plan) return fail(THORN_ERR_INVALID, "thorn_adam_timing_enable: null plan");
+    if (timer_enable(plan->timer, max_launches)) return fail(THORN_ERR_HIP, "thorn_adam_timing_enable: hipEventCreate failed");
+    return THORN_OK;
+}
+
+int thorn_adam_timing_read(thorn_adam_plan_t plan, double* ms, int* launches, int n_kinds) {
+    if (!plan || !ms || !launches || n_kinds < 0) return fail(THORN_ERR_INVALID, "thorn_adam_timing_read: bad argument");
+    const int rc = timer_read(plan->timer, ms, launches, n_kinds);
+    if (rc == THORN_ERR_HIP) return fail(rc, "thorn_adam_timing_read: event query failed");
+    if (rc) return fail(rc, "thorn_adam_timing_read: more launches than the enabled capacity");
+    return THORN_OK;
 }
 
 }  // extern "C"
