@@ -143,7 +143,8 @@ enum {
     THORN_KIND_MD_FACTOR = 7,  /* decouple_md renormalization factor */
     THORN_KIND_MD_RESCALE = 8, /* decouple_md reassembly */
     THORN_KIND_ADAM = 9,       /* multi-tensor Adam */
-    THORN_KIND_COUNT = 10
+    THORN_KIND_CAST = 10,      /* first iterate: u / ||u|| rounded to f16 */
+    THORN_KIND_COUNT = 11
 };
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
 int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);

@@ -70,7 +70,7 @@ SIGNATURES = {
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
     'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
-KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam']
+KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast']
 ABI_VERSION = 1
 
 _lib = None

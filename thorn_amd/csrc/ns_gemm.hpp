@@ -15,126 +15,119 @@
 
 namespace thorn {
 
-// Block tile BM x BN, K step BK, 256 threads as 2 x 2 waves, each wave (BM/2) x (BN/2).
-template <int BM_, int BN_, int BK_>
+// Block tile BM x BN (128 or 256 each), K step 32, 256 threads as 2 x 2 waves, each wave owning
+// (BM/2) x (BN/2) of the tile. S pipeline stages of LDS, filled by direct global->LDS loads.
+template <int BM_, int BN_, int S_ = 4>
 struct GemmCfg {
-    static constexpr int BM = BM_, BN = BN_, BK = BK_;
+    static constexpr int BM = BM_, BN = BN_, BK = 32, S = S_;
     static constexpr int WM = BM / 2, WN = BN / 2;
     static constexpr int TM = WM / 32, TN = WN / 32;
-    static constexpr int PADK = 8;    // row padding (halves) of K-major tiles: 144-byte rows for BK=64
-    static constexpr int PADM = 16;   // row padding (halves) of MN-major tiles
-    static constexpr int LDK = BK + PADK;
-    static constexpr int LDA_MN = BM + PADM;
-    static constexpr int LDB_MN = BN + PADM;
-    static constexpr int A_HALVES = (BM * LDK > BK * LDA_MN) ? BM * LDK : BK * LDA_MN;
-    static constexpr int B_HALVES = (BN * LDK > BK * LDB_MN) ? BN * LDK : BK * LDB_MN;
-    static constexpr int STAGE_HALVES = A_HALVES + B_HALVES;
-    static constexpr int LDS_HALVES = 2 * STAGE_HALVES;
-    static constexpr int A_CHUNKS = BM * BK / 8 / 256;   // 16-byte chunks per thread per K step
-    static constexpr int B_CHUNKS = BN * BK / 8 / 256;
-    static_assert(A_CHUNKS * 256 * 8 == BM * BK, "A tile must split evenly over 256 threads");
-    static_assert(B_CHUNKS * 256 * 8 == BN * BK, "B tile must split evenly over 256 threads");
+    static constexpr int A_BYTES = BM * BK * 2;          // one stage of A, no padding
+    static constexpr int B_BYTES = BN * BK * 2;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int LDS_BYTES = S * STAGE_BYTES;
+    static constexpr int A_LOADS = BM / 64;               // 1 KB direct loads per wave per stage
+    static constexpr int B_LOADS = BN / 64;
+    static constexpr int LOADS_PER_STAGE = A_LOADS + B_LOADS;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-// A GEMM operand in global memory: element (mn, k) lives at
+// A GEMM operand in global memory (f16): element (mn, k) lives at
 //   K-major:  ptr[mn * ld + k]     (rows = number of valid mn rows)
 //   MN-major: ptr[k * ld + mn]     (rows = number of valid k rows)
 // ld is a multiple of 8 and the padding columns [logical width, ld) hold zeros, so a 16-byte
-// chunk is either entirely inside a row or entirely outside it.
-// Sources are f16, or fp32 (the first iterate) converted to f16 after scaling by `scale` on its
-// way into LDS; the element type is a template parameter of the loader (F32).
+// chunk is either entirely inside a row or entirely outside it; chunks outside are read from
+// `zero`, a 16-byte block of zeros.
 struct Operand {
-    const void* ptr;
+    const _Float16* ptr;
     int64_t ld;
     int32_t rows;
     int32_t kmajor;
-    float scale;
 };
 
-// Loads this thread's 16-byte f16 chunks (or 32-byte fp32 chunks, two registers each) of a tile.
-template <int MNROWS, int BK, bool F32, int NREG>
-__device__ __forceinline__ void gload(const Operand& op, int mn0, int k0, uint4 (&r)[NREG]) {
-    constexpr int NCH = F32 ? NREG / 2 : NREG;
-    constexpr int ESZ = F32 ? 4 : 2;
-    const char* base = static_cast<const char*>(op.ptr);
+// LDS layouts of one stage, 16-byte chunks, XOR-swizzled so that the fragment reads of a wave
+// hit distinct banks:
+//   K-major:  MN rows x 4 chunks (64 B); chunk c of row r sits at r*64 + (c ^ ((r >> 2) & 3))*16.
+//             16 lanes reading rows r..r+15 at one chunk cover all 64 banks.
+//   MN-major: 32 k-rows x MN/8 chunks; chunk c of k-row k at k*MN*2 + (c ^ ((k & 3) << 2))*16.
+//             The 32 lanes of a ds_read_tr16_b64 pair read 4 k-rows x 4 chunks: 16 distinct
+//             chunks mod 16, all 64 banks.
+// The direct loads write 64 consecutive chunk slots per instruction, so each lane loads the
+// global chunk whose swizzled position is its slot.
+template <int MN>
+__device__ __forceinline__ void dma_tile(const Operand& op, int mn0, int k0, char* lds, const void* zero,
+                                         int wave, int lane) {
+    constexpr int PER_WAVE = MN / 64;
+    const char* base = reinterpret_cast<const char*>(op.ptr);
+    wave = __builtin_amdgcn_readfirstlane(wave);   // the LDS address (M0) must be wave-uniform
 #pragma unroll
-    for (int q = 0; q < NCH; ++q) {
-        const int id = threadIdx.x + 256 * q;
+    for (int q = 0; q < PER_WAVE; ++q) {
+        const int slot0 = (wave * PER_WAVE + q) * 64;
+        const int slot = slot0 + lane;
         int64_t row, col;
         if (op.kmajor) {
-            row = mn0 + id / (BK / 8);
-            col = k0 + (id % (BK / 8)) * 8;
+            const int r = slot >> 2, pc = slot & 3;
+            const int c = pc ^ ((r >> 2) & 3);
+            row = mn0 + r;
+            col = k0 + c * 8;
         } else {
-            row = k0 + id / (MNROWS / 8);
-            col = mn0 + (id % (MNROWS / 8)) * 8;
+            constexpr int CH = MN / 8;
+            const int k = slot / CH, pc = slot % CH;
+            const int c = pc ^ ((k & 3) << 2);
+            row = k0 + k;
+            col = mn0 + c * 8;
         }
-        const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
-        if (row < op.rows && col < op.ld) {
-            const uint4* src = reinterpret_cast<const uint4*>(base + (row * op.ld + col) * ESZ);
-            if (F32) {
-                r[2 * q] = src[0];
-                r[2 * q + 1] = src[1];
-            } else {
-                r[q] = src[0];
-            }
-        } else if (F32) {
-            r[2 * q] = zero;
-            r[2 * q + 1] = zero;
-        } else {
-            r[q] = zero;
-        }
-    }
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
-}
-
-__device__ __forceinline__ uint4 f32x8_to_f16x8(uint4 a, uint4 b, float s) {
-    uint4 o;
-    o.x = pack_h2(__uint_as_float(a.x) * s, __uint_as_float(a.y) * s);
-    o.y = pack_h2(__uint_as_float(a.z) * s, __uint_as_float(a.w) * s);
-    o.z = pack_h2(__uint_as_float(b.x) * s, __uint_as_float(b.y) * s);
-    o.w = pack_h2(__uint_as_float(b.z) * s, __uint_as_float(b.w) * s);
-    return o;
-}
-
-template <int MNROWS, int BK, int LDK, int LDMN, bool F32, int NREG>
-__device__ __forceinline__ void lstore(const Operand& op, _Float16* lds, uint4 (&r)[NREG]) {
-    constexpr int NCH = F32 ? NREG / 2 : NREG;
-#pragma unroll
-    for (int q = 0; q < NCH; ++q) {
-        const int id = threadIdx.x + 256 * q;
-        int off;
-        if (op.kmajor) off = (id / (BK / 8)) * LDK + (id % (BK / 8)) * 8;
-        else off = (id / (MNROWS / 8)) * LDMN + (id % (MNROWS / 8)) * 8;
-        const uint4 v = F32 ? f32x8_to_f16x8(r[2 * q], r[2 * q + 1], op.scale) : r[q];
-        *reinterpret_cast<uint4*>(lds + off) = v;
+        const void* src = (row < op.rows && col < op.ld) ? static_cast<const void*>(base + (row * op.ld + col) * 2)
+                                                          : zero;
+        __builtin_amdgcn_global_load_lds((const THORN_GLOBAL void*)(src),
+                                         (__attribute__((address_space(3))) void*)(lds + slot0 * 16), 16, 0, 0);
     }
 }
 
 typedef __attribute__((address_space(3))) short4v lds_s4;
 
-// MFMA fragment (8 halves) for 32-row tile `t0` (offset inside the block tile) at k step `kk`.
-template <int LDK, int LDMN>
-__device__ __forceinline__ half8 frag(const _Float16* lds, bool kmajor, int t0, int kk, int lane) {
+// MFMA fragment (8 halves) for the 32-wide sub-tile at `t0` and k16 step `ks` of a stage.
+template <int MN>
+__device__ __forceinline__ half8 frag(const char* lds, bool kmajor, int t0, int ks, int lane) {
     if (kmajor) {
-        return *reinterpret_cast<const half8*>(lds + (t0 + (lane & 31)) * LDK + kk + 8 * (lane >> 5));
+        const int r = t0 + (lane & 31);
+        const int c = 2 * ks + (lane >> 5);
+        return *reinterpret_cast<const half8*>(lds + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
     }
-    const int k = kk + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int k = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
     const int mn = t0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(lds + k * LDMN + mn));
-    short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(lds + (k + 4) * LDMN + mn));
+    const int c = mn >> 3, off = (mn & 7) * 2;
+    const char* p0 = lds + k * (MN * 2) + ((c ^ ((k & 3) << 2)) << 4) + off;
+    const char* p1 = lds + (k + 4) * (MN * 2) + ((c ^ (((k + 4) & 3) << 2)) << 4) + off;
+    short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
+    short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p1));
     half4 l4 = __builtin_bit_cast(half4, lo), h4 = __builtin_bit_cast(half4, hi);
     return half8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 }
 
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] at bits 3:0,
+// vmcnt[5:4] at bits 15:14, expcnt at 6:4, lgkmcnt at 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // acc[i][j] += A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over the whole K range.
-template <class C, bool AF32, bool BF32>
+// The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out transposed: lane l holds
+// row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3 in registers r..r+3,
+// which the epilogue writes to LDS as one 16-byte store.
+//
+// Pipeline over K tiles of 32 (S = 4 LDS stages, one block barrier per tile):
+//   tile t is loaded into stage t % S three tiles ahead of its use, by direct global->LDS loads;
+//   each tile is two k16 sub-steps; the LDS fragment reads of the next sub-step are in flight
+//   while the MFMAs of the current one run. Between the two sub-steps of tile t every wave waits
+//   for its own loads of tile t+1 and meets the others at the barrier: after it, tile t+1 is
+//   visible and nobody reads stage (t-1) % S any more, which then receives tile t+S-1.
+template <class C>
 __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B, int m0, int n0,
-                                              int K, floatx16 (&acc)[C::TM][C::TN], _Float16* smem) {
+                                              int K, floatx16 (&acc)[C::TM][C::TN], char* smem,
+                                              const void* zero) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
 #pragma unroll
@@ -142,52 +135,191 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
 
-    uint4 ra[C::A_CHUNKS * (AF32 ? 2 : 1)], rb[C::B_CHUNKS * (BF32 ? 2 : 1)];
     const int KT = (K + C::BK - 1) / C::BK;
-    gload<C::BM, C::BK, AF32>(A, m0, 0, ra);
-    gload<C::BN, C::BK, BF32>(B, n0, 0, rb);
-    lstore<C::BM, C::BK, C::LDK, C::LDA_MN, AF32>(A, smem, ra);
-    lstore<C::BN, C::BK, C::LDK, C::LDB_MN, BF32>(B, smem + C::A_HALVES, rb);
-    __syncthreads();
+    auto stage_a = [&](int t) { return smem + (t % C::S) * C::STAGE_BYTES; };
+    auto issue = [&](int t) {
+        char* st = stage_a(t);
+        dma_tile<C::BM>(A, m0, t * C::BK, st, zero, wave, lane);
+        dma_tile<C::BN>(B, n0, t * C::BK, st + C::A_BYTES, zero, wave, lane);
+    };
+#pragma unroll
+    for (int t = 0; t < C::S - 1; ++t)
+        if (t < KT) issue(t);
+    // tile 0 ready: loads of tiles 1 .. min(S-2, KT-1) may still be in flight
+    static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
+    if (C::S >= 5 && KT >= 4) wait_vmcnt<3 * C::LOADS_PER_STAGE>();
+    else if (C::S >= 4 && KT >= 3) wait_vmcnt<2 * C::LOADS_PER_STAGE>();
+    else if (KT >= 2) wait_vmcnt<C::LOADS_PER_STAGE>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
 
+    half8 fa[2][C::TM], fb[2][C::TN];
+    {
+        const char* sa = stage_a(0);
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM>(sa, A.kmajor, wm + 32 * i, 0, lane);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN>(sa + C::A_BYTES, B.kmajor, wn + 32 * j, 0, lane);
+    }
     for (int kt = 0; kt < KT; ++kt) {
-        _Float16* sa = smem + (kt & 1) * C::STAGE_HALVES;
-        _Float16* sb = sa + C::A_HALVES;
+        const char* sa = stage_a(kt);
+        // sub-step 0: read sub-step 1's fragments while the MFMAs of sub-step 0 run
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) fa[1][i] = frag<C::BM>(sa, A.kmajor, wm + 32 * i, 1, lane);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) fb[1][j] = frag<C::BN>(sa + C::A_BYTES, B.kmajor, wn + 32 * j, 1, lane);
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < C::TM * C::TN / 2; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // tile kt+1 ready (tiles kt+2 .. kt+S-2 may still be in flight), stage (kt-1) % S free
+        {
+            const int ahead = (KT - 1 < kt + C::S - 2 ? KT - 1 : kt + C::S - 2) - (kt + 1);
+            if (C::S >= 5 && ahead >= 2) wait_vmcnt<2 * C::LOADS_PER_STAGE>();
+            else if (C::S >= 4 && ahead >= 1) wait_vmcnt<C::LOADS_PER_STAGE>();
+            else wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
+        // sub-step 1: read the next tile's first fragments while the MFMAs of sub-step 1 run
         const bool more = kt + 1 < KT;
         if (more) {
-            gload<C::BM, C::BK, AF32>(A, m0, (kt + 1) * C::BK, ra);
-            gload<C::BN, C::BK, BF32>(B, n0, (kt + 1) * C::BK, rb);
+            const char* na = stage_a(kt + 1);
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM>(na, A.kmajor, wm + 32 * i, 0, lane);
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN>(na + C::A_BYTES, B.kmajor, wn + 32 * j, 0, lane);
         }
 #pragma unroll
-        for (int kk = 0; kk < C::BK; kk += 16) {
-            half8 fa[C::TM], fb[C::TN];
+        for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-            for (int i = 0; i < C::TM; ++i) fa[i] = frag<C::LDK, C::LDA_MN>(sa, A.kmajor, wm + 32 * i, kk, lane);
+            for (int j = 0; j < C::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j) fb[j] = frag<C::LDK, C::LDB_MN>(sb, B.kmajor, wn + 32 * j, kk, lane);
-#pragma unroll
-            for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int q = 0; q < C::TM * C::TN / 2; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        if (more) {
-            _Float16* na = smem + ((kt + 1) & 1) * C::STAGE_HALVES;
-            lstore<C::BM, C::BK, C::LDK, C::LDA_MN, AF32>(A, na, ra);
-            lstore<C::BN, C::BK, C::LDK, C::LDB_MN, BF32>(B, na + C::A_HALVES, rb);
-        }
-        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// Row index (inside the block tile) of accumulator register r of 32x32 tile i for this lane.
+// Epilogue: the tile is streamed through LDS (reusing the pipeline stages) in two halves of
+// WM = BM/2 rows, the rows owned by one row of waves:
+//   for_rows: N[row][col] staging (fp32); each thread then gets 8 consecutive columns of one row,
+//             so global traffic is 16-byte chunks with 32 lanes on one row;
+//   for_cols: transposed staging T[col][row]; each thread gets 8 consecutive rows of one column
+//             (the mirrored tile of a symmetric product).
 template <class C>
-__device__ __forceinline__ int acc_row(int wave, int lane, int i, int r) {
-    return (wave >> 1) * C::WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+struct Epi {
+    static constexpr int NS = C::BN + 4;    // N row stride (floats): 16 lanes x 16 B on distinct banks
+    static constexpr int TS = C::WM + 4;    // T row stride (floats)
+    static constexpr int N_BYTES = C::WM * NS * 4;
+    static constexpr int T_BYTES = C::BN * TS * 4;
+    static constexpr int BYTES = N_BYTES > T_BYTES ? N_BYTES : T_BYTES;
+    static constexpr int SMEM = BYTES > C::LDS_BYTES ? BYTES : C::LDS_BYTES;
+    static constexpr int ROW_CHUNKS = C::WM * (C::BN / 8) / 256;   // per thread per half
+    static constexpr int COL_CHUNKS = C::BN * (C::WM / 8) / 256;
+};
+
+// Chunk `it` of this thread in a half: 32 lanes of a wave share one row (row passes) or 16 lanes
+// one column (column passes), so every global access of a chunk pass is coalesced.
+template <class C>
+__device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
+    const int idx = it * 256 + threadIdx.x;
+    r = idx / (C::BN / 8);
+    c8 = (idx % (C::BN / 8)) * 8;
 }
 template <class C>
-__device__ __forceinline__ int acc_col(int wave, int lane, int j) {
-    return (wave & 1) * C::WN + 32 * j + (lane & 31);
+__device__ __forceinline__ void col_chunk(int it, int& c, int& r8) {
+    const int idx = it * 256 + threadIdx.x;
+    c = idx / (C::WM / 8);
+    r8 = (idx % (C::WM / 8)) * 8;
+}
+
+// fn(it, half, local_row, col8, float (&v)[8]): v = acc[row][col8 .. col8+7] (tile coordinates:
+// row = half * WM + local_row); `it` numbers this thread's chunks 0 .. ROW_CHUNKS-1, in the order
+// given by row_chunk().
+template <class C, class Fn>
+__device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
+    using E = Epi<C>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* N = reinterpret_cast<float*>(smem);
+    __syncthreads();   // the previous user of smem (main loop or another pass) is done
+    if ((wave >> 1) == half) {
+        const int wn = (wave & 1) * C::WN;
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 32 * i + (lane & 31);
+                    const int c = wn + 32 * j + 8 * q + 4 * (lane >> 5);
+                    *reinterpret_cast<floatx4*>(N + r * E::NS + c) =
+                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < E::ROW_CHUNKS; ++it) {
+        int r, c8;
+        row_chunk<C>(it, r, c8);
+        const floatx4 a = *reinterpret_cast<const floatx4*>(N + r * E::NS + c8);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(N + r * E::NS + c8 + 4);
+        float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        fn(it, half, r, c8, v);
+    }
+}
+
+// fn(it, half, col, local_row8, float (&v)[8]): v = acc[row8 .. row8+7][col] with
+// row8 = half*WM + local_row8; chunk order given by col_chunk().
+template <class C, class Fn>
+__device__ __forceinline__ void for_cols(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
+    using E = Epi<C>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* T = reinterpret_cast<float*>(smem);
+    __syncthreads();
+    if ((wave >> 1) == half) {
+        const int wn = (wave & 1) * C::WN;
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 32 * i + (lane & 31);
+                        const int c = wn + 32 * j + 8 * q + 4 * (lane >> 5) + e;
+                        T[c * E::TS + r] = acc[i][j][4 * q + e];
+                    }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < E::COL_CHUNKS; ++it) {
+        int c, r8;
+        col_chunk<C>(it, c, r8);
+        const floatx4 a = *reinterpret_cast<const floatx4*>(T + c * E::TS + r8);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(T + c * E::TS + r8 + 4);
+        float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        fn(it, half, c, r8, v);
+    }
+}
+
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ half8v to_half8(const float (&v)[8]) {
+    return half8v{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3],
+                  (_Float16)v[4], (_Float16)v[5], (_Float16)v[6], (_Float16)v[7]};
 }
 
 // Upper-triangle tile (ti <= tj) number q of a T x T tile grid, row by row.

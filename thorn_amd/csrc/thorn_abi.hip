@@ -195,7 +195,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     *out = nullptr;
     if (n < 0 || (n > 0 && !descs)) return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: bad matrix list");
     auto* plan = new thorn_ortho_plan();
-    size_t ws = 0;
+    size_t ws = kAlign;   // [0, 256): zeros, never written (source of out-of-range GEMM tile chunks)
     auto take = [&ws](size_t bytes) {
         if (bytes == 0) return kNone;
         const size_t o = ws;
@@ -253,14 +253,28 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     }
     plan->ws_bytes = std::max<size_t>(ws, kAlign);
 
-    // Task orders: symmetric phases longest contraction first, the rest in matrix order.
+    // Task orders. The GEMM kernels remap blocks so that each XCD runs a contiguous eighth of
+    // the tiles; to give every eighth the same mix of work, matrices are dealt to 8 bins in
+    // snake order by cost (s^2 * l per tile row), and the bins are concatenated.
     std::vector<int32_t> all(n);
     for (int i = 0; i < n; ++i) all[i] = i;
     plan->pre_order = all;
-    plan->sym_order = all;
-    std::stable_sort(plan->sym_order.begin(), plan->sym_order.end(),
-                     [&](int a, int b) { return plan->mats[a].l > plan->mats[b].l; });
-    plan->g3_order = plan->sym_order;
+    auto snake = [&](auto cost) {
+        std::vector<int32_t> by = all;
+        std::stable_sort(by.begin(), by.end(), [&](int a, int b) { return cost(a) > cost(b); });
+        std::vector<std::vector<int32_t>> bins(8);
+        for (size_t r = 0; r < by.size(); ++r) {
+            const size_t round = r / 8, pos = r % 8;
+            bins[(round & 1) ? 7 - pos : pos].push_back(by[r]);
+        }
+        std::vector<int32_t> out;
+        for (auto& bin : bins) out.insert(out.end(), bin.begin(), bin.end());
+        return out;
+    };
+    plan->sym_order = snake([&](int i) { return double(plan->mats[i].sym_tiles) * plan->mats[i].l; });
+    plan->g3_order = snake([&](int i) {
+        return double(plan->mats[i].g3_tiles_m) * plan->mats[i].g3_tiles_n * plan->mats[i].s;
+    });
     for (int i = 0; i < n; ++i) {
         if (plan->mats[i].flags & THORN_MAT_PER_ROW_NORM) plan->pnn_order.push_back(i);
         if (plan->mats[i].flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
@@ -330,6 +344,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.rgm = S.row_gain_moment; M.rgv = S.row_gain_variance;
         M.cgm = S.col_gain_moment; M.cgv = S.col_gain_variance;
         M.target = S.target_norm;
+        M.zero = ws;
         M.x0 = static_cast<float*>(at(L.x0));
         M.xa = static_cast<_Float16*>(at(L.xa));
         M.xb = static_cast<_Float16*>(at(L.xb));
@@ -392,24 +407,16 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
     const thorn::TaskList sym = task_list(dev, plan->sym), g3 = task_list(dev, plan->g3);
+    THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total), dim3(256), 0,
+                 st, mats, task_list(dev, plan->pre));
     for (int it = 0; it < iters; ++it) {
         const int fin = it == iters - 1 ? 1 : 0;
-        if (it == 0) {
-            THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel<true>, dim3(sym.total), dim3(256),
-                         0, st, mats, sym, it);
-        } else {
-            THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel<false>, dim3(sym.total), dim3(256),
-                         0, st, mats, sym, it);
-        }
+        THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel, dim3(sym.total), dim3(256), 0, st,
+                     mats, sym, it);
         THORN_LAUNCH(THORN_KIND_POLY, "ns_poly_kernel", thorn::ns_poly_kernel, dim3(sym.total), dim3(256), 0, st,
                      mats, sym, coeffs[3 * it], coeffs[3 * it + 1], coeffs[3 * it + 2]);
-        if (it == 0) {
-            THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel<true>, dim3(g3.total),
-                         dim3(256), 0, st, mats, g3, it, fin);
-        } else {
-            THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel<false>, dim3(g3.total),
-                         dim3(256), 0, st, mats, g3, it, fin);
-        }
+        THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel, dim3(g3.total), dim3(256), 0,
+                     st, mats, g3, it, fin);
     }
     if (plan->pnn.n > 0) {
         const thorn::TaskList pnn = task_list(dev, plan->pnn);

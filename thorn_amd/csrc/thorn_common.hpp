@@ -21,6 +21,30 @@ typedef short short4v __attribute__((vector_size(8)));
 
 constexpr int kWave = 64;
 
+// Global-memory views of generic pointers. Loads and stores through them compile to global_*
+// instructions (vmcnt only) instead of flat_* (which also count in lgkmcnt and so force the LDS
+// fragment reads of the GEMM pipeline to drain).
+#define THORN_GLOBAL __attribute__((address_space(1)))
+
+// (The host pass of the compiler type-checks device templates too but has no address space 1
+// view of these types; it never runs this code.)
+template <class T>
+__device__ __forceinline__ T ldg(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *reinterpret_cast<const THORN_GLOBAL T*>(reinterpret_cast<uintptr_t>(p));
+#else
+    return *reinterpret_cast<const T*>(p);
+#endif
+}
+template <class T>
+__device__ __forceinline__ void stg(void* p, const T& v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    *reinterpret_cast<THORN_GLOBAL T*>(reinterpret_cast<uintptr_t>(p)) = v;
+#else
+    *reinterpret_cast<T*>(p) = v;
+#endif
+}
+
 // ---------------------------------------------------------------------------------------------
 // Numeric helpers
 // ---------------------------------------------------------------------------------------------
@@ -60,6 +84,16 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
     return t;
 }
 
+// Workgroups of a launch are dispatched to the 8 XCDs round-robin (block b runs on XCD b % 8),
+// and each XCD has its own L2. Remapping makes XCD x run the contiguous range
+// [x*per + min(x, rem), ...) of logical tiles, so tiles that share operand panels share an L2.
+// A bijection on [0, total).
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+    const int x = b & 7, i = b >> 3;
+    const int per = total >> 3, rem = total & 7;
+    return x * per + (x < rem ? x : rem) + i;
+}
+
 // Finds the task k with starts[k] <= b < starts[k+1] (starts has n+1 entries, ascending).
 __device__ __forceinline__ int find_task(const int32_t* starts, int n, int b) {
     int lo = 0, hi = n - 1;
@@ -96,6 +130,7 @@ struct OrthoMat {
     float* cgm;
     float* cgv;
     const float* target;   // decoupled-magnitude target norm (0-d)
+    const void* zero;      // 256 bytes of zeros in the workspace (source of out-of-range tile chunks)
 
     float* x0;         // rows x ldx, u = g + beta1*m (fp32, unnormalized)
     _Float16* xa;      // rows x ldx, Newton-Schulz iterate (ping)
