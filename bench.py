@@ -184,6 +184,107 @@ def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
 
 
 # ---------------------------------------------------------------------------------------------
+# rocprofv3 summaries and the HBM-traffic calibration
+# ---------------------------------------------------------------------------------------------
+
+TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'ns_update_traffic_qwen3_300m.md')
+_TRAFFIC_RE = r'ns_update_kernel HBM bytes per launch: ([0-9.eE+]+)'
+
+
+def copy_calibration(mib: int, device) -> None:
+    """One plain fp32 elementwise kernel (torch.neg) over `mib` MiB: it reads and writes exactly
+    `mib` MiB, so what FETCH_SIZE / WRITE_SIZE report for it gives the counters' scale."""
+    import torch
+    src = torch.ones(mib << 18, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _short_kernel_name(name: str) -> str:
+    import re
+    name = re.sub(r'^void ', '', name)
+    depth, out = 0, []
+    for ch in name:          # drop argument lists, keep template arguments
+        if ch == '(':
+            depth += 1
+        elif ch == ')':
+            depth -= 1
+        elif depth == 0:
+            out.append(ch)
+    return ''.join(out).strip()
+
+
+def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
+    """Markdown summary of rocprofv3 CSV output directories: the kernel statistics table
+    (`*kernel_stats.csv`) and, when present, per-kernel counter averages per dispatch
+    (`*counter_collection.csv`, one directory per counter pass). With `cal_mib`, FETCH_SIZE /
+    WRITE_SIZE are scaled by what they read for the `torch.neg` calibration kernel of that many
+    MiB, and the HBM bytes per ns_update_kernel launch are printed."""
+    import csv
+    import glob
+
+    def found(pattern):
+        return sorted(f for p in paths for f in glob.glob(os.path.join(p, '**', pattern), recursive=True))
+
+    lines = []
+    for f in found('*kernel_stats.csv'):
+        rows = list(csv.DictReader(open(f)))
+        lines += ['| kernel | calls | total ms | avg us | min us | max us | % |',
+                  '|---|---:|---:|---:|---:|---:|---:|']
+        for r in rows:
+            n = _short_kernel_name(r['Name'])
+            n = n if len(n) <= 70 else n[:67] + '...'
+            lines.append(f"| `{n}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                         f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+                         f"{float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    per: dict = {}
+    for f in found('*counter_collection.csv'):
+        for r in csv.DictReader(open(f)):
+            key = (_short_kernel_name(r['Kernel_Name']), r['Counter_Name'])
+            per.setdefault(key, {})[(f, r['Dispatch_Id'])] = float(r['Counter_Value'])
+    if per:
+        counters = sorted({c for _, c in per})
+        kernels = sorted({k for k, _ in per})
+        scale = {}
+        for c in ('FETCH_SIZE', 'WRITE_SIZE'):
+            cal = [v for (k, cc), d in per.items() if cc == c and 'neg_kernel' in k for v in d.values()]
+            if cal_mib and cal:
+                scale[c] = cal_mib * 1024.0 / max(cal)      # KiB expected / KiB read
+        lines += ['', '| kernel | dispatches | ' + ' | '.join(f'{c} / dispatch' for c in counters) + ' |',
+                  '|---|---:|' + '---:|' * len(counters)]
+        for k in kernels:
+            vals = [per.get((k, c), {}) for c in counters]
+            nd = max(len(v) for v in vals)
+            cells = [f'{sum(v.values()) / len(v):.4g}' if v else '' for v in vals]
+            kk = k if len(k) <= 70 else k[:67] + '...'
+            lines.append(f'| `{kk}` | {nd} | ' + ' | '.join(cells) + ' |')
+        if scale:
+            lines += ['', 'Counter scale from the calibration kernel (expected KiB / counted KiB): ' +
+                      ', '.join(f'{c} x{s:.4f}' for c, s in scale.items())]
+            upd = [k for k in kernels if k.startswith('thorn::ns_update_kernel')]
+            tot = 0.0
+            for c, s in scale.items():
+                v = [x for k in upd for x in per.get((k, c), {}).values()]
+                if v:
+                    tot += sum(v) / len(v) * 1024.0 * s
+            if upd and len(scale) == 2:
+                lines.append(f'\nns_update_kernel HBM bytes per launch: {tot:.6g}')
+    return '\n'.join(lines)
+
+
+def traffic_from_profile() -> float | None:
+    """HBM bytes per ns_update_kernel launch from the committed counter summary, if present."""
+    import re
+    try:
+        m = re.search(_TRAFFIC_RE, open(TRAFFIC_PROFILE).read())
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
+
+
+# ---------------------------------------------------------------------------------------------
 # GPU measurement
 # ---------------------------------------------------------------------------------------------
 
@@ -194,8 +295,15 @@ def main() -> int:
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--config', type=int, default=2)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--cpu-budget', type=float, default=30.0)
+    ap.add_argument('--cpu-budget', type=float, default=20.0)
+    ap.add_argument('--copy-cal-mib', type=int, default=0,
+                    help='run one torch.neg over this many MiB first (counter calibration)')
+    ap.add_argument('--rocprof-summary', metavar='DIR', nargs='+',
+                    help='print a markdown summary of rocprofv3 CSV output directories and exit')
     args = ap.parse_args()
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib))
+        return 0
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: this build has no multi-GPU path (each matrix\'s step '
               'is independent; the sharding design is in DESIGN.md). Run with --gpus 1.', file=sys.stderr)
@@ -206,6 +314,8 @@ def main() -> int:
 
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
+    if args.copy_cal_mib:
+        copy_calibration(args.copy_cal_mib, dev)
     t0 = time.perf_counter()
     params, grads, groups, mats = build_workload(args.config, dev)
     gen_s = time.perf_counter() - t0
@@ -294,7 +404,8 @@ def main() -> int:
                    'hbm_frac': round(cbytes / (upd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if upd_ms > 0 else None},
         'roofline': {'kernel': 'ns_update_kernel', 'bound': 'mfma', 'achieved': round(achieved, 1),
                      'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_PEAK_TFLOPS, 4),
-                     'traffic': None, 'flops_per_launch': upd_flops, 'avg_launch_ms': round(u_avg, 4)},
+                     'traffic': traffic_from_profile(), 'flops_per_launch': upd_flops,
+                     'avg_launch_ms': round(u_avg, 4)},
         'phases': phases,
         'cpu_baseline': cpu,
         'workload_gen_s': round(gen_s, 1),
