@@ -15,11 +15,13 @@ Left out, because they are outside the single-GPU hot path: the FSDP2/DTensor en
 Triton kernels (thorn.py:53-280) and the compile wrapper (thorn.py:379-423). Magma
 ``momentum_align`` (thorn.py:800-836) is restated because it is tiny, but the product rejects it.
 
-How the pieces are pinned (tests/test_oracle_*.py):
+How the pieces are pinned (tests/test_oracle.py):
   * coefficients, restarts, single-function outputs and multi-step trajectories: golden vectors
     written from the reference itself (tests/golden/make_golden.py);
   * Newton-Schulz: the f64 closed form U*phi(S)*V^T from an SVD;
   * Adam: torch.optim.Adam / RAdam special cases; per-row normalization: its invariants.
+Parity unpinned: ``w1rand`` and ``momentum_aligned_mask`` (Magma), which no golden or closed form
+covers; the product rejects ``momentum_align=True``, so neither is used as a checker.
 """
 from __future__ import annotations
 
@@ -342,7 +344,7 @@ def compute_rect(group: Group, step) -> float:
 
 
 def w1rand(s: int) -> tuple[int, int]:
-    """64-bit hash PRNG of Magma masking (thorn.py:800-804)."""
+    """64-bit hash PRNG of Magma masking (thorn.py:800-804). Parity unpinned."""
     C = 0xD07EBC63274654C7
     s = (s + C) & 0xFFFFFFFFFFFFFFFF
     t = s * (s ^ C)
@@ -350,7 +352,7 @@ def w1rand(s: int) -> tuple[int, int]:
 
 
 def momentum_aligned_mask(g, state, group: Group, *, tau=2.0, p=0.9, moment=None) -> float:
-    """Magma masking, single-process branch (thorn.py:806-836)."""
+    """Magma masking, single-process branch (thorn.py:806-836). Parity unpinned."""
     if not group.momentum_align:
         return 1.0
     g_flat = g.flatten()
