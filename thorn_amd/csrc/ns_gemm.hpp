@@ -32,9 +32,10 @@ struct GemmCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-// A GEMM operand in global memory (f16): element (mn, k) lives at
-//   K-major:  ptr[mn * ld + k]     (rows = number of valid mn rows)
-//   MN-major: ptr[k * ld + mn]     (rows = number of valid k rows)
+// A GEMM operand in global memory (f16). Its layout is a compile-time property of the main loop
+// (template flag KM):
+//   K-major  (KM):  element (mn, k) at ptr[mn * ld + k]   (rows = number of valid mn rows)
+//   MN-major (!KM): element (mn, k) at ptr[k * ld + mn]   (rows = number of valid k rows)
 // ld is a multiple of 8 and the padding columns [logical width, ld) hold zeros, so a 16-byte
 // chunk is either entirely inside a row or entirely outside it; chunks outside are read from
 // `zero`, a 16-byte block of zeros.
@@ -42,7 +43,6 @@ struct Operand {
     const _Float16* ptr;
     int64_t ld;
     int32_t rows;
-    int32_t kmajor;
 };
 
 // LDS layouts of one stage, 16-byte chunks, XOR-swizzled so that the fragment reads of a wave
@@ -54,42 +54,68 @@ struct Operand {
 //             chunks mod 16, all 64 banks.
 // The direct loads write 64 consecutive chunk slots per instruction, so each lane loads the
 // global chunk whose swizzled position is its slot.
-template <int MN>
-__device__ __forceinline__ void dma_tile(const Operand& op, int mn0, int k0, char* lds, const void* zero,
-                                         int wave, int lane) {
-    constexpr int PER_WAVE = MN / 64;
-    const char* base = reinterpret_cast<const char*>(op.ptr);
-    wave = __builtin_amdgcn_readfirstlane(wave);   // the LDS address (M0) must be wave-uniform
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) {
-        const int slot0 = (wave * PER_WAVE + q) * 64;
-        const int slot = slot0 + lane;
-        int64_t row, col;
-        if (op.kmajor) {
-            const int r = slot >> 2, pc = slot & 3;
-            const int c = pc ^ ((r >> 2) & 3);
-            row = mn0 + r;
-            col = k0 + c * 8;
-        } else {
-            constexpr int CH = MN / 8;
-            const int k = slot / CH, pc = slot % CH;
-            const int c = pc ^ ((k & 3) << 2);
-            row = k0 + k;
-            col = mn0 + c * 8;
-        }
-        const void* src = (row < op.rows && col < op.ld) ? static_cast<const void*>(base + (row * op.ld + col) * 2)
-                                                          : zero;
-        __builtin_amdgcn_global_load_lds((const THORN_GLOBAL void*)(src),
-                                         (__attribute__((address_space(3))) void*)(lds + slot0 * 16), 16, 0, 0);
-    }
+//
+// DmaSrc holds, per lane, the global source of each of its MN/64 chunk loads for K tile 0 and
+// the bound that decides, per tile t, whether the chunk exists (t * 32 < lim) or comes from
+// `zero`; tile t's source is src + t * step bytes.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
 }
+
+template <int MN, bool KM>
+struct DmaSrc {
+    static constexpr int PER_WAVE = MN / 64;
+    const char* src[PER_WAVE];
+    int lim[PER_WAVE];
+    int64_t step;
+
+    __device__ __forceinline__ void init(const Operand& op, int mn0, int wave, int lane) {
+        const char* base = reinterpret_cast<const char*>(op.ptr);
+        step = KM ? int64_t(BKC * 2) : int64_t(BKC) * op.ld * 2;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const int slot = (wave * PER_WAVE + q) * 64 + lane;
+            if (KM) {
+                const int r = slot >> 2, pc = slot & 3;
+                const int c = pc ^ ((r >> 2) & 3);
+                const int64_t row = mn0 + r;
+                src[q] = base + (row * op.ld + c * 8) * 2;
+                lim[q] = row < op.rows ? static_cast<int>(op.ld) - c * 8 : 0;
+            } else {
+                constexpr int CH = MN / 8;
+                const int k = slot / CH, pc = slot % CH;
+                const int c = pc ^ ((k & 3) << 2);
+                const int64_t col = mn0 + c * 8;
+                src[q] = base + (int64_t(k) * op.ld + col) * 2;
+                lim[q] = col < op.ld ? op.rows - k : 0;
+            }
+        }
+    }
+
+    // The loads are written as inline assembly so that the compiler does not track them as LDS
+    // writes: its conservative aliasing would otherwise wait for every outstanding load before
+    // the next LDS fragment read and serialize the pipeline. The main loop orders them explicitly
+    // (lds_wait_barrier); the "memory" clobber keeps LDS accesses from moving across them.
+    __device__ __forceinline__ void issue(int t, char* lds, const void* zero, int wave) const {
+        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_address(lds) + wave * PER_WAVE * 1024);
+        const int64_t off = t * step;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const void* p = (t * BKC < lim[q]) ? static_cast<const void*>(src[q] + off) : zero;
+            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p), "{m0}"(base + q * 1024)
+                         : "memory");
+        }
+    }
+
+    static constexpr int BKC = 32;   // K elements per tile
+};
 
 typedef __attribute__((address_space(3))) short4v lds_s4;
 
 // MFMA fragment (8 halves) for the 32-wide sub-tile at `t0` and k16 step `ks` of a stage.
-template <int MN>
-__device__ __forceinline__ half8 frag(const char* lds, bool kmajor, int t0, int ks, int lane) {
-    if (kmajor) {
+template <int MN, bool KM>
+__device__ __forceinline__ half8 frag(const char* lds, int t0, int ks, int lane) {
+    if (KM) {
         const int r = t0 + (lane & 31);
         const int c = 2 * ks + (lane >> 5);
         return *reinterpret_cast<const half8*>(lds + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
@@ -105,26 +131,39 @@ __device__ __forceinline__ half8 frag(const char* lds, bool kmajor, int t0, int 
     return half8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 }
 
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] at bits 3:0,
-// vmcnt[5:4] at bits 15:14, expcnt at 6:4, lgkmcnt at 11:8).
+// This wave's direct loads except the newest N are complete, then the block barrier: after it,
+// every wave's loads up to that point are visible in LDS. The "memory" clobber keeps the
+// compiler from moving LDS reads above it.
 template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
+__device__ __forceinline__ void lds_wait_barrier() {
     static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// acc[i][j] += A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over the whole K range.
+// Scheduling hint for one k16 sub-step: NM MFMAs spread evenly between NR LDS fragment reads.
+template <int NM, int NR, int Q = 0>
+__device__ __forceinline__ void interleave_mfma_ds() {
+    if constexpr (Q < NR) {
+        constexpr int m = (Q + 1) * NM / NR - Q * NM / NR;
+        if constexpr (m > 0) __builtin_amdgcn_sched_group_barrier(0x008, m, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        interleave_mfma_ds<NM, NR, Q + 1>();
+    }
+}
+
+// acc[i][j] += A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over the whole K range, with
+// operand layouts AK / BK (true = K-major).
 // The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out transposed: lane l holds
 // row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3 in registers r..r+3,
 // which the epilogue writes to LDS as one 16-byte store.
 //
-// Pipeline over K tiles of 32 (S = 4 LDS stages, one block barrier per tile):
-//   tile t is loaded into stage t % S three tiles ahead of its use, by direct global->LDS loads;
+// Pipeline over K tiles of 32 (S LDS stages, one block barrier per tile):
+//   tile t is loaded into stage t % S S-1 tiles ahead of its use, by direct global->LDS loads;
 //   each tile is two k16 sub-steps; the LDS fragment reads of the next sub-step are in flight
 //   while the MFMAs of the current one run. Between the two sub-steps of tile t every wave waits
 //   for its own loads of tile t+1 and meets the others at the barrier: after it, tile t+1 is
 //   visible and nobody reads stage (t-1) % S any more, which then receives tile t+S-1.
-template <class C>
+template <class C, bool AK, bool BK>
 __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B, int m0, int n0,
                                               int K, floatx16 (&acc)[C::TM][C::TN], char* smem,
                                               const void* zero) {
@@ -135,58 +174,57 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
 
+    DmaSrc<C::BM, AK> da;
+    DmaSrc<C::BN, BK> db;
+    da.init(A, m0, wave, lane);
+    db.init(B, n0, wave, lane);
     const int KT = (K + C::BK - 1) / C::BK;
     auto stage_a = [&](int t) { return smem + (t % C::S) * C::STAGE_BYTES; };
     auto issue = [&](int t) {
         char* st = stage_a(t);
-        dma_tile<C::BM>(A, m0, t * C::BK, st, zero, wave, lane);
-        dma_tile<C::BN>(B, n0, t * C::BK, st + C::A_BYTES, zero, wave, lane);
+        da.issue(t, st, zero, wave);
+        db.issue(t, st + C::A_BYTES, zero, wave);
     };
 #pragma unroll
     for (int t = 0; t < C::S - 1; ++t)
         if (t < KT) issue(t);
     // tile 0 ready: loads of tiles 1 .. min(S-2, KT-1) may still be in flight
     static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
-    if (C::S >= 5 && KT >= 4) wait_vmcnt<3 * C::LOADS_PER_STAGE>();
-    else if (C::S >= 4 && KT >= 3) wait_vmcnt<2 * C::LOADS_PER_STAGE>();
-    else if (KT >= 2) wait_vmcnt<C::LOADS_PER_STAGE>();
-    else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
+    if (C::S >= 5 && KT >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
+    else if (C::S >= 4 && KT >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
+    else if (KT >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
+    else lds_wait_barrier<0>();
 
+    constexpr int NREAD = C::TM * (AK ? 1 : 2) + C::TN * (BK ? 1 : 2);   // LDS reads per sub-step
     half8 fa[2][C::TM], fb[2][C::TN];
     {
         const char* sa = stage_a(0);
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM>(sa, A.kmajor, wm + 32 * i, 0, lane);
+        for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(sa, wm + 32 * i, 0, lane);
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN>(sa + C::A_BYTES, B.kmajor, wn + 32 * j, 0, lane);
+        for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN, BK>(sa + C::A_BYTES, wn + 32 * j, 0, lane);
     }
     for (int kt = 0; kt < KT; ++kt) {
         const char* sa = stage_a(kt);
         // sub-step 0: read sub-step 1's fragments while the MFMAs of sub-step 0 run
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i) fa[1][i] = frag<C::BM>(sa, A.kmajor, wm + 32 * i, 1, lane);
+        for (int i = 0; i < C::TM; ++i) fa[1][i] = frag<C::BM, AK>(sa, wm + 32 * i, 1, lane);
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) fb[1][j] = frag<C::BN>(sa + C::A_BYTES, B.kmajor, wn + 32 * j, 1, lane);
+        for (int j = 0; j < C::TN; ++j) fb[1][j] = frag<C::BN, BK>(sa + C::A_BYTES, wn + 32 * j, 1, lane);
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < C::TM * C::TN / 2; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
+        interleave_mfma_ds<C::TM * C::TN, NREAD>();
         __builtin_amdgcn_sched_barrier(0);
         // tile kt+1 ready (tiles kt+2 .. kt+S-2 may still be in flight), stage (kt-1) % S free
         {
             const int ahead = (KT - 1 < kt + C::S - 2 ? KT - 1 : kt + C::S - 2) - (kt + 1);
-            if (C::S >= 5 && ahead >= 2) wait_vmcnt<2 * C::LOADS_PER_STAGE>();
-            else if (C::S >= 4 && ahead >= 1) wait_vmcnt<C::LOADS_PER_STAGE>();
-            else wait_vmcnt<0>();
+            if (C::S >= 5 && ahead >= 2) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
+            else if (C::S >= 4 && ahead >= 1) lds_wait_barrier<C::LOADS_PER_STAGE>();
+            else lds_wait_barrier<0>();
         }
-        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
         // sub-step 1: read the next tile's first fragments while the MFMAs of sub-step 1 run
@@ -194,20 +232,16 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
         if (more) {
             const char* na = stage_a(kt + 1);
 #pragma unroll
-            for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM>(na, A.kmajor, wm + 32 * i, 0, lane);
+            for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(na, wm + 32 * i, 0, lane);
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN>(na + C::A_BYTES, B.kmajor, wn + 32 * j, 0, lane);
+            for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN, BK>(na + C::A_BYTES, wn + 32 * j, 0, lane);
         }
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < C::TM * C::TN / 2; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
+        interleave_mfma_ds<C::TM * C::TN, NREAD>();
         __builtin_amdgcn_sched_barrier(0);
     }
 }

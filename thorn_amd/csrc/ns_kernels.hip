@@ -13,12 +13,11 @@ using NsCfg = GemmCfg<256, 256>;
 
 // Input iterate of iteration `it` (f16): iteration 0 reads xb (the scaled first iterate), then the
 // iterates alternate xa, xb, ...
-__device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int it, bool kmajor) {
+__device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int it) {
     Operand op;
     op.ptr = (it & 1) ? M.xa : M.xb;
     op.ld = M.ldx;
     op.rows = M.rows;
-    op.kmajor = kmajor;
     return op;
 }
 
@@ -27,7 +26,6 @@ __device__ __forceinline__ Operand square_operand(const _Float16* p, const Ortho
     op.ptr = p;
     op.ld = M.lds;
     op.rows = M.s;
-    op.kmajor = 1;
     return op;
 }
 
@@ -124,10 +122,10 @@ __global__ __launch_bounds__(256) void ns_gram_kernel(const OrthoMat* __restrict
     tri_decode(b - tl.starts[k], T, ti, tj);
     // wide (rows <= cols): A = X X^T, contraction over columns (K-major rows of X);
     // tall: A = X^T X, contraction over rows (MN-major columns of X).
-    const bool kmaj = !M.tall;
-    Operand A = iterate_operand(M, it, kmaj);
+    const Operand A = iterate_operand(M, it);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_mainloop<NsCfg>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
+    if (M.tall) gemm_mainloop<NsCfg, false, false>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
+    else gemm_mainloop<NsCfg, true, true>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
     sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, ti != tj,
                      1.f, 0.f, 0.f);
 }
@@ -142,9 +140,9 @@ __global__ __launch_bounds__(256) void ns_poly_kernel(const OrthoMat* __restrict
     const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
     int ti, tj;
     tri_decode(b - tl.starts[k], T, ti, tj);
-    Operand A = square_operand(M.gram, M);
+    const Operand A = square_operand(M.gram, M);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_mainloop<NsCfg>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.s, acc, smem, M.zero);
+    gemm_mainloop<NsCfg, true, true>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.s, acc, smem, M.zero);
     sym_store<NsCfg>(acc, smem, M.poly, M.gram, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, ti != tj,
                      cc, cb, ca);
 }
@@ -164,16 +162,12 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
     // the row panels of P
     const int ti = local % M.g3_tiles_m, tj = local / M.g3_tiles_m;
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    Operand A, B;
-    if (M.tall) {
-        A = iterate_operand(M, it, true);      // rows of X, contraction over columns
-        B = square_operand(M.poly, M);         // P symmetric: column n of P is row n
-    } else {
-        A = square_operand(M.poly, M);
-        B = iterate_operand(M, it, false);     // X[k][n], contraction over rows
-    }
+    const Operand X = iterate_operand(M, it), P = square_operand(M.poly, M);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_mainloop<NsCfg>(A, B, m0, n0, M.s, acc, smem, M.zero);
+    if (M.tall)   // X P: rows of X (K-major); P symmetric, so column n of P is row n (K-major)
+        gemm_mainloop<NsCfg, true, true>(X, P, m0, n0, M.s, acc, smem, M.zero);
+    else          // P X: X[k][n] is MN-major
+        gemm_mainloop<NsCfg, true, false>(P, X, m0, n0, M.s, acc, smem, M.zero);
 
     if (!final_iter) {
         _Float16* dst = (it & 1) ? M.xb : M.xa;
