@@ -140,6 +140,13 @@ __device__ __forceinline__ void lds_wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// Block barrier for LDS traffic only: this wave's LDS accesses are complete, then s_barrier.
+// Unlike __syncthreads() it does not wait for outstanding global stores, so an epilogue's
+// stores keep draining while the next staging pass runs.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Scheduling hint for one k16 sub-step: NM MFMAs spread evenly between NR LDS fragment reads.
 template <int NM, int NR, int Q = 0>
 __device__ __forceinline__ void interleave_mfma_ds() {
@@ -287,7 +294,7 @@ __device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* sm
     using E = Epi<C>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* N = reinterpret_cast<float*>(smem);
-    __syncthreads();   // the previous user of smem (main loop or another pass) is done
+    lds_barrier();   // the previous user of smem (main loop or another pass) is done
     if ((wave >> 1) == half) {
         const int wn = (wave & 1) * C::WN;
 #pragma unroll
@@ -302,7 +309,7 @@ __device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* sm
                         floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
                 }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int it = 0; it < E::ROW_CHUNKS; ++it) {
         int r, c8;
@@ -321,7 +328,7 @@ __device__ __forceinline__ void for_cols(floatx16 (&acc)[C::TM][C::TN], char* sm
     using E = Epi<C>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* T = reinterpret_cast<float*>(smem);
-    __syncthreads();
+    lds_barrier();
     if ((wave >> 1) == half) {
         const int wn = (wave & 1) * C::WN;
 #pragma unroll
@@ -337,7 +344,7 @@ __device__ __forceinline__ void for_cols(floatx16 (&acc)[C::TM][C::TN], char* sm
                         T[c * E::TS + r] = acc[i][j][4 * q + e];
                     }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int it = 0; it < E::COL_CHUNKS; ++it) {
         int c, r8;

@@ -84,7 +84,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
                 if (r == c + e) t += gamma;
                 v[e] = t;
             }
-            stg<half8v>(out + (int64_t)r * ld + c, to_half8(v));
+            stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
         });
         if (!mirror) continue;
         if (beta != 0.f) {
@@ -106,7 +106,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
                 if (r8 + e == c) t += gamma;
                 v[e] = t;
             }
-            stg<half8v>(out + (int64_t)c * ld + r8, to_half8(v));
+            stg_nt<half8v>(out + (int64_t)c * ld + r8, to_half8(v));
         });
     }
 }
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
                 const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
-                if (r < M.rows && c < M.ldx) stg<half8v>(dst + (int64_t)r * M.ldx + c, to_half8(v));
+                if (r < M.rows && c < M.ldx) stg_nt<half8v>(dst + (int64_t)r * M.ldx + c, to_half8(v));
             });
         return;
     }
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
                 const half8v hv = to_half8(v);
                 float sq = 0.f;
                 if (r < M.rows && c < M.ldx) {
-                    stg<half8v>(M.uout + (int64_t)r * M.ldx + c, hv);
+                    stg_nt<half8v>(M.uout + (int64_t)r * M.ldx + c, hv);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float f = static_cast<float>(hv[e]);
@@ -223,15 +223,15 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
                     psq += pv[e] * pv[e];
                 }
                 if (apply) {
-                    stg<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
-                    stg<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
+                    stg_nt<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
+                    stg_nt<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
                 }
             } else {
                 for (int e = 0; e < 8 && c + e < M.cols; ++e) {
                     float p = ldg<float>(pp + e);
                     if (apply) {
                         p = cautious_step(p, (float)(_Float16)v[e], M.eta, M.wd);
-                        stg<float>(pp + e, p);
+                        stg_nt<float>(pp + e, p);
                     }
                     psq += p * p;
                 }

@@ -44,6 +44,26 @@ __device__ __forceinline__ void stg(void* p, const T& v) {
     *reinterpret_cast<T*>(p) = v;
 #endif
 }
+// Streaming store: marked non-temporal, so large outputs that the next kernel reads from HBM
+// anyway do not displace the L2 lines the running GEMMs reuse.
+template <class T>
+__device__ __forceinline__ void stg_nt(void* p, const T& v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    if constexpr (sizeof(T) == 16)
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<THORN_GLOBAL u32x4*>(a));
+    else if constexpr (sizeof(T) == 8)
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x2, v), reinterpret_cast<THORN_GLOBAL u32x2*>(a));
+    else if constexpr (sizeof(T) == 4)
+        __builtin_nontemporal_store(__builtin_bit_cast(unsigned, v), reinterpret_cast<THORN_GLOBAL unsigned*>(a));
+    else
+        stg<T>(p, v);
+#else
+    *reinterpret_cast<T*>(p) = v;
+#endif
+}
 
 // ---------------------------------------------------------------------------------------------
 // Numeric helpers
