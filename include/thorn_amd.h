@@ -87,7 +87,10 @@ typedef struct thorn_ortho_plan* thorn_ortho_plan_t;
 
 int thorn_ortho_plan_create(const ThornOrthoMatDesc* mats, int n, thorn_ortho_plan_t* out);
 void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan);
-/* Device workspace; must be zero-filled once when allocated and kept for every later step. */
+/* Device workspace; must be zero-filled once when allocated and kept for every later step.
+ * Consecutive steps of a plan on the same workspace write the first Newton-Schulz iterate directly
+ * in f16, prescaled by a power of two the previous step stored there (rebuilt exactly when the
+ * gradient scale moved by more than 16x); the first step on a workspace takes the exact path. */
 size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,

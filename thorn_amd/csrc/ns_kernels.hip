@@ -37,18 +37,38 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
     const int local = b - tl.starts[k];
     const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (M.flags & kFlagPrescaled) return;   // ortho_pre_kernel wrote xb (ortho_repair_kernel checks it)
     const float sigma = M.scal[kScalSigma];
+    const int r0 = tr * 16 + wave * 4;
     const int c = tc * 256 + 4 * lane;
     if (c >= M.ldx) return;
+    // x0 and xb share the padded layout; the padding of x0 is zero, so whole 4-chunks are safe
+    float4 u[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+        if (r0 + rr < M.rows) u[rr] = ldg<float4>(M.x0 + (int64_t)(r0 + rr) * M.ldx + c);
+#pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-        const int row = tr * 16 + wave * 4 + rr;
-        if (row >= M.rows) break;
-        // x0 and xb share the padded layout; the padding of x0 is zero, so whole 4-chunks are safe
-        const float4 u = ldg<float4>(M.x0 + (int64_t)row * M.ldx + c);
-        const half4 h = half4{(_Float16)(u.x * sigma), (_Float16)(u.y * sigma), (_Float16)(u.z * sigma),
-                              (_Float16)(u.w * sigma)};
-        stg<half4>(M.xb + (int64_t)row * M.ldx + c, h);
+        if (r0 + rr >= M.rows) break;
+        const half4 h = half4{(_Float16)(u[rr].x * sigma), (_Float16)(u[rr].y * sigma), (_Float16)(u[rr].z * sigma),
+                              (_Float16)(u[rr].w * sigma)};
+        stg<half4>(M.xb + (int64_t)(r0 + rr) * M.ldx + c, h);
     }
+}
+
+// Prescaled first iterates whose scale drifted too far (kScalRepair): rebuild xb = f16(sigma * u)
+// exactly from the gradient and the updated moment, u = g + beta1 * m (such matrices have no
+// decouple_md). One block per matrix; the common case is an immediate exit.
+__global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __restrict__ mats) {
+    const OrthoMat& M = mats[blockIdx.x];
+    if (!(M.flags & kFlagPrescaled) || M.scal[kScalRepair] == 0.f) return;
+    const float sigma = M.scal[kScalSigma];
+    for (int r = 0; r < M.rows; ++r)
+        for (int c = threadIdx.x; c < M.cols; c += 256) {
+            const int64_t i = (int64_t)r * M.cols + c;
+            const float u = fmaf(ldg<float>(M.m + i), M.beta1, ldg<float>(M.g + i));
+            M.xb[(int64_t)r * M.ldx + c] = (_Float16)(u * sigma);
+        }
 }
 
 // out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile, and the same values
@@ -126,8 +146,10 @@ __global__ __launch_bounds__(256) void ns_gram_kernel(const OrthoMat* __restrict
     floatx16 acc[NsCfg::TM][NsCfg::TN];
     if (M.tall) gemm_mainloop<NsCfg, false, false>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
     else gemm_mainloop<NsCfg, true, true>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
+    // iteration 0 reads the stored first iterate, which is sigma * u up to the factor x0scale
+    const float osc = it == 0 ? M.scal[kScalX0Scale] : 1.f;
     sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, ti != tj,
-                     1.f, 0.f, 0.f);
+                     osc * osc, 0.f, 0.f);
 }
 
 // Phase 2: P = a I + b A + c A A (A symmetric, so both operands are K-major rows of A).
@@ -168,6 +190,15 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
         gemm_mainloop<NsCfg, true, true>(X, P, m0, n0, M.s, acc, smem, M.zero);
     else          // P X: X[k][n] is MN-major
         gemm_mainloop<NsCfg, true, false>(P, X, m0, n0, M.s, acc, smem, M.zero);
+    if (it == 0) {   // the stored first iterate is sigma * u up to the factor x0scale
+        const float osc = M.scal[kScalX0Scale];
+        if (osc != 1.f) {
+#pragma unroll
+            for (int i = 0; i < NsCfg::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] *= osc;
+        }
+    }
 
     if (!final_iter) {
         _Float16* dst = (it & 1) ? M.xb : M.xa;

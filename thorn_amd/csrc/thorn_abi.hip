@@ -119,6 +119,11 @@ struct thorn_ortho_plan {
     TaskOffsets pre{}, sym{}, g3{}, pnn{}, md{};
     std::vector<int32_t> pre_order, sym_order, g3_order, pnn_order, md_order;
     LaunchTimer timer;
+    // The first iterate of a step is written directly in f16, prescaled by the power of two the
+    // previous step stored in the workspace, when the previous step ran on the same workspace.
+    const void* filled_ws = nullptr;   // workspace of the last fill_table
+    const void* stepped_ws = nullptr;  // workspace of the last completed thorn_ortho_step
+    bool any_exact = true;             // the last filled table has matrices on the exact path
 };
 
 struct thorn_adam_plan {
@@ -324,6 +329,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     std::memset(host, 0, plan->table_bytes);
     char* ws = static_cast<char*>(workspace);
     auto at = [ws](size_t o) -> void* { return o == kNone ? nullptr : ws + o; };
+    bool any_exact = false;
     auto* mats = reinterpret_cast<thorn::OrthoMat*>(host + plan->mats_off);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
@@ -362,6 +368,8 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.ldx = L.ldx; M.lds = L.lds; M.tall = L.tall;
         int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
         if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m)) flags |= thorn::kFlagVec4;
+        if (workspace == plan->stepped_ws && !md && !mds) flags |= thorn::kFlagPrescaled;
+        else any_exact = true;
         M.flags = flags;
         M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
         M.gain_lr = S.gain_lr; M.gain_beta2 = S.gain_beta2; M.gain_w1 = S.gain_w1; M.gain_w2 = S.gain_w2;
@@ -383,6 +391,8 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     write_tasks(host, plan->g3, plan->g3_order, g3_blocks);
     write_tasks(host, plan->pnn, plan->pnn_order, mom_blocks);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
+    plan->filled_ws = workspace;
+    plan->any_exact = any_exact;
     return THORN_OK;
 }
 
@@ -407,8 +417,14 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
     const thorn::TaskList sym = task_list(dev, plan->sym), g3 = task_list(dev, plan->g3);
-    THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total), dim3(256), 0,
-                 st, mats, task_list(dev, plan->pre));
+    if (plan->any_exact) {
+        THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total),
+                     dim3(256), 0, st, mats, task_list(dev, plan->pre));
+    }
+    if (plan->filled_ws == plan->stepped_ws) {
+        THORN_LAUNCH(THORN_KIND_CAST, "ortho_repair_kernel", thorn::ortho_repair_kernel, dim3(n), dim3(256), 0, st,
+                     mats);
+    }
     for (int it = 0; it < iters; ++it) {
         const int fin = it == iters - 1 ? 1 : 0;
         THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel, dim3(sym.total), dim3(256), 0, st,
@@ -433,6 +449,7 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
                      dim3(md.total), dim3(256), 0, st, mats, md);
     }
 #undef THORN_LAUNCH
+    plan->stepped_ws = plan->filled_ws;
     return THORN_OK;
 }
 

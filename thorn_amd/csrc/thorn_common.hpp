@@ -135,6 +135,7 @@ enum OrthoFlags : int32_t {
     kFlagKeepGrad = 8,   // write g *= gain back into the user's gradient (none_grad=False)
     kFlagApply = 16,     // the parameter is updated this step
     kFlagVec4 = 32,      // p, g, m 16-byte aligned and cols % 4 == 0: float4 path
+    kFlagPrescaled = 64, // first iterate written in f16 as u * 2^k, 2^k from the previous step
 };
 
 // One matrix of an orthogonalized group. All user tensors are fp32, row-major rows x cols,
@@ -185,6 +186,9 @@ enum ScalSlot : int {
     kScalSigma = 0,    // 1 / (||u||_F + 1e-8)
     kScalGamma = 1,    // per-row-normalization Frobenius rescale
     kScalMDFactor = 2, // target / (||p||_F + 1e-8)
+    kScalX0Scale = 3,  // factor from the stored f16 first iterate to sigma * u (1 when exact)
+    kScalPrescale = 4, // 2^k nearest sigma: the next step's first-iterate prescale
+    kScalRepair = 5,   // 1: the prescaled first iterate is out of range; ortho_cast_kernel rebuilds it
 };
 
 // A grouped launch: task k covers blocks [starts[k], starts[k+1]) and works on matrix order[k].

@@ -34,7 +34,10 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
     const bool vec = M.flags & kFlagVec4;
     const bool keep_grad = M.flags & kFlagKeepGrad;
+    const bool presc = M.flags & kFlagPrescaled;   // never combined with md
+    const float prescale = presc ? M.scal[kScalPrescale] : 1.f;
     const float beta1 = M.beta1;
+    const int nrows = M.rows - r0;   // rows of this wave's 4 that exist (may be <= 0)
 
     float spc[4] = {1.f, 1.f, 1.f, 1.f};
     bool cok[4];
@@ -45,25 +48,24 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
         if (md && cok[e]) spc[e] = softplus_f(M.cg[c]);
     }
     const float sp_scalar = mds ? softplus_f(M.rg[0]) : 1.f;
-    float colacc[4] = {0.f, 0.f, 0.f, 0.f};
-    float nrm = 0.f;
 
+    // all loads of the wave's 4 rows first, so they are in flight together
+    float gv[4][4], mv[4][4], pv[4][4];
+#pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-        const int row = r0 + rr;
-        if (row >= M.rows) break;   // uniform over the wave
-        const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
-        const int64_t rbase = (int64_t)row * M.cols;
-        float gv[4], mv[4], pv[4];
+        const int64_t rbase = (int64_t)(r0 + rr) * M.cols;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[rr][e] = mv[rr][e] = pv[rr][e] = 0.f;
+        if (rr >= nrows) continue;
         if (vec) {
-            const int c = c0 + 4 * lane;
             if (cok[0]) {
-                float4 t = *reinterpret_cast<const float4*>(M.g + rbase + c);
-                gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
-                t = *reinterpret_cast<const float4*>(M.m + rbase + c);
-                mv[0] = t.x; mv[1] = t.y; mv[2] = t.z; mv[3] = t.w;
+                const int c = c0 + 4 * lane;
+                const float4 g4 = ldg<float4>(M.g + rbase + c), m4 = ldg<float4>(M.m + rbase + c);
+                gv[rr][0] = g4.x; gv[rr][1] = g4.y; gv[rr][2] = g4.z; gv[rr][3] = g4.w;
+                mv[rr][0] = m4.x; mv[rr][1] = m4.y; mv[rr][2] = m4.z; mv[rr][3] = m4.w;
                 if (md || mds) {
-                    t = *reinterpret_cast<const float4*>(M.p + rbase + c);
-                    pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
+                    const float4 p4 = ldg<float4>(M.p + rbase + c);
+                    pv[rr][0] = p4.x; pv[rr][1] = p4.y; pv[rr][2] = p4.z; pv[rr][3] = p4.w;
                 }
             }
         } else {
@@ -71,29 +73,39 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
             for (int e = 0; e < 4; ++e) {
                 if (!cok[e]) continue;
                 const int c = tile_col(c0, lane, e, false);
-                gv[e] = M.g[rbase + c];
-                mv[e] = M.m[rbase + c];
-                if (md || mds) pv[e] = M.p[rbase + c];
+                gv[rr][e] = ldg<float>(M.g + rbase + c);
+                mv[rr][e] = ldg<float>(M.m + rbase + c);
+                if (md || mds) pv[rr][e] = ldg<float>(M.p + rbase + c);
             }
         }
+    }
+
+    float colacc[4] = {0.f, 0.f, 0.f, 0.f};
+    float nrm = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        if (rr >= nrows) break;   // uniform over the wave
+        const int row = r0 + rr;
+        const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
+        const int64_t rbase = (int64_t)row * M.cols;
         float rowacc = 0.f;
         float xv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!cok[e]) { xv[e] = 0.f; continue; }
-            float g = gv[e];
+            float g = gv[rr][e];
             if (md || mds) {
                 const float G = md ? spr * spc[e] : sp_scalar;
-                const float p = pv[e] / G;
+                const float p = pv[rr][e] / G;
                 const float pg = p * g;
                 g = g * G;
-                pv[e] = p;
-                gv[e] = g;
+                pv[rr][e] = p;
+                gv[rr][e] = g;
                 rowacc += md ? pg * spc[e] : pg;
                 colacc[e] += pg * spr;
             }
-            const float m = mv[e] * beta1 + g;
-            mv[e] = m;
+            const float m = mv[rr][e] * beta1 + g;
+            mv[rr][e] = m;
             const float u = fmaf(m, beta1, g);
             xv[e] = u;
             nrm += u * u;
@@ -102,29 +114,37 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
             rowacc = wave_sum(rowacc);
             if (lane == 0) M.rowpart[(int64_t)tc * M.rows + row] = rowacc;
         }
+        // first iterate: exact fp32 u (scaled and rounded by ortho_cast_kernel once sigma is
+        // known), or directly f16(u * 2^k) with the previous step's power of two
         float* xrow = M.x0 + (int64_t)row * M.ldx;
+        _Float16* hrow = M.xb + (int64_t)row * M.ldx;
         if (vec) {
             if (cok[0]) {
                 const int c = c0 + 4 * lane;
-                *reinterpret_cast<float4*>(M.m + rbase + c) = make_float4(mv[0], mv[1], mv[2], mv[3]);
+                stg_nt<float4>(M.m + rbase + c, make_float4(mv[rr][0], mv[rr][1], mv[rr][2], mv[rr][3]));
                 if (md || mds) {
-                    *reinterpret_cast<float4*>(M.p + rbase + c) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+                    stg_nt<float4>(M.p + rbase + c, make_float4(pv[rr][0], pv[rr][1], pv[rr][2], pv[rr][3]));
                     if (keep_grad)
-                        *reinterpret_cast<float4*>(M.g + rbase + c) = make_float4(gv[0], gv[1], gv[2], gv[3]);
+                        stg_nt<float4>(M.g + rbase + c, make_float4(gv[rr][0], gv[rr][1], gv[rr][2], gv[rr][3]));
                 }
-                *reinterpret_cast<float4*>(xrow + c) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+                if (presc)
+                    stg<half4>(hrow + c, half4{(_Float16)(xv[0] * prescale), (_Float16)(xv[1] * prescale),
+                                               (_Float16)(xv[2] * prescale), (_Float16)(xv[3] * prescale)});
+                else
+                    stg<float4>(xrow + c, make_float4(xv[0], xv[1], xv[2], xv[3]));
             }
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (!cok[e]) continue;
                 const int c = tile_col(c0, lane, e, false);
-                M.m[rbase + c] = mv[e];
+                stg_nt<float>(M.m + rbase + c, mv[rr][e]);
                 if (md || mds) {
-                    M.p[rbase + c] = pv[e];
-                    if (keep_grad) M.g[rbase + c] = gv[e];
+                    stg_nt<float>(M.p + rbase + c, pv[rr][e]);
+                    if (keep_grad) stg_nt<float>(M.g + rbase + c, gv[rr][e]);
                 }
-                xrow[c] = xv[e];
+                if (presc) hrow[c] = (_Float16)(xv[e] * prescale);
+                else stg<float>(xrow + c, xv[e]);
             }
         }
     }
@@ -156,7 +176,28 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
     float s = 0.f;
     for (int t = threadIdx.x; t < ntiles; t += 256) s += M.normpart[t];
     s = block_sum(s, scratch);
-    if (threadIdx.x == 0) M.scal[kScalSigma] = 1.f / (sqrtf(s) + 1e-8f);
+    if (threadIdx.x == 0) {
+        const float nrm = sqrtf(s);
+        const float sigma = 1.f / (nrm + 1e-8f);
+        float x0scale = 1.f, repair = 0.f;
+        if (M.flags & kFlagPrescaled) {
+            // the stored iterate is u * 2^k; it matches the exact f16(sigma * u) range while 2^k
+            // is within a factor 16 of sigma, otherwise ortho_cast_kernel rebuilds it exactly
+            const float ratio = M.scal[kScalPrescale] / sigma;
+            if (ratio > 16.f || ratio < 0.0625f || !(ratio == ratio)) repair = 1.f;
+            else x0scale = sigma / M.scal[kScalPrescale];
+        }
+        M.scal[kScalSigma] = sigma;
+        M.scal[kScalX0Scale] = x0scale;
+        M.scal[kScalRepair] = repair;
+        // next step's prescale: the power of two nearest sigma (kept when sigma is not finite)
+        if (sigma > 0.f && sigma < 3.0e38f) {
+            const int e = (int)rintf(log2f(sigma));
+            M.scal[kScalPrescale] = ldexpf(1.f, e < -120 ? -120 : (e > 120 ? 120 : e));
+        } else if (!(M.scal[kScalPrescale] > 0.f)) {
+            M.scal[kScalPrescale] = 1.f;
+        }
+    }
 
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
     if (!(md || mds) || !(M.flags & kFlagApply)) return;
@@ -231,21 +272,55 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     const float gamma = M.scal[kScalGamma];
     const bool md = M.flags & (kFlagMD | kFlagMDScalar);
+    const bool vec = M.flags & kFlagVec4;
+    const int nrows = M.rows - r0;
     float psq = 0.f;
-    for (int rr = 0; rr < 4; ++rr) {
-        const int row = r0 + rr;
-        if (row >= M.rows) break;
-        const float s = M.rowscale[row];
-        const int64_t rbase = (int64_t)row * M.cols;
-        const _Float16* urow = M.uout + (int64_t)row * M.ldx;
+    if (vec) {
+        // lane owns columns c .. c+3 of each of the wave's 4 rows; loads first
+        const int c = c0 + 4 * lane;
+        const bool ok = c < M.cols;
+        float4 pv[4];
+        half4 uv[4];
+        float sv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int c = c0 + lane + 64 * e;
-            if (c >= M.cols) continue;
-            const float u = ((float)urow[c] * s) * gamma;
-            const float p = cautious_step(M.p[rbase + c], u, M.eta, M.wd);
-            M.p[rbase + c] = p;
-            psq += p * p;
+        for (int rr = 0; rr < 4; ++rr) {
+            pv[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+            uv[rr] = half4{};
+            sv[rr] = 0.f;
+            if (rr >= nrows || !ok) continue;
+            const int row = r0 + rr;
+            pv[rr] = ldg<float4>(M.p + (int64_t)row * M.cols + c);
+            uv[rr] = ldg<half4>(M.uout + (int64_t)row * M.ldx + c);
+            sv[rr] = ldg<float>(M.rowscale + row);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            if (rr >= nrows || !ok) continue;
+            float p[4] = {pv[rr].x, pv[rr].y, pv[rr].z, pv[rr].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float u = ((float)uv[rr][e] * sv[rr]) * gamma;
+                p[e] = cautious_step(p[e], u, M.eta, M.wd);
+                psq += p[e] * p[e];
+            }
+            stg_nt<float4>(M.p + (int64_t)(r0 + rr) * M.cols + c, make_float4(p[0], p[1], p[2], p[3]));
+        }
+    } else {
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = r0 + rr;
+            if (row >= M.rows) break;
+            const float s = M.rowscale[row];
+            const int64_t rbase = (int64_t)row * M.cols;
+            const _Float16* urow = M.uout + (int64_t)row * M.ldx;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = c0 + lane + 64 * e;
+                if (c >= M.cols) continue;
+                const float u = ((float)urow[c] * s) * gamma;
+                const float p = cautious_step(M.p[rbase + c], u, M.eta, M.wd);
+                M.p[rbase + c] = p;
+                psq += p * p;
+            }
         }
     }
     if (md) {
@@ -321,30 +396,28 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict_
     s.apply = T.flags & kAdamApply;
     s.degenerate = T.flags & kAdamDegenerate;
     s.atan2_mode = T.flags & kAdamAtan2;
-    if (T.flags & kAdamVec4) {
+    constexpr int Q = kAdamChunk / 1024;
+    if ((T.flags & kAdamVec4) && base + kAdamChunk <= T.n) {
+        // whole chunk: every thread loads its 4 float4 groups of p, g, m, v before computing
+        float4 p4[Q], g4[Q], m4[Q], v4[Q];
 #pragma unroll
-        for (int q = 0; q < kAdamChunk / 1024; ++q) {
+        for (int q = 0; q < Q; ++q) {
             const int64_t i = base + (int64_t)(q * 256 + threadIdx.x) * 4;
-            if (i + 3 < T.n) {
-                float4 p4 = s.apply ? *reinterpret_cast<const float4*>(T.p + i) : make_float4(0, 0, 0, 0);
-                const float4 g4 = *reinterpret_cast<const float4*>(T.g + i);
-                float4 m4 = *reinterpret_cast<const float4*>(T.m + i);
-                float4 v4 = *reinterpret_cast<const float4*>(T.v + i);
-                adam_elem(p4.x, g4.x, m4.x, v4.x, s);
-                adam_elem(p4.y, g4.y, m4.y, v4.y, s);
-                adam_elem(p4.z, g4.z, m4.z, v4.z, s);
-                adam_elem(p4.w, g4.w, m4.w, v4.w, s);
-                *reinterpret_cast<float4*>(T.m + i) = m4;
-                *reinterpret_cast<float4*>(T.v + i) = v4;
-                if (s.apply) *reinterpret_cast<float4*>(T.p + i) = p4;
-            } else {
-                for (int64_t j = i; j < T.n && j < i + 4; ++j) {
-                    float p = s.apply ? T.p[j] : 0.f, m = T.m[j], v = T.v[j];
-                    adam_elem(p, T.g[j], m, v, s);
-                    T.m[j] = m; T.v[j] = v;
-                    if (s.apply) T.p[j] = p;
-                }
-            }
+            p4[q] = s.apply ? ldg<float4>(T.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            g4[q] = ldg<float4>(T.g + i);
+            m4[q] = ldg<float4>(T.m + i);
+            v4[q] = ldg<float4>(T.v + i);
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int64_t i = base + (int64_t)(q * 256 + threadIdx.x) * 4;
+            adam_elem(p4[q].x, g4[q].x, m4[q].x, v4[q].x, s);
+            adam_elem(p4[q].y, g4[q].y, m4[q].y, v4[q].y, s);
+            adam_elem(p4[q].z, g4[q].z, m4[q].z, v4[q].z, s);
+            adam_elem(p4[q].w, g4[q].w, m4[q].w, v4[q].w, s);
+            stg_nt<float4>(T.m + i, m4[q]);
+            stg_nt<float4>(T.v + i, v4[q]);
+            if (s.apply) stg_nt<float4>(T.p + i, p4[q]);
         }
     } else {
         for (int q = 0; q < kAdamChunk / 256; ++q) {
