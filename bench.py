@@ -60,6 +60,44 @@ def ns_flops(shapes, iters=5) -> float:
     return total
 
 
+def ns_schedule(iters: int, restart_mask: int) -> dict:
+    """Launch counts of the Gram Newton-Schulz schedule the library runs for a restart mask (bit i:
+    restart before iteration i): Gram matrices, polynomials P, symmetric products and X updates."""
+    def restart(i):
+        return 0 < i < 32 and (restart_mask >> i) & 1
+    n = {'gram': 1, 'poly': 0, 'symprod': 0, 'update': 1}
+    q = False
+    for i in range(iters):
+        if restart(i):
+            n['update'] += 1
+            n['gram'] += 1
+            q = False
+        n['poly'] += 1
+        if q:
+            n['symprod'] += 1
+        q = True
+        if i < iters - 1 and not restart(i + 1):
+            n['symprod'] += 2
+    return n
+
+
+def schedule_flops(shapes, iters: int, restart_mask: int) -> float:
+    """Algorithmic flops of the schedules the library runs: Gram Newton-Schulz with `restart_mask`
+    on matrices at least twice as long as wide, the plain quintic (a restart before every
+    iteration) on the others;
+    s^2 l per Gram matrix, s^3 per polynomial or symmetric product (symmetric results counted
+    once), 2 s^2 l per update. The plain schedule gives ns_flops."""
+    plain = ns_schedule(iters, (1 << iters) - 2)
+    gram = ns_schedule(iters, restart_mask)
+    total = 0.0
+    for r, c in shapes:
+        s, l = min(r, c), max(r, c)
+        sched = gram if l >= 2 * s else plain
+        total += (sched['gram'] * s * s * l + (sched['poly'] + sched['symprod']) * s ** 3
+                  + sched['update'] * 2.0 * s * s * l)
+    return total
+
+
 def build_workload(config: int, device):
     """Parameters and gradients drawn on the CPU from seed 3407 (params first, then grads), moved
     to `device` bit for bit."""
@@ -187,8 +225,8 @@ def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
 # rocprofv3 summaries and the HBM-traffic calibration
 # ---------------------------------------------------------------------------------------------
 
-TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'ns_update_traffic_qwen3_300m.md')
-_TRAFFIC_RE = r'ns_update_kernel HBM bytes per launch: ([0-9.eE+]+)'
+TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'ns_phase_traffic_qwen3_300m.md')
+_TRAFFIC_RE = r'ns_phase_kernel HBM bytes per launch: ([0-9.eE+]+)'
 
 
 def copy_calibration(mib: int, device) -> None:
@@ -221,7 +259,7 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
     (`*kernel_stats.csv`) and, when present, per-kernel counter averages per dispatch
     (`*counter_collection.csv`, one directory per counter pass). With `cal_mib`, FETCH_SIZE /
     WRITE_SIZE are scaled by what they read for the `torch.neg` calibration kernel of that many
-    MiB, and the HBM bytes per ns_update_kernel launch are printed."""
+    MiB, and the HBM bytes per ns_phase_kernel launch are printed."""
     import csv
     import glob
 
@@ -263,19 +301,19 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
         if scale:
             lines += ['', 'Counter scale from the calibration kernel (expected KiB / counted KiB): ' +
                       ', '.join(f'{c} x{s:.4f}' for c, s in scale.items())]
-            upd = [k for k in kernels if k.startswith('thorn::ns_update_kernel')]
+            upd = [k for k in kernels if k.startswith('thorn::ns_phase_kernel')]
             tot = 0.0
             for c, s in scale.items():
                 v = [x for k in upd for x in per.get((k, c), {}).values()]
                 if v:
                     tot += sum(v) / len(v) * 1024.0 * s
             if upd and len(scale) == 2:
-                lines.append(f'\nns_update_kernel HBM bytes per launch: {tot:.6g}')
+                lines.append(f'\nns_phase_kernel HBM bytes per launch: {tot:.6g}')
     return '\n'.join(lines)
 
 
 def traffic_from_profile() -> float | None:
-    """HBM bytes per ns_update_kernel launch from the committed counter summary, if present."""
+    """HBM bytes per ns_phase_kernel launch from the committed counter summary, if present."""
     import re
     try:
         m = re.search(_TRAFFIC_RE, open(TRAFFIC_PROFILE).read())
@@ -361,15 +399,18 @@ def main() -> int:
             kinds[k] = (tot + ms, cnt + n)
         r.plan.timing_enable(0)
 
-    F = ns_flops(mats)
-    ns_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('gram', 'poly', 'update')) / args.steps
+    grp0 = thorn_amd.optim._Group.from_kwargs(**opt.param_groups[0])
+    mask = thorn_amd.optim._OrthoRunner.restart_mask(grp0, grp0.iters)
+    F = schedule_flops(mats, grp0.iters, mask)
+    ns_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('gram', 'poly', 'symprod', 'update')) / args.steps
     upd_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('pre', 'norm', 'rowstats', 'pnn_apply', 'adam')) / args.steps
     cbytes = compulsory_bytes(mats, params, n_m)
-    # dominant kernel: the Newton-Schulz update GEMM (2 s^2 l flops per matrix per launch)
-    upd_flops = sum(2.0 * min(r, c) ** 2 * max(r, c) for r, c in mats)
-    u_ms, u_n = kinds.get('update', (0.0, 1))
-    u_avg = u_ms / max(u_n, 1)
-    achieved = upd_flops / (u_avg * 1e-3) / 1e12 if u_avg > 0 else 0.0
+    # dominant kernel: ns_phase_kernel, which runs every Newton-Schulz GEMM (one launch per
+    # schedule step); its algorithmic flops per launch are the step's F over its launch count
+    ns_launches = sum(kinds.get(k, (0.0, 0))[1] for k in ('gram', 'poly', 'symprod', 'update')) / args.steps
+    ns_flops_per_launch = F / max(ns_launches, 1)
+    u_avg = ns_ms / max(ns_launches, 1)
+    achieved = ns_flops_per_launch / (u_avg * 1e-3) / 1e12 if u_avg > 0 else 0.0
     phases = {k: {'ms_per_launch': round(ms / n, 4), 'launches_per_step': n / args.steps}
               for k, (ms, n) in sorted(kinds.items())}
 
@@ -396,16 +437,18 @@ def main() -> int:
                    'ns_arith': 'f16 MFMA, fp32 accumulate; fp32 state'},
         'gpu_event_ms_per_step': round(gpu_ms, 3),
         'first_step_ms': round(first_ms, 1),
-        'ns': {'flops_per_step': F, 'ms_per_step': round(ns_ms, 3),
+        'ns': {'schedule': {'square': ns_schedule(grp0.iters, (1 << grp0.iters) - 2),
+                            'other': ns_schedule(grp0.iters, mask), 'restart_mask': mask}, 'flops_per_step': F,
+               'plain_quintic_flops': ns_flops(mats), 'ms_per_step': round(ns_ms, 3),
                'tflops': round(F / (ns_ms * 1e-3) / 1e12, 1) if ns_ms > 0 else None,
                'mfma_frac': round(F / (ns_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4) if ns_ms > 0 else None},
         'update': {'compulsory_bytes': cbytes, 'ms_per_step': round(upd_ms, 3),
                    'gbps': round(cbytes / (upd_ms * 1e-3) / 1e9, 1) if upd_ms > 0 else None,
                    'hbm_frac': round(cbytes / (upd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if upd_ms > 0 else None},
-        'roofline': {'kernel': 'ns_update_kernel', 'bound': 'mfma', 'achieved': round(achieved, 1),
+        'roofline': {'kernel': 'ns_phase_kernel', 'bound': 'mfma', 'achieved': round(achieved, 1),
                      'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_PEAK_TFLOPS, 4),
-                     'traffic': traffic_from_profile(), 'flops_per_launch': upd_flops,
-                     'avg_launch_ms': round(u_avg, 4)},
+                     'traffic': traffic_from_profile(), 'flops_per_launch': ns_flops_per_launch,
+                     'launches_per_step': ns_launches, 'avg_launch_ms': round(u_avg, 4)},
         'phases': phases,
         'cpu_baseline': cpu,
         'workload_gen_s': round(gen_s, 1),

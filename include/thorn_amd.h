@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 1
+#define THORN_ABI_VERSION 2
 
 enum {
     THORN_OK = 0,
@@ -95,9 +95,15 @@ size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);
-/* Runs the whole step for the group: coeffs holds iters (a, b, c) triples (thorn.py:425-480). */
+/* Runs the whole step for the group: coeffs holds iters (a, b, c) triples (thorn.py:425-480),
+ * 1 <= iters <= 32. Matrices with max(rows, cols) >= 2 min(rows, cols) run Gram Newton-Schulz
+ * (thorn.py:637-653) with a restart before iteration i for every bit i (1 <= i < iters) set in
+ * restart_mask, the restart positions of _gram_ns_restarts (thorn.py:483-514); the others run the
+ * plain quintic (thorn.py:655-658), which is Gram Newton-Schulz restarted before every iteration.
+ * The reference takes the Gram form for every non-square matrix; in exact arithmetic both are the
+ * same map, and below 2:1 the plain one is the more accurate in f16. */
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
-                     void* stream);
+                     uint32_t restart_mask, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Non-orthogonalized group: Adam / Adam-atan2 / rectified Adam with cautious weight decay, all
@@ -138,16 +144,17 @@ int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream)
 enum {
     THORN_KIND_PRE = 0,        /* momentum + first iterate (ortho_pre_kernel) */
     THORN_KIND_NORM = 1,       /* per-matrix norm, decouple_md gains */
-    THORN_KIND_GRAM = 2,       /* Newton-Schulz Gram matrix */
-    THORN_KIND_POLY = 3,       /* Newton-Schulz polynomial a I + b A + c A^2 */
-    THORN_KIND_UPDATE = 4,     /* Newton-Schulz update P X / X P (and the fused apply) */
+    THORN_KIND_GRAM = 2,       /* Newton-Schulz Gram matrix R of the iterate */
+    THORN_KIND_POLY = 3,       /* Newton-Schulz polynomial P = a I + b R + c R^2 */
+    THORN_KIND_UPDATE = 4,     /* Newton-Schulz update Q X / X Q (and the fused apply) */
     THORN_KIND_ROWSTATS = 5,   /* per-row normalization statistics */
     THORN_KIND_PNN_APPLY = 6,  /* per-row normalized apply */
     THORN_KIND_MD_FACTOR = 7,  /* decouple_md renormalization factor */
     THORN_KIND_MD_RESCALE = 8, /* decouple_md reassembly */
     THORN_KIND_ADAM = 9,       /* multi-tensor Adam */
     THORN_KIND_CAST = 10,      /* first iterate: u / ||u|| rounded to f16 */
-    THORN_KIND_COUNT = 11
+    THORN_KIND_SYMPROD = 11,   /* Gram Newton-Schulz products Q P, R P, P (R P) */
+    THORN_KIND_COUNT = 12
 };
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
 int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);

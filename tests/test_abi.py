@@ -77,10 +77,12 @@ def test_fill_table_validates_pointers_without_gpu():
         plan.fill_table(steps, 100, 64, host.ctypes.data)
 
 
-def test_step_rejects_zero_iterations():
+def test_step_rejects_bad_iteration_counts():
     plan = _lib.OrthoPlan([8], [8], [0])
-    with pytest.raises(_lib.ThornError, match='iters >= 1'):
-        plan.step(64, np.zeros((0, 3), dtype=np.float32), 0)
+    with pytest.raises(_lib.ThornError, match='1 <= iters <= 32'):
+        plan.step(64, np.zeros((0, 3), dtype=np.float32), 0, 0)
+    with pytest.raises(_lib.ThornError, match='1 <= iters <= 32'):
+        plan.step(64, np.zeros((33, 3), dtype=np.float32), 0, 0)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

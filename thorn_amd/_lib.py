@@ -59,7 +59,7 @@ SIGNATURES = {
     'thorn_ortho_workspace_bytes': (_sz, [_vp]),
     'thorn_ortho_table_bytes': (_sz, [_vp]),
     'thorn_ortho_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
-    'thorn_ortho_step': (_i, [_vp, _vp, _vp, _i, _vp]),
+    'thorn_ortho_step': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp]),
     'thorn_adam_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
     'thorn_adam_plan_destroy': (None, [_vp]),
     'thorn_adam_table_bytes': (_sz, [_vp]),
@@ -70,8 +70,9 @@ SIGNATURES = {
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
     'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
-KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast']
-ABI_VERSION = 1
+KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
+         'symprod']
+ABI_VERSION = 2
 
 _lib = None
 
@@ -140,9 +141,10 @@ class OrthoPlan:
         check(self._lib.thorn_ortho_fill_table(self.handle, steps.ctypes.data, workspace, table_dev,
                                                table_host), 'thorn_ortho_fill_table')
 
-    def step(self, table_dev: int, coeffs: np.ndarray, stream: int) -> None:
+    def step(self, table_dev: int, coeffs: np.ndarray, restart_mask: int, stream: int) -> None:
+        """coeffs: (iters, 3) float32; restart_mask: bit i = restart before iteration i."""
         iters = coeffs.shape[0]
-        check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, stream),
+        check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, restart_mask, stream),
               'thorn_ortho_step')
 
     def timing_enable(self, max_launches: int) -> None:

@@ -158,35 +158,31 @@ __device__ __forceinline__ void interleave_mfma_ds() {
     }
 }
 
-// acc[i][j] += A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over the whole K range, with
-// operand layouts AK / BK (true = K-major).
+// acc[i][j] += A[m0 + wm + 32i .., K tiles kt0 .. kt_end) * B[.., n0 + wn + 32j ..] with operand
+// layouts AK / BK (true = K-major).
 // The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out transposed: lane l holds
 // row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3 in registers r..r+3,
 // which the epilogue writes to LDS as one 16-byte store.
 //
 // Pipeline over K tiles of 32 (S LDS stages, one block barrier per tile):
-//   tile t is loaded into stage t % S S-1 tiles ahead of its use, by direct global->LDS loads;
-//   each tile is two k16 sub-steps; the LDS fragment reads of the next sub-step are in flight
-//   while the MFMAs of the current one run. Between the two sub-steps of tile t every wave waits
-//   for its own loads of tile t+1 and meets the others at the barrier: after it, tile t+1 is
-//   visible and nobody reads stage (t-1) % S any more, which then receives tile t+S-1.
+//   tile t is loaded into stage (t - kt0) % S S-1 tiles ahead of its use, by direct global->LDS
+//   loads; each tile is two k16 sub-steps; the LDS fragment reads of the next sub-step are in
+//   flight while the MFMAs of the current one run. Between the two sub-steps of tile t every wave
+//   waits for its own loads of tile t+1 and meets the others at the barrier: after it, tile t+1
+//   is visible and nobody reads stage (t-1) % S any more, which then receives tile t+S-1. The
+//   range ends with every load complete and a barrier, so the stages are free again.
 template <class C, bool AK, bool BK>
-__device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B, int m0, int n0,
-                                              int K, floatx16 (&acc)[C::TM][C::TN], char* smem,
-                                              const void* zero) {
+__device__ __forceinline__ void mainloop_range(const Operand& A, const Operand& B, int m0, int n0, int kt0,
+                                               int kt_end, floatx16 (&acc)[C::TM][C::TN], char* smem,
+                                               const void* zero) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
-
     DmaSrc<C::BM, AK> da;
     DmaSrc<C::BN, BK> db;
     da.init(A, m0, wave, lane);
     db.init(B, n0, wave, lane);
-    const int KT = (K + C::BK - 1) / C::BK;
-    auto stage_a = [&](int t) { return smem + (t % C::S) * C::STAGE_BYTES; };
+    const int KT = kt_end;
+    auto stage_a = [&](int t) { return smem + ((t - kt0) % C::S) * C::STAGE_BYTES; };
     auto issue = [&](int t) {
         char* st = stage_a(t);
         da.issue(t, st, zero, wave);
@@ -194,24 +190,25 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
     };
 #pragma unroll
     for (int t = 0; t < C::S - 1; ++t)
-        if (t < KT) issue(t);
-    // tile 0 ready: loads of tiles 1 .. min(S-2, KT-1) may still be in flight
+        if (kt0 + t < KT) issue(kt0 + t);
+    // tile kt0 ready: loads of the next min(S-2, n-1) tiles may still be in flight
     static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
-    if (C::S >= 5 && KT >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
-    else if (C::S >= 4 && KT >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
-    else if (KT >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
+    const int n = KT - kt0;
+    if (C::S >= 5 && n >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
+    else if (C::S >= 4 && n >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
+    else if (n >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
     else lds_wait_barrier<0>();
 
     constexpr int NREAD = C::TM * (AK ? 1 : 2) + C::TN * (BK ? 1 : 2);   // LDS reads per sub-step
     half8 fa[2][C::TM], fb[2][C::TN];
     {
-        const char* sa = stage_a(0);
+        const char* sa = stage_a(kt0);
 #pragma unroll
         for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(sa, wm + 32 * i, 0, lane);
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN, BK>(sa + C::A_BYTES, wn + 32 * j, 0, lane);
     }
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = kt0; kt < KT; ++kt) {
         const char* sa = stage_a(kt);
         // sub-step 0: read sub-step 1's fragments while the MFMAs of sub-step 0 run
 #pragma unroll
@@ -235,8 +232,7 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
         __builtin_amdgcn_sched_barrier(0);
         if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
         // sub-step 1: read the next tile's first fragments while the MFMAs of sub-step 1 run
-        const bool more = kt + 1 < KT;
-        if (more) {
+        if (kt + 1 < KT) {
             const char* na = stage_a(kt + 1);
 #pragma unroll
             for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(na, wm + 32 * i, 0, lane);
@@ -251,6 +247,103 @@ __device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B
         interleave_mfma_ds<C::TM * C::TN, NREAD>();
         __builtin_amdgcn_sched_barrier(0);
     }
+    lds_barrier();   // every wave is done with the stages
+}
+
+// acc = A[m0 .., 0:K] * B[0:K, n0 ..] where A is read MN-major for K tiles t < a_k0 and K-major
+// from there on, B likewise with b_k0: a symmetric matrix stored as its upper block triangle is
+// read K-major from its diagonal block on and MN-major, from the transposed mirror block, before
+// it. One pipelined loop: the direct loads and the fragment reads of a tile branch on its layout
+// (uniformly), the MFMAs do not, so the accumulators keep one register assignment.
+template <class C>
+__device__ __forceinline__ void gemm_mainloop_mixed(const Operand& A, const Operand& B, int m0, int n0, int K,
+                                                    int a_k0, int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem,
+                                                    const void* zero) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
+    DmaSrc<C::BM, true> dak;
+    DmaSrc<C::BM, false> dam;
+    DmaSrc<C::BN, true> dbk;
+    DmaSrc<C::BN, false> dbm;
+    dak.init(A, m0, wave, lane);
+    dam.init(A, m0, wave, lane);
+    dbk.init(B, n0, wave, lane);
+    dbm.init(B, n0, wave, lane);
+    const int KT = (K + C::BK - 1) / C::BK;
+    auto stage_a = [&](int t) { return smem + (t % C::S) * C::STAGE_BYTES; };
+    auto issue = [&](int t) {
+        char* st = stage_a(t);
+        if (t >= a_k0) dak.issue(t, st, zero, wave);
+        else dam.issue(t, st, zero, wave);
+        if (t >= b_k0) dbk.issue(t, st + C::A_BYTES, zero, wave);
+        else dbm.issue(t, st + C::A_BYTES, zero, wave);
+    };
+    auto read = [&](int t, int ks, half8 (&ra)[C::TM], half8 (&rb)[C::TN]) {
+        const char* st = stage_a(t);
+        if (t >= a_k0) {
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, true>(st, wm + 32 * i, ks, lane);
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, false>(st, wm + 32 * i, ks, lane);
+        }
+        if (t >= b_k0) {
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, true>(st + C::A_BYTES, wn + 32 * j, ks, lane);
+        } else {
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, false>(st + C::A_BYTES, wn + 32 * j, ks, lane);
+        }
+    };
+    auto mfmas = [&](const half8 (&ra)[C::TM], const half8 (&rb)[C::TN]) {
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(rb[j], ra[i], acc[i][j], 0, 0, 0);
+    };
+#pragma unroll
+    for (int t = 0; t < C::S - 1; ++t)
+        if (t < KT) issue(t);
+    static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
+    if (C::S >= 5 && KT >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
+    else if (C::S >= 4 && KT >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
+    else if (KT >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
+    else lds_wait_barrier<0>();
+    half8 fa[2][C::TM], fb[2][C::TN];
+    if (KT > 0) read(0, 0, fa[0], fb[0]);
+    for (int kt = 0; kt < KT; ++kt) {
+        read(kt, 1, fa[1], fb[1]);   // sub-step 1's fragments, in flight during sub-step 0's MFMAs
+        mfmas(fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const int ahead = (KT - 1 < kt + C::S - 2 ? KT - 1 : kt + C::S - 2) - (kt + 1);
+            if (C::S >= 5 && ahead >= 2) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
+            else if (C::S >= 4 && ahead >= 1) lds_wait_barrier<C::LOADS_PER_STAGE>();
+            else lds_wait_barrier<0>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
+        if (kt + 1 < KT) read(kt + 1, 0, fa[0], fb[0]);   // next tile's first fragments
+        mfmas(fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Single-layout main loop: AK / BK = whether A / B are K-major.
+template <class C, bool AK, bool BK>
+__device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B, int m0, int n0,
+                                              int K, floatx16 (&acc)[C::TM][C::TN], char* smem,
+                                              const void* zero) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
+    mainloop_range<C, AK, BK>(A, B, m0, n0, 0, (K + C::BK - 1) / C::BK, acc, smem, zero);
 }
 
 // Epilogue: the tile is streamed through LDS (reusing the pipeline stages) in two halves of

@@ -1,24 +1,35 @@
 // Grouped Newton-Schulz phase kernels over an orthogonalized parameter group (gfx950).
 //
-// Reference semantics: thorn.py:626-662 (_polar_decomp_impl). The build runs the plain quintic for
-// every shape, on the Gram matrix of the short side, in f16 with fp32 accumulation; the first
-// iterate is the fp32 momentum update u scaled by 1/(||u||_F + 1e-8) and rounded to f16
-// (thorn.py:632-635) by ortho_cast_kernel.
+// Reference semantics: thorn.py:626-662 (_polar_decomp_impl), Gram Newton-Schulz with restarts,
+// in f16 with fp32 accumulation. With R the Gram matrix of the short side and
+// P_i = a_i I + b_i R + c_i R^2, iteration i multiplies Q by P_i and advances R to P_i R P_i;
+// at a restart (and at the end) the iterate is updated, X <- Q X, and R is formed again from it.
+// A restart before every iteration is the plain quintic X <- P_i X (thorn.py:655-658). The first
+// iterate is u / (||u||_F + 1e-8) rounded to f16 (thorn.py:632-635).
 #include "ns_gemm.hpp"
 #include "thorn_kernels.hpp"
 
 namespace thorn {
 
-using NsCfg = GemmCfg<256, 256>;
+// One tile configuration for every Newton-Schulz GEMM: 256 x 256 tiles, one block per CU.
+using NsCfg = GemmCfg<256, 256, 4>;
 
-// Input iterate of iteration `it` (f16): iteration 0 reads xb (the scaled first iterate), then the
-// iterates alternate xa, xb, ...
-__device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int it) {
+__device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) {
     Operand op;
-    op.ptr = (it & 1) ? M.xa : M.xb;
+    op.ptr = xsel == kXA ? M.xa : M.xb;
     op.ld = M.ldx;
     op.rows = M.rows;
     return op;
+}
+
+__device__ __forceinline__ _Float16* sym_buf(const OrthoMat& M, int sel) {
+    switch (sel) {
+        case kBufR: return M.gram;
+        case kBufP: return M.poly;
+        case kBufQA: return M.qa;
+        case kBufQB: return M.qb;
+        default: return M.tmp;
+    }
 }
 
 __device__ __forceinline__ Operand square_operand(const _Float16* p, const OrthoMat& M) {
@@ -71,14 +82,17 @@ __global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __res
         }
 }
 
-// out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile, and the same values
-// mirrored into the transposed tile below the diagonal. Csym is symmetric, so the term for
-// (r, c) can be read from row r or row c alike.
+// out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile of a symmetric s x s
+// matrix. Only the upper block triangle is stored: consumers read a block below the diagonal as
+// the transpose of its mirror above. A diagonal tile keeps its upper triangle and mirrors it into
+// its lower one, so it is exactly symmetric and reads the same either way; Csym's diagonal tile
+// is exactly symmetric too, so its term for (r, c) can be read from row r or row c alike.
 template <class C>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
-                                          const _Float16* csym, int64_t ld, int n, int m0, int n0,
-                                          bool mirror, float alpha, float beta, float gamma) {
+                                          const _Float16* csym, int64_t ld, int n, int m0, int n0, float alpha,
+                                          float beta, float gamma) {
     using E = Epi<C>;
+    const bool diag = m0 == n0;
 #pragma unroll 1
     for (int h = 0; h < 2; ++h) {
         // the beta * Csym chunks of a pass are all requested before any of them is needed (the
@@ -97,6 +111,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
         for_rows<C>(acc, smem, h, [&](int it, int half, int lr, int c8, float (&v)[8]) {
             const int r = m0 + half * C::WM + lr, c = n0 + c8;
             if (r >= n || c >= ld) return;
+            if (diag && c + 7 < r) return;   // entirely below the diagonal: written by the mirror pass
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float t = alpha * v[e];
@@ -104,9 +119,17 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
                 if (r == c + e) t += gamma;
                 v[e] = t;
             }
-            stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
+            _Float16* dst = out + (int64_t)r * ld + c;
+            if (!diag || c >= r) {
+                stg_nt<half8v>(dst, to_half8(v));
+            } else {   // the chunk holding the diagonal element: its upper part only
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (c + e >= r) dst[e] = (_Float16)v[e];
+            }
         });
-        if (!mirror) continue;
+        if (!diag) continue;
+        // diagonal tile: the lower triangle from the transposed staging
         if (beta != 0.f) {
 #pragma unroll
             for (int it = 0; it < E::COL_CHUNKS; ++it) {
@@ -117,8 +140,9 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
             }
         }
         for_cols<C>(acc, smem, h, [&](int it, int half, int cl, int lr8, float (&v)[8]) {
-            const int c = n0 + cl, r8 = m0 + half * C::WM + lr8;   // v[e] is (r8 + e, c)
+            const int c = n0 + cl, r8 = m0 + half * C::WM + lr8;   // v[e] is (r8 + e, c), stored at (c, r8 + e)
             if (c >= n || r8 >= ld) return;
+            if (c <= r8) return;   // no destination below the diagonal
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float t = alpha * v[e];
@@ -126,71 +150,72 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
                 if (r8 + e == c) t += gamma;
                 v[e] = t;
             }
-            stg_nt<half8v>(out + (int64_t)c * ld + r8, to_half8(v));
+            _Float16* dst = out + (int64_t)c * ld + r8;
+            if (c > r8 + 7) {
+                stg_nt<half8v>(dst, to_half8(v));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (r8 + e < c) dst[e] = (_Float16)v[e];
+            }
         });
     }
 }
 
-// Phase 1: Gram matrix of the short side of iterate `it`.
-__global__ __launch_bounds__(256) void ns_gram_kernel(const OrthoMat* __restrict__ mats, TaskList tl, int it) {
-    __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
-    const int b = xcd_remap(blockIdx.x, gridDim.x);
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
+// One Newton-Schulz operation of a phase launch (see ns_phase_kernel).
+enum NsOpKind : int32_t { kOpNone = 0, kOpGram = 1, kOpSym = 2, kOpUpdate = 3 };
+struct NsOp {
+    int32_t kind;
+    int32_t xsel, first, final_iter;   // gram, update: iterate buffer, first-iterate scaling, last update
+    int32_t asel, bsel, csel, osel;    // sym: out = alpha * A B + beta * C + gamma * I
+    int32_t qsel;                      // update: X <- Q X
+    float alpha, beta, gamma;
+};
+
+// R = X X^T (wide) or X^T X (tall) of the iterate in buffer `xsel`; `first`: that iterate is the
+// stored first iterate, sigma * u up to the factor x0scale. Upper-triangle tile number `local`.
+// Each layout has its own main loop and epilogue (no accumulator merge between alternatives).
+__device__ __forceinline__ void gram_tile(const OrthoMat& M, int local, const NsOp& op, char* smem) {
     const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
     int ti, tj;
-    tri_decode(b - tl.starts[k], T, ti, tj);
-    // wide (rows <= cols): A = X X^T, contraction over columns (K-major rows of X);
-    // tall: A = X^T X, contraction over rows (MN-major columns of X).
-    const Operand A = iterate_operand(M, it);
-    floatx16 acc[NsCfg::TM][NsCfg::TN];
-    if (M.tall) gemm_mainloop<NsCfg, false, false>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
-    else gemm_mainloop<NsCfg, true, true>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.l, acc, smem, M.zero);
-    // iteration 0 reads the stored first iterate, which is sigma * u up to the factor x0scale
-    const float osc = it == 0 ? M.scal[kScalX0Scale] : 1.f;
-    sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, ti != tj,
-                     osc * osc, 0.f, 0.f);
-}
-
-// Phase 2: P = a I + b A + c A A (A symmetric, so both operands are K-major rows of A).
-__global__ __launch_bounds__(256) void ns_poly_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
-                                                      float ca, float cb, float cc) {
-    __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
-    const int b = xcd_remap(blockIdx.x, gridDim.x);
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
-    int ti, tj;
-    tri_decode(b - tl.starts[k], T, ti, tj);
-    const Operand A = square_operand(M.gram, M);
-    floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_mainloop<NsCfg, true, true>(A, A, ti * NsCfg::BM, tj * NsCfg::BN, M.s, acc, smem, M.zero);
-    sym_store<NsCfg>(acc, smem, M.poly, M.gram, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, ti != tj,
-                     cc, cb, ca);
-}
-
-// Phase 3: X' = P X (wide) or X P (tall). Not final: store the f16 iterate. Final: either apply
-// the update to p directly (cautious weight decay, thorn.py:669-702) or store u' in f16 with
-// per-row sums of squares for the per-row normalization (thorn.py:758-762).
-__global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
-                                                        int it, int final_iter) {
-    __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
-    __shared__ float scratch[4];
-    const int b = xcd_remap(blockIdx.x, gridDim.x);
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int local = b - tl.starts[k];
-    // column-major tile order: consecutive tiles share the column panel of X and, a few apart,
-    // the row panels of P
-    const int ti = local % M.g3_tiles_m, tj = local / M.g3_tiles_m;
+    tri_decode(local, T, ti, tj);
+    const Operand A = iterate_operand(M, op.xsel);
+    const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    const Operand X = iterate_operand(M, it), P = square_operand(M.poly, M);
+    if (M.tall) {   // contraction over rows: MN-major columns of X
+        floatx16 acc[NsCfg::TM][NsCfg::TN];
+        gemm_mainloop<NsCfg, false, false>(A, A, m0, n0, M.l, acc, smem, M.zero);
+        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
+    } else {        // contraction over columns: K-major rows of X
+        floatx16 acc[NsCfg::TM][NsCfg::TN];
+        gemm_mainloop<NsCfg, true, true>(A, A, m0, n0, M.l, acc, smem, M.zero);
+        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
+    }
+}
+
+// out = alpha * A B + beta * C + gamma * I over s x s workspace matrices that are symmetric and
+// commute (all are polynomials in the same R), so the product is symmetric: upper-triangle tiles.
+// A's block row ti and B's block row tj (B symmetric: its column is its row); a matrix stored as
+// its upper block triangle is read MN-major (transposed, from the mirror block) before its
+// diagonal block. C may be absent (csel < 0).
+__device__ __forceinline__ void sym_tile(const OrthoMat& M, int local, const NsOp& op, char* smem) {
+    const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
+    int ti, tj;
+    tri_decode(local, T, ti, tj);
+    const Operand A = square_operand(sym_buf(M, op.asel), M), B = square_operand(sym_buf(M, op.bsel), M);
+    constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    if (M.tall)   // X P: rows of X (K-major); P symmetric, so column n of P is row n (K-major)
-        gemm_mainloop<NsCfg, true, true>(X, P, m0, n0, M.s, acc, smem, M.zero);
-    else          // P X: X[k][n] is MN-major
-        gemm_mainloop<NsCfg, true, false>(P, X, m0, n0, M.s, acc, smem, M.zero);
-    if (it == 0) {   // the stored first iterate is sigma * u up to the factor x0scale
+    gemm_mainloop_mixed<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, M.s, ti * KB, tj * KB, acc, smem, M.zero);
+    sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), op.csel >= 0 ? sym_buf(M, op.csel) : nullptr, M.lds, M.s,
+                     ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.csel >= 0 ? op.beta : 0.f, op.gamma);
+}
+
+// Epilogue of an update tile (see update_tile); instantiated once per main-loop path.
+__device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
+                                              int ti, int tj, const NsOp& op, char* smem, float* scratch) {
+    const int xsel = op.xsel, first = op.first, final_iter = op.final_iter;
+    const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
+    if (first) {   // the stored first iterate is sigma * u up to the factor x0scale
         const float osc = M.scal[kScalX0Scale];
         if (osc != 1.f) {
 #pragma unroll
@@ -201,7 +226,7 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
     }
 
     if (!final_iter) {
-        _Float16* dst = (it & 1) ? M.xb : M.xa;
+        _Float16* dst = xsel == kXA ? M.xb : M.xa;
 #pragma unroll 1
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
@@ -213,7 +238,7 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
 
     if (M.flags & kFlagPNN) {
         // u' in f16 (the reference's polar factor is f16 rounded, thorn.py:635, 662) and per-row
-        // partial sums of u'^2 over this tile's columns: the 32 lanes of a half-wave cover a row.
+        // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
 #pragma unroll 1
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
@@ -228,8 +253,10 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
                         sq += f * f;
                     }
                 }
-                sq = halfwave_sum(sq);
-                if ((threadIdx.x & 31) == 0 && r < M.rows) stg<float>(M.rowsqpart + (int64_t)tj * M.rows + r, sq);
+                constexpr int kLanesPerRow = NsCfg::BN / 8;   // one 8-column chunk per lane
+                sq = group_sum<kLanesPerRow>(sq);
+                if ((threadIdx.x & (kLanesPerRow - 1)) == 0 && r < M.rows)
+                    stg<float>(M.rowsqpart + (int64_t)tj * M.rows + r, sq);
             });
         return;
     }
@@ -272,6 +299,66 @@ __global__ __launch_bounds__(256) void ns_update_kernel(const OrthoMat* __restri
         const float t = block_sum(psq, scratch);
         if (threadIdx.x == 0) M.psqpart[local] = t;
     }
+}
+
+// X' = Q X (wide) or X Q (tall) with X in buffer `xsel` and Q the workspace matrix `qsel` (stored
+// as its upper block triangle), output tile number `local` (column-major). Not final: store the
+// f16 iterate into the other X buffer. Final: either apply the update to p directly (cautious
+// weight decay, thorn.py:669-702) or store u' in f16 with per-row sums of squares for the
+// per-row normalization (thorn.py:758-762). `first`: X is the stored first iterate (sigma * u up
+// to the factor x0scale). Each orientation is two pipelined K ranges: Q's blocks before the
+// diagonal block, read transposed from their mirror above it, then the rest.
+__device__ __forceinline__ void update_tile(const OrthoMat& M, int local, const NsOp& op, char* smem,
+                                            float* scratch) {
+    // column-major tile order: consecutive tiles share the column panel of X and, a few apart,
+    // the row panels of Q
+    const int ti = local % M.g3_tiles_m, tj = local / M.g3_tiles_m;
+    const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
+    const Operand X = iterate_operand(M, op.xsel), Q = square_operand(sym_buf(M, op.qsel), M);
+    constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
+    const int KT = (M.s + NsCfg::BK - 1) / NsCfg::BK;
+    if (M.tall) {   // X Q: rows of X (K-major); column n of Q is its row n
+        floatx16 acc[NsCfg::TM][NsCfg::TN];
+#pragma unroll
+        for (int i = 0; i < NsCfg::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] = floatx16{};
+        const int e = tj * KB < KT ? tj * KB : KT;
+        mainloop_range<NsCfg, true, false>(X, Q, m0, n0, 0, e, acc, smem, M.zero);
+        mainloop_range<NsCfg, true, true>(X, Q, m0, n0, e, KT, acc, smem, M.zero);
+        update_finish(M, acc, local, ti, tj, op, smem, scratch);
+    } else {        // Q X: X[k][n] is MN-major
+        floatx16 acc[NsCfg::TM][NsCfg::TN];
+#pragma unroll
+        for (int i = 0; i < NsCfg::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] = floatx16{};
+        const int e = ti * KB < KT ? ti * KB : KT;
+        mainloop_range<NsCfg, false, false>(Q, X, m0, n0, 0, e, acc, smem, M.zero);
+        mainloop_range<NsCfg, true, false>(Q, X, m0, n0, e, KT, acc, smem, M.zero);
+        update_finish(M, acc, local, ti, tj, op, smem, scratch);
+    }
+}
+
+// A Newton-Schulz phase launch: blocks [0, t0.total) run op0 over the tiles of task list t0, the
+// next t1.total blocks run op1 over t1. The two operations belong to disjoint sets of matrices
+// (the square ones, on the plain quintic, and the others, on Gram Newton-Schulz), so one launch
+// carries a step of each schedule.
+__global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
+                                                       TaskList t1, NsOp op1) {
+    __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
+    __shared__ float scratch[4];
+    int b = xcd_remap(blockIdx.x, gridDim.x);
+    const bool second = b >= t0.total;
+    const TaskList& tl = second ? t1 : t0;
+    const NsOp& op = second ? op1 : op0;
+    if (second) b -= t0.total;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    if (op.kind == kOpGram) gram_tile(M, local, op, smem);
+    else if (op.kind == kOpSym) sym_tile(M, local, op, smem);
+    else if (op.kind == kOpUpdate) update_tile(M, local, op, smem, scratch);
 }
 
 }  // namespace thorn

@@ -34,7 +34,7 @@ constexpr size_t kNone = ~size_t(0);
 struct MatLayout {
     int32_t rows, cols, s, l, ldx, lds, tall, flags;
     int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
-    size_t x0, xa, xb, gram, poly, uout, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
+    size_t x0, xa, xb, gram, poly, qa, qb, tmp, uout, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
 };
 
 struct TaskOffsets {
@@ -116,8 +116,10 @@ struct thorn_ortho_plan {
     size_t ws_bytes = 0;
     size_t table_bytes = 0;
     size_t mats_off = 0;
-    TaskOffsets pre{}, sym{}, g3{}, pnn{}, md{};
-    std::vector<int32_t> pre_order, sym_order, g3_order, pnn_order, md_order;
+    // Newton-Schulz task lists per matrix set: [0] square matrices (plain quintic), [1] the others
+    // (Gram Newton-Schulz); sym = upper-triangle tiles of s x s products, g3 = tiles of X updates.
+    TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, md{};
+    std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, md_order;
     LaunchTimer timer;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
@@ -177,6 +179,75 @@ thorn::TaskList task_list(const char* dev, const TaskOffsets& t) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct ScheduledOp {
+    thorn::NsOp op;
+    int kind;   // THORN_KIND_* for launch timing
+};
+
+// The Newton-Schulz launch sequence of one matrix set: Gram Newton-Schulz (thorn.py:637-653) in
+// the P-form of its recurrences. With P_i = a_i I + b_i R + c_i R^2: Q <- Q P_i (Q = P_i right after
+// a restart) and, unless the next iteration restarts or this is the last, R <- P_i (R P_i). A
+// restart before iteration i (bit i of `mask`) and the end apply X <- Q X and form R from the new
+// X. A restart before every iteration is the plain quintic X <- P_i X (thorn.py:655-658).
+std::vector<ScheduledOp> ns_schedule(int iters, uint32_t mask, const float* coeffs) {
+    using namespace thorn;
+    auto restarts_at = [&](int i) { return i > 0 && i < 32 && ((mask >> i) & 1u); };
+    auto make = [](int32_t kind) {
+        NsOp o{};
+        o.kind = kind;
+        o.csel = -1;
+        return o;
+    };
+    std::vector<ScheduledOp> ops;
+    auto gram = [&](int xsel, bool first) {
+        NsOp o = make(kOpGram);
+        o.xsel = xsel;
+        o.first = first ? 1 : 0;
+        ops.push_back({o, THORN_KIND_GRAM});
+    };
+    auto update = [&](int xsel, int qsel, bool first, bool fin) {
+        NsOp o = make(kOpUpdate);
+        o.xsel = xsel;
+        o.qsel = qsel;
+        o.first = first ? 1 : 0;
+        o.final_iter = fin ? 1 : 0;
+        ops.push_back({o, THORN_KIND_UPDATE});
+    };
+    auto sym = [&](int a, int b, int c, int out, float alpha, float beta, float gamma, int kind) {
+        NsOp o = make(kOpSym);
+        o.asel = a; o.bsel = b; o.csel = c; o.osel = out;
+        o.alpha = alpha; o.beta = beta; o.gamma = gamma;
+        ops.push_back({o, kind});
+    };
+    int xsel = kXB;    // the first iterate
+    bool first = true; // xsel still holds it
+    int qsel = -1;     // buffer of Q; -1 before the first P after a restart
+    gram(xsel, true);
+    for (int i = 0; i < iters; ++i) {
+        const float a = coeffs[3 * i], b = coeffs[3 * i + 1], c = coeffs[3 * i + 2];
+        if (restarts_at(i)) {
+            update(xsel, qsel, first, false);
+            xsel = xsel == kXB ? kXA : kXB;
+            first = false;
+            gram(xsel, false);
+            qsel = -1;
+        }
+        const int psel = qsel < 0 ? (qsel = kBufQA) : kBufP;   // right after a restart P_i is Q
+        sym(kBufR, kBufR, kBufR, psel, c, b, a, THORN_KIND_POLY);
+        if (psel == kBufP) {
+            const int qnew = qsel == kBufQA ? kBufQB : kBufQA;
+            sym(qsel, kBufP, -1, qnew, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
+            qsel = qnew;
+        }
+        if (i < iters - 1 && !restarts_at(i + 1)) {
+            sym(kBufR, psel, -1, kBufT, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
+            sym(psel, kBufT, -1, kBufR, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
+        }
+    }
+    update(xsel, qsel, first, true);
+    return ops;
+}
 
 }  // namespace
 
@@ -246,6 +317,9 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.xb = take(xbytes);
         L.gram = take(sbytes);
         L.poly = take(sbytes);
+        L.qa = take(sbytes);
+        L.qb = take(sbytes);
+        L.tmp = take(sbytes);
         L.uout = pnn ? take(xbytes) : kNone;
         L.normpart = take(sizeof(float) * mom_tiles);
         L.rowpart = md ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
@@ -264,8 +338,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     std::vector<int32_t> all(n);
     for (int i = 0; i < n; ++i) all[i] = i;
     plan->pre_order = all;
-    auto snake = [&](auto cost) {
-        std::vector<int32_t> by = all;
+    auto snake = [&](const std::vector<int32_t>& set, auto cost) {
+        std::vector<int32_t> by = set;
         std::stable_sort(by.begin(), by.end(), [&](int a, int b) { return cost(a) > cost(b); });
         std::vector<std::vector<int32_t>> bins(8);
         for (size_t r = 0; r < by.size(); ++r) {
@@ -276,10 +350,17 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         for (auto& bin : bins) out.insert(out.end(), bin.begin(), bin.end());
         return out;
     };
-    plan->sym_order = snake([&](int i) { return double(plan->mats[i].sym_tiles) * plan->mats[i].l; });
-    plan->g3_order = snake([&](int i) {
-        return double(plan->mats[i].g3_tiles_m) * plan->mats[i].g3_tiles_n * plan->mats[i].s;
-    });
+    // Gram Newton-Schulz for matrices at least twice as long as they are wide; the others (square
+    // ones included) take the plain quintic: below 2:1 the Gram schedule saves few flops and its
+    // f16 error grows (it is the same map in exact arithmetic).
+    std::vector<int32_t> sets[2];
+    for (int i = 0; i < n; ++i) sets[plan->mats[i].l >= 2 * plan->mats[i].s ? 1 : 0].push_back(i);
+    for (int q = 0; q < 2; ++q) {
+        plan->sym_order[q] = snake(sets[q], [&](int i) { return double(plan->mats[i].sym_tiles) * plan->mats[i].l; });
+        plan->g3_order[q] = snake(sets[q], [&](int i) {
+            return double(plan->mats[i].g3_tiles_m) * plan->mats[i].g3_tiles_n * plan->mats[i].s;
+        });
+    }
     for (int i = 0; i < n; ++i) {
         if (plan->mats[i].flags & THORN_MAT_PER_ROW_NORM) plan->pnn_order.push_back(i);
         if (plan->mats[i].flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
@@ -295,12 +376,19 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     plan->mats_off = 0;
     off = align_up(sizeof(thorn::OrthoMat) * std::max(1, n), 64);
     plan->pre = add_tasks(off, plan->pre_order, mom_blocks);
-    plan->sym = add_tasks(off, plan->sym_order, sym_blocks);
-    plan->g3 = add_tasks(off, plan->g3_order, g3_blocks);
+    for (int q = 0; q < 2; ++q) {
+        plan->sym[q] = add_tasks(off, plan->sym_order[q], sym_blocks);
+        plan->g3[q] = add_tasks(off, plan->g3_order[q], g3_blocks);
+    }
     plan->pnn = add_tasks(off, plan->pnn_order, mom_blocks);
     plan->md = add_tasks(off, plan->md_order, mom_blocks);
     plan->table_bytes = off;
-    for (const TaskOffsets* t : {&plan->pre, &plan->sym, &plan->g3}) {
+    if (int64_t(plan->sym[0].total) + plan->sym[1].total + plan->g3[0].total + plan->g3[1].total >=
+        (int64_t(1) << 31) - 1) {
+        delete plan;
+        return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: grid too large");
+    }
+    for (const TaskOffsets* t : {&plan->pre}) {
         if (int64_t(t->total) >= (int64_t(1) << 31) - 1) {
             delete plan;
             return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: grid too large");
@@ -356,6 +444,9 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.xb = static_cast<_Float16*>(at(L.xb));
         M.gram = static_cast<_Float16*>(at(L.gram));
         M.poly = static_cast<_Float16*>(at(L.poly));
+        M.qa = static_cast<_Float16*>(at(L.qa));
+        M.qb = static_cast<_Float16*>(at(L.qb));
+        M.tmp = static_cast<_Float16*>(at(L.tmp));
         M.uout = static_cast<_Float16*>(at(L.uout));
         M.normpart = static_cast<float*>(at(L.normpart));
         M.rowpart = static_cast<float*>(at(L.rowpart));
@@ -387,8 +478,10 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
     }
     write_tasks(host, plan->pre, plan->pre_order, mom_blocks);
-    write_tasks(host, plan->sym, plan->sym_order, sym_blocks);
-    write_tasks(host, plan->g3, plan->g3_order, g3_blocks);
+    for (int q = 0; q < 2; ++q) {
+        write_tasks(host, plan->sym[q], plan->sym_order[q], sym_blocks);
+        write_tasks(host, plan->g3[q], plan->g3_order[q], g3_blocks);
+    }
     write_tasks(host, plan->pnn, plan->pnn_order, mom_blocks);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
@@ -397,9 +490,10 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
 }
 
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
-                     void* stream) {
+                     uint32_t restart_mask, void* stream) {
     if (!plan || !table_dev) return fail(THORN_ERR_INVALID, "thorn_ortho_step: null argument");
-    if (iters < 1 || !coeffs) return fail(THORN_ERR_INVALID, "thorn_ortho_step: need iters >= 1 and coefficients");
+    if (iters < 1 || iters > 32 || !coeffs)
+        return fail(THORN_ERR_INVALID, "thorn_ortho_step: need 1 <= iters <= 32 and coefficients");
     const int n = static_cast<int>(plan->mats.size());
     if (n == 0) return THORN_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -416,7 +510,6 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
-    const thorn::TaskList sym = task_list(dev, plan->sym), g3 = task_list(dev, plan->g3);
     if (plan->any_exact) {
         THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total),
                      dim3(256), 0, st, mats, task_list(dev, plan->pre));
@@ -425,14 +518,29 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         THORN_LAUNCH(THORN_KIND_CAST, "ortho_repair_kernel", thorn::ortho_repair_kernel, dim3(n), dim3(256), 0, st,
                      mats);
     }
-    for (int it = 0; it < iters; ++it) {
-        const int fin = it == iters - 1 ? 1 : 0;
-        THORN_LAUNCH(THORN_KIND_GRAM, "ns_gram_kernel", thorn::ns_gram_kernel, dim3(sym.total), dim3(256), 0, st,
-                     mats, sym, it);
-        THORN_LAUNCH(THORN_KIND_POLY, "ns_poly_kernel", thorn::ns_poly_kernel, dim3(sym.total), dim3(256), 0, st,
-                     mats, sym, coeffs[3 * it], coeffs[3 * it + 1], coeffs[3 * it + 2]);
-        THORN_LAUNCH(THORN_KIND_UPDATE, "ns_update_kernel", thorn::ns_update_kernel, dim3(g3.total), dim3(256), 0,
-                     st, mats, g3, it, fin);
+    // Newton-Schulz: matrices of aspect ratio below 2 on the plain quintic, the others on Gram
+    // Newton-Schulz with the given restarts (thorn.py:628, 637-658); step k of both schedules
+    // shares launch k.
+    const uint32_t plain = iters >= 32 ? 0xFFFFFFFEu : ((1u << iters) - 2u);
+    const std::vector<ScheduledOp> sched[2] = {ns_schedule(iters, plain, coeffs),
+                                               ns_schedule(iters, restart_mask, coeffs)};
+    const thorn::TaskList sym[2] = {task_list(dev, plan->sym[0]), task_list(dev, plan->sym[1])};
+    const thorn::TaskList g3[2] = {task_list(dev, plan->g3[0]), task_list(dev, plan->g3[1])};
+    const size_t steps = std::max(sched[0].size(), sched[1].size());
+    for (size_t k = 0; k < steps; ++k) {
+        thorn::NsOp op[2]{};
+        thorn::TaskList tl[2]{};
+        int kind = -1;
+        for (int q = 1; q >= 0; --q) {   // the Gram set first: it names the launch for timing
+            if (k >= sched[q].size() || sym[q].n == 0) continue;
+            op[q] = sched[q][k].op;
+            tl[q] = op[q].kind == thorn::kOpUpdate ? g3[q] : sym[q];
+            if (kind < 0) kind = sched[q][k].kind;
+        }
+        const int total = tl[1].total + tl[0].total;
+        if (total == 0) continue;
+        THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(256), 0, st, mats, tl[1],
+                     op[1], tl[0], op[0]);
     }
     if (plan->pnn.n > 0) {
         const thorn::TaskList pnn = task_list(dev, plan->pnn);

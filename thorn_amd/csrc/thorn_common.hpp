@@ -84,10 +84,12 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 reduced separately).
-__device__ __forceinline__ float halfwave_sum(float v) {
+// Sum over each aligned group of G lanes (G a power of two <= 64), reduced separately.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "lane group");
 #pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
 }
 
@@ -156,8 +158,11 @@ struct OrthoMat {
     float* x0;         // rows x ldx, u = g + beta1*m (fp32, unnormalized)
     _Float16* xa;      // rows x ldx, Newton-Schulz iterate (ping)
     _Float16* xb;      // rows x ldx, Newton-Schulz iterate (pong)
-    _Float16* gram;    // s x lds
-    _Float16* poly;    // s x lds
+    _Float16* gram;    // s x lds: R, the Gram matrix of the short side
+    _Float16* poly;    // s x lds: P = a I + b R + c R^2 of the current iteration
+    _Float16* qa;      // s x lds: Q, the accumulated product of the P's since the last restart
+    _Float16* qb;      // s x lds: (ping-pong with qa)
+    _Float16* tmp;     // s x lds: R P while R is advanced to P R P
     _Float16* uout;    // rows x ldx, final update (per-row-normalized matrices only)
     float* normpart;   // [mom_tiles] partial sums of u^2
     float* rowpart;    // [mom_tiles_c][rows] partial row sums of p*g*softplus(cg)
@@ -190,6 +195,10 @@ enum ScalSlot : int {
     kScalPrescale = 4, // 2^k nearest sigma: the next step's first-iterate prescale
     kScalRepair = 5,   // 1: the prescaled first iterate is out of range; ortho_cast_kernel rebuilds it
 };
+
+// Selectors of the s x s workspace matrices and of the two iterate buffers.
+enum SymBuf : int { kBufR = 0, kBufP = 1, kBufQA = 2, kBufQB = 3, kBufT = 4 };
+enum XBuf : int { kXB = 0, kXA = 1 };   // the first iterate is written to xb
 
 // A grouped launch: task k covers blocks [starts[k], starts[k+1]) and works on matrix order[k].
 struct TaskList {

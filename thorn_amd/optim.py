@@ -287,7 +287,15 @@ class _OrthoRunner:
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
-        self.plan.step(self.table.data_ptr(), coeffs, torch.cuda.current_stream(self.device).cuda_stream)
+        self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
+                       torch.cuda.current_stream(self.device).cuda_stream)
+
+    @staticmethod
+    def restart_mask(group: _Group, iters: int) -> int:
+        """Gram Newton-Schulz restart positions (thorn.py:582, 637-653) as a bit mask for the
+        library, which runs Gram Newton-Schulz on matrices at least twice as long as wide and the
+        plain quintic on the others (thorn.py:628, 655-658)."""
+        return sum(1 << i for i in group.restarts if 0 < i < iters)
 
 
 class _AdamRunner:
