@@ -184,18 +184,23 @@ def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
         times.sort()
         return times[len(times) // 2]
 
-    for sh in sorted(counts, key=lambda x: ns_flops([x])):   # cheapest shapes first
+    # the oracle runs the reference's schedules: Gram Newton-Schulz (restart before iteration 2 at
+    # the default coefficients) for every non-square matrix, the plain quintic for square ones
+    def ref_flops(sh):
+        return schedule_flops([sh], 5, 0b100 if sh[0] != sh[1] else (1 << 5) - 2)
+
+    for sh in sorted(counts, key=ref_flops):   # cheapest shapes first
         if time.perf_counter() - t_start > budget_s:
             break
         p = torch.nn.Parameter(torch.randn(sh, generator=gen) * 0.02)
         opt = O.OracleTHORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3, 'weight_decay': 0.1,
                               'scaling_mode': 'moonlight'}])
         per_shape[sh] = timed_steps(opt, p, sh, 3)
-    measured_flops = sum(ns_flops([sh]) for sh in per_shape)
+    measured_flops = sum(ref_flops(sh) for sh in per_shape)
     sec_per_flop = sum(per_shape.values()) / max(measured_flops, 1.0)
     est = 0.0
     for sh, n in counts.items():
-        est += n * per_shape.get(sh, ns_flops([sh]) * sec_per_flop)
+        est += n * per_shape.get(sh, ref_flops(sh) * sec_per_flop)
     # Adam: a 1/10 slice of the non-orthogonalized elements (at least 1 Mi)
     adam_total = sum(math.prod(sh) for shapes, _ in others for sh in shapes)
     adam_time = 0.0
