@@ -92,21 +92,6 @@ struct DmaSrc {
         }
     }
 
-    // The loads are written as inline assembly so that the compiler does not track them as LDS
-    // writes: its conservative aliasing would otherwise wait for every outstanding load before
-    // the next LDS fragment read and serialize the pipeline. The main loop orders them explicitly
-    // (lds_wait_barrier); the "memory" clobber keeps LDS accesses from moving across them.
-    __device__ __forceinline__ void issue(int t, char* lds, const void* zero, int wave) const {
-        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_address(lds) + wave * PER_WAVE * 1024);
-        const int64_t off = t * step;
-#pragma unroll
-        for (int q = 0; q < PER_WAVE; ++q) {
-            const void* p = (t * BKC < lim[q]) ? static_cast<const void*>(src[q] + off) : zero;
-            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p), "{m0}"(base + q * 1024)
-                         : "memory");
-        }
-    }
-
     static constexpr int BKC = 32;   // K elements per tile
 };
 
@@ -158,214 +143,168 @@ __device__ __forceinline__ void interleave_mfma_ds() {
     }
 }
 
-// acc[i][j] += A[m0 + wm + 32i .., K tiles kt0 .. kt_end) * B[.., n0 + wn + 32j ..] with operand
-// layouts AK / BK (true = K-major).
-// The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out transposed: lane l holds
-// row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3 in registers r..r+3,
-// which the epilogue writes to LDS as one 16-byte store.
-//
-// Pipeline over K tiles of 32 (S LDS stages, one block barrier per tile):
-//   tile t is loaded into stage (t - kt0) % S S-1 tiles ahead of its use, by direct global->LDS
-//   loads; each tile is two k16 sub-steps; the LDS fragment reads of the next sub-step are in
-//   flight while the MFMAs of the current one run. Between the two sub-steps of tile t every wave
-//   waits for its own loads of tile t+1 and meets the others at the barrier: after it, tile t+1
-//   is visible and nobody reads stage (t-1) % S any more, which then receives tile t+S-1. The
-//   range ends with every load complete and a barrier, so the stages are free again.
-template <class C, bool AK, bool BK>
-__device__ __forceinline__ void mainloop_range(const Operand& A, const Operand& B, int m0, int n0, int kt0,
-                                               int kt_end, floatx16 (&acc)[C::TM][C::TN], char* smem,
-                                               const void* zero) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
-    DmaSrc<C::BM, AK> da;
-    DmaSrc<C::BN, BK> db;
-    da.init(A, m0, wave, lane);
-    db.init(B, n0, wave, lane);
-    const int KT = kt_end;
-    auto stage_a = [&](int t) { return smem + ((t - kt0) % C::S) * C::STAGE_BYTES; };
-    auto issue = [&](int t) {
-        char* st = stage_a(t);
-        da.issue(t, st, zero, wave);
-        db.issue(t, st + C::A_BYTES, zero, wave);
-    };
-#pragma unroll
-    for (int t = 0; t < C::S - 1; ++t)
-        if (kt0 + t < KT) issue(kt0 + t);
-    // tile kt0 ready: loads of the next min(S-2, n-1) tiles may still be in flight
-    static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
-    const int n = KT - kt0;
-    if (C::S >= 5 && n >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
-    else if (C::S >= 4 && n >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
-    else if (n >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
-    else lds_wait_barrier<0>();
+// The A and B operand sources of one tile: each is read MN-major for K tiles t < k0 and K-major
+// from there on (k0 = 0: always K-major; k0 >= the tile count: always MN-major). A symmetric
+// matrix stored as its upper block triangle is read MN-major, from the transposed mirror block,
+// before its diagonal block and K-major from there on.
+template <int MN>
+struct DmaPair {
+    static constexpr int PER_WAVE = MN / 64;
+    DmaSrc<MN, true> kmaj;
+    DmaSrc<MN, false> mnmaj;
+    int k0;
 
-    constexpr int NREAD = C::TM * (AK ? 1 : 2) + C::TN * (BK ? 1 : 2);   // LDS reads per sub-step
-    half8 fa[2][C::TM], fb[2][C::TN];
-    {
-        const char* sa = stage_a(kt0);
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(sa, wm + 32 * i, 0, lane);
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN, BK>(sa + C::A_BYTES, wn + 32 * j, 0, lane);
+    __device__ __forceinline__ void init(const Operand& op, int mn0, int wave, int lane, int k0_) {
+        kmaj.init(op, mn0, wave, lane);
+        mnmaj.init(op, mn0, wave, lane);
+        k0 = k0_;
     }
-    for (int kt = kt0; kt < KT; ++kt) {
-        const char* sa = stage_a(kt);
-        // sub-step 0: read sub-step 1's fragments while the MFMAs of sub-step 0 run
+
+    // Direct load q of this wave for K tile t into the stage at `lds` (a wave-uniform LDS byte
+    // address of this operand's part of the stage). The layout is selected per lane, not by a
+    // branch, so the loads interleave with the MFMAs of the loop body. Every address is inside
+    // the operand (chunks past its end come from `zero`) for any t >= 0.
+    // The load is inline assembly so that the compiler does not track it as an LDS write: its
+    // conservative aliasing would otherwise wait for every outstanding load before the next LDS
+    // fragment read and serialize the pipeline. The main loop orders the loads explicitly
+    // (lds_wait_barrier); the "memory" clobber keeps LDS accesses from moving across them.
+    __device__ __forceinline__ void issue_one(int t, int q, uint32_t lds, const void* zero) const {
+        const bool km = t >= k0;
+        const char* src = km ? kmaj.src[q] + t * kmaj.step : mnmaj.src[q] + t * mnmaj.step;
+        const int lim = km ? kmaj.lim[q] : mnmaj.lim[q];
+        const void* p = t * DmaSrc<MN, true>::BKC < lim ? static_cast<const void*>(src) : zero;
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p), "{m0}"(lds + q * 1024)
+                     : "memory");
+    }
+};
+
+// Reads this wave's MFMA fragments of k16 step `ks` of the stage at `st` (A at st, B at
+// st + A_BYTES) in the layouts AK / BK (true = K-major).
+template <class C, bool AK, bool BK>
+__device__ __forceinline__ void read_frags(const char* st, int ks, int wm, int wn, int lane, half8 (&ra)[C::TM],
+                                           half8 (&rb)[C::TN]) {
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i) fa[1][i] = frag<C::BM, AK>(sa, wm + 32 * i, 1, lane);
+    for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, AK>(st, wm + 32 * i, ks, lane);
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) fb[1][j] = frag<C::BN, BK>(sa + C::A_BYTES, wn + 32 * j, 1, lane);
+    for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, BK>(st + C::A_BYTES, wn + 32 * j, ks, lane);
+}
+
+// The K tiles [lo, hi) of gemm_tile in one operand layout (AK / BK). On entry the stages hold
+// tiles lo .. lo+S-2 (tile lo visible to every wave); on exit they hold hi .. hi+S-2 likewise.
+// Each iteration is one basic block: two k16 sub-steps of 16 MFMAs, with the second sub-step's
+// fragment reads interleaved into the first, and the direct loads of tile kt+S-1 and the next
+// tile's first fragment reads interleaved into the second. Between the two, every wave waits for
+// its own loads of tile kt+1 and meets the others at the block barrier: after it, tile kt+1 is
+// visible and nobody reads stage (kt-1) % S any more, which then receives tile kt+S-1. Tiles
+// past the end of K are loaded (zeros or in-bounds data) and read but never used, which keeps
+// the loop body free of branches.
+template <class C, bool AK, bool BK>
+__device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM>& da, const DmaPair<C::BN>& db,
+                                             floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
+                                             half8 (&fb)[2][C::TN], char* smem, const void* zero) {
+    if (lo >= hi) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    constexpr int NM = C::TM * C::TN;                                      // MFMAs per sub-step
+    constexpr int NREAD = C::TM * (AK ? 1 : 2) + C::TN * (BK ? 1 : 2);   // LDS reads per sub-step
+    constexpr int NA = DmaPair<C::BM>::PER_WAVE, NB = DmaPair<C::BN>::PER_WAVE;
+    static_assert(NA + NB <= NM, "one direct load per MFMA at most");
+    read_frags<C, AK, BK>(smem + (lo % C::S) * C::STAGE_BYTES, 0, wm, wn, lane, fa[0], fb[0]);
+    for (int kt = lo; kt < hi; ++kt) {
+        const char* sa = smem + (kt % C::S) * C::STAGE_BYTES;
+        read_frags<C, AK, BK>(sa, 1, wm, wn, lane, fa[1], fb[1]);
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
-        interleave_mfma_ds<C::TM * C::TN, NREAD>();
+        interleave_mfma_ds<NM, NREAD>();
         __builtin_amdgcn_sched_barrier(0);
-        // tile kt+1 ready (tiles kt+2 .. kt+S-2 may still be in flight), stage (kt-1) % S free
-        {
-            const int ahead = (KT - 1 < kt + C::S - 2 ? KT - 1 : kt + C::S - 2) - (kt + 1);
-            if (C::S >= 5 && ahead >= 2) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
-            else if (C::S >= 4 && ahead >= 1) lds_wait_barrier<C::LOADS_PER_STAGE>();
-            else lds_wait_barrier<0>();
-        }
+        lds_wait_barrier<(C::S - 3) * C::LOADS_PER_STAGE>();
         __builtin_amdgcn_sched_barrier(0);
-        if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
-        // sub-step 1: read the next tile's first fragments while the MFMAs of sub-step 1 run
-        if (kt + 1 < KT) {
-            const char* na = stage_a(kt + 1);
+        const int tn = kt + C::S - 1;
+        const uint32_t st_new = lds0 + (tn % C::S) * C::STAGE_BYTES;
 #pragma unroll
-            for (int i = 0; i < C::TM; ++i) fa[0][i] = frag<C::BM, AK>(na, wm + 32 * i, 0, lane);
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j) fb[0][j] = frag<C::BN, BK>(na + C::A_BYTES, wn + 32 * j, 0, lane);
+        for (int q = 0; q < NM; ++q) {
+            const int i = q / C::TN, j = q % C::TN;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+            if (q < NA + NB) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (q < NA) da.issue_one(tn, q, st_new + wave * NA * 1024, zero);
+                else db.issue_one(tn, q - NA, st_new + C::A_BYTES + wave * NB * 1024, zero);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
-        interleave_mfma_ds<C::TM * C::TN, NREAD>();
+        read_frags<C, AK, BK>(smem + ((kt + 1) % C::S) * C::STAGE_BYTES, 0, wm, wn, lane, fa[0], fb[0]);
+        interleave_mfma_ds<NM - NA - NB, NREAD>();
         __builtin_amdgcn_sched_barrier(0);
     }
-    lds_barrier();   // every wave is done with the stages
 }
 
-// acc = A[m0 .., 0:K] * B[0:K, n0 ..] where A is read MN-major for K tiles t < a_k0 and K-major
-// from there on, B likewise with b_k0: a symmetric matrix stored as its upper block triangle is
-// read K-major from its diagonal block on and MN-major, from the transposed mirror block, before
-// it. One pipelined loop: the direct loads and the fragment reads of a tile branch on its layout
-// (uniformly), the MFMAs do not, so the accumulators keep one register assignment.
+// acc = A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over KT K tiles of 32, A read
+// MN-major for tiles t < a_k0 and K-major from there on, B likewise with b_k0 (a_k0 <= b_k0):
+// at most three segments, MN/MN, K/MN and K/K, in that order, through one S-stage pipeline of
+// direct global->LDS loads. The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out
+// transposed: lane l holds row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3
+// in registers r..r+3, which the epilogue writes to LDS as one 16-byte store. Ends with every
+// load and LDS read complete and a block barrier, so the stages are free for the epilogue.
 template <class C>
-__device__ __forceinline__ void gemm_mainloop_mixed(const Operand& A, const Operand& B, int m0, int n0, int K,
-                                                    int a_k0, int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem,
-                                                    const void* zero) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
-    DmaSrc<C::BM, true> dak;
-    DmaSrc<C::BM, false> dam;
-    DmaSrc<C::BN, true> dbk;
-    DmaSrc<C::BN, false> dbm;
-    dak.init(A, m0, wave, lane);
-    dam.init(A, m0, wave, lane);
-    dbk.init(B, n0, wave, lane);
-    dbm.init(B, n0, wave, lane);
-    const int KT = (K + C::BK - 1) / C::BK;
-    auto stage_a = [&](int t) { return smem + (t % C::S) * C::STAGE_BYTES; };
-    auto issue = [&](int t) {
-        char* st = stage_a(t);
-        if (t >= a_k0) dak.issue(t, st, zero, wave);
-        else dam.issue(t, st, zero, wave);
-        if (t >= b_k0) dbk.issue(t, st + C::A_BYTES, zero, wave);
-        else dbm.issue(t, st + C::A_BYTES, zero, wave);
-    };
-    auto read = [&](int t, int ks, half8 (&ra)[C::TM], half8 (&rb)[C::TN]) {
-        const char* st = stage_a(t);
-        if (t >= a_k0) {
-#pragma unroll
-            for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, true>(st, wm + 32 * i, ks, lane);
-        } else {
-#pragma unroll
-            for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, false>(st, wm + 32 * i, ks, lane);
-        }
-        if (t >= b_k0) {
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, true>(st + C::A_BYTES, wn + 32 * j, ks, lane);
-        } else {
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, false>(st + C::A_BYTES, wn + 32 * j, ks, lane);
-        }
-    };
-    auto mfmas = [&](const half8 (&ra)[C::TM], const half8 (&rb)[C::TN]) {
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(rb[j], ra[i], acc[i][j], 0, 0, 0);
-    };
-#pragma unroll
-    for (int t = 0; t < C::S - 1; ++t)
-        if (t < KT) issue(t);
+__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0, int KT, int a_k0,
+                                          int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem, const void* zero) {
     static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
-    if (C::S >= 5 && KT >= 4) lds_wait_barrier<3 * C::LOADS_PER_STAGE>();
-    else if (C::S >= 4 && KT >= 3) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
-    else if (KT >= 2) lds_wait_barrier<C::LOADS_PER_STAGE>();
-    else lds_wait_barrier<0>();
-    half8 fa[2][C::TM], fb[2][C::TN];
-    if (KT > 0) read(0, 0, fa[0], fb[0]);
-    for (int kt = 0; kt < KT; ++kt) {
-        read(kt, 1, fa[1], fb[1]);   // sub-step 1's fragments, in flight during sub-step 0's MFMAs
-        mfmas(fa[0], fb[0]);
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            const int ahead = (KT - 1 < kt + C::S - 2 ? KT - 1 : kt + C::S - 2) - (kt + 1);
-            if (C::S >= 5 && ahead >= 2) lds_wait_barrier<2 * C::LOADS_PER_STAGE>();
-            else if (C::S >= 4 && ahead >= 1) lds_wait_barrier<C::LOADS_PER_STAGE>();
-            else lds_wait_barrier<0>();
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + C::S - 1 < KT) issue(kt + C::S - 1);
-        if (kt + 1 < KT) read(kt + 1, 0, fa[0], fb[0]);   // next tile's first fragments
-        mfmas(fa[1], fb[1]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// Single-layout main loop: AK / BK = whether A / B are K-major.
-template <class C, bool AK, bool BK>
-__device__ __forceinline__ void gemm_mainloop(const Operand& A, const Operand& B, int m0, int n0,
-                                              int K, floatx16 (&acc)[C::TM][C::TN], char* smem,
-                                              const void* zero) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
-    mainloop_range<C, AK, BK>(A, B, m0, n0, 0, (K + C::BK - 1) / C::BK, acc, smem, zero);
+    DmaPair<C::BM> da;
+    DmaPair<C::BN> db;
+    da.init(A, m0, wave, lane, a_k0);
+    db.init(B, n0, wave, lane, b_k0);
+    constexpr int NA = DmaPair<C::BM>::PER_WAVE, NB = DmaPair<C::BN>::PER_WAVE;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+#pragma unroll
+    for (int t = 0; t < C::S - 1; ++t) {
+        const uint32_t st = lds0 + t * C::STAGE_BYTES;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) da.issue_one(t, q, st + wave * NA * 1024, zero);
+#pragma unroll
+        for (int q = 0; q < NB; ++q) db.issue_one(t, q, st + C::A_BYTES + wave * NB * 1024, zero);
+    }
+    lds_wait_barrier<(C::S - 2) * C::LOADS_PER_STAGE>();   // tile 0 visible
+    half8 fa[2][C::TM], fb[2][C::TN];
+    const int k1 = a_k0 < KT ? a_k0 : KT;
+    const int k2 = b_k0 < k1 ? k1 : (b_k0 < KT ? b_k0 : KT);
+    gemm_segment<C, false, false>(0, k1, da, db, acc, fa, fb, smem, zero);
+    gemm_segment<C, true, false>(k1, k2, da, db, acc, fa, fb, smem, zero);
+    gemm_segment<C, true, true>(k2, KT, da, db, acc, fa, fb, smem, zero);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Epilogue: the tile is streamed through LDS (reusing the pipeline stages) in two halves of
-// WM = BM/2 rows, the rows owned by one row of waves:
-//   for_rows: N[row][col] staging (fp32); each thread then gets 8 consecutive columns of one row,
-//             so global traffic is 16-byte chunks with 32 lanes on one row;
-//   for_cols: transposed staging T[col][row]; each thread gets 8 consecutive rows of one column
-//             (the mirrored tile of a symmetric product).
+// WM = BM/2 rows, the rows owned by one row of waves. stage_rows writes a half to the row-major
+// staging N (fp32; row r starts at row_base(r)); then
+//   each_row_chunk gives each thread 8 consecutive columns of one row, so global traffic is
+//     16-byte chunks with 32 lanes on one row;
+//   each_col_chunk gives each thread 8 consecutive rows of one column (the mirrored part of a
+//     symmetric tile), 16 lanes on one column and 16 consecutive row chunks, so each output row
+//     of the mirror gets 256 contiguous bytes.
+// Rows are NS floats apart plus 4 more after every 8 rows: the 64 lanes of a column read (16
+// row chunks x 4 columns) then hit 64 distinct banks, and 16-byte row accesses stay aligned.
 template <class C>
 struct Epi {
-    static constexpr int NS = C::BN + 4;    // N row stride (floats): 16 lanes x 16 B on distinct banks
-    static constexpr int TS = C::WM + 4;    // T row stride (floats)
-    static constexpr int N_BYTES = C::WM * NS * 4;
-    static constexpr int T_BYTES = C::BN * TS * 4;
-    static constexpr int BYTES = N_BYTES > T_BYTES ? N_BYTES : T_BYTES;
-    static constexpr int SMEM = BYTES > C::LDS_BYTES ? BYTES : C::LDS_BYTES;
+    static constexpr int NS = C::BN + 4;
+    static constexpr int N_BYTES = (C::WM * NS + (C::WM / 8) * 4) * 4;
+    static constexpr int SMEM = N_BYTES > C::LDS_BYTES ? N_BYTES : C::LDS_BYTES;
     static constexpr int ROW_CHUNKS = C::WM * (C::BN / 8) / 256;   // per thread per half
     static constexpr int COL_CHUNKS = C::BN * (C::WM / 8) / 256;
+    static_assert(C::WM / 8 == 16, "each_col_chunk: 16 row chunks per column");
+    __device__ static __forceinline__ int row_base(int r) { return r * NS + (r >> 3) * 4; }
 };
 
-// Chunk `it` of this thread in a half: 32 lanes of a wave share one row (row passes) or 16 lanes
-// one column (column passes), so every global access of a chunk pass is coalesced.
+// Chunk `it` of this thread in a half: 32 lanes of a wave share one row (row passes); 16 lanes
+// share one column and take its 16 row chunks (column passes).
 template <class C>
 __device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
     const int idx = it * 256 + threadIdx.x;
@@ -375,19 +314,18 @@ __device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
 template <class C>
 __device__ __forceinline__ void col_chunk(int it, int& c, int& r8) {
     const int idx = it * 256 + threadIdx.x;
-    c = idx / (C::WM / 8);
-    r8 = (idx % (C::WM / 8)) * 8;
+    c = idx >> 4;
+    r8 = (idx & 15) * 8;
 }
 
-// fn(it, half, local_row, col8, float (&v)[8]): v = acc[row][col8 .. col8+7] (tile coordinates:
-// row = half * WM + local_row); `it` numbers this thread's chunks 0 .. ROW_CHUNKS-1, in the order
-// given by row_chunk().
-template <class C, class Fn>
-__device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
+// Writes rows [half * WM, half * WM + WM) of the tile to the staging N, between two block
+// barriers (the previous user of smem, the main loop or another pass, is done before).
+template <class C>
+__device__ __forceinline__ void stage_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half) {
     using E = Epi<C>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* N = reinterpret_cast<float*>(smem);
-    lds_barrier();   // the previous user of smem (main loop or another pass) is done
+    lds_barrier();
     if ((wave >> 1) == half) {
         const int wn = (wave & 1) * C::WN;
 #pragma unroll
@@ -398,55 +336,57 @@ __device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* sm
                 for (int q = 0; q < 4; ++q) {
                     const int r = 32 * i + (lane & 31);
                     const int c = wn + 32 * j + 8 * q + 4 * (lane >> 5);
-                    *reinterpret_cast<floatx4*>(N + r * E::NS + c) =
+                    *reinterpret_cast<floatx4*>(N + E::row_base(r) + c) =
                         floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
                 }
     }
     lds_barrier();
+}
+
+// fn(it, local_row, col8, float (&v)[8]): v = staged[local_row][col8 .. col8+7] for the chunks
+// with keep(local_row, col8); `it` numbers this thread's chunks 0 .. ROW_CHUNKS-1, in the order
+// given by row_chunk().
+template <class C, class Keep, class Fn>
+__device__ __forceinline__ void each_row_chunk(const char* smem, Keep keep, Fn fn) {
+    using E = Epi<C>;
+    const float* N = reinterpret_cast<const float*>(smem);
 #pragma unroll
     for (int it = 0; it < E::ROW_CHUNKS; ++it) {
         int r, c8;
         row_chunk<C>(it, r, c8);
-        const floatx4 a = *reinterpret_cast<const floatx4*>(N + r * E::NS + c8);
-        const floatx4 b = *reinterpret_cast<const floatx4*>(N + r * E::NS + c8 + 4);
+        if (!keep(r, c8)) continue;
+        const floatx4 a = *reinterpret_cast<const floatx4*>(N + E::row_base(r) + c8);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(N + E::row_base(r) + c8 + 4);
         float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        fn(it, half, r, c8, v);
+        fn(it, r, c8, v);
     }
 }
 
-// fn(it, half, col, local_row8, float (&v)[8]): v = acc[row8 .. row8+7][col] with
-// row8 = half*WM + local_row8; chunk order given by col_chunk().
-template <class C, class Fn>
-__device__ __forceinline__ void for_cols(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
+// fn(it, col, local_row8, float (&v)[8]): v = staged[local_row8 .. local_row8+7][col] for the
+// chunks with keep(col, local_row8); chunk order given by col_chunk().
+template <class C, class Keep, class Fn>
+__device__ __forceinline__ void each_col_chunk(const char* smem, Keep keep, Fn fn) {
     using E = Epi<C>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* T = reinterpret_cast<float*>(smem);
-    lds_barrier();
-    if ((wave >> 1) == half) {
-        const int wn = (wave & 1) * C::WN;
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 32 * i + (lane & 31);
-                        const int c = wn + 32 * j + 8 * q + 4 * (lane >> 5) + e;
-                        T[c * E::TS + r] = acc[i][j][4 * q + e];
-                    }
-    }
-    lds_barrier();
+    const float* N = reinterpret_cast<const float*>(smem);
 #pragma unroll
     for (int it = 0; it < E::COL_CHUNKS; ++it) {
         int c, r8;
         col_chunk<C>(it, c, r8);
-        const floatx4 a = *reinterpret_cast<const floatx4*>(T + c * E::TS + r8);
-        const floatx4 b = *reinterpret_cast<const floatx4*>(T + c * E::TS + r8 + 4);
-        float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        fn(it, half, c, r8, v);
+        if (!keep(c, r8)) continue;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = N[E::row_base(r8 + e) + c];
+        fn(it, c, r8, v);
     }
+}
+
+// fn(it, half, local_row, col8, float (&v)[8]) over the row chunks of one half (see
+// each_row_chunk), row = half * WM + local_row.
+template <class C, class Fn>
+__device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
+    stage_rows<C>(acc, smem, half);
+    each_row_chunk<C>(smem, [](int, int) { return true; },
+                      [&](int it, int r, int c8, float (&v)[8]) { fn(it, half, r, c8, v); });
 }
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));

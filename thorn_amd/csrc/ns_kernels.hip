@@ -85,18 +85,28 @@ __global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __res
 // out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile of a symmetric s x s
 // matrix. Only the upper block triangle is stored: consumers read a block below the diagonal as
 // the transpose of its mirror above. A diagonal tile keeps its upper triangle and mirrors it into
-// its lower one, so it is exactly symmetric and reads the same either way; Csym's diagonal tile
-// is exactly symmetric too, so its term for (r, c) can be read from row r or row c alike.
+// its lower one, so it is exactly symmetric and reads the same either way: the row pass writes
+// every 8-column chunk that reaches the diagonal (the elements of the diagonal chunk below the
+// diagonal taken from the staged mirror), the column pass the chunks entirely below it. Csym's
+// diagonal tile is exactly symmetric too, so its term for (r, c) can be read from row r or row c
+// alike.
 template <class C>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
                                           const _Float16* csym, int64_t ld, int n, int m0, int n0, float alpha,
                                           float beta, float gamma) {
     using E = Epi<C>;
+    const float* N = reinterpret_cast<const float*>(smem);
     const bool diag = m0 == n0;
 #pragma unroll 1
     for (int h = 0; h < 2; ++h) {
+        const int rb = m0 + h * C::WM;   // first row of this half
+        // row pass: chunk (r, c) with c + 8 > r on a diagonal tile
+        auto keep_row = [&](int lr, int c8) {
+            const int r = rb + lr, c = n0 + c8;
+            return r < n && c < ld && !(diag && c + 7 < r);
+        };
         // the beta * Csym chunks of a pass are all requested before any of them is needed (the
-        // loads overlap the LDS staging)
+        // row pass's loads overlap the LDS staging)
         half8v cpre[E::ROW_CHUNKS];
         static_assert(E::ROW_CHUNKS == E::COL_CHUNKS, "one prefetch buffer serves both passes");
         if (beta != 0.f) {
@@ -104,14 +114,18 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
             for (int it = 0; it < E::ROW_CHUNKS; ++it) {
                 int lr, c8;
                 row_chunk<C>(it, lr, c8);
-                const int r = m0 + h * C::WM + lr, c = n0 + c8;
-                cpre[it] = (r < n && c < ld) ? ldg<half8v>(csym + (int64_t)r * ld + c) : half8v{};
+                cpre[it] = keep_row(lr, c8) ? ldg<half8v>(csym + (int64_t)(rb + lr) * ld + n0 + c8) : half8v{};
             }
         }
-        for_rows<C>(acc, smem, h, [&](int it, int half, int lr, int c8, float (&v)[8]) {
-            const int r = m0 + half * C::WM + lr, c = n0 + c8;
-            if (r >= n || c >= ld) return;
-            if (diag && c + 7 < r) return;   // entirely below the diagonal: written by the mirror pass
+        stage_rows<C>(acc, smem, h);
+        each_row_chunk<C>(smem, keep_row, [&](int it, int lr, int c8, float (&v)[8]) {
+            const int r = rb + lr, c = n0 + c8;
+            if (diag && c < r) {   // the chunk holding the diagonal: elements c + e < r from the mirror (c + e, r)
+                const int lc = h * C::WM + lr;
+#pragma unroll
+                for (int e = 0; e < 7; ++e)
+                    if (c + e < r) v[e] = N[E::row_base(c8 + e - h * C::WM) + lc];
+            }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float t = alpha * v[e];
@@ -119,45 +133,32 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
                 if (r == c + e) t += gamma;
                 v[e] = t;
             }
-            _Float16* dst = out + (int64_t)r * ld + c;
-            if (!diag || c >= r) {
-                stg_nt<half8v>(dst, to_half8(v));
-            } else {   // the chunk holding the diagonal element: its upper part only
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (c + e >= r) dst[e] = (_Float16)v[e];
-            }
+            stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
         });
         if (!diag) continue;
-        // diagonal tile: the lower triangle from the transposed staging
+        // diagonal tile, column pass: element (c, r) of a chunk entirely below the diagonal from
+        // the staged (r, c)
+        auto keep_col = [&](int cl, int lr8) {
+            const int c = n0 + cl, r8 = rb + lr8;
+            return c < n && r8 < ld && c > r8 + 7;
+        };
         if (beta != 0.f) {
 #pragma unroll
             for (int it = 0; it < E::COL_CHUNKS; ++it) {
                 int cl, lr8;
                 col_chunk<C>(it, cl, lr8);
-                const int c = n0 + cl, r8 = m0 + h * C::WM + lr8;
-                cpre[it] = (c < n && r8 < ld) ? ldg<half8v>(csym + (int64_t)c * ld + r8) : half8v{};
+                cpre[it] = keep_col(cl, lr8) ? ldg<half8v>(csym + (int64_t)(n0 + cl) * ld + rb + lr8) : half8v{};
             }
         }
-        for_cols<C>(acc, smem, h, [&](int it, int half, int cl, int lr8, float (&v)[8]) {
-            const int c = n0 + cl, r8 = m0 + half * C::WM + lr8;   // v[e] is (r8 + e, c), stored at (c, r8 + e)
-            if (c >= n || r8 >= ld) return;
-            if (c <= r8) return;   // no destination below the diagonal
+        each_col_chunk<C>(smem, keep_col, [&](int it, int cl, int lr8, float (&v)[8]) {
+            const int c = n0 + cl, r8 = rb + lr8;   // v[e] is (r8 + e, c), stored at (c, r8 + e)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float t = alpha * v[e];
                 if (beta != 0.f) t += beta * static_cast<float>(cpre[it][e]);
-                if (r8 + e == c) t += gamma;
-                v[e] = t;
+                v[e] = t;   // never on the diagonal
             }
-            _Float16* dst = out + (int64_t)c * ld + r8;
-            if (c > r8 + 7) {
-                stg_nt<half8v>(dst, to_half8(v));
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (r8 + e < c) dst[e] = (_Float16)v[e];
-            }
+            stg<half8v>(out + (int64_t)c * ld + r8, to_half8(v));
         });
     }
 }
@@ -172,58 +173,14 @@ struct NsOp {
     float alpha, beta, gamma;
 };
 
-// R = X X^T (wide) or X^T X (tall) of the iterate in buffer `xsel`; `first`: that iterate is the
-// stored first iterate, sigma * u up to the factor x0scale. Upper-triangle tile number `local`.
-// Each layout has its own main loop and epilogue (no accumulator merge between alternatives).
-__device__ __forceinline__ void gram_tile(const OrthoMat& M, int local, const NsOp& op, char* smem) {
-    const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
-    int ti, tj;
-    tri_decode(local, T, ti, tj);
-    const Operand A = iterate_operand(M, op.xsel);
-    const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
-    const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    if (M.tall) {   // contraction over rows: MN-major columns of X
-        floatx16 acc[NsCfg::TM][NsCfg::TN];
-        gemm_mainloop<NsCfg, false, false>(A, A, m0, n0, M.l, acc, smem, M.zero);
-        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
-    } else {        // contraction over columns: K-major rows of X
-        floatx16 acc[NsCfg::TM][NsCfg::TN];
-        gemm_mainloop<NsCfg, true, true>(A, A, m0, n0, M.l, acc, smem, M.zero);
-        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
-    }
-}
-
-// out = alpha * A B + beta * C + gamma * I over s x s workspace matrices that are symmetric and
-// commute (all are polynomials in the same R), so the product is symmetric: upper-triangle tiles.
-// A's block row ti and B's block row tj (B symmetric: its column is its row); a matrix stored as
-// its upper block triangle is read MN-major (transposed, from the mirror block) before its
-// diagonal block. C may be absent (csel < 0).
-__device__ __forceinline__ void sym_tile(const OrthoMat& M, int local, const NsOp& op, char* smem) {
-    const int T = (M.s + NsCfg::BM - 1) / NsCfg::BM;
-    int ti, tj;
-    tri_decode(local, T, ti, tj);
-    const Operand A = square_operand(sym_buf(M, op.asel), M), B = square_operand(sym_buf(M, op.bsel), M);
-    constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
-    floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_mainloop_mixed<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, M.s, ti * KB, tj * KB, acc, smem, M.zero);
-    sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), op.csel >= 0 ? sym_buf(M, op.csel) : nullptr, M.lds, M.s,
-                     ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.csel >= 0 ? op.beta : 0.f, op.gamma);
-}
-
-// Epilogue of an update tile (see update_tile); instantiated once per main-loop path.
+// Epilogue of an update tile (see ns_phase_kernel).
 __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
     const int xsel = op.xsel, first = op.first, final_iter = op.final_iter;
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    if (first) {   // the stored first iterate is sigma * u up to the factor x0scale
-        const float osc = M.scal[kScalX0Scale];
-        if (osc != 1.f) {
-#pragma unroll
-            for (int i = 0; i < NsCfg::TM; ++i)
-#pragma unroll
-                for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] *= osc;
-        }
-    }
+    // the stored first iterate is sigma * u up to the factor x0scale; applied per output chunk
+    // (x * 1 is exact), so the accumulators stay in their registers
+    const float osc = first ? M.scal[kScalX0Scale] : 1.f;
 
     if (!final_iter) {
         _Float16* dst = xsel == kXA ? M.xb : M.xa;
@@ -231,6 +188,8 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
                 const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] *= osc;
                 if (r < M.rows && c < M.ldx) stg_nt<half8v>(dst + (int64_t)r * M.ldx + c, to_half8(v));
             });
         return;
@@ -243,6 +202,8 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
                 const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] *= osc;
                 const half8v hv = to_half8(v);
                 float sq = 0.f;
                 if (r < M.rows && c < M.ldx) {
@@ -271,6 +232,8 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
             const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
             if (r >= M.rows || c >= M.cols) return;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] *= osc;
             float* pp = M.p + (int64_t)r * M.cols + c;
             if (vec && c + 8 <= M.cols) {
                 float4 p0 = ldg<float4>(pp), p1 = ldg<float4>(pp + 4);
@@ -301,49 +264,24 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     }
 }
 
-// X' = Q X (wide) or X Q (tall) with X in buffer `xsel` and Q the workspace matrix `qsel` (stored
-// as its upper block triangle), output tile number `local` (column-major). Not final: store the
-// f16 iterate into the other X buffer. Final: either apply the update to p directly (cautious
-// weight decay, thorn.py:669-702) or store u' in f16 with per-row sums of squares for the
-// per-row normalization (thorn.py:758-762). `first`: X is the stored first iterate (sigma * u up
-// to the factor x0scale). Each orientation is two pipelined K ranges: Q's blocks before the
-// diagonal block, read transposed from their mirror above it, then the rest.
-__device__ __forceinline__ void update_tile(const OrthoMat& M, int local, const NsOp& op, char* smem,
-                                            float* scratch) {
-    // column-major tile order: consecutive tiles share the column panel of X and, a few apart,
-    // the row panels of Q
-    const int ti = local % M.g3_tiles_m, tj = local / M.g3_tiles_m;
-    const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    const Operand X = iterate_operand(M, op.xsel), Q = square_operand(sym_buf(M, op.qsel), M);
-    constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
-    const int KT = (M.s + NsCfg::BK - 1) / NsCfg::BK;
-    if (M.tall) {   // X Q: rows of X (K-major); column n of Q is its row n
-        floatx16 acc[NsCfg::TM][NsCfg::TN];
-#pragma unroll
-        for (int i = 0; i < NsCfg::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] = floatx16{};
-        const int e = tj * KB < KT ? tj * KB : KT;
-        mainloop_range<NsCfg, true, false>(X, Q, m0, n0, 0, e, acc, smem, M.zero);
-        mainloop_range<NsCfg, true, true>(X, Q, m0, n0, e, KT, acc, smem, M.zero);
-        update_finish(M, acc, local, ti, tj, op, smem, scratch);
-    } else {        // Q X: X[k][n] is MN-major
-        floatx16 acc[NsCfg::TM][NsCfg::TN];
-#pragma unroll
-        for (int i = 0; i < NsCfg::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < NsCfg::TN; ++j) acc[i][j] = floatx16{};
-        const int e = ti * KB < KT ? ti * KB : KT;
-        mainloop_range<NsCfg, false, false>(Q, X, m0, n0, 0, e, acc, smem, M.zero);
-        mainloop_range<NsCfg, true, false>(Q, X, m0, n0, e, KT, acc, smem, M.zero);
-        update_finish(M, acc, local, ti, tj, op, smem, scratch);
-    }
-}
-
 // A Newton-Schulz phase launch: blocks [0, t0.total) run op0 over the tiles of task list t0, the
 // next t1.total blocks run op1 over t1. The two operations belong to disjoint sets of matrices
 // (the square ones, on the plain quintic, and the others, on Gram Newton-Schulz), so one launch
-// carries a step of each schedule.
+// carries a step of each schedule. Each block computes one 256 x 256 tile:
+//   Gram (kOpGram): R = X X^T (wide) or X^T X (tall) of the iterate in buffer `xsel`, rows of X
+//     read K-major or its columns MN-major; upper-triangle tile number `local`. `first`: the
+//     iterate is the stored first iterate, sigma * u up to the factor x0scale.
+//   Symmetric product (kOpSym): out = alpha * A B + beta * C + gamma * I over s x s workspace
+//     matrices that are symmetric and commute (all are polynomials in the same R), so the product
+//     is symmetric: upper-triangle tiles. A's block row ti and B's block row tj (B symmetric: its
+//     column is its row); a matrix stored as its upper block triangle is read MN-major (from the
+//     transposed mirror block) before its diagonal block. C may be absent (csel < 0).
+//   Update (kOpUpdate): X' = Q X (wide) or X Q (tall) with X in buffer `xsel` and Q the workspace
+//     matrix `qsel`, output tile number `local` in column-major order (consecutive tiles share
+//     the column panel of X and, a few apart, the row panels of Q); Q's blocks before the
+//     diagonal block are read transposed from their mirror above it. See update_finish for the
+//     epilogue.
+// All three run the same main loop (gemm_tile) with per-operation operands and layouts.
 __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
                                                        TaskList t1, NsOp op1) {
     __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
@@ -353,12 +291,57 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     const TaskList& tl = second ? t1 : t0;
     const NsOp& op = second ? op1 : op0;
     if (second) b -= t0.total;
+    if (op.kind == kOpNone) return;
     const int k = find_task(tl.starts, tl.n, b);
     const OrthoMat& M = mats[tl.order[k]];
     const int local = b - tl.starts[k];
-    if (op.kind == kOpGram) gram_tile(M, local, op, smem);
-    else if (op.kind == kOpSym) sym_tile(M, local, op, smem);
-    else if (op.kind == kOpUpdate) update_tile(M, local, op, smem, scratch);
+
+    constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
+    const int KTs = (M.s + NsCfg::BK - 1) / NsCfg::BK;
+    int ti, tj, KT, a_k0, b_k0;
+    Operand A, B;
+    if (op.kind == kOpUpdate) {
+        ti = local % M.g3_tiles_m;
+        tj = local / M.g3_tiles_m;
+        const Operand X = iterate_operand(M, op.xsel), Q = square_operand(sym_buf(M, op.qsel), M);
+        KT = KTs;
+        if (M.tall) {   // X Q: rows of X (K-major); column n of Q is its row n
+            A = X;
+            B = Q;
+            a_k0 = 0;
+            b_k0 = tj * KB;
+        } else {        // Q X: X[k][n] is MN-major
+            A = Q;
+            B = X;
+            a_k0 = ti * KB;
+            b_k0 = KT;
+        }
+    } else {
+        tri_decode(local, (M.s + NsCfg::BM - 1) / NsCfg::BM, ti, tj);
+        if (op.kind == kOpGram) {
+            A = B = iterate_operand(M, op.xsel);
+            KT = (M.l + NsCfg::BK - 1) / NsCfg::BK;
+            a_k0 = b_k0 = M.tall ? KT : 0;   // tall: contraction over rows, MN-major columns of X
+        } else {
+            A = square_operand(sym_buf(M, op.asel), M);
+            B = square_operand(sym_buf(M, op.bsel), M);
+            KT = KTs;
+            a_k0 = ti * KB;
+            b_k0 = tj * KB;
+        }
+    }
+    floatx16 acc[NsCfg::TM][NsCfg::TN];
+    gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero);
+    if (op.kind == kOpUpdate) {
+        update_finish(M, acc, local, ti, tj, op, smem, scratch);
+    } else if (op.kind == kOpGram) {
+        const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
+        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, osc * osc, 0.f,
+                         0.f);
+    } else {
+        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), op.csel >= 0 ? sym_buf(M, op.csel) : nullptr, M.lds, M.s,
+                         ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.csel >= 0 ? op.beta : 0.f, op.gamma);
+    }
 }
 
 }  // namespace thorn
