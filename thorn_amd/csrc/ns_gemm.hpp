@@ -286,12 +286,13 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // WM = BM/2 rows, the rows owned by one row of waves. stage_rows writes a half to the row-major
 // staging N (fp32; row r starts at row_base(r)); then
 //   each_row_chunk gives each thread 8 consecutive columns of one row, so global traffic is
-//     16-byte chunks with 32 lanes on one row;
+//     16-byte chunks with BN/8 lanes on one row;
 //   each_col_chunk gives each thread 8 consecutive rows of one column (the mirrored part of a
-//     symmetric tile), 16 lanes on one column and 16 consecutive row chunks, so each output row
-//     of the mirror gets 256 contiguous bytes.
+//     symmetric tile), WM/8 lanes on one column taking its WM/8 row chunks, so each output row
+//     of the mirror gets 2*WM contiguous bytes.
 // Rows are NS floats apart plus 4 more after every 8 rows: the 64 lanes of a column read (16
-// row chunks x 4 columns) then hit 64 distinct banks, and 16-byte row accesses stay aligned.
+// row chunks x 4 columns, for WM = 128) then hit 64 distinct banks, and 16-byte row accesses
+// stay aligned.
 template <class C>
 struct Epi {
     static constexpr int NS = C::BN + 4;
@@ -299,12 +300,12 @@ struct Epi {
     static constexpr int SMEM = N_BYTES > C::LDS_BYTES ? N_BYTES : C::LDS_BYTES;
     static constexpr int ROW_CHUNKS = C::WM * (C::BN / 8) / 256;   // per thread per half
     static constexpr int COL_CHUNKS = C::BN * (C::WM / 8) / 256;
-    static_assert(C::WM / 8 == 16, "each_col_chunk: 16 row chunks per column");
+    static constexpr int RC = C::WM / 8;                           // row chunks per column in a half
     __device__ static __forceinline__ int row_base(int r) { return r * NS + (r >> 3) * 4; }
 };
 
-// Chunk `it` of this thread in a half: 32 lanes of a wave share one row (row passes); 16 lanes
-// share one column and take its 16 row chunks (column passes).
+// Chunk `it` of this thread in a half: BN/8 lanes of a wave share one row (row passes); WM/8
+// lanes share one column and take its WM/8 row chunks (column passes).
 template <class C>
 __device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
     const int idx = it * 256 + threadIdx.x;
@@ -314,8 +315,8 @@ __device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
 template <class C>
 __device__ __forceinline__ void col_chunk(int it, int& c, int& r8) {
     const int idx = it * 256 + threadIdx.x;
-    c = idx >> 4;
-    r8 = (idx & 15) * 8;
+    c = idx / Epi<C>::RC;
+    r8 = (idx % Epi<C>::RC) * 8;
 }
 
 // Writes rows [half * WM, half * WM + WM) of the tile to the staging N, between two block

@@ -82,84 +82,96 @@ __global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __res
         }
 }
 
+// The beta * Csym chunks of half h of a tile, in row_chunk() order (zeros outside the matrix).
+template <class C>
+__device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS], const _Float16* csym, int64_t ld,
+                                             int n, int m0, int n0, int h) {
+#pragma unroll
+    for (int it = 0; it < Epi<C>::ROW_CHUNKS; ++it) {
+        int lr, c8;
+        row_chunk<C>(it, lr, c8);
+        const int r = m0 + h * C::WM + lr, c = n0 + c8;
+        cpre[it] = (r < n && c < ld) ? ldg<half8v>(csym + (int64_t)r * ld + c) : half8v{};
+    }
+}
+
 // out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile of a symmetric s x s
-// matrix. Only the upper block triangle is stored: consumers read a block below the diagonal as
-// the transpose of its mirror above. A diagonal tile keeps its upper triangle and mirrors it into
-// its lower one, so it is exactly symmetric and reads the same either way: the row pass writes
-// every 8-column chunk that reaches the diagonal (the elements of the diagonal chunk below the
-// diagonal taken from the staged mirror), the column pass the chunks entirely below it. Csym's
-// diagonal tile is exactly symmetric too, so its term for (r, c) can be read from row r or row c
-// alike.
+// matrix (Csym optional). Only the upper block triangle is stored: consumers read a block below
+// the diagonal as the transpose of its mirror above it, and a diagonal block either way, so a
+// diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the Gram
+// iteration): its upper triangle is computed and its lower triangle is the mirror. A diagonal
+// tile is written in three parts per half:
+//   the row pass stores the 8-column chunks right of each 8 x 8 diagonal block and writes their
+//     final fp32 values back into the staging;
+//   one thread per row assembles its row of the diagonal block: upper elements computed, lower
+//     ones computed from the mirrored accumulator with Csym's own row (Csym's diagonal tile is
+//     exactly symmetric), so they equal their mirrors bit for bit;
+//   the column pass stores the chunks left of the diagonal blocks from the staged final values.
+// crow holds half 0's row-pass Csym chunks on entry (sym_prefetch, issued by the caller ahead of
+// the main loop) and receives half 1's once half 0's row pass is done.
 template <class C>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
                                           const _Float16* csym, int64_t ld, int n, int m0, int n0, float alpha,
-                                          float beta, float gamma) {
+                                          float beta, float gamma, half8v (&crow)[Epi<C>::ROW_CHUNKS]) {
     using E = Epi<C>;
-    const float* N = reinterpret_cast<const float*>(smem);
+    float* N = reinterpret_cast<float*>(smem);
     const bool diag = m0 == n0;
-#pragma unroll 1
+#pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int rb = m0 + h * C::WM;   // first row of this half
-        // row pass: chunk (r, c) with c + 8 > r on a diagonal tile
-        auto keep_row = [&](int lr, int c8) {
-            const int r = rb + lr, c = n0 + c8;
-            return r < n && c < ld && !(diag && c + 7 < r);
-        };
-        // the beta * Csym chunks of a pass are all requested before any of them is needed (the
-        // row pass's loads overlap the LDS staging)
-        half8v cpre[E::ROW_CHUNKS];
-        static_assert(E::ROW_CHUNKS == E::COL_CHUNKS, "one prefetch buffer serves both passes");
-        if (beta != 0.f) {
-#pragma unroll
-            for (int it = 0; it < E::ROW_CHUNKS; ++it) {
-                int lr, c8;
-                row_chunk<C>(it, lr, c8);
-                cpre[it] = keep_row(lr, c8) ? ldg<half8v>(csym + (int64_t)(rb + lr) * ld + n0 + c8) : half8v{};
-            }
-        }
+        // diagonal-block pass (diagonal tiles): local row dl, columns dc .. dc+7
+        const int dl = threadIdx.x;
+        const int dr = rb + dl, dc = rb + (dl & ~7);
+        const bool dkeep = diag && dl < C::WM && dr < n && dc < ld;
+        half8v cdg{};
+        if (dkeep && csym) cdg = ldg<half8v>(csym + (int64_t)dr * ld + dc);
         stage_rows<C>(acc, smem, h);
-        each_row_chunk<C>(smem, keep_row, [&](int it, int lr, int c8, float (&v)[8]) {
-            const int r = rb + lr, c = n0 + c8;
-            if (diag && c < r) {   // the chunk holding the diagonal: elements c + e < r from the mirror (c + e, r)
-                const int lc = h * C::WM + lr;
+        each_row_chunk<C>(
+            smem,
+            [&](int lr, int c8) {
+                const int r = rb + lr, c = n0 + c8;
+                return r < n && c < ld && !(diag && c < (r & ~7) + 8);
+            },
+            [&](int it, int lr, int c8, float (&v)[8]) {
+                const int r = rb + lr, c = n0 + c8;
 #pragma unroll
-                for (int e = 0; e < 7; ++e)
-                    if (c + e < r) v[e] = N[E::row_base(c8 + e - h * C::WM) + lc];
-            }
+                for (int e = 0; e < 8; ++e) {
+                    float t = alpha * v[e];
+                    if (csym) t += beta * static_cast<float>(crow[it][e]);
+                    if (r == c + e) t += gamma;
+                    v[e] = t;
+                }
+                stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
+                if (diag) {   // the final values, for the column pass
+                    *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8) = floatx4{v[0], v[1], v[2], v[3]};
+                    *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8 + 4) = floatx4{v[4], v[5], v[6], v[7]};
+                }
+            });
+        if (h == 0 && csym) sym_prefetch<C>(crow, csym, ld, n, m0, n0, 1);
+        if (!diag) continue;
+        if (dkeep) {   // reads only diagonal blocks, which the row pass leaves as staged
+            const int ri = dl & 7, lc = h * C::WM + (dl & ~7);   // tile-local column of dc
+            float v[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                float t = alpha * v[e];
-                if (beta != 0.f) t += beta * static_cast<float>(cpre[it][e]);
-                if (r == c + e) t += gamma;
+                const float x = e >= ri ? N[E::row_base(dl) + lc + e] : N[E::row_base((dl & ~7) + e) + lc + ri];
+                float t = alpha * x;
+                if (csym) t += beta * static_cast<float>(cdg[e]);
+                if (e == ri) t += gamma;
                 v[e] = t;
             }
-            stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
-        });
-        if (!diag) continue;
-        // diagonal tile, column pass: element (c, r) of a chunk entirely below the diagonal from
-        // the staged (r, c)
-        auto keep_col = [&](int cl, int lr8) {
-            const int c = n0 + cl, r8 = rb + lr8;
-            return c < n && r8 < ld && c > r8 + 7;
-        };
-        if (beta != 0.f) {
-#pragma unroll
-            for (int it = 0; it < E::COL_CHUNKS; ++it) {
-                int cl, lr8;
-                col_chunk<C>(it, cl, lr8);
-                cpre[it] = keep_col(cl, lr8) ? ldg<half8v>(csym + (int64_t)(n0 + cl) * ld + rb + lr8) : half8v{};
-            }
+            stg<half8v>(out + (int64_t)dr * ld + dc, to_half8(v));
         }
-        each_col_chunk<C>(smem, keep_col, [&](int it, int cl, int lr8, float (&v)[8]) {
-            const int c = n0 + cl, r8 = rb + lr8;   // v[e] is (r8 + e, c), stored at (c, r8 + e)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float t = alpha * v[e];
-                if (beta != 0.f) t += beta * static_cast<float>(cpre[it][e]);
-                v[e] = t;   // never on the diagonal
-            }
-            stg<half8v>(out + (int64_t)c * ld + r8, to_half8(v));
-        });
+        lds_barrier();   // the row pass's final values are in the staging
+        each_col_chunk<C>(
+            smem,
+            [&](int cl, int lr8) {
+                const int c = n0 + cl, r8 = rb + lr8;
+                return c < n && r8 < ld && c > r8 + 7;
+            },
+            [&](int, int cl, int lr8, float (&v)[8]) {   // v[e] is (r8 + e, c), stored at (c, r8 + e)
+                stg<half8v>(out + (int64_t)(n0 + cl) * ld + rb + lr8, to_half8(v));
+            });
     }
 }
 
@@ -330,6 +342,11 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
             b_k0 = tj * KB;
         }
     }
+    // the C term of a symmetric product is requested before the main loop (it arrives with the
+    // first operand tiles and waits in registers)
+    const _Float16* csym = op.kind == kOpSym && op.csel >= 0 && op.beta != 0.f ? sym_buf(M, op.csel) : nullptr;
+    half8v c0[Epi<NsCfg>::ROW_CHUNKS];
+    if (csym) sym_prefetch<NsCfg>(c0, csym, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, 0);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
     gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero);
     if (op.kind == kOpUpdate) {
@@ -337,10 +354,10 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     } else if (op.kind == kOpGram) {
         const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
         sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, osc * osc, 0.f,
-                         0.f);
+                         0.f, c0);
     } else {
-        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), op.csel >= 0 ? sym_buf(M, op.csel) : nullptr, M.lds, M.s,
-                         ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.csel >= 0 ? op.beta : 0.f, op.gamma);
+        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), csym, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, op.alpha,
+                         op.beta, op.gamma, c0);
     }
 }
 
