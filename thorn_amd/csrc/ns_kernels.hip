@@ -185,31 +185,35 @@ struct NsOp {
     float alpha, beta, gamma;
 };
 
-// Epilogue of an update tile (see ns_phase_kernel).
+// Epilogue of an update tile (see ns_phase_kernel). Every field of the matrix table it needs is
+// read once into a register first: stores through the matrix pointers could alias the table in
+// global memory as far as the compiler knows, and it would reload fields after every store.
 __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
-    const int xsel = op.xsel, first = op.first, final_iter = op.final_iter;
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
+    const int rows = M.rows, cols = M.cols, ldx = M.ldx, flags = M.flags;
     // the stored first iterate is sigma * u up to the factor x0scale; applied per output chunk
     // (x * 1 is exact), so the accumulators stay in their registers
-    const float osc = first ? M.scal[kScalX0Scale] : 1.f;
+    const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
 
-    if (!final_iter) {
-        _Float16* dst = xsel == kXA ? M.xb : M.xa;
+    if (!op.final_iter) {
+        _Float16* const dst = op.xsel == kXA ? M.xb : M.xa;
 #pragma unroll 1
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
                 const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] *= osc;
-                if (r < M.rows && c < M.ldx) stg_nt<half8v>(dst + (int64_t)r * M.ldx + c, to_half8(v));
+                if (r < rows && c < ldx) stg_nt<half8v>(dst + (int64_t)r * ldx + c, to_half8(v));
             });
         return;
     }
 
-    if (M.flags & kFlagPNN) {
+    if (flags & kFlagPNN) {
         // u' in f16 (the reference's polar factor is f16 rounded, thorn.py:635, 662) and per-row
         // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
+        _Float16* const uout = M.uout;
+        float* const rowsq = M.rowsqpart + (int64_t)tj * rows;
 #pragma unroll 1
         for (int h = 0; h < 2; ++h)
             for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
@@ -218,57 +222,78 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
                 for (int e = 0; e < 8; ++e) v[e] *= osc;
                 const half8v hv = to_half8(v);
                 float sq = 0.f;
-                if (r < M.rows && c < M.ldx) {
-                    stg_nt<half8v>(M.uout + (int64_t)r * M.ldx + c, hv);
+                if (r < rows && c < ldx) {
+                    stg_nt<half8v>(uout + (int64_t)r * ldx + c, hv);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float f = static_cast<float>(hv[e]);
                         sq += f * f;
                     }
                 }
-                constexpr int kLanesPerRow = NsCfg::BN / 8;   // one 8-column chunk per lane
-                sq = group_sum<kLanesPerRow>(sq);
-                if ((threadIdx.x & (kLanesPerRow - 1)) == 0 && r < M.rows)
-                    stg<float>(M.rowsqpart + (int64_t)tj * M.rows + r, sq);
+                static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
+                sq = sum32_upper(sq);
+                if ((threadIdx.x & 31) == 31 && r < rows) stg<float>(rowsq + r, sq);
             });
         return;
     }
 
     // Direct apply: p <- p - eta * (u + wd * p * [u * p >= 0]) (thorn.py:679-680, 702).
-    const bool md = (M.flags & (kFlagMD | kFlagMDScalar)) != 0;
-    const bool apply = (M.flags & kFlagApply) != 0;
-    const bool vec = (M.flags & kFlagVec4) != 0;
+    const bool md = (flags & (kFlagMD | kFlagMDScalar)) != 0;
+    const bool apply = (flags & kFlagApply) != 0;
+    const bool vec = (flags & kFlagVec4) != 0;
+    const float eta = M.eta, wd = M.wd;
+    float* const p = M.p;
     float psq = 0.f;
-#pragma unroll 1
+    // p chunks (vector path) are requested ahead of their use: those of half 0 before it is
+    // staged, each chunk of half 1 as soon as the same slot of half 0 has been used (p is read and
+    // written through one pointer, so the compiler would otherwise keep every load behind the
+    // previous chunk's stores).
+    using E = Epi<NsCfg>;
+    float4 pre[E::ROW_CHUNKS][2];
+    auto fetch = [&](int h, int it) {
+        int lr, c8;
+        row_chunk<NsCfg>(it, lr, c8);
+        const int r = m0 + h * NsCfg::WM + lr, c = n0 + c8;
+        if (vec && r < rows && c + 8 <= cols) {
+            const float* pp = p + (int64_t)r * cols + c;
+            pre[it][0] = ldg<float4>(pp);
+            pre[it][1] = ldg<float4>(pp + 4);
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < E::ROW_CHUNKS; ++it) fetch(0, it);
+#pragma unroll
     for (int h = 0; h < 2; ++h)
-        for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
+        for_rows<NsCfg>(acc, smem, h, [&](int it, int half, int lr, int c8, float (&v)[8]) {
             const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
-            if (r >= M.rows || c >= M.cols) return;
+            if (r < rows && c < cols) {
+                float* pp = p + (int64_t)r * cols + c;
+                if (vec && c + 8 <= cols) {
+                    const float4 p0 = pre[it][0], p1 = pre[it][1];
+                    float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] *= osc;
-            float* pp = M.p + (int64_t)r * M.cols + c;
-            if (vec && c + 8 <= M.cols) {
-                float4 p0 = ldg<float4>(pp), p1 = ldg<float4>(pp + 4);
-                float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if (apply) pv[e] = cautious_step(pv[e], (float)(_Float16)v[e], M.eta, M.wd);
-                    psq += pv[e] * pv[e];
-                }
-                if (apply) {
-                    stg_nt<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
-                    stg_nt<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
-                }
-            } else {
-                for (int e = 0; e < 8 && c + e < M.cols; ++e) {
-                    float p = ldg<float>(pp + e);
-                    if (apply) {
-                        p = cautious_step(p, (float)(_Float16)v[e], M.eta, M.wd);
-                        stg_nt<float>(pp + e, p);
+                    for (int e = 0; e < 8; ++e) {
+                        const float q = cautious_step(pv[e], (float)(_Float16)(v[e] * osc), eta, wd);
+                        pv[e] = apply ? q : pv[e];
+                        psq += pv[e] * pv[e];
                     }
-                    psq += p * p;
+                    if (apply) {   // each of the two stores covers every other 16 bytes: plain
+                                   // stores, which L2 merges into whole lines
+                        stg<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
+                        stg<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
+                    }
+                } else {
+                    for (int e = 0; e < 8 && c + e < cols; ++e) {
+                        float x = ldg<float>(pp + e);
+                        if (apply) {
+                            x = cautious_step(x, (float)(_Float16)(v[e] * osc), eta, wd);
+                            stg<float>(pp + e, x);
+                        }
+                        psq += x * x;
+                    }
                 }
             }
+            if (half == 0) fetch(1, it);
         });
     if (md) {
         const float t = block_sum(psq, scratch);

@@ -78,19 +78,34 @@ __device__ __forceinline__ float sigmoid_f(float x) {
     return 1.f / (1.f + expf(-x));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// v from the lane selected by the DPP control CTRL; lanes of the 16-lane rows outside ROW_MASK
+// (and lanes without a source) get 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF,
+                                                                 false));
+}
+
+// Sum over each aligned group of 32 lanes with DPP moves (register to register, no LDS round
+// trip): pairs and quads by quad permutes, 8 and 16 lanes by the half-row and row mirrors, then
+// row_bcast15 adds row 0's sum into row 1 (and row 2's into row 3). The group sum is exact in
+// lanes 16..31 and 48..63 (the upper row of each group); other lanes hold partial sums. All
+// lanes must be active.
+__device__ __forceinline__ float sum32_upper(float v) {
+    v += dpp_mov<0xB1>(v);          // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);          // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);         // row_half_mirror
+    v += dpp_mov<0x140>(v);         // row_mirror
+    v += dpp_mov<0x142, 0xA>(v);    // row_bcast15 into rows 1 and 3 (rows 0 and 2 add 0)
     return v;
 }
 
-// Sum over each aligned group of G lanes (G a power of two <= 64), reduced separately.
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "lane group");
-#pragma unroll
-    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+// Sum over the wave (all 64 lanes active), returned to every lane: the two 32-lane sums joined
+// by row_bcast31 into rows 2 and 3, then read from lane 63.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum32_upper(v);
+    v += dpp_mov<0x143, 0xC>(v);    // row_bcast31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Deterministic block reduction over blockDim.x threads (a multiple of 64, at most 1024).
