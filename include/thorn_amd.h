@@ -101,7 +101,11 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
  * restart_mask, the restart positions of _gram_ns_restarts (thorn.py:483-514); the others run the
  * plain quintic (thorn.py:655-658), which is Gram Newton-Schulz restarted before every iteration.
  * The reference takes the Gram form for every non-square matrix; in exact arithmetic both are the
- * same map, and below 2:1 the plain one is the more accurate in f16. */
+ * same map, and below 2:1 the plain one is the more accurate in f16.
+ * A matrix without THORN_STEP_APPLY updates its momentum (and, with decouple_md, goes through the
+ * gain round trip p / G * G) but not its parameter, as the reference does for a step that is not
+ * due under update_rate (thorn.py:1395, 1403-1421). iters = 0 runs only that part, for a table in
+ * which no matrix has THORN_STEP_APPLY (coeffs may then be null). */
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
                      uint32_t restart_mask, void* stream);
 

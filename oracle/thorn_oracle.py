@@ -19,7 +19,10 @@ How the pieces are pinned (tests/test_oracle.py):
   * coefficients, restarts, single-function outputs and multi-step trajectories: golden vectors
     written from the reference itself (tests/golden/make_golden.py);
   * Newton-Schulz: the f64 closed form U*phi(S)*V^T from an SVD;
-  * Adam: torch.optim.Adam / RAdam special cases; per-row normalization: its invariants.
+  * Adam: torch.optim.Adam / RAdam special cases; per-row normalization: its invariants;
+  * update_rate and gradient release: properties (the momentum and the Adam moments follow their
+    recurrences every step, parameters move only on due steps, a due step is an ordinary step,
+    a decouple_md parameter goes through p / G * G otherwise, hooks drop the gradients).
 Parity unpinned: ``w1rand`` and ``momentum_aligned_mask`` (Magma), which no golden or closed form
 covers; the product rejects ``momentum_align=True``, so neither is used as a checker.
 """
@@ -607,6 +610,28 @@ class OracleTHORN(Optimizer):
         else:
             self._step_params([param], Group.from_dict(self._param_to_group[id(param)]))
         return loss
+
+
+    # thorn.py:1755-1776
+    def setup_gradient_release(self, model: nn.Module, update_rate: int = 1, ignore_existing_hooks: bool = False):
+        """Every parameter steps from its post-accumulate-grad hook (step(param=p), then its grad is
+        dropped); update_rate > 1 makes only every update_rate-th step of a parameter update it."""
+        def hook(param, optimizer):
+            optimizer.step(param=param)
+            param.grad = None
+
+        hooks = []
+        for prm in model.parameters():
+            if not prm.requires_grad:
+                continue
+            if prm._post_accumulate_grad_hooks and not ignore_existing_hooks:
+                for h in hooks:
+                    h.remove()
+                raise ValueError('Model already has post_accumulate_grad_hooks. If this is expected, '
+                                 'pass `ignore_existing_hooks=True`.')
+            hooks.append(prm.register_post_accumulate_grad_hook(lambda t, o=self: hook(t, o)))
+        model._gradient_release_hooks = hooks
+        self._update_rate = update_rate
 
 
 def auto_assign(module: nn.Module, **keys) -> list[dict]:

@@ -79,10 +79,12 @@ def test_fill_table_validates_pointers_without_gpu():
 
 def test_step_rejects_bad_iteration_counts():
     plan = _lib.OrthoPlan([8], [8], [0])
-    with pytest.raises(_lib.ThornError, match='1 <= iters <= 32'):
-        plan.step(64, np.zeros((0, 3), dtype=np.float32), 0, 0)
-    with pytest.raises(_lib.ThornError, match='1 <= iters <= 32'):
+    with pytest.raises(_lib.ThornError, match='0 <= iters <= 32'):
         plan.step(64, np.zeros((33, 3), dtype=np.float32), 0, 0)
+    # iters = 0 is a momentum-only step: refused while matrices are flagged THORN_STEP_APPLY (a
+    # plan with no filled table counts as such)
+    with pytest.raises(_lib.ThornError, match='momentum only'):
+        plan.step(64, np.zeros((0, 3), dtype=np.float32), 0, 0)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -344,3 +344,99 @@ def test_full_size_against_exact(shape):
         _log(f'[gpu]   step {step}: dp vs exact {r:.3e}, moment {r_state:.1e}')
         assert r_state <= 1e-6
         assert r <= 2e-2
+
+
+@pytest.mark.parametrize('name,rate', [('mixed_small', 2), ('mixed_small', 3), ('md_small', 2)])
+def test_update_rate(name, rate):
+    """update_rate > 1 (thorn.py:1395, 1706-1707), teacher-forced against the oracle: the momentum,
+    Adam moments and gains agree every step (<= 1e-5); on a due step the update agrees as in any
+    step; on the others a parameter is untouched (bit for bit), or, with decouple_md, goes through
+    the gain round trip (equal to the oracle's to 1e-6)."""
+    _log(f'[gpu] update_rate {rate} {name}')
+    thorn_amd = _thorn()
+    params, groups, grads = getattr(workloads, name)()
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    cpu = O.OracleTHORN(groups)
+    gpu = thorn_amd.THORN(_clone_groups(groups, gparams))
+    cpu._update_rate = gpu._update_rate = rate
+    group_of = {id(p): g for g in groups for p in g['params']}
+    worst = {'state': 0.0, 'dp': 0.0, 'dp_adam': 0.0, 'md_roundtrip': 0.0}
+    for s in range(1, 8):
+        if s > 1:
+            _copy_state_to(gpu, gparams, cpu, params)
+        due = (s + 1) % rate == 0
+        before_c = [p.detach().clone() for p in params]
+        before_g = [p.detach().clone() for p in gparams]
+        m_prev = [cpu.state[p]['moment'].clone() if 'moment' in cpu.state[p] else torch.zeros_like(p)
+                  for p in params]
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            g = grads(s, i, pc)
+            pc.grad = g.clone()
+            pg.grad = g.clone().to(DEV)
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            grp = group_of[id(pc)]
+            for k, v in cpu.state[pc].items():
+                if torch.is_tensor(v) and k != 'target_norm':
+                    worst['state'] = max(worst['state'], rel(gpu.state[pg][k], v))
+                elif not torch.is_tensor(v):
+                    assert gpu.state[pg][k] == v, (k, gpu.state[pg][k], v)
+            dpc = pc.detach() - before_c[i]
+            dpg = pg.detach().cpu() - before_g[i].cpu()
+            if not due:
+                if grp.get('decouple_md'):
+                    worst['md_roundtrip'] = max(worst['md_roundtrip'], rel(pg.detach(), pc.detach()))
+                else:
+                    assert torch.equal(pg.detach().cpu(), before_g[i].cpu()), (s, i, 'moved on a step not due')
+                    assert torch.equal(pc.detach(), before_c[i]), (s, i)
+                continue
+            r = rel(dpg, dpc)
+            if not grp['orthogonalize']:
+                worst['dp_adam'] = max(worst['dp_adam'], r)
+            elif grp.get('decouple_md'):
+                worst['dp'] = max(worst['dp'], r)
+                assert r <= 2e-2, (s, i, r)
+            else:
+                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp)
+                check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
+    _log(f'[gpu]   {worst}')
+    assert worst['state'] <= 1e-5, worst
+    assert worst['dp_adam'] <= 1e-4, worst
+    assert worst['md_roundtrip'] <= 1e-6, worst
+
+
+@pytest.mark.parametrize('rate', [1, 2])
+def test_gradient_release(rate):
+    """setup_gradient_release (thorn.py:1755-1776): every parameter steps from its own hook during
+    backward (step(param=p), one single-matrix step each). A small model trained for four
+    iterations from identical weights and inputs on the GPU and in the oracle (free running: the
+    gradients of later iterations come from each side's own weights); parameters and moments agree
+    to 2e-2, and with rate 2 nothing moves on the second and fourth backward."""
+    _log(f'[gpu] gradient release, update_rate {rate}')
+    thorn_amd = _thorn()
+    torch.manual_seed(5)
+    model_c = torch.nn.Sequential(torch.nn.Linear(24, 48), torch.nn.Tanh(), torch.nn.Linear(48, 40),
+                                  torch.nn.Tanh(), torch.nn.Linear(40, 16))
+    model_g = copy.deepcopy(model_c).to(DEV)
+    conf = dict(lr=2e-3, weight_decay=0.1, betas=(0.9, 0.95))
+    cpu = O.OracleTHORN(model_c, **conf)
+    gpu = thorn_amd.THORN(model_g, **conf)
+    cpu.setup_gradient_release(model_c, update_rate=rate)
+    gpu.setup_gradient_release(model_g, update_rate=rate)
+    x = torch.randn(32, 24, generator=torch.Generator().manual_seed(9))
+    for it in range(4):
+        before_g = [p.detach().clone() for p in model_g.parameters()]
+        model_c(x).square().mean().backward()
+        model_g(x.to(DEV)).square().mean().backward()
+        torch.cuda.synchronize()
+        for (pc, pg, bg) in zip(model_c.parameters(), model_g.parameters(), before_g):
+            assert pg.grad is None and pc.grad is None
+            r = rel(pg.detach(), pc.detach())
+            rm = rel(gpu.state[pg]['moment'], cpu.state[pc]['moment'])
+            assert r <= 2e-2 and rm <= 2e-2, (it, tuple(pc.shape), r, rm)
+            assert gpu.state[pg]['step'] == cpu.state[pc]['step'] == it + 2
+            if rate == 2 and it % 2 == 1:
+                assert torch.equal(pg.detach(), bg), (it, 'moved on a step not due')
+    _log('[gpu]   ok')

@@ -184,3 +184,99 @@ def test_trajectories_match_reference(name, build, steps):
     assert set(keys) == set(got), sorted(set(keys) ^ set(got))
     for k in keys:
         np.testing.assert_array_equal(got[k], z[k], err_msg=k)
+
+
+def _clone_opt(opt, params_src, params_dst, update_rate):
+    """A fresh oracle over params_dst (same groups) carrying opt's state, with update_rate."""
+    groups = []
+    index = {id(p): i for i, p in enumerate(params_src)}
+    for g in opt.param_groups:
+        d = {k: v for k, v in g.items() if k != 'params'}
+        d['params'] = [params_dst[index[id(p)]] for p in g['params']]
+        groups.append(d)
+    new = O.OracleTHORN(groups)
+    new._update_rate = update_rate
+    for ps, pd in zip(params_src, params_dst):
+        new.state[pd] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in opt.state[ps].items()}
+    return new
+
+
+@pytest.mark.parametrize('build,rate', [(workloads.mixed_small, 2), (workloads.mixed_small, 3),
+                                        (workloads.md_small, 2)])
+def test_update_rate_properties(build, rate):
+    """update_rate > 1 (thorn.py:1395, 1483-1486, 1706-1707): the momentum and the Adam moments take
+    every gradient; a parameter moves only when its step is due, (step + 1) % rate == 0, and a due
+    step is exactly an ordinary step from the same state; on other steps a parameter stays put,
+    except that a decouple_md one goes through p / G * softplus(rg) * softplus(cg) with unchanged
+    gains."""
+    params, groups, grads = build()
+    opt = O.OracleTHORN(groups)
+    opt._update_rate = rate
+    md = {id(p) for g in groups if g.get('decouple_md') for p in g['params']}
+    adam = {id(p) for g in groups if not g['orthogonalize'] for p in g['params']}
+    beta1 = {id(p): g.get('betas', (0.9, 0.95))[0] for g in groups for p in g['params']}
+    for s in range(1, 7):
+        due = (s + 1) % rate == 0
+        before = [p.detach().clone() for p in params]
+        st_before = [{k: (v.clone() if torch.is_tensor(v) else v) for k, v in opt.state[p].items()}
+                     for p in params]
+        shadow_params = [torch.nn.Parameter(p.detach().clone()) for p in params]
+        shadow = _clone_opt(opt, params, shadow_params, 1) if s > 1 else None
+        for i, p in enumerate(params):
+            p.grad = grads(s, i, p).clone()
+            shadow_params[i].grad = grads(s, i, p).clone()
+        opt.step()
+        if shadow is not None:
+            shadow.step()
+        for i, p in enumerate(params):
+            st = opt.state[p]
+            g = grads(s, i, p)
+            if id(p) not in md and s > 1:
+                m_prev = st_before[i]['moment']
+                if id(p) in adam:   # m <- lerp(m, g, 1 - beta1) (thorn.py:876)
+                    torch.testing.assert_close(st['moment'], m_prev.lerp(g, 1 - beta1[id(p)]), rtol=0, atol=0)
+                else:               # m <- beta1 m + g (thorn.py:1376-1381)
+                    torch.testing.assert_close(st['moment'], m_prev * beta1[id(p)] + g, rtol=0, atol=0)
+            if due:
+                if shadow is not None:   # the same as an ordinary step from the same state
+                    assert torch.equal(p.detach(), shadow_params[i].detach()), (s, i)
+                    if id(p) not in md and id(p) not in adam:   # (rectified Adam may not move yet)
+                        assert not torch.equal(p.detach(), before[i]), (s, i)
+            elif id(p) in md and s > 1:
+                sb = st_before[i]
+                if 'row_gain' in sb:
+                    G = torch.nn.functional.softplus(sb['row_gain']) * torch.nn.functional.softplus(sb['col_gain'])
+                    want = (before[i] / G) * torch.nn.functional.softplus(sb['row_gain'])
+                    want = want * torch.nn.functional.softplus(sb['col_gain'])
+                else:
+                    G = torch.nn.functional.softplus(sb['gain'])
+                    want = (before[i] / G) * G
+                assert torch.equal(p.detach(), want), (s, i)
+                for k in ('row_gain', 'col_gain', 'gain'):
+                    if k in sb:
+                        assert torch.equal(st[k], sb[k]), (s, i, k)
+            elif id(p) not in md:
+                assert torch.equal(p.detach(), before[i]), (s, i)
+            assert st['step'] == s + 1
+
+
+def test_gradient_release_hooks():
+    """setup_gradient_release (thorn.py:1755-1776): each backward steps every parameter from its
+    hook and drops its gradient; with update_rate = 2 the parameters move on the first backward
+    (step 1 is due) and stay put on the second; a second registration without
+    ignore_existing_hooks raises."""
+    torch.manual_seed(3)
+    model = torch.nn.Sequential(torch.nn.Linear(12, 20), torch.nn.Tanh(), torch.nn.Linear(20, 6))
+    opt = O.OracleTHORN(model, lr=1e-2, weight_decay=0.1)
+    opt.setup_gradient_release(model, update_rate=2)
+    x = torch.randn(8, 12)
+    for it in range(3):
+        before = [p.detach().clone() for p in model.parameters()]
+        model(x).square().sum().backward()
+        after = list(model.parameters())
+        assert all(p.grad is None for p in after)
+        moved = [not torch.equal(a.detach(), b) for a, b in zip(after, before)]
+        assert all(moved) if it % 2 == 0 else not any(moved), (it, moved)
+        assert all(opt.state[p]['step'] == it + 2 for p in after)
+    with pytest.raises(ValueError, match='post_accumulate_grad_hooks'):
+        O.OracleTHORN(model, lr=1e-2).setup_gradient_release(model)

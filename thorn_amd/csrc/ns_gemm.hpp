@@ -132,17 +132,6 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Scheduling hint for one k16 sub-step: NM MFMAs spread evenly between NR LDS fragment reads.
-template <int NM, int NR, int Q = 0>
-__device__ __forceinline__ void interleave_mfma_ds() {
-    if constexpr (Q < NR) {
-        constexpr int m = (Q + 1) * NM / NR - Q * NM / NR;
-        if constexpr (m > 0) __builtin_amdgcn_sched_group_barrier(0x008, m, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        interleave_mfma_ds<NM, NR, Q + 1>();
-    }
-}
-
 // The A and B operand sources of one tile: each is read MN-major for K tiles t < k0 and K-major
 // from there on (k0 = 0: always K-major; k0 >= the tile count: always MN-major). A symmetric
 // matrix stored as its upper block triangle is read MN-major, from the transposed mirror block,
@@ -178,26 +167,28 @@ struct DmaPair {
     }
 };
 
-// Reads this wave's MFMA fragments of k16 step `ks` of the stage at `st` (A at st, B at
-// st + A_BYTES) in the layouts AK / BK (true = K-major).
+// Reads fragment q of this wave's k16 step `ks` from the stage at `st` (A at st, B at
+// st + A_BYTES) in the layouts AK / BK (true = K-major), numbered in the order the MFMAs of a
+// sub-step use them: A0, B0 .. B(TN-1), A1 .. A(TM-1).
 template <class C, bool AK, bool BK>
-__device__ __forceinline__ void read_frags(const char* st, int ks, int wm, int wn, int lane, half8 (&ra)[C::TM],
-                                           half8 (&rb)[C::TN]) {
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) ra[i] = frag<C::BM, AK>(st, wm + 32 * i, ks, lane);
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) rb[j] = frag<C::BN, BK>(st + C::A_BYTES, wn + 32 * j, ks, lane);
+__device__ __forceinline__ void read_frag(const char* st, int ks, int q, int wm, int wn, int lane, half8 (&ra)[C::TM],
+                                          half8 (&rb)[C::TN]) {
+    if (q == 0) ra[0] = frag<C::BM, AK>(st, wm, ks, lane);
+    else if (q <= C::TN) rb[q - 1] = frag<C::BN, BK>(st + C::A_BYTES, wn + 32 * (q - 1), ks, lane);
+    else ra[q - C::TN] = frag<C::BM, AK>(st, wm + 32 * (q - C::TN), ks, lane);
 }
 
 // The K tiles [lo, hi) of gemm_tile in one operand layout (AK / BK). On entry the stages hold
 // tiles lo .. lo+S-2 (tile lo visible to every wave); on exit they hold hi .. hi+S-2 likewise.
-// Each iteration is one basic block: two k16 sub-steps of 16 MFMAs, with the second sub-step's
-// fragment reads interleaved into the first, and the direct loads of tile kt+S-1 and the next
-// tile's first fragment reads interleaved into the second. Between the two, every wave waits for
-// its own loads of tile kt+1 and meets the others at the block barrier: after it, tile kt+1 is
-// visible and nobody reads stage (kt-1) % S any more, which then receives tile kt+S-1. Tiles
-// past the end of K are loaded (zeros or in-bounds data) and read but never used, which keeps
-// the loop body free of branches.
+// Each iteration is one basic block of two k16 sub-steps of TM * TN MFMAs, the order of every
+// instruction fixed explicitly: after MFMA q of the first sub-step, fragment q of the second;
+// after MFMA q of the second, fragment q of the next tile's first sub-step and then direct load
+// q of tile kt+S-1 (fragments in the order the MFMAs use them, so each is read as early as
+// possible before its use). Between the two sub-steps every wave waits for its own loads of tile
+// kt+1 and meets the others at the block barrier: after it, tile kt+1 is visible and nobody
+// reads stage (kt-1) % S any more, which then receives tile kt+S-1. Tiles past the end of K are
+// loaded (zeros or in-bounds data) and read but never used, which keeps the loop body free of
+// branches.
 template <class C, bool AK, bool BK>
 __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM>& da, const DmaPair<C::BN>& db,
                                              floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
@@ -206,39 +197,40 @@ __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-    constexpr int NM = C::TM * C::TN;                                      // MFMAs per sub-step
-    constexpr int NREAD = C::TM * (AK ? 1 : 2) + C::TN * (BK ? 1 : 2);   // LDS reads per sub-step
+    constexpr int NM = C::TM * C::TN;   // MFMAs per sub-step
+    constexpr int NF = C::TM + C::TN;   // fragments per sub-step
     constexpr int NA = DmaPair<C::BM>::PER_WAVE, NB = DmaPair<C::BN>::PER_WAVE;
-    static_assert(NA + NB <= NM, "one direct load per MFMA at most");
-    read_frags<C, AK, BK>(smem + (lo % C::S) * C::STAGE_BYTES, 0, wm, wn, lane, fa[0], fb[0]);
+    static_assert(NF <= NM && NA + NB <= NM, "one fragment and one direct load per MFMA at most");
+    {
+        const char* s0 = smem + (lo % C::S) * C::STAGE_BYTES;
+#pragma unroll
+        for (int q = 0; q < NF; ++q) read_frag<C, AK, BK>(s0, 0, q, wm, wn, lane, fa[0], fb[0]);
+    }
     for (int kt = lo; kt < hi; ++kt) {
         const char* sa = smem + (kt % C::S) * C::STAGE_BYTES;
-        read_frags<C, AK, BK>(sa, 1, wm, wn, lane, fa[1], fb[1]);
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
-        interleave_mfma_ds<NM, NREAD>();
-        __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < NM; ++q) {
+            const int i = q / C::TN, j = q % C::TN;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q < NF) read_frag<C, AK, BK>(sa, 1, q, wm, wn, lane, fa[1], fb[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         lds_wait_barrier<(C::S - 3) * C::LOADS_PER_STAGE>();
         __builtin_amdgcn_sched_barrier(0);
         const int tn = kt + C::S - 1;
         const uint32_t st_new = lds0 + (tn % C::S) * C::STAGE_BYTES;
+        const char* na = smem + ((kt + 1) % C::S) * C::STAGE_BYTES;
 #pragma unroll
         for (int q = 0; q < NM; ++q) {
             const int i = q / C::TN, j = q % C::TN;
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
-            if (q < NA + NB) {
-                __builtin_amdgcn_sched_barrier(0);
-                if (q < NA) da.issue_one(tn, q, st_new + wave * NA * 1024, zero);
-                else db.issue_one(tn, q - NA, st_new + C::A_BYTES + wave * NB * 1024, zero);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (q < NF) read_frag<C, AK, BK>(na, 0, q, wm, wn, lane, fa[0], fb[0]);
+            if (q < NA) da.issue_one(tn, q, st_new + wave * NA * 1024, zero);
+            else if (q < NA + NB) db.issue_one(tn, q - NA, st_new + C::A_BYTES + wave * NB * 1024, zero);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        read_frags<C, AK, BK>(smem + ((kt + 1) % C::S) * C::STAGE_BYTES, 0, wm, wn, lane, fa[0], fb[0]);
-        interleave_mfma_ds<NM - NA - NB, NREAD>();
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

@@ -126,6 +126,7 @@ struct thorn_ortho_plan {
     const void* filled_ws = nullptr;   // workspace of the last fill_table
     const void* stepped_ws = nullptr;  // workspace of the last completed thorn_ortho_step
     bool any_exact = true;             // the last filled table has matrices on the exact path
+    bool any_apply = true;             // the last filled table has matrices flagged THORN_STEP_APPLY
 };
 
 struct thorn_adam_plan {
@@ -417,7 +418,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     std::memset(host, 0, plan->table_bytes);
     char* ws = static_cast<char*>(workspace);
     auto at = [ws](size_t o) -> void* { return o == kNone ? nullptr : ws + o; };
-    bool any_exact = false;
+    bool any_exact = false, any_apply = false;
     auto* mats = reinterpret_cast<thorn::OrthoMat*>(host + plan->mats_off);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
@@ -462,6 +463,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         if (workspace == plan->stepped_ws && !md && !mds) flags |= thorn::kFlagPrescaled;
         else any_exact = true;
         M.flags = flags;
+        any_apply = any_apply || (flags & thorn::kFlagApply);
         M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
         M.gain_lr = S.gain_lr; M.gain_beta2 = S.gain_beta2; M.gain_w1 = S.gain_w1; M.gain_w2 = S.gain_w2;
         M.gain_eps = S.gain_eps; M.gain_bc1 = S.gain_bc1; M.gain_bc2 = S.gain_bc2;
@@ -486,14 +488,18 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
     plan->any_exact = any_exact;
+    plan->any_apply = any_apply;
     return THORN_OK;
 }
 
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
                      uint32_t restart_mask, void* stream) {
     if (!plan || !table_dev) return fail(THORN_ERR_INVALID, "thorn_ortho_step: null argument");
-    if (iters < 1 || iters > 32 || !coeffs)
-        return fail(THORN_ERR_INVALID, "thorn_ortho_step: need 1 <= iters <= 32 and coefficients");
+    if (iters < 0 || iters > 32 || (iters > 0 && !coeffs))
+        return fail(THORN_ERR_INVALID, "thorn_ortho_step: need 0 <= iters <= 32 and coefficients");
+    if (iters == 0 && plan->any_apply)
+        return fail(THORN_ERR_INVALID,
+                    "thorn_ortho_step: iters = 0 (momentum only) with matrices flagged THORN_STEP_APPLY");
     const int n = static_cast<int>(plan->mats.size());
     if (n == 0) return THORN_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -510,6 +516,15 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
+    if (iters == 0) {   // momentum only (no update is due): the decouple_md round trip and done
+        if (plan->md.n > 0) {   // p *= softplus(gains), the gains unchanged
+            const thorn::TaskList md = task_list(dev, plan->md);
+            THORN_LAUNCH(THORN_KIND_MD_RESCALE, "ortho_md_rescale_kernel", thorn::ortho_md_rescale_kernel,
+                         dim3(md.total), dim3(256), 0, st, mats, md);
+        }
+        plan->stepped_ws = plan->filled_ws;
+        return THORN_OK;
+    }
     if (plan->any_exact) {
         THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total),
                      dim3(256), 0, st, mats, task_list(dev, plan->pre));

@@ -270,6 +270,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
     const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
     const float gamma = M.scal[kScalGamma];
     const bool md = M.flags & (kFlagMD | kFlagMDScalar);
     const bool vec = M.flags & kFlagVec4;

@@ -9,7 +9,7 @@ on the current stream (see ``thorn_amd.csrc``), driven through the C ABI in incl
 Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
 behaviour): Magma ``momentum_align`` (thorn.py:800-836), sparse gradients (thorn.py:1667-1700),
 DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), ``decouple_md`` on non-orthogonalized
-groups, non-fp32 parameters, and gradient release with ``update_rate > 1``.
+groups and non-fp32 parameters.
 """
 from __future__ import annotations
 
@@ -247,8 +247,11 @@ class _OrthoRunner:
         steps['eta'] = (group.lr * self.scale)[own]
         steps['weight_decay'] = group.weight_decay
         steps['beta1'] = group.betas[0]
-        flags = _lib.STEP_APPLY | (0 if group.none_grad else _lib.STEP_KEEP_GRAD)
-        steps['step_flags'] = flags
+        # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
+        # momentum (and the decouple_md round trip) runs every step
+        due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 for s in states], dtype=bool)[own]
+        keep = 0 if group.none_grad else _lib.STEP_KEEP_GRAD
+        steps['step_flags'] = np.where(due, _lib.STEP_APPLY | keep, keep)
         if self.md:
             gb1, gb2 = group.gain_betas
             steps['gain_lr'] = group.gain_lr_
@@ -287,6 +290,8 @@ class _OrthoRunner:
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
+        if not due.any():   # no polar factor this step: momentum (and gains round trip) only
+            coeffs = coeffs[:0]
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
                        torch.cuda.current_stream(self.device).cuda_stream)
 
@@ -308,8 +313,9 @@ class _AdamRunner:
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
 
-    def run(self, entries: list) -> None:
-        """entries: (p, state, group) per tensor, in plan order."""
+    def run(self, entries: list, update_rate: int = 1) -> None:
+        """entries: (p, state, group) per tensor, in plan order. A tensor's parameter is written
+        only when its step is due under update_rate (thorn.py:1706-1707); m and v always are."""
         s = self.steps
         for k, (p, state, group) in enumerate(entries):
             step = state['step']
@@ -327,7 +333,7 @@ class _AdamRunner:
             s[k]['bc1'] = 1 / (1 - beta1 ** step)
             s[k]['bc2'] = 1 / (1 - beta2 ** step)
             s[k]['eps'] = group.eps
-            s[k]['apply'] = 1
+            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 else 0
             s[k]['degenerate'] = 1 if rect == 0.0 else 0
         host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
         self.plan.fill_table(s, self.table.data_ptr(), host.data_ptr())
@@ -438,9 +444,6 @@ class THORN(Optimizer):
         if not group.orthogonalize and group.decouple_md:
             raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
                                       'on the MI355X path')
-        if self._update_rate != 1:
-            raise NotImplementedError('gradient release with update_rate > 1 is not implemented '
-                                      'on the MI355X path')
 
     def _runner(self, key, factory):
         r = self._runners.get(key)
@@ -474,7 +477,7 @@ class THORN(Optimizer):
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
                     runner = self._runner(key, lambda: _AdamRunner(ps, dev))
-                    runner.run([(p, self.state[p], group) for p in ps])
+                    runner.run([(p, self.state[p], group) for p in ps], self._update_rate)
         for p in live:
             if group.none_grad:
                 p.grad = None
