@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 2
+#define THORN_ABI_VERSION 3
 
 enum {
     THORN_OK = 0,
@@ -47,7 +47,8 @@ enum {
 int thorn_abi_version(void);
 const char* thorn_last_error(void);
 /* sizeof of the ABI structs, so bindings can verify their layout:
- * 0 = ThornOrthoMatDesc, 1 = ThornOrthoMatStep, 2 = ThornAdamTensorStep; 0 for anything else. */
+ * 0 = ThornOrthoMatDesc, 1 = ThornOrthoMatStep, 2 = ThornAdamTensorStep, 3 = ThornAdamSparseStep;
+ * 0 for anything else. */
 size_t thorn_abi_struct_size(int which);
 
 /* ------------------------------------------------------------------------------------------
@@ -138,6 +139,24 @@ size_t thorn_adam_table_bytes(thorn_adam_plan_t plan);
 int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* table_dev,
                           void* table_host);
 int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream);
+
+/* One tensor with a row-sparse gradient (e.g. nn.Embedding(sparse=True)): the sparse branch of
+ * _step_params (thorn.py:1667-1700). The gradient comes coalesced, its row indices distinct (as
+ * torch's coalesce() leaves them); row g_rows[k] of p, m and v takes gradient row g_values[k]
+ * with the arithmetic of thorn_adam_step, and every other row keeps its parameter and state.
+ * Row indices outside [0, rows) are skipped. nnz = 0 launches nothing. */
+typedef struct ThornAdamSparseStep {
+    float* p;             /* rows x row_len, contiguous */
+    float* m;             /* state['moment'], like p */
+    float* v;             /* state['variance'], like p */
+    const float* g_values;  /* nnz x row_len, contiguous */
+    const int64_t* g_rows;  /* nnz row indices */
+    int64_t rows, row_len, nnz;
+    float lr, weight_decay, beta2, w1, w2, bc1, bc2, eps;   /* as in ThornAdamTensorStep */
+    int32_t apply;
+    int32_t degenerate;
+} ThornAdamSparseStep;
+int thorn_adam_sparse_step(const ThornAdamSparseStep* step, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Optional launch timing (measurement only; no counterpart in the reference). While enabled, the

@@ -11,8 +11,8 @@ order is kept, because it fixes the fp32 rounding of the state, and Newton-Schul
 with Gram Newton-Schulz for non-square matrices, exactly as thorn.py:626-662 does.
 
 Left out, because they are outside the single-GPU hot path: the FSDP2/DTensor engine
-(thorn.py:979-1186, 1333-1374, 1459-1581), sparse embedding gradients (thorn.py:1667-1700), the
-Triton kernels (thorn.py:53-280) and the compile wrapper (thorn.py:379-423). Magma
+(thorn.py:979-1186, 1333-1374, 1459-1581), the Triton kernels (thorn.py:53-280) and the compile
+wrapper (thorn.py:379-423). Magma
 ``momentum_align`` (thorn.py:800-836) is restated because it is tiny, but the product rejects it.
 
 How the pieces are pinned (tests/test_oracle.py):
@@ -22,7 +22,9 @@ How the pieces are pinned (tests/test_oracle.py):
   * Adam: torch.optim.Adam / RAdam special cases; per-row normalization: its invariants;
   * update_rate and gradient release: properties (the momentum and the Adam moments follow their
     recurrences every step, parameters move only on due steps, a due step is an ordinary step,
-    a decouple_md parameter goes through p / G * G otherwise, hooks drop the gradients).
+    a decouple_md parameter goes through p / G * G otherwise, hooks drop the gradients);
+  * sparse (row) gradients: torch.optim.SparseAdam (eps > 0, no weight decay), untouched rows
+    left alone, duplicate indices summed, an empty gradient taking no step.
 Parity unpinned: ``w1rand`` and ``momentum_aligned_mask`` (Magma), which no golden or closed form
 covers; the product rejects ``momentum_align=True``, so neither is used as a checker.
 """
@@ -574,8 +576,31 @@ class OracleTHORN(Optimizer):
             step = state['step']
             beta1, beta2 = group.betas
             rect = compute_rect(group, step)
-            if g.is_sparse:
-                raise NotImplementedError('sparse gradients are outside the oracle')
+            # thorn.py:1667-1700: a row-sparse gradient updates only its rows (lazy Adam)
+            if g.is_sparse and (group.decouple_md or g.sparse_dim() != 1):
+                p.grad = g = g.to_dense()
+            elif g.is_sparse:
+                g = g.coalesce()
+                g_rows = g.values()
+                idxs = g.indices()[0]
+                if idxs.numel() == 0:
+                    continue
+                moment_rows = state['moment'].index_select(0, idxs)
+                variance_rows = state['variance'].index_select(0, idxs)
+                magma = momentum_aligned_mask(g_rows, state, group, moment=moment_rows)
+                apply = magma != 0.0 and (step + 1) % self._update_rate == 0
+                p_rows = p.index_select(0, idxs) if apply else None
+                adam_update(p_rows, g_rows, moment_rows, variance_rows, step, beta1=beta1, beta2=beta2,
+                            lr=group.lr * rect * magma, weight_decay=group.weight_decay, eps=group.eps,
+                            degenerate=rect == 0.0)
+                state['moment'].index_copy_(0, idxs, moment_rows)
+                state['variance'].index_copy_(0, idxs, variance_rows)
+                if p_rows is not None:
+                    p.index_copy_(0, idxs, p_rows)
+                state['step'] += 1
+                if group.none_grad:
+                    p.grad = None
+                continue
             magma = momentum_aligned_mask(g, state, group)
             if group.decouple_md:
                 g, p_g, gains = recover_direction(p, state)

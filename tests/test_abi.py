@@ -38,7 +38,26 @@ def test_abi_version_and_struct_sizes():
     assert lib.thorn_abi_struct_size(0) == _lib.ORTHO_MAT_DESC.itemsize
     assert lib.thorn_abi_struct_size(1) == _lib.ORTHO_MAT_STEP.itemsize
     assert lib.thorn_abi_struct_size(2) == _lib.ADAM_TENSOR_STEP.itemsize
+    assert lib.thorn_abi_struct_size(3) == _lib.ADAM_SPARSE_STEP.itemsize
     assert lib.thorn_abi_struct_size(99) == 0
+
+
+def test_sparse_adam_validates_without_gpu():
+    """thorn_adam_sparse_step: bad records fail before any launch; nnz = 0 is a no-op."""
+    rec = np.zeros(1, dtype=_lib.ADAM_SPARSE_STEP)
+    with pytest.raises(_lib.ThornError, match='null argument'):
+        _lib.check(_lib.load().thorn_adam_sparse_step(None, None), 'thorn_adam_sparse_step')
+    rec['rows'], rec['row_len'], rec['nnz'] = 10, 4, 0
+    _lib.adam_sparse_step(rec, 0)   # no rows: nothing to do
+    rec['nnz'] = -1
+    with pytest.raises(_lib.ThornError, match='negative size'):
+        _lib.adam_sparse_step(rec, 0)
+    rec['nnz'] = 3
+    with pytest.raises(_lib.ThornError, match='null pointer'):
+        _lib.adam_sparse_step(rec, 0)
+    rec['p'], rec['m'], rec['v'], rec['g_values'], rec['g_rows'] = 4096, 8192, 12288, 16384, 20484
+    with pytest.raises(_lib.ThornError, match='misaligned'):
+        _lib.adam_sparse_step(rec, 0)
 
 
 def test_plan_rejects_bad_shapes():

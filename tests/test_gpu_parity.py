@@ -440,3 +440,102 @@ def test_gradient_release(rate):
             if rate == 2 and it % 2 == 1:
                 assert torch.equal(pg.detach(), bg), (it, 'moved on a step not due')
     _log('[gpu]   ok')
+
+
+@pytest.mark.parametrize('rate', [1, 2])
+def test_sparse_gradients(rate):
+    """Row-sparse gradients (thorn.py:1667-1700) against the oracle over six steps: an embedding
+    with repeated and changing rows (Adam-atan2, weight decay), one with eps > 0 and rectification,
+    a not-row-sparse gradient (sparse_dim 2, made dense) and, at step 4, an empty gradient (no step
+    for that tensor), next to an orthogonalized matrix with a dense gradient. State <= 1e-5, Adam
+    parameters <= 1e-4, the matrix's update as any step. A sparse gradient on an orthogonalized
+    matrix raises RuntimeError on both sides."""
+    _log(f'[gpu] sparse gradients, update_rate {rate}')
+    thorn_amd = _thorn()
+    gen = torch.Generator().manual_seed(31)
+    shapes = [(300, 16), (40, 12), (120, 8), (64, 24)]   # in group order (see _clone_groups)
+    params = [torch.nn.Parameter(torch.randn(s, generator=gen) * 0.02) for s in shapes]
+    groups = [
+        {'orthogonalize': False, 'params': [params[0], params[1]], 'lr': 1e-2, 'weight_decay': 0.1},
+        {'orthogonalize': False, 'params': [params[2]], 'lr': 1e-2, 'weight_decay': 0.0, 'eps': 1e-8,
+         'rectify': True, 'betas': (0.9, 0.99)},
+        {'orthogonalize': True, 'params': [params[3]], 'lr': 1e-3, 'weight_decay': 0.1},
+    ]
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    cpu = O.OracleTHORN(groups)
+    gpu = thorn_amd.THORN(_clone_groups(groups, gparams))
+    cpu._update_rate = gpu._update_rate = rate
+
+    def grad(s, i):
+        rows, cols = shapes[i]
+        if i == 3:
+            return torch.randn(rows, cols, generator=gen) * 1e-3
+        if i == 1:
+            dense = torch.zeros(rows, cols)
+            dense[s % rows] = torch.randn(cols, generator=gen) * 1e-2
+            return dense.to_sparse(2)
+        n = 0 if (i == 0 and s == 4) else 7
+        idx = torch.randint(0, rows, (n,), generator=gen)
+        if n:
+            idx[-1] = idx[0]   # a repeated row
+        vals = torch.randn(n, cols, generator=gen) * 1e-2
+        return torch.sparse_coo_tensor(idx[None], vals, (rows, cols))
+
+    worst = {'state': 0.0, 'dp_adam': 0.0, 'dp': 0.0}
+    for s in range(1, 7):
+        before_c = [p.detach().clone() for p in params]
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            g = grad(s, i)
+            pc.grad = g.clone()
+            pg.grad = g.clone().to(DEV)
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            assert gpu.state[pg]['step'] == cpu.state[pc]['step'], (s, i)
+            assert (pg.grad is None) == (pc.grad is None), (s, i)
+            for k, v in cpu.state[pc].items():
+                if torch.is_tensor(v):
+                    worst['state'] = max(worst['state'], rel(gpu.state[pg][k], v))
+            dpc = pc.detach() - before_c[i]
+            dpg = pg.detach().cpu() - before_c[i]
+            r = rel(dpg, dpc) if dpc.norm() > 0 else dpg.norm().item()
+            key = 'dp' if i == 3 else 'dp_adam'
+            worst[key] = max(worst[key], r)
+        _copy_state_to(gpu, gparams, cpu, params)   # keep the matrix's f16 Newton-Schulz from drifting
+    _log(f'[gpu]   {worst}')
+    assert worst['state'] <= 1e-5, worst
+    assert worst['dp_adam'] <= 1e-4, worst
+    assert worst['dp'] <= 2e-2, worst
+    sg = torch.sparse_coo_tensor(torch.tensor([[1, 5]]), torch.ones(2, 24), (64, 24))
+    params[3].grad = sg.clone()
+    gparams[3].grad = sg.clone().to(DEV)
+    with pytest.raises(RuntimeError, match='add\\(sparse, dense\\)'):
+        cpu.step()
+    with pytest.raises(RuntimeError, match='add\\(sparse, dense\\)'):
+        gpu.step()
+
+
+def test_sparse_embedding_backward():
+    """nn.Embedding(sparse=True): the gradient autograd produces (uncoalesced, repeated rows) goes
+    through the row-sparse path; one step against the oracle."""
+    _log('[gpu] sparse embedding backward')
+    thorn_amd = _thorn()
+    torch.manual_seed(2)
+    emb_c = torch.nn.Embedding(500, 32, sparse=True)
+    emb_g = copy.deepcopy(emb_c).to(DEV)
+    cpu = O.OracleTHORN([{'orthogonalize': False, 'params': [emb_c.weight], 'lr': 1e-2}])
+    gpu = thorn_amd.THORN([{'orthogonalize': False, 'params': [emb_g.weight], 'lr': 1e-2}])
+    tok = torch.randint(0, 500, (4, 64), generator=torch.Generator().manual_seed(3))
+    for _ in range(3):
+        before = emb_c.weight.detach().clone()
+        emb_c(tok).square().sum().backward()
+        emb_g(tok.to(DEV)).square().sum().backward()
+        assert emb_g.weight.grad.is_sparse
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        r = rel(emb_g.weight.detach().cpu() - before, emb_c.weight.detach() - before)
+        rs = max(rel(gpu.state[emb_g.weight][k], cpu.state[emb_c.weight][k]) for k in ('moment', 'variance'))
+        assert r <= 1e-4 and rs <= 1e-5, (r, rs)
+    _log('[gpu]   ok')

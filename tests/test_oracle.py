@@ -280,3 +280,71 @@ def test_gradient_release_hooks():
         assert all(opt.state[p]['step'] == it + 2 for p in after)
     with pytest.raises(ValueError, match='post_accumulate_grad_hooks'):
         O.OracleTHORN(model, lr=1e-2).setup_gradient_release(model)
+
+
+def _sparse_grad(gen, idx, rows, cols, scale=0.1):
+    idx = torch.tensor(idx, dtype=torch.int64)
+    vals = torch.randn(len(idx), cols, generator=gen) * scale
+    return torch.sparse_coo_tensor(idx[None], vals, (rows, cols))
+
+
+def test_sparse_adam_matches_torch_sparse_adam():
+    """The sparse branch (thorn.py:1667-1700) with eps > 0, no weight decay and no rectification is
+    torch.optim.SparseAdam (lazy Adam on the gradient's rows; the two differ only in where eps
+    enters the denominator, negligible next to sqrt(v) here); gradients with repeated rows."""
+    gen = torch.Generator().manual_seed(21)
+    w0 = torch.randn(50, 8, generator=gen)
+    w = torch.nn.Parameter(w0.clone())
+    ref = torch.nn.Parameter(w0.clone())
+    opt = O.OracleTHORN([{'orthogonalize': False, 'params': [w], 'lr': 1e-2, 'betas': (0.9, 0.99),
+                          'weight_decay': 0.0, 'eps': 1e-8}])
+    tref = torch.optim.SparseAdam([ref], lr=1e-2, betas=(0.9, 0.99), eps=1e-8)
+    for idx in ([3, 7, 3, 12], [0, 49, 7], [3, 3, 3], [10, 11, 12, 13, 14, 7]):
+        g = _sparse_grad(gen, idx, 50, 8)
+        w.grad = g.clone()
+        ref.grad = g.clone()
+        opt.step()
+        tref.step()
+        torch.testing.assert_close(w.detach(), ref.detach(), rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(opt.state[w]['moment'], tref.state[ref]['exp_avg'], rtol=1e-6, atol=1e-9)
+        torch.testing.assert_close(opt.state[w]['variance'], tref.state[ref]['exp_avg_sq'], rtol=1e-6, atol=1e-12)
+
+
+def test_sparse_rows_invariants():
+    """Rows outside the gradient keep parameter and state bit for bit; repeated rows act as their
+    sum (coalesce); an empty gradient takes no step at all (thorn.py:1677-1678); a gradient that
+    is not row-sparse (sparse_dim 2) becomes dense and takes the dense step."""
+    gen = torch.Generator().manual_seed(5)
+    grp = {'orthogonalize': False, 'lr': 1e-2, 'betas': (0.9, 0.95), 'weight_decay': 0.1}
+    w0 = torch.randn(20, 6, generator=gen)
+    a, b, c = (torch.nn.Parameter(w0.clone()) for _ in range(3))
+    oa = O.OracleTHORN([dict(grp, params=[a])])
+    ob = O.OracleTHORN([dict(grp, params=[b])])
+    oc = O.OracleTHORN([dict(grp, params=[c])])
+    for s in range(3):
+        vals = torch.randn(3, 6, generator=gen) * 0.1
+        a.grad = torch.sparse_coo_tensor(torch.tensor([[4, 9, 4]]), vals, (20, 6))
+        b.grad = torch.sparse_coo_tensor(torch.tensor([[4, 9]]), torch.stack([vals[0] + vals[2], vals[1]]), (20, 6))
+        dense = torch.zeros(20, 6)
+        dense[4] = vals[0] + vals[2]
+        dense[9] = vals[1]
+        c.grad = dense.to_sparse(2)
+        before = a.detach().clone()
+        oa.step()
+        ob.step()
+        oc.step()
+        assert torch.equal(a.detach(), b.detach())
+        keep = [i for i in range(20) if i not in (4, 9)]
+        assert torch.equal(a.detach()[keep], before[keep])
+        assert not torch.equal(a.detach()[[4, 9]], before[[4, 9]])
+        for k in ('moment', 'variance'):
+            assert torch.equal(oa.state[a][k][keep], torch.zeros(len(keep), 6))
+    # the dense (sparse_dim 2) one takes the dense step: weight decay reaches the untouched rows
+    # (u = 0 there passes the cautious mask), which the row-sparse step leaves alone
+    assert not torch.equal(c.detach()[keep], a.detach()[keep])
+    assert c.grad is None
+    step = oa.state[a]['step']
+    before = a.detach().clone()
+    a.grad = torch.sparse_coo_tensor(torch.zeros(1, 0, dtype=torch.int64), torch.zeros(0, 6), (20, 6))
+    oa.step()
+    assert oa.state[a]['step'] == step and a.grad is not None and torch.equal(a.detach(), before)

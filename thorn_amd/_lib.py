@@ -48,6 +48,14 @@ ADAM_TENSOR_STEP = np.dtype([
     ('eps', np.float32), ('apply', np.int32), ('degenerate', np.int32),
 ], align=True)
 
+ADAM_SPARSE_STEP = np.dtype([
+    ('p', np.uint64), ('m', np.uint64), ('v', np.uint64), ('g_values', np.uint64), ('g_rows', np.uint64),
+    ('rows', np.int64), ('row_len', np.int64), ('nnz', np.int64),
+    ('lr', np.float32), ('weight_decay', np.float32), ('beta2', np.float32),
+    ('w1', np.float32), ('w2', np.float32), ('bc1', np.float32), ('bc2', np.float32),
+    ('eps', np.float32), ('apply', np.int32), ('degenerate', np.int32),
+], align=True)
+
 # every exported symbol of include/thorn_amd.h: name -> (restype, argtypes)
 _vp, _sz, _i, _f, _cp = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
 SIGNATURES = {
@@ -65,6 +73,7 @@ SIGNATURES = {
     'thorn_adam_table_bytes': (_sz, [_vp]),
     'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp]),
     'thorn_adam_step': (_i, [_vp, _vp, _vp]),
+    'thorn_adam_sparse_step': (_i, [_vp, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
@@ -72,7 +81,7 @@ SIGNATURES = {
 }
 KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
          'symprod']
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 
@@ -93,7 +102,7 @@ def load() -> ctypes.CDLL:
     ver = lib.thorn_abi_version()
     if ver != ABI_VERSION:
         raise ImportError(f'{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it')
-    for which, dt in enumerate((ORTHO_MAT_DESC, ORTHO_MAT_STEP, ADAM_TENSOR_STEP)):
+    for which, dt in enumerate((ORTHO_MAT_DESC, ORTHO_MAT_STEP, ADAM_TENSOR_STEP, ADAM_SPARSE_STEP)):
         size = lib.thorn_abi_struct_size(which)
         if size != dt.itemsize:
             raise ImportError(f'ABI struct {which} is {size} bytes in the library but {dt.itemsize} '
@@ -192,3 +201,9 @@ class AdamPlan:
         if h is not None and h.value:
             self._lib.thorn_adam_plan_destroy(h)
             self.handle = None
+
+
+def adam_sparse_step(step: np.ndarray, stream: int) -> None:
+    """step: one ADAM_SPARSE_STEP record (see include/thorn_amd.h)."""
+    assert step.dtype == ADAM_SPARSE_STEP and step.size == 1
+    check(load().thorn_adam_sparse_step(step.ctypes.data, stream), 'thorn_adam_sparse_step')

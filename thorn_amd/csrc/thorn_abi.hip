@@ -263,6 +263,7 @@ size_t thorn_abi_struct_size(int which) {
         case 0: return sizeof(ThornOrthoMatDesc);
         case 1: return sizeof(ThornOrthoMatStep);
         case 2: return sizeof(ThornAdamTensorStep);
+        case 3: return sizeof(ThornAdamSparseStep);
         default: return 0;
     }
 }
@@ -676,6 +677,33 @@ int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream)
                        reinterpret_cast<const thorn::AdamTensor*>(dev), tl);
     plan->timer.end(slot, st);
     return check_launch("adam_kernel");
+}
+
+int thorn_adam_sparse_step(const ThornAdamSparseStep* S, void* stream) {
+    if (!S) return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: null argument");
+    if (S->nnz < 0 || S->rows < 0 || S->row_len < 0)
+        return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: negative size");
+    if (S->nnz == 0 || S->row_len == 0) return THORN_OK;
+    if (S->nnz > INT32_MAX) return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: more than 2^31 - 1 gradient rows");
+    if (!S->p || !S->m || !S->v || !S->g_values || !S->g_rows)
+        return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: null pointer");
+    if (((reinterpret_cast<uintptr_t>(S->p) | reinterpret_cast<uintptr_t>(S->m) |
+          reinterpret_cast<uintptr_t>(S->v) | reinterpret_cast<uintptr_t>(S->g_values)) & 3u) != 0 ||
+        (reinterpret_cast<uintptr_t>(S->g_rows) & 7u) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: misaligned tensor");
+    thorn::SparseAdamArgs a;
+    a.p = S->p; a.m = S->m; a.v = S->v;
+    a.gv = S->g_values; a.rows_idx = S->g_rows;
+    a.rows = S->rows; a.row_len = S->row_len;
+    a.s.lr = S->lr; a.s.wd = S->weight_decay; a.s.beta2 = S->beta2; a.s.w1 = S->w1; a.s.w2 = S->w2;
+    a.s.bc1 = S->bc1; a.s.bc2 = S->bc2; a.s.eps = S->eps;
+    a.s.apply = S->apply != 0;
+    a.s.degenerate = S->degenerate != 0;
+    a.s.atan2_mode = S->eps == 0.f;
+    a.vec = S->row_len % 4 == 0 && aligned16(S->p) && aligned16(S->m) && aligned16(S->v) && aligned16(S->g_values);
+    hipLaunchKernelGGL(thorn::adam_sparse_kernel, dim3(static_cast<unsigned>(S->nnz)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+    return check_launch("adam_sparse_kernel");
 }
 
 int thorn_adam_timing_enable(thorn_adam_plan_t plan, int max_launches) {

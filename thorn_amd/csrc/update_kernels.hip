@@ -432,4 +432,50 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict_
     }
 }
 
+// Row-sparse Adam (thorn.py:1673-1700): block k updates row rows_idx[k] of p, m, v with gradient
+// row k, the same per-element arithmetic as adam_kernel; rows outside [0, rows) are skipped.
+struct SparseAdamArgs {
+    float* p;
+    float* m;
+    float* v;
+    const float* gv;
+    const int64_t* rows_idx;
+    int64_t rows, row_len;
+    AdamScalars s;
+    int32_t vec;   // row_len % 4 == 0 and p, m, v, gv 16-byte aligned
+};
+
+__global__ __launch_bounds__(256) void adam_sparse_kernel(SparseAdamArgs a) {
+    const int64_t k = blockIdx.x;
+    const int64_t r = ldg<int64_t>(a.rows_idx + k);
+    if (r < 0 || r >= a.rows) return;
+    const AdamScalars& s = a.s;
+    const float* g = a.gv + k * a.row_len;
+    float* p = a.p + r * a.row_len;
+    float* m = a.m + r * a.row_len;
+    float* v = a.v + r * a.row_len;
+    if (a.vec) {
+        for (int64_t c = (int64_t)threadIdx.x * 4; c < a.row_len; c += 1024) {
+            float4 p4 = s.apply ? ldg<float4>(p + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 g4 = ldg<float4>(g + c);
+            float4 m4 = ldg<float4>(m + c), v4 = ldg<float4>(v + c);
+            adam_elem(p4.x, g4.x, m4.x, v4.x, s);
+            adam_elem(p4.y, g4.y, m4.y, v4.y, s);
+            adam_elem(p4.z, g4.z, m4.z, v4.z, s);
+            adam_elem(p4.w, g4.w, m4.w, v4.w, s);
+            stg<float4>(m + c, m4);
+            stg<float4>(v + c, v4);
+            if (s.apply) stg<float4>(p + c, p4);
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < a.row_len; c += 256) {
+            float pe = s.apply ? p[c] : 0.f, me = m[c], ve = v[c];
+            adam_elem(pe, g[c], me, ve, s);
+            m[c] = me;
+            v[c] = ve;
+            if (s.apply) p[c] = pe;
+        }
+    }
+}
+
 }  // namespace thorn

@@ -7,9 +7,9 @@ What runs underneath is different: every group's whole step is a handful of grou
 on the current stream (see ``thorn_amd.csrc``), driven through the C ABI in include/thorn_amd.h.
 
 Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
-behaviour): Magma ``momentum_align`` (thorn.py:800-836), sparse gradients (thorn.py:1667-1700),
-DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), ``decouple_md`` on non-orthogonalized
-groups and non-fp32 parameters.
+behaviour): Magma ``momentum_align`` (thorn.py:800-836), DTensor/FSDP2 parameters
+(thorn.py:979-1186, 1459-1581), ``decouple_md`` on non-orthogonalized groups or with sparse
+gradients, and non-fp32 parameters.
 """
 from __future__ import annotations
 
@@ -431,19 +431,61 @@ class THORN(Optimizer):
         if group.momentum_align:
             raise NotImplementedError('momentum_align (Magma) is not implemented on the MI355X path')
         g = p.grad
-        if g.is_sparse:
-            raise NotImplementedError('sparse gradients are not implemented on the MI355X path')
+        if g.is_sparse and group.orthogonalize:
+            # the reference's momentum step g + beta1 * m (thorn.py:1381) fails the same way
+            raise RuntimeError('add(sparse, dense) is not supported: an orthogonalized parameter needs a '
+                               'dense gradient')
+        if g.is_sparse and group.decouple_md:
+            raise NotImplementedError('sparse gradients with decouple_md are not implemented on the MI355X path')
         if type(p.data).__name__ == 'DTensor' or type(g).__name__ == 'DTensor':
             raise NotImplementedError('DTensor / FSDP2 parameters are not implemented on the MI355X path')
         if g.shape != p.shape:
             raise AssertionError(f'gradient shape {tuple(g.shape)} != parameter shape {tuple(p.shape)}')
         _check_tensor(p, 'parameter')
-        _check_tensor(g, 'gradient')
+        if g.is_sparse:
+            if g.dtype != torch.float32 or not g.is_cuda:
+                raise NotImplementedError('THORN on MI355X needs fp32 device gradients')
+        else:
+            _check_tensor(g, 'gradient')
         if g.device != p.device:
             raise RuntimeError('gradient and parameter are on different devices')
         if not group.orthogonalize and group.decouple_md:
             raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
                                       'on the MI355X path')
+
+    def _sparse_adam(self, p: torch.Tensor, g: torch.Tensor, group: _Group) -> None:
+        """Row-sparse Adam on the coalesced gradient g (thorn.py:1673-1700): the gradient's rows
+        of p, m and v take the ordinary Adam step (thorn_adam_sparse_step); the other rows keep
+        their parameter and state."""
+        state = self.state[p]
+        step = state['step']
+        beta1, beta2 = group.betas
+        rect = _compute_rect(group, step)
+        rows = p.shape[0]
+        row_len = p.numel() // rows if rows else 0
+        idx = g.indices()[0].contiguous()
+        vals = g.values().reshape(idx.numel(), row_len).contiguous()
+        rec = np.zeros(1, dtype=_lib.ADAM_SPARSE_STEP)
+        rec['p'] = p.data_ptr()
+        rec['m'] = state['moment'].data_ptr()
+        rec['v'] = state['variance'].data_ptr()
+        rec['g_values'] = vals.data_ptr()
+        rec['g_rows'] = idx.data_ptr()
+        rec['rows'] = rows
+        rec['row_len'] = row_len
+        rec['nnz'] = idx.numel()
+        rec['lr'] = group.lr * rect * 1.0
+        rec['weight_decay'] = group.weight_decay
+        rec['beta2'] = beta2
+        rec['w1'] = 1 - beta1
+        rec['w2'] = 1 - beta2
+        rec['bc1'] = 1 / (1 - beta1 ** step)
+        rec['bc2'] = 1 / (1 - beta2 ** step)
+        rec['eps'] = group.eps
+        rec['apply'] = 1 if (step + 1) % self._update_rate == 0 else 0
+        rec['degenerate'] = 1 if rect == 0.0 else 0
+        with torch.cuda.device(p.device):
+            _lib.adam_sparse_step(rec, torch.cuda.current_stream(p.device).cuda_stream)
 
     def _runner(self, key, factory):
         r = self._runners.get(key)
@@ -455,12 +497,29 @@ class THORN(Optimizer):
     # -- step (thorn.py:1583-1753) ---------------------------------------------------------------
     def _step_params(self, params: list, group: _Group, gi: int) -> None:
         live = []
+        sparse = []
         for p in params:
             if p is None or p.grad is None:
                 continue
             self._validate(p, group)
             self._init_state(p, group)
+            g = p.grad
+            if g.is_sparse and not group.orthogonalize:
+                if g.sparse_dim() != 1:   # thorn.py:1671-1672
+                    p.grad = g.to_dense()
+                else:
+                    g = g.coalesce()
+                    if g.indices().numel() == 0:   # thorn.py:1677-1678: no step for this one
+                        continue
+                    sparse.append((p, g))
+                    continue
             live.append(p)
+        for p, g in sparse:
+            self._sparse_adam(p, g, group)
+        for p, _ in sparse:
+            if group.none_grad:
+                p.grad = None
+            self.state[p]['step'] += 1
         if not live:
             return
         by_dev: dict = {}
