@@ -60,6 +60,27 @@ def ns_flops(shapes, iters=5) -> float:
     return total
 
 
+def schedule_ops(iters: int, restart_mask: int) -> list:
+    """The operation sequence the library launches for one matrix (thorn_abi.hip, ns_schedule):
+    'gram' (R = X X^T), 'poly' (P), 'sym' (Q P, R P or P (R P)) and 'update' (Q X)."""
+    def restart(i):
+        return 0 < i < 32 and (restart_mask >> i) & 1
+    ops = ['gram']
+    q = False
+    for i in range(iters):
+        if restart(i):
+            ops += ['update', 'gram']
+            q = False
+        ops.append('poly')
+        if q:
+            ops.append('sym')
+        q = True
+        if i < iters - 1 and not restart(i + 1):
+            ops += ['sym', 'sym']
+    ops.append('update')
+    return ops
+
+
 def ns_schedule(iters: int, restart_mask: int) -> dict:
     """Launch counts of the Gram Newton-Schulz schedule the library runs for a restart mask (bit i:
     restart before iteration i): Gram matrices, polynomials P, symmetric products and X updates."""
@@ -272,6 +293,35 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
         return sorted(f for p in paths for f in glob.glob(os.path.join(p, '**', pattern), recursive=True))
 
     lines = []
+    traces = found('*kernel_trace.csv')
+    if traces:   # the Newton-Schulz launches of the last complete step, config 2's schedules
+        rows = sorted(csv.DictReader(open(traces[0])), key=lambda r: int(r['Start_Timestamp']))
+        starts = [i for i, r in enumerate(rows) if 'ortho_pre_kernel' in r['Kernel_Name']]
+        if len(starts) >= 2:
+            mats, _ = config_shapes(2)
+            gram = schedule_ops(5, 4)
+            plain = schedule_ops(5, (1 << 5) - 2)
+            fl = {'gram': lambda s_, l_: s_ * s_ * l_, 'poly': lambda s_, l_: s_ ** 3,
+                  'sym': lambda s_, l_: s_ ** 3, 'update': lambda s_, l_: 2.0 * s_ * s_ * l_}
+            lines += ['Newton-Schulz launches of the last complete step (config 2; Gram-schedule op on the '
+                      '100 matrices >= 2:1 / plain-schedule op on the 40 square ones):', '',
+                      '| launch | ops | TFLOP (algorithmic) | us | TFLOP/s |', '|---:|---|---:|---:|---:|']
+            k = 0
+            for r in rows[starts[-2]:starts[-1]]:
+                if 'ns_phase_kernel' not in r['Kernel_Name']:
+                    continue
+                us = (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
+                f = 0.0
+                names = []
+                for sched, pick in ((gram, lambda s_, l_: l_ >= 2 * s_), (plain, lambda s_, l_: l_ < 2 * s_)):
+                    op = sched[k] if k < len(sched) else None
+                    names.append(op or '-')
+                    if op:
+                        f += sum(fl[op](min(sh), max(sh)) for sh in mats if pick(min(sh), max(sh)))
+                k += 1
+                lines.append(f'| {k} | {names[0]} / {names[1]} | {f / 1e12:.3f} | {us:.1f} | '
+                             f'{f / (us * 1e-6) / 1e12:.1f} |')
+            lines.append('')
     for f in found('*kernel_stats.csv'):
         rows = list(csv.DictReader(open(f)))
         lines += ['| kernel | calls | total ms | avg us | min us | max us | % |',
