@@ -12,8 +12,8 @@ with Gram Newton-Schulz for non-square matrices, exactly as thorn.py:626-662 doe
 
 Left out, because they are outside the single-GPU hot path: the FSDP2/DTensor engine
 (thorn.py:979-1186, 1333-1374, 1459-1581), the Triton kernels (thorn.py:53-280) and the compile
-wrapper (thorn.py:379-423). Magma
-``momentum_align`` (thorn.py:800-836) is restated because it is tiny, but the product rejects it.
+wrapper (thorn.py:379-423). Magma ``momentum_align`` (thorn.py:800-836, 1616-1634) is restated
+in its single-process form.
 
 How the pieces are pinned (tests/test_oracle.py):
   * coefficients, restarts, single-function outputs and multi-step trajectories: golden vectors
@@ -24,9 +24,10 @@ How the pieces are pinned (tests/test_oracle.py):
     recurrences every step, parameters move only on due steps, a due step is an ordinary step,
     a decouple_md parameter goes through p / G * G otherwise, hooks drop the gradients);
   * sparse (row) gradients: torch.optim.SparseAdam (eps > 0, no weight decay), untouched rows
-    left alone, duplicate indices summed, an empty gradient taking no step.
-Parity unpinned: ``w1rand`` and ``momentum_aligned_mask`` (Magma), which no golden or closed form
-covers; the product rejects ``momentum_align=True``, so neither is used as a checker.
+    left alone, duplicate indices summed, an empty gradient taking no step, and reference
+    trajectories with row-sparse gradients;
+  * Magma: reference outputs of the PRNG and of the mask function, Magma trajectories (mixed,
+    decouple_md, sparse), and properties (s stays in (0, 1], the EMA of sigmoid(cos / 2)).
 """
 from __future__ import annotations
 
@@ -349,7 +350,8 @@ def compute_rect(group: Group, step) -> float:
 
 
 def w1rand(s: int) -> tuple[int, int]:
-    """64-bit hash PRNG of Magma masking (thorn.py:800-804). Parity unpinned."""
+    """64-bit hash PRNG of Magma masking (thorn.py:800-804): a Weyl step s += C, then the xor of the
+    two halves of the 128-bit product s * (s ^ C)."""
     C = 0xD07EBC63274654C7
     s = (s + C) & 0xFFFFFFFFFFFFFFFF
     t = s * (s ^ C)
@@ -357,7 +359,9 @@ def w1rand(s: int) -> tuple[int, int]:
 
 
 def momentum_aligned_mask(g, state, group: Group, *, tau=2.0, p=0.9, moment=None) -> float:
-    """Magma masking, single-process branch (thorn.py:806-836). Parity unpinned."""
+    """Magma masking, single-process branch (thorn.py:806-836): s <- p s + (1 - p) sigmoid(cos(g, m)
+    / tau) with the moment before this step's update; the step is skipped (0.0) when the PRNG
+    draw is odd, otherwise the learning rate is scaled by s."""
     if not group.momentum_align:
         return 1.0
     g_flat = g.flatten()
@@ -536,7 +540,7 @@ class OracleTHORN(Optimizer):
                     p, _, ctx = pending[i]
                     self._ortho_post(p, group, u, ctx)
 
-    # thorn.py:1583-1732 (no DTensor, no sparse)
+    # thorn.py:1583-1732 (no DTensor)
     def _step_params(self, params, group: Group):
         regular = []
         for p in params:
@@ -562,7 +566,9 @@ class OracleTHORN(Optimizer):
                         state['gain_variance'] = torch.zeros((), dtype=p.dtype, device=p.device)
                     state['target_norm'] = group.target_norm_(p)
                 if group.momentum_align:
-                    state['random_state'] = torch.randint(0, (1 << 63) - 1, (), dtype=torch.uint64).item()
+                    # thorn.py:1616-1621: drawn from the generator of the gradient's device
+                    state['random_state'] = torch.randint(0, (1 << 63) - 1, (), device=p.grad.device,
+                                                          dtype=torch.uint64).item()
                     state['s'] = torch.ones((), dtype=p.dtype, device=p.device)
             regular.append(p)
 

@@ -16,9 +16,12 @@ What the fixtures pin, and why they need the reference itself (closed forms cove
   * pnn.npz, adam.npz - single-function outputs of _per_neuron_norm_update and _adam_update;
   * traj_config1.npz  - 10 full THORN steps on the 512x256 Linear of BASELINE config 1;
   * traj_mixed.npz    - 20 steps over a mixed set (tall/wide/square/3-D/vectors, rectify, eps>0);
-  * traj_md.npz       - 20 steps with decouple_md on the orthogonalized group (config-3 branch).
+  * traj_md.npz       - 20 steps with decouple_md on the orthogonalized group (config-3 branch);
+  * magma.npz         - _w1rand sequences and _momentum_aligned_mask outputs (Magma);
+  * traj_magma*.npz   - Magma trajectories: the mixed and decouple_md sets with momentum_align on
+    every group, and row-sparse embedding gradients with and without it.
 
-Usage: python tests/golden/make_golden.py
+Usage: python tests/golden/make_golden.py [fixture ...]   (e.g. `magma traj_magma`; default: all)
 """
 from __future__ import annotations
 
@@ -115,6 +118,52 @@ def pnn_adam_fixtures(ref) -> None:
     save('adam.npz', **out)
 
 
+def magma_fixtures(ref) -> None:
+    out = {}
+    seeds = [0, 1, 2, 0xD07EBC63274654C7, (1 << 63) - 2, (1 << 64) - 1, 0x0123456789ABCDEF, 987654321987654321]
+    states, draws = [], []
+    for seed in seeds:
+        st, row_s, row_d = seed, [], []
+        for _ in range(40):
+            st, d = ref._w1rand(st)
+            row_s.append(st)
+            row_d.append(d)
+        states.append(row_s)
+        draws.append(row_d)
+    out['w1_seeds'] = np.asarray(seeds, dtype=np.uint64)
+    out['w1_states'] = np.asarray(states, dtype=np.uint64)
+    out['w1_draws'] = np.asarray(draws, dtype=np.uint64)
+
+    g = torch.Generator().manual_seed(4321)
+    group = types.SimpleNamespace(momentum_align=True)
+    k = 0
+    for shape, mode, s0 in [((64,), 'zero', 1.0), ((64,), 'aligned', 0.8), ((64,), 'opposed', 0.6),
+                            ((24, 40), 'aligned', 0.9), ((3, 8, 12), 'random', 0.5),
+                            ((5, 16), 'rows', 0.7), ((1000,), 'random', 0.95), ((16, 16), 'tiny', 0.3)]:
+        gr = torch.randn(shape, generator=g) * 1e-3
+        noise = torch.randn(shape, generator=g) * 1e-3
+        m = {'zero': torch.zeros(shape), 'aligned': 0.7 * gr + 0.3 * noise, 'opposed': -0.5 * gr + 0.2 * noise,
+             'random': noise, 'rows': noise, 'tiny': gr * 1e-30}[mode]
+        for seed in (seeds[k % len(seeds)], seeds[(k + 3) % len(seeds)]):
+            state = {'s': torch.tensor(s0), 'random_state': seed}
+            if mode == 'rows':   # the sparse path passes the gathered moment rows (thorn.py:1679)
+                state['moment'] = torch.full(shape, 123.0)
+                scale = ref._momentum_aligned_mask(gr, state, group, moment=m)
+            else:
+                state['moment'] = m
+                scale = ref._momentum_aligned_mask(gr, state, group)
+            out[f'mask{k}_g'], out[f'mask{k}_m'] = gr, m
+            out[f'mask{k}_s0'] = np.float32(s0)
+            out[f'mask{k}_seed'] = np.uint64(seed)
+            out[f'mask{k}_rows'] = np.bool_(mode == 'rows')
+            out[f'mask{k}_scale'] = np.float64(scale)
+            out[f'mask{k}_s1'] = state['s']
+            out[f'mask{k}_state1'] = np.uint64(state['random_state'])
+            k += 1
+    out['n_mask'] = np.int64(k)
+    save('magma.npz', **out)
+
+
 def run_trajectory(ref, name: str, build, steps: int, snapshot_every: int) -> None:
     torch.manual_seed(0)
     params, groups, grads = build()
@@ -137,16 +186,28 @@ def run_trajectory(ref, name: str, build, steps: int, snapshot_every: int) -> No
     save(name, **out)
 
 
-def main() -> None:
+def main(only: list[str]) -> None:
+    """Writes every fixture, or only those whose file names start with one of `only`."""
     torch.set_num_threads(1)
     ref = load_reference()
-    coefficient_fixtures(ref)
-    polar_fixtures(ref)
-    pnn_adam_fixtures(ref)
-    run_trajectory(ref, 'traj_config1.npz', workloads.config1, 10, 10)
-    run_trajectory(ref, 'traj_mixed.npz', workloads.mixed_small, 20, 10)
-    run_trajectory(ref, 'traj_md.npz', workloads.md_small, 20, 10)
+    jobs = [
+        ('coeffs', lambda: coefficient_fixtures(ref)),
+        ('polar', lambda: polar_fixtures(ref)),
+        ('pnn', lambda: pnn_adam_fixtures(ref)),
+        ('traj_config1', lambda: run_trajectory(ref, 'traj_config1.npz', workloads.config1, 10, 10)),
+        ('traj_mixed', lambda: run_trajectory(ref, 'traj_mixed.npz', workloads.mixed_small, 20, 10)),
+        ('traj_md', lambda: run_trajectory(ref, 'traj_md.npz', workloads.md_small, 20, 10)),
+        ('magma', lambda: magma_fixtures(ref)),
+        ('traj_magma', lambda: run_trajectory(ref, 'traj_magma.npz', workloads.magma_small, 20, 10)),
+        ('traj_magma_md', lambda: run_trajectory(ref, 'traj_magma_md.npz', workloads.magma_md_small, 20, 10)),
+        ('traj_sparse', lambda: run_trajectory(ref, 'traj_sparse.npz', workloads.sparse_small, 12, 4)),
+        ('traj_magma_sparse', lambda: run_trajectory(ref, 'traj_magma_sparse.npz', workloads.magma_sparse_small,
+                                                     12, 4)),
+    ]
+    for name, job in jobs:
+        if not only or name in only:
+            job()
 
 
 if __name__ == '__main__':
-    main()
+    main(sys.argv[1:])

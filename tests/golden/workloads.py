@@ -87,3 +87,50 @@ def md_small(steps: int = 20):
          'weight_decay': 0.0},
     ]
     return params, groups, lambda s, i, prm: grads[(s, i)]
+
+
+def _with_magma(build):
+    params, groups, grads = build()
+    for g in groups:
+        g['momentum_align'] = True
+    return params, groups, grads
+
+
+def magma_small(steps: int = 20):
+    """mixed_small with Magma momentum-aligned masking on every group."""
+    return _with_magma(lambda: mixed_small(steps))
+
+
+def magma_md_small(steps: int = 20):
+    """md_small with Magma momentum-aligned masking on every group (recovered direction on md)."""
+    return _with_magma(lambda: md_small(steps))
+
+
+def sparse_small(steps: int = 12, momentum_align: bool = False):
+    """Row-sparse embedding gradients (uncoalesced, repeated rows, one empty step) beside a dense
+    vector and an orthogonalized matrix."""
+    gen = torch.Generator().manual_seed(23)
+    shapes = [(300, 16), (64,), (64, 24)]
+    params = [_leaf(torch.randn(300, 16, generator=gen) * 0.02), _leaf(torch.ones(64)),
+              _leaf(torch.randn(64, 24, generator=gen) * 0.02)]
+    grads = {}
+    for s in range(1, steps + 1):
+        nnz = 0 if s == 4 else 24
+        idx = torch.randint(0, 300, (nnz,), generator=gen)
+        if nnz:
+            idx[-3:] = idx[:3]   # repeated rows, summed by coalesce()
+        vals = torch.randn(nnz, 16, generator=gen) * 1e-3
+        grads[(s, 0)] = torch.sparse_coo_tensor(idx[None], vals, (300, 16))
+        grads[(s, 1)] = torch.randn(64, generator=gen) * 1e-3
+        grads[(s, 2)] = torch.randn(64, 24, generator=gen) * 1e-3
+    groups = [
+        {'orthogonalize': False, 'params': params[:2], 'lr': 1e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.1,
+         'momentum_align': momentum_align},
+        {'orthogonalize': True, 'params': params[2:], 'lr': 2e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.1,
+         'momentum_align': momentum_align},
+    ]
+    return params, groups, lambda s, i, prm: grads[(s, i)]
+
+
+def magma_sparse_small(steps: int = 12):
+    return sparse_small(steps, momentum_align=True)

@@ -6,6 +6,7 @@ in-place op order of every step.
 """
 from __future__ import annotations
 
+import math
 from pathlib import Path
 
 import numpy as np
@@ -174,12 +175,16 @@ def _run_oracle(build, steps, snap):
     return got
 
 
-@pytest.mark.parametrize('name,build,steps', [('traj_config1.npz', workloads.config1, 10),
-                                              ('traj_mixed.npz', workloads.mixed_small, 20),
-                                              ('traj_md.npz', workloads.md_small, 20)])
-def test_trajectories_match_reference(name, build, steps):
+@pytest.mark.parametrize('name,build,steps,snap', [('traj_config1.npz', workloads.config1, 10, 10),
+                                                   ('traj_mixed.npz', workloads.mixed_small, 20, 10),
+                                                   ('traj_md.npz', workloads.md_small, 20, 10),
+                                                   ('traj_magma.npz', workloads.magma_small, 20, 10),
+                                                   ('traj_magma_md.npz', workloads.magma_md_small, 20, 10),
+                                                   ('traj_sparse.npz', workloads.sparse_small, 12, 4),
+                                                   ('traj_magma_sparse.npz', workloads.magma_sparse_small, 12, 4)])
+def test_trajectories_match_reference(name, build, steps, snap):
     z = np.load(GOLD / name)
-    got = _run_oracle(build, steps, 10)
+    got = _run_oracle(build, steps, snap)
     keys = [k for k in z.files if not k.startswith('init_')]
     assert set(keys) == set(got), sorted(set(keys) ^ set(got))
     for k in keys:
@@ -348,3 +353,57 @@ def test_sparse_rows_invariants():
     a.grad = torch.sparse_coo_tensor(torch.zeros(1, 0, dtype=torch.int64), torch.zeros(0, 6), (20, 6))
     oa.step()
     assert oa.state[a]['step'] == step and a.grad is not None and torch.equal(a.detach(), before)
+
+
+def test_w1rand_matches_reference():
+    """Magma's PRNG (thorn.py:800-804) against the reference's own sequences, 40 draws per seed."""
+    z = np.load(GOLD / 'magma.npz')
+    for seed, states, draws in zip(z['w1_seeds'], z['w1_states'], z['w1_draws']):
+        st = int(seed)
+        for want_s, want_d in zip(states, draws):
+            st, d = O.w1rand(st)
+            assert (st, d) == (int(want_s), int(want_d))
+    assert {int(d) & 1 for d in z['w1_draws'].ravel()} == {0, 1}
+
+
+def test_momentum_aligned_mask_matches_reference():
+    """_momentum_aligned_mask (thorn.py:806-836): the scale it returns, the new s and the new PRNG
+    state, for a zero moment, aligned, opposed and random moments, an explicit `moment` (the
+    sparse path's gathered rows) and a moment too small to normalize."""
+    z = np.load(GOLD / 'magma.npz')
+    grp = O.Group(orthogonalize=False, params=[], lr=1e-3, momentum_align=True)
+    scales = []
+    for k in range(int(z['n_mask'])):
+        g, m = torch.from_numpy(z[f'mask{k}_g']), torch.from_numpy(z[f'mask{k}_m'])
+        state = {'s': torch.tensor(float(z[f'mask{k}_s0'])), 'random_state': int(z[f'mask{k}_seed'])}
+        if bool(z[f'mask{k}_rows']):
+            state['moment'] = torch.full_like(m, 123.0)
+            scale = O.momentum_aligned_mask(g, state, grp, moment=m)
+        else:
+            state['moment'] = m
+            scale = O.momentum_aligned_mask(g, state, grp)
+        assert scale == float(z[f'mask{k}_scale']), k
+        np.testing.assert_array_equal(state['s'].numpy(), z[f'mask{k}_s1'], err_msg=str(k))
+        assert state['random_state'] == int(z[f'mask{k}_state1'])
+        scales.append(scale)
+    assert 0.0 in scales and any(s > 0 for s in scales)
+
+
+def test_momentum_aligned_mask_closed_forms():
+    """s_t = sigmoid(cos / 2) with the pre-update moment: exactly aligned, opposed and orthogonal
+    moments give sigmoid(1/2), sigmoid(-1/2) and 1/2; a zero moment gives 1/2 (the norms are
+    clamped at 1e-8); an odd PRNG draw returns 0.0 and still moves s and the PRNG state."""
+    grp = O.Group(orthogonalize=False, params=[], lr=1e-3, momentum_align=True)
+    g = torch.tensor([3.0, -4.0, 0.0, 12.0])
+    even = next(s for s in range(100) if O.w1rand(s)[1] % 2 == 0)
+    odd = next(s for s in range(100) if O.w1rand(s)[1] % 2 == 1)
+    for m, want in [(2.5 * g, 1 / (1 + math.exp(-0.5))), (-0.1 * g, 1 / (1 + math.exp(0.5))),
+                    (torch.tensor([4.0, 3.0, 7.0, 0.0]), 0.5), (torch.zeros(4), 0.5)]:
+        state = {'s': torch.tensor(1.0), 'moment': m, 'random_state': even}
+        scale = O.momentum_aligned_mask(g, state, grp)
+        assert abs(state['s'].item() - (0.9 + 0.1 * want)) < 1e-6
+        assert scale == state['s'].item()
+        assert state['random_state'] == O.w1rand(even)[0]
+        state = {'s': torch.tensor(0.5), 'moment': m, 'random_state': odd}
+        assert O.momentum_aligned_mask(g, state, grp) == 0.0
+        assert abs(state['s'].item() - (0.45 + 0.1 * want)) < 1e-6
