@@ -15,6 +15,13 @@
  *   - Tables: the caller gets their size from *_table_bytes, lets *_fill_table write the bytes
  *     into host memory (device addresses inside refer to `table_dev`), copies those bytes to
  *     `table_dev` on the same stream, then calls the *_step function.
+ *   - Magma (momentum_align, thorn.py:800-836): a tensor whose step record carries `magma_s`
+ *     (state['s'], a 0-d fp32 device tensor) has its Magma statistics computed on the device, with
+ *     no host sync: cos = cosine similarity of the gradient and the moment before this step's
+ *     update (eps 1e-8 on each norm), then *magma_s = 0.9 * s + 0.1 * sigmoid(cos / 2), and, if the
+ *     tensor is applied this step, its learning rate is multiplied by the new *magma_s. The random
+ *     mask (thorn.py:831-833) stays with the caller, who runs the PRNG on the host and clears the
+ *     apply flag of a masked step; s moves on every step either way.
  */
 #ifndef THORN_AMD_H
 #define THORN_AMD_H
@@ -26,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 3
+#define THORN_ABI_VERSION 4
 
 enum {
     THORN_OK = 0,
@@ -82,6 +89,8 @@ typedef struct ThornOrthoMatStep {
     float gain_bc1, gain_bc2;  /* 1/(1 - beta1^step), 1/(1 - beta2^step) of the gain Adam */
     int32_t step_flags;   /* THORN_STEP_* */
     int32_t reserved;
+    float* magma_s;       /* Magma: state['s'] (0-d) or null. Consecutive matrices with the same
+                             magma_s are one parameter: the cosine similarity spans them all. */
 } ThornOrthoMatStep;
 
 typedef struct thorn_ortho_plan* thorn_ortho_plan_t;
@@ -129,6 +138,7 @@ typedef struct ThornAdamTensorStep {
     float eps;            /* 0 selects Adam-atan2 (thorn.py:879-880) */
     int32_t apply;        /* update p (thorn.py:1707) */
     int32_t degenerate;   /* rect == 0: u = m (thorn.py:883-885) */
+    float* magma_s;       /* Magma: state['s'] (0-d) or null */
 } ThornAdamTensorStep;
 
 typedef struct thorn_adam_plan* thorn_adam_plan_t;
@@ -136,8 +146,12 @@ typedef struct thorn_adam_plan* thorn_adam_plan_t;
 int thorn_adam_plan_create(const int64_t* numel, int n, thorn_adam_plan_t* out);
 void thorn_adam_plan_destroy(thorn_adam_plan_t plan);
 size_t thorn_adam_table_bytes(thorn_adam_plan_t plan);
-int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* table_dev,
-                          void* table_host);
+/* Device workspace for the Magma statistics (16 bytes per 4096 elements), 256-byte aligned, kept
+ * for the plan's lifetime; its contents need no initialization. Only needed when a step record
+ * carries magma_s (fill_table accepts a null workspace otherwise). */
+size_t thorn_adam_workspace_bytes(thorn_adam_plan_t plan);
+int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* workspace,
+                          void* table_dev, void* table_host);
 int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream);
 
 /* One tensor with a row-sparse gradient (e.g. nn.Embedding(sparse=True)): the sparse branch of
@@ -155,7 +169,12 @@ typedef struct ThornAdamSparseStep {
     float lr, weight_decay, beta2, w1, w2, bc1, bc2, eps;   /* as in ThornAdamTensorStep */
     int32_t apply;
     int32_t degenerate;
+    float* magma_s;       /* Magma: state['s'] (0-d) or null; the cosine similarity is over the
+                             gradient rows and the gathered moment rows (thorn.py:1676-1679) */
+    void* magma_work;     /* with magma_s: THORN_SPARSE_MAGMA_WORK_BYTES of device scratch,
+                             16-byte aligned; calls that share it must not overlap */
 } ThornAdamSparseStep;
+#define THORN_SPARSE_MAGMA_WORK_BYTES 16384
 int thorn_adam_sparse_step(const ThornAdamSparseStep* step, void* stream);
 
 /* ------------------------------------------------------------------------------------------
@@ -177,7 +196,8 @@ enum {
     THORN_KIND_ADAM = 9,       /* multi-tensor Adam */
     THORN_KIND_CAST = 10,      /* first iterate: u / ||u|| rounded to f16 */
     THORN_KIND_SYMPROD = 11,   /* Gram Newton-Schulz products Q P, R P, P (R P) */
-    THORN_KIND_COUNT = 12
+    THORN_KIND_MAGMA = 12,     /* Magma statistics of the Adam tensors */
+    THORN_KIND_COUNT = 13
 };
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
 int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);

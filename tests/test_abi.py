@@ -60,6 +60,53 @@ def test_sparse_adam_validates_without_gpu():
         _lib.adam_sparse_step(rec, 0)
 
 
+def test_magma_records_validate_without_gpu():
+    """Magma fields (ABI 4): the scratch buffers they need are checked before any launch."""
+    rec = np.zeros(1, dtype=_lib.ADAM_SPARSE_STEP)
+    rec['rows'], rec['row_len'], rec['nnz'] = 10, 4, 3
+    rec['p'], rec['m'], rec['v'], rec['g_values'], rec['g_rows'] = 4096, 8192, 12288, 16384, 20480
+    rec['magma_s'] = 24576
+    with pytest.raises(_lib.ThornError, match='needs magma_work'):
+        _lib.adam_sparse_step(rec, 0)
+    rec['magma_work'] = 28680
+    with pytest.raises(_lib.ThornError, match='misaligned Magma'):
+        _lib.adam_sparse_step(rec, 0)
+
+    plan = _lib.AdamPlan([5000, 0, 4096])
+    assert plan.workspace_bytes >= 16 * 3 and plan.workspace_bytes % 256 == 0
+    steps = np.zeros(3, dtype=_lib.ADAM_TENSOR_STEP)
+    for k in range(3):
+        steps[k]['g'], steps[k]['m'], steps[k]['v'] = 4096, 8192, 12288
+    host = np.zeros(plan.table_bytes, dtype=np.uint8)
+    plan.fill_table(steps, None, 64, host.ctypes.data)   # no Magma: no workspace needed
+    steps[0]['magma_s'] = 16384
+    with pytest.raises(_lib.ThornError, match='needs the workspace'):
+        plan.fill_table(steps, None, 64, host.ctypes.data)
+    with pytest.raises(_lib.ThornError, match='256-byte aligned'):
+        plan.fill_table(steps, 100, 64, host.ctypes.data)
+    steps[0]['magma_s'] = 16386
+    with pytest.raises(_lib.ThornError, match='magma_s must be 4-byte aligned'):
+        plan.fill_table(steps, 256, 64, host.ctypes.data)
+
+    oplan = _lib.OrthoPlan([8], [8], [0])
+    osteps = np.zeros(1, dtype=_lib.ORTHO_MAT_STEP)
+    osteps['p'], osteps['g'], osteps['m'], osteps['magma_s'] = 4096, 8192, 12288, 16386
+    ohost = np.zeros(oplan.table_bytes, dtype=np.uint8)
+    with pytest.raises(_lib.ThornError, match='magma_s must be 4-byte aligned'):
+        oplan.fill_table(osteps, 256, 64, ohost.ctypes.data)
+
+
+def test_w1rand_host_prng_matches_reference():
+    """The product's host PRNG (Magma masks) against the reference's own sequences."""
+    from thorn_amd import optim
+    z = np.load(Path(__file__).resolve().parent / 'golden' / 'magma.npz')
+    for seed, states, draws in zip(z['w1_seeds'], z['w1_states'], z['w1_draws']):
+        st = int(seed)
+        for want_s, want_d in zip(states, draws):
+            st, d = optim._w1rand(st)
+            assert (st, d) == (int(want_s), int(want_d))
+
+
 def test_plan_rejects_bad_shapes():
     with pytest.raises(_lib.ThornError, match='unsupported shape'):
         _lib.OrthoPlan([0], [4], [0])

@@ -57,9 +57,9 @@ def test_invalid_hyperparameters_raise_value_error_at_step(bad, msg):
 
 def test_unsupported_features_raise_not_implemented():
     p = nn.Parameter(torch.zeros(3, 3))
-    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3, 'momentum_align': True}])
+    opt = thorn_amd.THORN([{'orthogonalize': False, 'params': [p], 'lr': 1e-3, 'decouple_md': True}])
     p.grad = torch.zeros(3, 3)
-    with pytest.raises(NotImplementedError, match='momentum_align'):
+    with pytest.raises(NotImplementedError, match='decouple_md on a non-orthogonalized group'):
         opt.step()
 
 

@@ -407,6 +407,117 @@ def test_update_rate(name, rate):
     assert worst['md_roundtrip'] <= 1e-6, worst
 
 
+_W1_C = 0xD07EBC63274654C7
+
+
+@pytest.mark.parametrize('name,rate', [('magma_small', 1), ('magma_md_small', 1), ('magma_sparse_small', 1),
+                                       ('magma_small', 2)])
+def test_magma(name, rate, monkeypatch):
+    """Magma momentum_align (thorn.py:800-836, 1616-1634), teacher-forced against the oracle.
+
+    Each side seeds its PRNG from its own device's generator (thorn.py:1619), so the product's draw
+    is replaced by the oracle's, recovered from the oracle's state after its first step (one Weyl
+    step, state - C). From there the masks must agree exactly (the PRNG state is compared every
+    step). s, the cosine-similarity EMA the product computes on the device, agrees to 1e-5 like
+    the rest of the state. A masked step leaves a non-md parameter bit for bit unchanged (a
+    decouple_md one takes the gain round trip, to 1e-6); an unmasked one agrees as any step, with
+    the exact update scaled by s."""
+    _log(f'[gpu] magma {name}, update_rate {rate}')
+    thorn_amd = _thorn()
+    from thorn_amd import optim as product_optim
+    params, groups, grads = getattr(workloads, name)()
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    cpu = O.OracleTHORN(groups)
+    gpu = thorn_amd.THORN(_clone_groups(groups, gparams))
+    cpu._update_rate = gpu._update_rate = rate
+    cpu_of = {id(pg): pc for pc, pg in zip(params, gparams)}
+    monkeypatch.setattr(product_optim, '_magma_seed',
+                        lambda p: (cpu.state[cpu_of[id(p)]]['random_state'] - _W1_C) % (1 << 64))
+    group_of = {id(p): g for g in groups for p in g['params']}
+    worst = {'state': 0.0, 'dp': 0.0, 'dp_adam': 0.0, 'md_roundtrip': 0.0, 'masked': 0, 'applied': 0}
+    prev_rs = {}
+    for s in range(1, 9):
+        if s > 1:
+            _copy_state_to(gpu, gparams, cpu, params)
+        before_c = [p.detach().clone() for p in params]
+        before_g = [p.detach().clone() for p in gparams]
+        m_prev = [cpu.state[p]['moment'].clone() if 'moment' in cpu.state[p] else torch.zeros_like(p)
+                  for p in params]
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            g = grads(s, i, pc)
+            pc.grad = g.clone()
+            pg.grad = g.clone().to(DEV)
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        for i, (pc, pg) in enumerate(zip(params, gparams)):
+            grp = group_of[id(pc)]
+            cst, gst = cpu.state[pc], gpu.state[pg]
+            assert list(gst.keys()) == list(cst.keys()), (list(gst.keys()), list(cst.keys()))
+            for k, v in cst.items():
+                if torch.is_tensor(v) and k != 'target_norm':
+                    worst['state'] = max(worst['state'], rel(gst[k], v))
+                elif not torch.is_tensor(v):
+                    assert gst[k] == v, (s, i, k, gst[k], v)
+            rs = cst['random_state']
+            stepped = prev_rs.get(i) != rs
+            prev_rs[i] = rs
+            if not stepped:   # an empty sparse gradient: no step, no draw (thorn.py:1677-1678)
+                assert torch.equal(pg.detach().cpu(), before_g[i].cpu()), (s, i)
+                continue
+            unmasked = O.w1rand((rs - _W1_C) % (1 << 64))[1] % 2 == 0
+            due = unmasked and (cst['step'] % rate == 0)   # the step counter has moved on by one
+            dpc = pc.detach() - before_c[i]
+            dpg = pg.detach().cpu() - before_g[i].cpu()
+            if not due:
+                worst['masked'] += 1
+                if grp.get('decouple_md'):
+                    worst['md_roundtrip'] = max(worst['md_roundtrip'], rel(pg.detach(), pc.detach()))
+                else:
+                    assert torch.equal(pg.detach().cpu(), before_g[i].cpu()), (s, i, 'moved on a masked step')
+                    assert torch.equal(pc.detach(), before_c[i]), (s, i)
+                continue
+            worst['applied'] += 1
+            r = rel(dpg, dpc)
+            if not grp['orthogonalize']:
+                worst['dp_adam'] = max(worst['dp_adam'], r)
+            elif grp.get('decouple_md'):
+                worst['dp'] = max(worst['dp'], r)
+                assert r <= 2e-2, (s, i, r)
+            else:
+                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp) * float(cst['s'])
+                check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
+    _log(f'[gpu]   {worst}')
+    assert worst['masked'] > 0 and worst['applied'] > 0, worst
+    assert worst['state'] <= 1e-5, worst
+    assert worst['dp_adam'] <= 1e-4, worst
+    assert worst['md_roundtrip'] <= 1e-6, worst
+
+
+def test_magma_seed_from_device_generator():
+    """Without substitution the product draws each parameter's Magma seed as the reference does on
+    a GPU (thorn.py:1616-1619): 63 bits from the device generator, so torch.manual_seed fixes it."""
+    _log('[gpu] magma seed from the device generator')
+    thorn_amd = _thorn()
+    torch.manual_seed(123)
+    want = [int(torch.randint(0, (1 << 63) - 1, (), device=DEV, dtype=torch.uint64).item()) for _ in range(2)]
+    pa = torch.nn.Parameter(torch.randn(32, 16, device=DEV) * 0.02)
+    pb = torch.nn.Parameter(torch.ones(16, device=DEV))
+    opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [pa], 'lr': 1e-3, 'momentum_align': True},
+                           {'orthogonalize': False, 'params': [pb], 'lr': 1e-3, 'momentum_align': True}])
+    pa.grad = torch.randn(32, 16, device=DEV) * 1e-3
+    pb.grad = torch.randn(16, device=DEV) * 1e-3
+    torch.manual_seed(123)
+    opt.step()
+    torch.cuda.synchronize()
+    for p, seed in zip([pa, pb], want):
+        st = opt.state[p]
+        assert st['random_state'] == O.w1rand(seed)[0]
+        # first step: the moment is zero, so cos = 0 and s = 0.9 + 0.1 * sigmoid(0)
+        assert abs(st['s'].item() - 0.95) < 1e-7
+    _log(f'[gpu]   seeds {want}')
+
+
 @pytest.mark.parametrize('rate', [1, 2])
 def test_gradient_release(rate):
     """setup_gradient_release (thorn.py:1755-1776): every parameter steps from its own hook during

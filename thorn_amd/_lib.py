@@ -9,6 +9,7 @@ from __future__ import annotations
 import ctypes
 import os
 from pathlib import Path
+from typing import Optional
 
 import numpy as np
 import torch  # noqa: F401  (loads the HIP runtime first)
@@ -40,12 +41,14 @@ ORTHO_MAT_STEP = np.dtype([
     ('gain_w2', np.float32), ('gain_eps', np.float32),
     ('gain_bc1', np.float32), ('gain_bc2', np.float32),
     ('step_flags', np.int32), ('reserved', np.int32),
+    ('magma_s', np.uint64),
 ], align=True)
 ADAM_TENSOR_STEP = np.dtype([
     ('p', np.uint64), ('g', np.uint64), ('m', np.uint64), ('v', np.uint64),
     ('lr', np.float32), ('weight_decay', np.float32), ('beta2', np.float32),
     ('w1', np.float32), ('w2', np.float32), ('bc1', np.float32), ('bc2', np.float32),
     ('eps', np.float32), ('apply', np.int32), ('degenerate', np.int32),
+    ('magma_s', np.uint64),
 ], align=True)
 
 ADAM_SPARSE_STEP = np.dtype([
@@ -54,7 +57,9 @@ ADAM_SPARSE_STEP = np.dtype([
     ('lr', np.float32), ('weight_decay', np.float32), ('beta2', np.float32),
     ('w1', np.float32), ('w2', np.float32), ('bc1', np.float32), ('bc2', np.float32),
     ('eps', np.float32), ('apply', np.int32), ('degenerate', np.int32),
+    ('magma_s', np.uint64), ('magma_work', np.uint64),
 ], align=True)
+SPARSE_MAGMA_WORK_BYTES = 16384
 
 # every exported symbol of include/thorn_amd.h: name -> (restype, argtypes)
 _vp, _sz, _i, _f, _cp = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -71,7 +76,8 @@ SIGNATURES = {
     'thorn_adam_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
     'thorn_adam_plan_destroy': (None, [_vp]),
     'thorn_adam_table_bytes': (_sz, [_vp]),
-    'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp]),
+    'thorn_adam_workspace_bytes': (_sz, [_vp]),
+    'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
     'thorn_adam_step': (_i, [_vp, _vp, _vp]),
     'thorn_adam_sparse_step': (_i, [_vp, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
@@ -80,8 +86,8 @@ SIGNATURES = {
     'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
 KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
-         'symprod']
-ABI_VERSION = 3
+         'symprod', 'magma']
+ABI_VERSION = 4
 
 _lib = None
 
@@ -182,9 +188,10 @@ class AdamPlan:
         self.handle = h
         self.n = len(arr)
         self.table_bytes = lib.thorn_adam_table_bytes(h)
+        self.workspace_bytes = lib.thorn_adam_workspace_bytes(h)
 
-    def fill_table(self, steps: np.ndarray, table_dev: int, table_host: int) -> None:
-        check(self._lib.thorn_adam_fill_table(self.handle, steps.ctypes.data, table_dev, table_host),
+    def fill_table(self, steps: np.ndarray, workspace: Optional[int], table_dev: int, table_host: int) -> None:
+        check(self._lib.thorn_adam_fill_table(self.handle, steps.ctypes.data, workspace, table_dev, table_host),
               'thorn_adam_fill_table')
 
     def step(self, table_dev: int, stream: int) -> None:

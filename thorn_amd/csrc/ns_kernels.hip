@@ -241,7 +241,9 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const bool md = (flags & (kFlagMD | kFlagMDScalar)) != 0;
     const bool apply = (flags & kFlagApply) != 0;
     const bool vec = (flags & kFlagVec4) != 0;
-    const float eta = M.eta, wd = M.wd;
+    // Magma scales the step by the parameter's s, updated on the device by ortho_norm_kernel
+    // (thorn.py:1405)
+    const float eta = (flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta, wd = M.wd;
     float* const p = M.p;
     float psq = 0.f;
     // p chunks (vector path) are requested ahead of their use: those of half 0 before it is

@@ -35,6 +35,7 @@ struct MatLayout {
     int32_t rows, cols, s, l, ldx, lds, tall, flags;
     int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
     size_t x0, xa, xb, gram, poly, qa, qb, tmp, uout, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
+    size_t magpart;
 };
 
 struct TaskOffsets {
@@ -133,9 +134,13 @@ struct thorn_adam_plan {
     std::vector<int64_t> numel;
     std::vector<int32_t> order;
     std::vector<int32_t> starts;
+    std::vector<int64_t> chunk0;   // per tensor: its first 4096-element chunk in the launch
     size_t table_bytes = 0;
     size_t starts_off = 0, order_off = 0;
+    size_t mg_starts_off = 0, mg_order_off = 0;   // task list of the Magma tensors (per step)
+    size_t ws_bytes = 0;
     int32_t total = 0;
+    int32_t mg_n = 0, mg_total = 0;   // Magma tensors and their chunks in the last filled table
     LaunchTimer timer;
 };
 
@@ -330,6 +335,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.rowscale = pnn ? take(sizeof(float) * L.rows) : kNone;
         L.scal = take(sizeof(float) * 8);
         L.psqpart = md ? take(sizeof(float) * L.n_psq) : kNone;
+        L.magpart = take(sizeof(float4) * mom_tiles);
         plan->mats.push_back(L);
     }
     plan->ws_bytes = std::max<size_t>(ws, kAlign);
@@ -457,12 +463,25 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.rowscale = static_cast<float*>(at(L.rowscale));
         M.scal = static_cast<float*>(at(L.scal));
         M.psqpart = static_cast<float*>(at(L.psqpart));
+        M.magpart = static_cast<float4*>(at(L.magpart));
+        M.magma_s = S.magma_s;
+        M.magma_n = 0;
+        if (S.magma_s && (i == 0 || steps[i - 1].magma_s != S.magma_s)) {   // first matrix of a parameter
+            int cnt = 1;
+            while (i + cnt < n && steps[i + cnt].magma_s == S.magma_s) ++cnt;
+            M.magma_n = cnt;
+        }
         M.rows = L.rows; M.cols = L.cols; M.s = L.s; M.l = L.l;
         M.ldx = L.ldx; M.lds = L.lds; M.tall = L.tall;
         int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
         if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m)) flags |= thorn::kFlagVec4;
         if (workspace == plan->stepped_ws && !md && !mds) flags |= thorn::kFlagPrescaled;
         else any_exact = true;
+        if (S.magma_s) {
+            if (reinterpret_cast<uintptr_t>(S.magma_s) & 3u)
+                return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: magma_s must be 4-byte aligned");
+            flags |= thorn::kFlagMagma;
+        }
         M.flags = flags;
         any_apply = any_apply || (flags & thorn::kFlagApply);
         M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
@@ -597,12 +616,14 @@ int thorn_adam_plan_create(const int64_t* numel, int n, thorn_adam_plan_t* out) 
     if (n < 0 || (n > 0 && !numel)) return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: bad tensor list");
     auto* plan = new thorn_adam_plan();
     plan->numel.assign(numel, numel + n);
+    plan->chunk0.assign(n, 0);
     int64_t acc = 0;
     for (int i = 0; i < n; ++i) {
         if (numel[i] < 0) {
             delete plan;
             return fail(THORN_ERR_INVALID, "thorn_adam_plan_create: negative numel");
         }
+        plan->chunk0[i] = acc;
         if (numel[i] == 0) continue;
         plan->order.push_back(i);
         plan->starts.push_back(static_cast<int32_t>(acc));
@@ -619,7 +640,12 @@ int thorn_adam_plan_create(const int64_t* numel, int n, thorn_adam_plan_t* out) 
     off = align_up(off + sizeof(int32_t) * std::max<size_t>(1, plan->order.size()), 16);
     plan->starts_off = off;
     off = align_up(off + sizeof(int32_t) * plan->starts.size(), 16);
+    plan->mg_order_off = off;
+    off = align_up(off + sizeof(int32_t) * std::max<size_t>(1, plan->order.size()), 16);
+    plan->mg_starts_off = off;
+    off = align_up(off + sizeof(int32_t) * (plan->order.size() + 1), 16);
     plan->table_bytes = off;
+    plan->ws_bytes = align_up(sizeof(float4) * std::max<int64_t>(1, acc), kAlign);
     *out = plan;
     return THORN_OK;
 }
@@ -628,16 +654,22 @@ void thorn_adam_plan_destroy(thorn_adam_plan_t plan) { delete plan; }
 
 size_t thorn_adam_table_bytes(thorn_adam_plan_t plan) { return plan ? plan->table_bytes : 0; }
 
-int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* table_dev,
-                          void* table_host) {
+size_t thorn_adam_workspace_bytes(thorn_adam_plan_t plan) { return plan ? plan->ws_bytes : 0; }
+
+int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* steps, void* workspace,
+                          void* table_dev, void* table_host) {
     if (!plan || !table_dev || !table_host) return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: null argument");
     const int n = static_cast<int>(plan->numel.size());
     if (n > 0 && !steps) return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: null steps");
     if ((reinterpret_cast<uintptr_t>(table_dev) % 64) != 0)
         return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: table_dev must be 64-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(workspace) % kAlign) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: workspace must be 256-byte aligned");
     char* host = static_cast<char*>(table_host);
     std::memset(host, 0, plan->table_bytes);
     auto* ts = reinterpret_cast<thorn::AdamTensor*>(host);
+    std::vector<int32_t> mg_order, mg_starts;
+    int64_t mg_acc = 0;
     for (int i = 0; i < n; ++i) {
         const ThornAdamTensorStep& S = steps[i];
         if (plan->numel[i] > 0 && (!S.g || !S.m || !S.v || (S.apply && !S.p)))
@@ -655,10 +687,27 @@ int thorn_adam_fill_table(thorn_adam_plan_t plan, const ThornAdamTensorStep* ste
         if (S.degenerate) f |= thorn::kAdamDegenerate;
         if (S.eps == 0.f) f |= thorn::kAdamAtan2;
         if ((!S.apply || aligned16(S.p)) && aligned16(S.g) && aligned16(S.m) && aligned16(S.v)) f |= thorn::kAdamVec4;
+        if (S.magma_s && plan->numel[i] > 0) {
+            if (!workspace)
+                return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: Magma needs the workspace");
+            if (reinterpret_cast<uintptr_t>(S.magma_s) & 3u)
+                return fail(THORN_ERR_INVALID, "thorn_adam_fill_table: magma_s must be 4-byte aligned");
+            f |= thorn::kAdamMagma;
+            T.magma_s = S.magma_s;
+            T.magpart = static_cast<float4*>(workspace) + plan->chunk0[i];
+            mg_order.push_back(i);
+            mg_starts.push_back(static_cast<int32_t>(mg_acc));
+            mg_acc += cdiv(plan->numel[i], thorn::kAdamChunk);
+        }
         T.flags = f;
     }
+    mg_starts.push_back(static_cast<int32_t>(mg_acc));
     std::memcpy(host + plan->order_off, plan->order.data(), sizeof(int32_t) * plan->order.size());
     std::memcpy(host + plan->starts_off, plan->starts.data(), sizeof(int32_t) * plan->starts.size());
+    std::memcpy(host + plan->mg_order_off, mg_order.data(), sizeof(int32_t) * mg_order.size());
+    std::memcpy(host + plan->mg_starts_off, mg_starts.data(), sizeof(int32_t) * mg_starts.size());
+    plan->mg_n = static_cast<int32_t>(mg_order.size());
+    plan->mg_total = static_cast<int32_t>(mg_acc);
     return THORN_OK;
 }
 
@@ -672,9 +721,23 @@ int thorn_adam_step(thorn_adam_plan_t plan, const void* table_dev, void* stream)
     tl.n = static_cast<int32_t>(plan->order.size());
     tl.total = plan->total;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int slot = plan->timer.begin(THORN_KIND_ADAM, st);
-    hipLaunchKernelGGL(thorn::adam_kernel, dim3(plan->total), dim3(256), 0, st,
-                       reinterpret_cast<const thorn::AdamTensor*>(dev), tl);
+    const auto* ts = reinterpret_cast<const thorn::AdamTensor*>(dev);
+    int slot;
+    if (plan->mg_n > 0) {   // Magma: the statistics of g and m must be complete before any p moves
+        thorn::TaskList mg;
+        mg.order = reinterpret_cast<const int32_t*>(dev + plan->mg_order_off);
+        mg.starts = reinterpret_cast<const int32_t*>(dev + plan->mg_starts_off);
+        mg.n = plan->mg_n;
+        mg.total = plan->mg_total;
+        slot = plan->timer.begin(THORN_KIND_MAGMA, st);
+        hipLaunchKernelGGL(thorn::adam_magma_stats_kernel, dim3(mg.total), dim3(256), 0, st, ts, mg);
+        if (int rc = check_launch("adam_magma_stats_kernel")) return rc;
+        hipLaunchKernelGGL(thorn::adam_magma_finalize_kernel, dim3(mg.n), dim3(256), 0, st, ts, mg.order);
+        plan->timer.end(slot, st);
+        if (int rc = check_launch("adam_magma_finalize_kernel")) return rc;
+    }
+    slot = plan->timer.begin(THORN_KIND_ADAM, st);
+    hipLaunchKernelGGL(thorn::adam_kernel, dim3(plan->total), dim3(256), 0, st, ts, tl);
     plan->timer.end(slot, st);
     return check_launch("adam_kernel");
 }
@@ -701,8 +764,23 @@ int thorn_adam_sparse_step(const ThornAdamSparseStep* S, void* stream) {
     a.s.degenerate = S->degenerate != 0;
     a.s.atan2_mode = S->eps == 0.f;
     a.vec = S->row_len % 4 == 0 && aligned16(S->p) && aligned16(S->m) && aligned16(S->v) && aligned16(S->g_values);
-    hipLaunchKernelGGL(thorn::adam_sparse_kernel, dim3(static_cast<unsigned>(S->nnz)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
+    a.magma_s = S->magma_s;
+    a.magma_work = static_cast<float4*>(S->magma_work);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (S->magma_s) {
+        if (!S->magma_work) return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: Magma needs magma_work");
+        if ((reinterpret_cast<uintptr_t>(S->magma_s) & 3u) != 0 ||
+            (reinterpret_cast<uintptr_t>(S->magma_work) & 15u) != 0)
+            return fail(THORN_ERR_INVALID, "thorn_adam_sparse_step: misaligned Magma buffer");
+        constexpr int64_t kSlots = THORN_SPARSE_MAGMA_WORK_BYTES / sizeof(float4);
+        const int nb = static_cast<int>(std::min<int64_t>(S->nnz, kSlots));
+        hipLaunchKernelGGL(thorn::adam_sparse_magma_kernel, dim3(nb), dim3(256), 0, st, a, S->nnz);
+        if (int rc = check_launch("adam_sparse_magma_kernel")) return rc;
+        hipLaunchKernelGGL(thorn::adam_sparse_magma_finalize_kernel, dim3(1), dim3(256), 0, st, a.magma_work, nb,
+                           S->magma_s);
+        if (int rc = check_launch("adam_sparse_magma_finalize_kernel")) return rc;
+    }
+    hipLaunchKernelGGL(thorn::adam_sparse_kernel, dim3(static_cast<unsigned>(S->nnz)), dim3(256), 0, st, a);
     return check_launch("adam_sparse_kernel");
 }
 

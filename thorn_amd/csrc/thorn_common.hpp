@@ -153,6 +153,7 @@ enum OrthoFlags : int32_t {
     kFlagApply = 16,     // the parameter is updated this step
     kFlagVec4 = 32,      // p, g, m 16-byte aligned and cols % 4 == 0: float4 path
     kFlagPrescaled = 64, // first iterate written in f16 as u * 2^k, 2^k from the previous step
+    kFlagMagma = 128,    // Magma: statistics into magpart, eta scaled by *magma_s
 };
 
 // One matrix of an orthogonalized group. All user tensors are fp32, row-major rows x cols,
@@ -186,6 +187,8 @@ struct OrthoMat {
     float* rowscale;   // [rows] per-row rsqrt(mean u'^2)
     float* scal;       // [8] per-matrix scalars (see kScal*)
     float* psqpart;    // [n_psq] partial sums of p^2 after the update
+    float* magma_s;    // Magma: state['s'] of the parameter this matrix belongs to
+    float4* magpart;   // [mom_tiles] Magma partial sums (g.m, g.g, m.m, 0) per elementwise tile
 
     int32_t rows, cols, s, l;
     int32_t ldx, lds;
@@ -200,6 +203,7 @@ struct OrthoMat {
     int32_t g3_tiles_m, g3_tiles_n;
     int32_t n_psq;
     int32_t apply_tiles;   // elementwise tiles of the per-row-normalized apply kernel
+    int32_t magma_n;       // Magma: matrices of the parameter when this is its first one, else 0
 };
 
 enum ScalSlot : int {
@@ -237,6 +241,8 @@ struct AdamTensor {
     float bc1, bc2;
     float eps;
     int32_t flags;  // kAdam*
+    float* magma_s;    // Magma: state['s']
+    float4* magpart;   // Magma: [chunks] partial sums (g.m, g.g, m.m, 0) per 4096-element chunk
 };
 
 enum AdamFlags : int32_t {
@@ -244,6 +250,7 @@ enum AdamFlags : int32_t {
     kAdamDegenerate = 2,  // rectification says rho <= 4: u = m, lr*rect == 0
     kAdamAtan2 = 4,       // eps == 0: Adam-atan2
     kAdamVec4 = 8,        // all four pointers 16-byte aligned: float4 path
+    kAdamMagma = 16,      // Magma statistics, lr scaled by *magma_s
 };
 
 }  // namespace thorn

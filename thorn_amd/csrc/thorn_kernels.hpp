@@ -47,4 +47,50 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
     p = cautious_step(p, u, s.lr, s.wd);
 }
 
+// Magma statistics (thorn.py:806-836): sums of g*m, g*g and m*m, where m is the moment before this
+// step's update.
+struct MagmaSums {
+    float gm = 0.f, gg = 0.f, mm = 0.f;
+    __device__ __forceinline__ void add(float g, float m) {
+        gm = fmaf(g, m, gm);
+        gg = fmaf(g, g, gg);
+        mm = fmaf(m, m, mm);
+    }
+    __device__ __forceinline__ void add(const float4& part) {
+        gm += part.x;
+        gg += part.y;
+        mm += part.z;
+    }
+};
+
+// Block reduction of MagmaSums in a fixed order; every thread returns the totals. `scratch` holds
+// at least 3 * blockDim.x / 64 floats.
+__device__ __forceinline__ MagmaSums block_sum(MagmaSums v, float* scratch) {
+    v.gm = wave_sum(v.gm);
+    v.gg = wave_sum(v.gg);
+    v.mm = wave_sum(v.mm);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        scratch[3 * wid] = v.gm;
+        scratch[3 * wid + 1] = v.gg;
+        scratch[3 * wid + 2] = v.mm;
+    }
+    __syncthreads();
+    MagmaSums t;
+    for (int i = 0; i < nw; ++i) t.add(make_float4(scratch[3 * i], scratch[3 * i + 1], scratch[3 * i + 2], 0.f));
+    return t;
+}
+
+// s <- p s + (1 - p) sigmoid(cos / tau) with p = 0.9, tau = 2 (thorn.py:806-830); cos as
+// torch.nn.functional.cosine_similarity computes it, each norm clamped at eps = 1e-8. The constants
+// are the fp32 roundings of the reference's Python scalars, as its fp32 tensor ops use them.
+__device__ __forceinline__ void magma_update(const MagmaSums& t, float* s) {
+    const float gn = fmaxf(sqrtf(t.gg), 1e-8f), mn = fmaxf(sqrtf(t.mm), 1e-8f);
+    const float cs = t.gm / (gn * mn);
+    const float st = sigmoid_f(cs / 2.f);
+    const float s_old = ldg<float>(s);
+    stg<float>(s, 0.9f * s_old + 0.1f * st);
+}
+
 }  // namespace thorn

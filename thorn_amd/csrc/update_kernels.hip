@@ -20,10 +20,11 @@ __device__ __forceinline__ int tile_col(int c0, int lane, int e, bool vec) {
 // ---------------------------------------------------------------------------------------------
 //   md:   G = softplus(rg_i) * softplus(cg_j); p /= G; pg = p * g; g *= G
 //         rowpart += pg * softplus(cg_j); colpart += pg * softplus(rg_i)
+//   magma: magpart += (g*m, g*g, m*m) with the moment before the update (thorn.py:1390-1392)
 //   m = m * beta1 + g;  u = g + beta1 * m;  x0 = u (fp32);  normpart += u^2
 __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
     __shared__ float colred[4][kTileC];
-    __shared__ float scratch[4];
+    __shared__ float scratch[12];
     const int b = blockIdx.x;
     const int k = find_task(tl.starts, tl.n, b);
     const OrthoMat& M = mats[tl.order[k]];
@@ -35,6 +36,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const bool vec = M.flags & kFlagVec4;
     const bool keep_grad = M.flags & kFlagKeepGrad;
     const bool presc = M.flags & kFlagPrescaled;   // never combined with md
+    const bool magma = M.flags & kFlagMagma;
     const float prescale = presc ? M.scal[kScalPrescale] : 1.f;
     const float beta1 = M.beta1;
     const int nrows = M.rows - r0;   // rows of this wave's 4 that exist (may be <= 0)
@@ -82,6 +84,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
 
     float colacc[4] = {0.f, 0.f, 0.f, 0.f};
     float nrm = 0.f;
+    MagmaSums ms;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         if (rr >= nrows) break;   // uniform over the wave
@@ -104,6 +107,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                 rowacc += md ? pg * spc[e] : pg;
                 colacc[e] += pg * spr;
             }
+            if (magma) ms.add(g, mv[rr][e]);
             const float m = mv[rr][e] * beta1 + g;
             mv[rr][e] = m;
             const float u = fmaf(m, beta1, g);
@@ -162,6 +166,10 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     }
     const float total = block_sum(nrm, scratch);
     if (threadIdx.x == 0) M.normpart[local] = total;
+    if (magma) {
+        const MagmaSums t = block_sum(ms, scratch);
+        if (threadIdx.x == 0) stg<float4>(M.magpart + local, make_float4(t.gm, t.gg, t.mm, 0.f));
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -170,7 +178,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
 // before the parameter update, so they run here, before Newton-Schulz.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats) {
-    __shared__ float scratch[4];
+    __shared__ float scratch[12];
     const OrthoMat& M = mats[blockIdx.x];
     const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
     float s = 0.f;
@@ -197,6 +205,19 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
         } else if (!(M.scal[kScalPrescale] > 0.f)) {
             M.scal[kScalPrescale] = 1.f;
         }
+    }
+
+    // Magma (thorn.py:822-830): the first matrix of a parameter reduces the tile sums of all of
+    // the parameter's matrices and moves s, which the apply kernels read later in the stream
+    if ((M.flags & kFlagMagma) && M.magma_n > 0) {
+        MagmaSums t;
+        for (int q = 0; q < M.magma_n && (int)blockIdx.x + q < n_mats; ++q) {
+            const OrthoMat& Q = mats[blockIdx.x + q];
+            const int nt = Q.mom_tiles_r * Q.mom_tiles_c;
+            for (int i = threadIdx.x; i < nt; i += 256) t.add(ldg<float4>(Q.magpart + i));
+        }
+        t = block_sum(t, scratch);
+        if (threadIdx.x == 0) magma_update(t, M.magma_s);
     }
 
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
@@ -272,6 +293,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
     const float gamma = M.scal[kScalGamma];
+    const float eta = (M.flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta;   // thorn.py:1405
     const bool md = M.flags & (kFlagMD | kFlagMDScalar);
     const bool vec = M.flags & kFlagVec4;
     const int nrows = M.rows - r0;
@@ -301,7 +323,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float u = ((float)uv[rr][e] * sv[rr]) * gamma;
-                p[e] = cautious_step(p[e], u, M.eta, M.wd);
+                p[e] = cautious_step(p[e], u, eta, M.wd);
                 psq += p[e] * p[e];
             }
             stg_nt<float4>(M.p + (int64_t)(r0 + rr) * M.cols + c, make_float4(p[0], p[1], p[2], p[3]));
@@ -318,7 +340,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
                 const int c = c0 + lane + 64 * e;
                 if (c >= M.cols) continue;
                 const float u = ((float)urow[c] * s) * gamma;
-                const float p = cautious_step(M.p[rbase + c], u, M.eta, M.wd);
+                const float p = cautious_step(M.p[rbase + c], u, eta, M.wd);
                 M.p[rbase + c] = p;
                 psq += p * p;
             }
@@ -395,6 +417,7 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict_
     s.lr = T.lr; s.wd = T.wd; s.beta2 = T.beta2; s.w1 = T.w1; s.w2 = T.w2;
     s.bc1 = T.bc1; s.bc2 = T.bc2; s.eps = T.eps;
     s.apply = T.flags & kAdamApply;
+    if (s.apply && (T.flags & kAdamMagma)) s.lr *= ldg<float>(T.magma_s);   // thorn.py:1712
     s.degenerate = T.flags & kAdamDegenerate;
     s.atan2_mode = T.flags & kAdamAtan2;
     constexpr int Q = kAdamChunk / 1024;
@@ -432,6 +455,49 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict_
     }
 }
 
+// Magma statistics of the Adam tensors (thorn.py:1702): g and the moment before the update, per
+// 4096-element chunk (the chunks of adam_kernel), over the tensors of the Magma task list.
+__global__ __launch_bounds__(256) void adam_magma_stats_kernel(const AdamTensor* __restrict__ ts, TaskList tl) {
+    __shared__ float scratch[12];
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const AdamTensor& T = ts[tl.order[k]];
+    const int local = b - tl.starts[k];
+    const int64_t base = (int64_t)local * kAdamChunk;
+    MagmaSums ms;
+    if ((T.flags & kAdamVec4) && base + kAdamChunk <= T.n) {
+#pragma unroll
+        for (int q = 0; q < kAdamChunk / 1024; ++q) {
+            const int64_t i = base + (int64_t)(q * 256 + threadIdx.x) * 4;
+            const float4 g4 = ldg<float4>(T.g + i), m4 = ldg<float4>(T.m + i);
+            ms.add(g4.x, m4.x);
+            ms.add(g4.y, m4.y);
+            ms.add(g4.z, m4.z);
+            ms.add(g4.w, m4.w);
+        }
+    } else {
+        for (int q = 0; q < kAdamChunk / 256; ++q) {
+            const int64_t j = base + q * 256 + threadIdx.x;
+            if (j >= T.n) break;
+            ms.add(ldg<float>(T.g + j), ldg<float>(T.m + j));
+        }
+    }
+    const MagmaSums t = block_sum(ms, scratch);
+    if (threadIdx.x == 0) stg<float4>(T.magpart + local, make_float4(t.gm, t.gg, t.mm, 0.f));
+}
+
+// One block per Magma tensor (order[blockIdx.x]): its chunk sums in order, then s (thorn.py:822-830).
+__global__ __launch_bounds__(256) void adam_magma_finalize_kernel(const AdamTensor* __restrict__ ts,
+                                                                  const int32_t* __restrict__ order) {
+    __shared__ float scratch[12];
+    const AdamTensor& T = ts[order[blockIdx.x]];
+    const int64_t chunks = (T.n + kAdamChunk - 1) / kAdamChunk;
+    MagmaSums t;
+    for (int64_t i = threadIdx.x; i < chunks; i += 256) t.add(ldg<float4>(T.magpart + i));
+    t = block_sum(t, scratch);
+    if (threadIdx.x == 0) magma_update(t, T.magma_s);
+}
+
 // Row-sparse Adam (thorn.py:1673-1700): block k updates row rows_idx[k] of p, m, v with gradient
 // row k, the same per-element arithmetic as adam_kernel; rows outside [0, rows) are skipped.
 struct SparseAdamArgs {
@@ -443,13 +509,52 @@ struct SparseAdamArgs {
     int64_t rows, row_len;
     AdamScalars s;
     int32_t vec;   // row_len % 4 == 0 and p, m, v, gv 16-byte aligned
+    float* magma_s;     // Magma: state['s'] (lr scaled by it), or null
+    float4* magma_work; // Magma: one partial-sum slot per block of adam_sparse_magma_kernel
 };
+
+// Magma statistics of a row-sparse gradient (thorn.py:1676-1679): gradient rows against the
+// gathered moment rows. Block b takes gradient rows b, b + gridDim.x, ... and writes one partial
+// sum; adam_sparse_magma_finalize_kernel reduces the gridDim.x partials in order.
+__global__ __launch_bounds__(256) void adam_sparse_magma_kernel(SparseAdamArgs a, int64_t nnz) {
+    __shared__ float scratch[12];
+    MagmaSums ms;
+    for (int64_t k = blockIdx.x; k < nnz; k += gridDim.x) {
+        const int64_t r = ldg<int64_t>(a.rows_idx + k);
+        if (r < 0 || r >= a.rows) continue;
+        const float* g = a.gv + k * a.row_len;
+        const float* m = a.m + r * a.row_len;
+        if (a.vec) {
+            for (int64_t c = (int64_t)threadIdx.x * 4; c < a.row_len; c += 1024) {
+                const float4 g4 = ldg<float4>(g + c), m4 = ldg<float4>(m + c);
+                ms.add(g4.x, m4.x);
+                ms.add(g4.y, m4.y);
+                ms.add(g4.z, m4.z);
+                ms.add(g4.w, m4.w);
+            }
+        } else {
+            for (int64_t c = threadIdx.x; c < a.row_len; c += 256) ms.add(ldg<float>(g + c), ldg<float>(m + c));
+        }
+    }
+    const MagmaSums t = block_sum(ms, scratch);
+    if (threadIdx.x == 0) stg<float4>(a.magma_work + blockIdx.x, make_float4(t.gm, t.gg, t.mm, 0.f));
+}
+
+__global__ __launch_bounds__(256) void adam_sparse_magma_finalize_kernel(const float4* __restrict__ part, int n,
+                                                                         float* s) {
+    __shared__ float scratch[12];
+    MagmaSums t;
+    for (int i = threadIdx.x; i < n; i += 256) t.add(ldg<float4>(part + i));
+    t = block_sum(t, scratch);
+    if (threadIdx.x == 0) magma_update(t, s);
+}
 
 __global__ __launch_bounds__(256) void adam_sparse_kernel(SparseAdamArgs a) {
     const int64_t k = blockIdx.x;
     const int64_t r = ldg<int64_t>(a.rows_idx + k);
     if (r < 0 || r >= a.rows) return;
-    const AdamScalars& s = a.s;
+    AdamScalars s = a.s;
+    if (s.apply && a.magma_s) s.lr *= ldg<float>(a.magma_s);   // thorn.py:1687
     const float* g = a.gv + k * a.row_len;
     float* p = a.p + r * a.row_len;
     float* m = a.m + r * a.row_len;

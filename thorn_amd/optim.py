@@ -6,10 +6,14 @@ parameter-group keys and defaults, the validation errors, the per-parameter stat
 What runs underneath is different: every group's whole step is a handful of grouped HIP launches
 on the current stream (see ``thorn_amd.csrc``), driven through the C ABI in include/thorn_amd.h.
 
+Magma ``momentum_align`` (thorn.py:800-836) runs without the reference's ``.item()`` host sync:
+the random mask comes from the per-parameter PRNG state, a host integer as in the reference, and
+the cosine-similarity EMA ``s`` stays on the device, where the kernels read it as a learning-rate
+factor.
+
 Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
-behaviour): Magma ``momentum_align`` (thorn.py:800-836), DTensor/FSDP2 parameters
-(thorn.py:979-1186, 1459-1581), ``decouple_md`` on non-orthogonalized groups or with sparse
-gradients, and non-fp32 parameters.
+behaviour): DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), ``decouple_md`` on
+non-orthogonalized groups or with sparse gradients, and non-fp32 parameters.
 """
 from __future__ import annotations
 
@@ -189,6 +193,31 @@ def _needs_neuron_norm(shape, group: _Group) -> bool:
     return group.betas[1] > 0 and (shape[-2] > shape[-1] or group.force_per_neuron_norm)
 
 
+_W1_C = 0xD07EBC63274654C7
+_U64 = (1 << 64) - 1
+
+
+def _w1rand(s: int) -> tuple[int, int]:
+    """Magma's PRNG (thorn.py:800-804): a Weyl step s += C, then the xor of the high and low
+    64-bit halves of the 128-bit product s * (s ^ C). Returns (new state, draw)."""
+    s = (s + _W1_C) & _U64
+    t = s * (s ^ _W1_C)
+    return s, ((t >> 64) ^ t) & _U64
+
+
+def _magma_seed(p: torch.Tensor) -> int:
+    """Initial Magma PRNG state (thorn.py:1616-1619): 63 random bits from the generator of the
+    parameter's device, so that torch.manual_seed fixes it as in the reference."""
+    return int(torch.randint(0, (1 << 63) - 1, (), device=p.device, dtype=torch.uint64).item())
+
+
+def _magma_unmasked(state: dict) -> bool:
+    """Advances the parameter's PRNG; False when this step is masked (an odd draw,
+    thorn.py:831-833). The new s, which scales an unmasked step, is computed on the device."""
+    state['random_state'], draw = _w1rand(state['random_state'])
+    return draw % 2 == 0
+
+
 def _check_tensor(t: torch.Tensor, what: str) -> None:
     if t.dtype != torch.float32:
         raise NotImplementedError(f'THORN on MI355X supports fp32 tensors only; {what} is {t.dtype}')
@@ -231,7 +260,8 @@ class _OrthoRunner:
         self.md = group.decouple_md
         self.split_gain = group.split_gain
 
-    def run(self, opt: 'THORN', group: _Group) -> None:
+    def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None) -> None:
+        """unmasked: id(p) -> False for a parameter whose Magma mask skips this step."""
         params, steps = self.params, self.steps
         n = len(self.owner)
         elem = np.asarray([p.shape[-2] * p.shape[-1] for p in params], dtype=np.int64)[self.owner]
@@ -249,9 +279,13 @@ class _OrthoRunner:
         steps['beta1'] = group.betas[0]
         # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
         # momentum (and the decouple_md round trip) runs every step
-        due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 for s in states], dtype=bool)[own]
+        due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 and (unmasked is None or unmasked[id(p)])
+                          for p, s in zip(params, states)], dtype=bool)[own]
         keep = 0 if group.none_grad else _lib.STEP_KEEP_GRAD
         steps['step_flags'] = np.where(due, _lib.STEP_APPLY | keep, keep)
+        # Magma: every matrix of a parameter carries the parameter's s (thorn.py:1392, 1405)
+        steps['magma_s'] = (np.asarray([s['s'].data_ptr() for s in states], dtype=np.uint64)[own]
+                            if group.momentum_align else 0)
         if self.md:
             gb1, gb2 = group.gain_betas
             steps['gain_lr'] = group.gain_lr_
@@ -290,7 +324,7 @@ class _OrthoRunner:
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
-        if not due.any():   # no polar factor this step: momentum (and gains round trip) only
+        if not due.any():   # no polar factor this step: momentum (gains round trip, Magma s) only
             coeffs = coeffs[:0]
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
                        torch.cuda.current_stream(self.device).cuda_stream)
@@ -311,11 +345,13 @@ class _AdamRunner:
         self.device = device
         self.plan = _lib.AdamPlan([p.numel() for p in params])
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
+        self.workspace = torch.empty(max(256, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
 
-    def run(self, entries: list, update_rate: int = 1) -> None:
+    def run(self, entries: list, update_rate: int = 1, unmasked: Optional[dict] = None) -> None:
         """entries: (p, state, group) per tensor, in plan order. A tensor's parameter is written
-        only when its step is due under update_rate (thorn.py:1706-1707); m and v always are."""
+        only when its step is due under update_rate (thorn.py:1706-1707) and not masked by Magma;
+        m and v always are."""
         s = self.steps
         for k, (p, state, group) in enumerate(entries):
             step = state['step']
@@ -333,10 +369,11 @@ class _AdamRunner:
             s[k]['bc1'] = 1 / (1 - beta1 ** step)
             s[k]['bc2'] = 1 / (1 - beta2 ** step)
             s[k]['eps'] = group.eps
-            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 else 0
+            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 and (unmasked is None or unmasked[id(p)]) else 0
             s[k]['degenerate'] = 1 if rect == 0.0 else 0
+            s[k]['magma_s'] = state['s'].data_ptr() if group.momentum_align else 0
         host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
-        self.plan.fill_table(s, self.table.data_ptr(), host.data_ptr())
+        self.plan.fill_table(s, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
         self.plan.step(self.table.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
 
@@ -383,6 +420,7 @@ class THORN(Optimizer):
             for p in group['params']:
                 self._param_to_group[id(p)] = group
         self._runners: dict = {}
+        self._magma_scratch: dict = {}
         if isinstance(params, nn.Module) and conf.get('gradient_release', False):
             self.setup_gradient_release(params)
 
@@ -426,11 +464,15 @@ class THORN(Optimizer):
                 state['gain_moment'] = torch.zeros((), dtype=p.dtype, device=p.device)
                 state['gain_variance'] = torch.zeros((), dtype=p.dtype, device=p.device)
             state['target_norm'] = group.target_norm_(p)
+        if group.momentum_align:
+            state['random_state'] = _magma_seed(p)
+            state['s'] = torch.ones((), dtype=p.dtype, device=p.device)
 
     def _validate(self, p: torch.Tensor, group: _Group) -> None:
-        if group.momentum_align:
-            raise NotImplementedError('momentum_align (Magma) is not implemented on the MI355X path')
         g = p.grad
+        if not group.orthogonalize and group.decouple_md:
+            raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
+                                      'on the MI355X path')
         if g.is_sparse and group.orthogonalize:
             # the reference's momentum step g + beta1 * m (thorn.py:1381) fails the same way
             raise RuntimeError('add(sparse, dense) is not supported: an orthogonalized parameter needs a '
@@ -449,14 +491,12 @@ class THORN(Optimizer):
             _check_tensor(g, 'gradient')
         if g.device != p.device:
             raise RuntimeError('gradient and parameter are on different devices')
-        if not group.orthogonalize and group.decouple_md:
-            raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
-                                      'on the MI355X path')
 
-    def _sparse_adam(self, p: torch.Tensor, g: torch.Tensor, group: _Group) -> None:
+    def _sparse_adam(self, p: torch.Tensor, g: torch.Tensor, group: _Group, unmasked: bool = True) -> None:
         """Row-sparse Adam on the coalesced gradient g (thorn.py:1673-1700): the gradient's rows
         of p, m and v take the ordinary Adam step (thorn_adam_sparse_step); the other rows keep
-        their parameter and state."""
+        their parameter and state. With Magma, s moves from the gradient rows and the gathered
+        moment rows, and a masked step updates m and v only."""
         state = self.state[p]
         step = state['step']
         beta1, beta2 = group.betas
@@ -482,10 +522,21 @@ class THORN(Optimizer):
         rec['bc1'] = 1 / (1 - beta1 ** step)
         rec['bc2'] = 1 / (1 - beta2 ** step)
         rec['eps'] = group.eps
-        rec['apply'] = 1 if (step + 1) % self._update_rate == 0 else 0
+        rec['apply'] = 1 if (step + 1) % self._update_rate == 0 and unmasked else 0
         rec['degenerate'] = 1 if rect == 0.0 else 0
+        if group.momentum_align:
+            rec['magma_s'] = state['s'].data_ptr()
+            rec['magma_work'] = self._magma_work(p.device).data_ptr()
         with torch.cuda.device(p.device):
             _lib.adam_sparse_step(rec, torch.cuda.current_stream(p.device).cuda_stream)
+
+    def _magma_work(self, dev: torch.device) -> torch.Tensor:
+        """Device scratch of the sparse Magma statistics (one per device; steps on one stream)."""
+        w = self._magma_scratch.get(dev)
+        if w is None:
+            w = torch.empty(_lib.SPARSE_MAGMA_WORK_BYTES, dtype=torch.uint8, device=dev)
+            self._magma_scratch[dev] = w
+        return w
 
     def _runner(self, key, factory):
         r = self._runners.get(key)
@@ -514,8 +565,12 @@ class THORN(Optimizer):
                     sparse.append((p, g))
                     continue
             live.append(p)
+        # Magma masks, one PRNG draw per parameter that steps (thorn.py:1392, 1679, 1702)
+        unmasked = None
+        if group.momentum_align:
+            unmasked = {id(p): _magma_unmasked(self.state[p]) for p in live + [q for q, _ in sparse]}
         for p, g in sparse:
-            self._sparse_adam(p, g, group)
+            self._sparse_adam(p, g, group, True if unmasked is None else unmasked[id(p)])
         for p, _ in sparse:
             if group.none_grad:
                 p.grad = None
@@ -532,11 +587,11 @@ class THORN(Optimizer):
                            group.decouple_md, group.split_gain, group.force_per_neuron_norm,
                            group.betas[1] > 0)
                     runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev))
-                    runner.run(self, group)
+                    runner.run(self, group, unmasked)
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
                     runner = self._runner(key, lambda: _AdamRunner(ps, dev))
-                    runner.run([(p, self.state[p], group) for p in ps], self._update_rate)
+                    runner.run([(p, self.state[p], group) for p in ps], self._update_rate, unmasked)
         for p in live:
             if group.none_grad:
                 p.grad = None
