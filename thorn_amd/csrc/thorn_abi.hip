@@ -121,6 +121,10 @@ struct thorn_ortho_plan {
     // (Gram Newton-Schulz); sym = upper-triangle tiles of s x s products, g3 = tiles of X updates.
     TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, md{};
     std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, md_order;
+    // The Newton-Schulz and per-row-normalization lists of the last filled table: only the
+    // matrices applied this step (the reference skips the polar factor of the others,
+    // thorn.py:1395-1396, 1436-1441). Same table offsets, fewer entries.
+    TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{};
     LaunchTimer timer;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
@@ -499,12 +503,27 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         sym_blocks[i] = L.sym_tiles;
         g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
     }
+    auto applied_only = [&](const std::vector<int32_t>& order, const TaskOffsets& full,
+                            const std::vector<int64_t>& blocks_of, TaskOffsets& live) {
+        std::vector<int32_t> kept;
+        kept.reserve(order.size());
+        int64_t total = 0;
+        for (int32_t i : order) {
+            if (!(mats[i].flags & thorn::kFlagApply)) continue;
+            kept.push_back(i);
+            total += blocks_of[i];
+        }
+        write_tasks(host, full, kept, blocks_of);
+        live = full;
+        live.n = static_cast<int32_t>(kept.size());
+        live.total = static_cast<int32_t>(total);
+    };
     write_tasks(host, plan->pre, plan->pre_order, mom_blocks);
     for (int q = 0; q < 2; ++q) {
-        write_tasks(host, plan->sym[q], plan->sym_order[q], sym_blocks);
-        write_tasks(host, plan->g3[q], plan->g3_order[q], g3_blocks);
+        applied_only(plan->sym_order[q], plan->sym[q], sym_blocks, plan->sym_live[q]);
+        applied_only(plan->g3_order[q], plan->g3[q], g3_blocks, plan->g3_live[q]);
     }
-    write_tasks(host, plan->pnn, plan->pnn_order, mom_blocks);
+    applied_only(plan->pnn_order, plan->pnn, mom_blocks, plan->pnn_live);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
     plan->any_exact = any_exact;
@@ -559,8 +578,8 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     const uint32_t plain = iters >= 32 ? 0xFFFFFFFEu : ((1u << iters) - 2u);
     const std::vector<ScheduledOp> sched[2] = {ns_schedule(iters, plain, coeffs),
                                                ns_schedule(iters, restart_mask, coeffs)};
-    const thorn::TaskList sym[2] = {task_list(dev, plan->sym[0]), task_list(dev, plan->sym[1])};
-    const thorn::TaskList g3[2] = {task_list(dev, plan->g3[0]), task_list(dev, plan->g3[1])};
+    const thorn::TaskList sym[2] = {task_list(dev, plan->sym_live[0]), task_list(dev, plan->sym_live[1])};
+    const thorn::TaskList g3[2] = {task_list(dev, plan->g3_live[0]), task_list(dev, plan->g3_live[1])};
     const size_t steps = std::max(sched[0].size(), sched[1].size());
     for (size_t k = 0; k < steps; ++k) {
         thorn::NsOp op[2]{};
@@ -577,8 +596,8 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(256), 0, st, mats, tl[1],
                      op[1], tl[0], op[0]);
     }
-    if (plan->pnn.n > 0) {
-        const thorn::TaskList pnn = task_list(dev, plan->pnn);
+    if (plan->pnn_live.n > 0) {
+        const thorn::TaskList pnn = task_list(dev, plan->pnn_live);
         THORN_LAUNCH(THORN_KIND_ROWSTATS, "ortho_rowstats_kernel", thorn::ortho_rowstats_kernel, dim3(pnn.n),
                      dim3(256), 0, st, mats, pnn.order);
         THORN_LAUNCH(THORN_KIND_PNN_APPLY, "ortho_pnn_apply_kernel", thorn::ortho_pnn_apply_kernel, dim3(pnn.total),
