@@ -387,6 +387,9 @@ def main() -> int:
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--config', type=int, default=2)
+    ap.add_argument('--momentum-align', action='store_true',
+                    help='Magma on every group (a variant of the workload, not the headline line: masked '
+                         'matrices skip Newton-Schulz, so the per-launch flops vary and no roofline is given)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--cpu-budget', type=float, default=20.0)
     ap.add_argument('--copy-cal-mib', type=int, default=0,
@@ -411,6 +414,9 @@ def main() -> int:
         copy_calibration(args.copy_cal_mib, dev)
     t0 = time.perf_counter()
     params, grads, groups, mats = build_workload(args.config, dev)
+    if args.momentum_align:
+        for g in groups:
+            g['momentum_align'] = True
     gen_s = time.perf_counter() - t0
     n_m = len(mats)
     opt = thorn_amd.THORN(groups)
@@ -469,7 +475,7 @@ def main() -> int:
     phases = {k: {'ms_per_launch': round(ms / n, 4), 'launches_per_step': n / args.steps}
               for k, (ms, n) in sorted(kinds.items())}
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.config, args.cpu_budget)
+    cpu = None if (args.no_cpu_baseline or args.momentum_align) else cpu_baseline(args.config, args.cpu_budget)
     ms = wall_ms
     out = {
         'metric': 'THORN step ms, 300M Qwen3 param set, 1 GPU; NS TFLOP/s and % MFMA peak',
@@ -485,7 +491,8 @@ def main() -> int:
         'dtype': 'f16',
         'data': 'synthetic',
         'config': {'workload': {2: 'qwen3-300m (BASELINE config 2)', 3: 'qwen3-300m decouple_md (config 3)',
-                                4: 'earshot conv VAD (config 4)', 5: 'qwen3-1.7b matrices (config 5)'}[args.config],
+                                4: 'earshot conv VAD (config 4)', 5: 'qwen3-1.7b matrices (config 5)'}[args.config]
+                   + (' + Magma momentum_align' if args.momentum_align else ''),
                    'matrices': n_m, 'adam_tensors': len(params) - n_m,
                    'ortho_elements': sum(r * c for r, c in mats),
                    'adam_elements': sum(p.numel() for p in params[n_m:]), 'ns_iters': 5,
@@ -508,6 +515,9 @@ def main() -> int:
         'cpu_baseline': cpu,
         'workload_gen_s': round(gen_s, 1),
     }
+    if args.momentum_align:   # NS flops depend on which matrices each step's masks applied
+        out['roofline'] = None
+        out['ns'] = {'ms_per_step': round(ns_ms, 3), 'launches_per_step': ns_launches}
     print(json.dumps(out), flush=True)
     return 0
 
