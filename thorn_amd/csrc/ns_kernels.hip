@@ -246,41 +246,67 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const float eta = (flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta, wd = M.wd;
     float* const p = M.p;
     float psq = 0.f;
-    // p chunks (vector path) are requested ahead of their use: those of half 0 before it is
-    // staged, each chunk of half 1 as soon as the same slot of half 0 has been used (p is read and
-    // written through one pointer, so the compiler would otherwise keep every load behind the
-    // previous chunk's stores).
-    using E = Epi<NsCfg>;
-    float4 pre[E::ROW_CHUNKS][2];
-    auto fetch = [&](int h, int it) {
-        int lr, c8;
-        row_chunk<NsCfg>(it, lr, c8);
-        const int r = m0 + h * NsCfg::WM + lr, c = n0 + c8;
-        if (vec && r < rows && c + 8 <= cols) {
-            const float* pp = p + (int64_t)r * cols + c;
-            pre[it][0] = ldg<float4>(pp);
-            pre[it][1] = ldg<float4>(pp + 4);
+    auto step8 = [&](float (&pv)[8], const float (&v)[8]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float q = cautious_step(pv[e], (float)(_Float16)(v[e] * osc), eta, wd);
+            pv[e] = apply ? q : pv[e];
+            psq += pv[e] * pv[e];
         }
     };
+    using E = Epi<NsCfg>;
+    if (vec && m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols) {
+        // Whole tile inside the matrix (every tile of a matrix with 256-multiple sides). Chunk
+        // `it` of half h is row m0 + h*WM + 8*it + tid/32, columns n0 + 8*(tid%32) .. +7 (the
+        // row_chunk() order); numbered L = h * ROW_CHUNKS + it, chunk L is requested into ring
+        // slot L % D as soon as chunk L - D has been used (the first D before half 0 is staged).
+        // Buffer instructions address it as one resource over the tile's rows (scalar
+        // registers), a per-lane offset shared by every chunk and a wave-uniform row offset, so
+        // no per-chunk address occupies vector registers. No memory operation in the pass is
+        // conditional, so each wait covers exactly the load it needs.
+        static_assert(NsCfg::BN / 8 == 32, "32 lanes per row chunk");
+        constexpr int D = 2;
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
+        const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
+        auto soff = [&](int L) { return ((L / E::ROW_CHUNKS) * NsCfg::WM + 8 * (L % E::ROW_CHUNKS)) * cols * 4; };
+        float4 ring[D][2];
+        auto fetch = [&](int L) {
+            ring[L % D][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, soff(L), 0));
+            ring[L % D][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff + 16, soff(L), 0));
+        };
 #pragma unroll
-    for (int it = 0; it < E::ROW_CHUNKS; ++it) fetch(0, it);
+        for (int L = 0; L < D; ++L) fetch(L);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        for_rows<NsCfg>(acc, smem, h, [&](int it, int half, int lr, int c8, float (&v)[8]) {
-            const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
-            if (r < rows && c < cols) {
+        for (int h = 0; h < 2; ++h)
+            for_rows<NsCfg>(acc, smem, h, [&](int it, int half, int, int, float (&v)[8]) {
+                const int L = half * E::ROW_CHUNKS + it;
+                const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
+                float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                step8(pv, v);
+                // Stored whether or not the matrix is applied (the launch's task lists hold only
+                // applied matrices; otherwise p is written back unchanged). Each of the two
+                // stores covers every other 16 bytes: plain stores, which L2 merges into lines.
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[0], pv[1], pv[2], pv[3])),
+                                                       prs, voff, soff(L), 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[4], pv[5], pv[6], pv[7])),
+                                                       prs, voff + 16, soff(L), 0);
+                if (L + D < 2 * E::ROW_CHUNKS) fetch(L + D);
+                __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: no hoisted LDS reads
+            });
+    } else {   // edge tiles: each chunk loaded where it is used
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
+                const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
+                if (r >= rows || c >= cols) return;
                 float* pp = p + (int64_t)r * cols + c;
                 if (vec && c + 8 <= cols) {
-                    const float4 p0 = pre[it][0], p1 = pre[it][1];
+                    const float4 p0 = ldg<float4>(pp), p1 = ldg<float4>(pp + 4);
                     float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float q = cautious_step(pv[e], (float)(_Float16)(v[e] * osc), eta, wd);
-                        pv[e] = apply ? q : pv[e];
-                        psq += pv[e] * pv[e];
-                    }
-                    if (apply) {   // each of the two stores covers every other 16 bytes: plain
-                                   // stores, which L2 merges into whole lines
+                    step8(pv, v);
+                    if (apply) {
                         stg<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
                         stg<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
                     }
@@ -294,9 +320,8 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
                         psq += x * x;
                     }
                 }
-            }
-            if (half == 0) fetch(1, it);
-        });
+            });
+    }
     if (md) {
         const float t = block_sum(psq, scratch);
         if (threadIdx.x == 0) M.psqpart[local] = t;
