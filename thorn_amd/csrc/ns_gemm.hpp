@@ -339,17 +339,26 @@ __device__ __forceinline__ void stage_rows(floatx16 (&acc)[C::TM][C::TN], char* 
 // fn(it, local_row, col8, float (&v)[8]): v = staged[local_row][col8 .. col8+7] for the chunks
 // with keep(local_row, col8); `it` numbers this thread's chunks 0 .. ROW_CHUNKS-1, in the order
 // given by row_chunk().
+// Chunk `it` is row 8*it + tid/(BN/8) (256 threads cover 8 rows per chunk), so its staging
+// address is one per-thread base plus the constant it * (8 * NS + 4) floats (row_base adds 4 every
+// 8 rows): no per-chunk address stays live in registers.
 template <class C, class Keep, class Fn>
 __device__ __forceinline__ void each_row_chunk(const char* smem, Keep keep, Fn fn) {
     using E = Epi<C>;
-    const float* N = reinterpret_cast<const float*>(smem);
+    static_assert(256 / (C::BN / 8) == 8, "8 rows per chunk");
+    const int tr = threadIdx.x / (C::BN / 8), c8 = (threadIdx.x % (C::BN / 8)) * 8;
+    int off = tr * E::NS + c8;
+    // opaque per pass: the compiler would otherwise keep every chunk address of the first half
+    // live for the second (same staging offsets) instead of recomputing it
+    asm volatile("" : "+v"(off));
+    const float* base = reinterpret_cast<const float*>(smem) + off;
 #pragma unroll
     for (int it = 0; it < E::ROW_CHUNKS; ++it) {
-        int r, c8;
-        row_chunk<C>(it, r, c8);
+        const int r = 8 * it + tr;
         if (!keep(r, c8)) continue;
-        const floatx4 a = *reinterpret_cast<const floatx4*>(N + E::row_base(r) + c8);
-        const floatx4 b = *reinterpret_cast<const floatx4*>(N + E::row_base(r) + c8 + 4);
+        const float* q = base + it * (8 * E::NS + 4);
+        const floatx4 a = *reinterpret_cast<const floatx4*>(q);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(q + 4);
         float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         fn(it, r, c8, v);
     }

@@ -82,25 +82,50 @@ __global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __res
         }
 }
 
+// Buffer access to an s x ld f16 workspace matrix. Every load and store of the symmetric
+// epilogue is a buffer instruction issued unconditionally: a chunk outside the matrix, or one the
+// epilogue does not write, gets the offset kOutOfRange, past the resource's size, so the load
+// returns zeros and the store is dropped. With no conditional memory operation, the compiler's
+// waits count exactly the operations still needed (a conditional one made it wait for every
+// outstanding store before each chunk). A null matrix gets a resource of size 0: all zeros.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOutOfRange = 0x80000000u;   // > the byte size of any matrix (s <= 32768)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sym_rsrc(const _Float16* m, int64_t ld, int n) {
+    const uint32_t bytes = m ? static_cast<uint32_t>(int64_t(n) * ld * 2) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(m), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint32_t sym_off(bool ok, int r, int c, int64_t ld) {
+    return ok ? static_cast<uint32_t>((int64_t(r) * ld + c) * 2) : kOutOfRange;
+}
+__device__ __forceinline__ half8v buf_load8(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_bit_cast(half8v, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
+}
+// aux 2: non-temporal
+template <int AUX = 0>
+__device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t rs, uint32_t off, const half8v& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, static_cast<int>(off), 0, AUX);
+}
+
 // The beta * Csym chunks of half h of a tile, in row_chunk() order (zeros outside the matrix).
 template <class C>
-__device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS], const _Float16* csym, int64_t ld,
-                                             int n, int m0, int n0, int h) {
+__device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS], __amdgpu_buffer_rsrc_t crs,
+                                             int64_t ld, int n, int m0, int n0, int h) {
 #pragma unroll
     for (int it = 0; it < Epi<C>::ROW_CHUNKS; ++it) {
         int lr, c8;
         row_chunk<C>(it, lr, c8);
         const int r = m0 + h * C::WM + lr, c = n0 + c8;
-        cpre[it] = (r < n && c < ld) ? ldg<half8v>(csym + (int64_t)r * ld + c) : half8v{};
+        cpre[it] = buf_load8(crs, sym_off(r < n && c < ld, r, c, ld));
     }
 }
 
 // out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile of a symmetric s x s
-// matrix (Csym optional). Only the upper block triangle is stored: consumers read a block below
-// the diagonal as the transpose of its mirror above it, and a diagonal block either way, so a
-// diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the Gram
-// iteration): its upper triangle is computed and its lower triangle is the mirror. A diagonal
-// tile is written in three parts per half:
+// matrix (Csym optional: crs of size 0). Only the upper block triangle is stored: consumers read
+// a block below the diagonal as the transpose of its mirror above it, and a diagonal block either
+// way, so a diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the
+// Gram iteration): its upper triangle is computed and its lower triangle is the mirror. A
+// diagonal tile is written in three parts per half:
 //   the row pass stores the 8-column chunks right of each 8 x 8 diagonal block and writes their
 //     final fp32 values back into the staging;
 //   one thread per row assembles its row of the diagonal block: upper elements computed, lower
@@ -111,11 +136,13 @@ __device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS],
 // the main loop) and receives half 1's once half 0's row pass is done.
 template <class C>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
-                                          const _Float16* csym, int64_t ld, int n, int m0, int n0, float alpha,
-                                          float beta, float gamma, half8v (&crow)[Epi<C>::ROW_CHUNKS]) {
+                                          __amdgpu_buffer_rsrc_t crs, bool has_c, int64_t ld, int n, int m0, int n0,
+                                          float alpha, float beta, float gamma,
+                                          half8v (&crow)[Epi<C>::ROW_CHUNKS]) {
     using E = Epi<C>;
     float* N = reinterpret_cast<float*>(smem);
     const bool diag = m0 == n0;
+    const __amdgpu_buffer_rsrc_t ors = sym_rsrc(out, ld, n);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int rb = m0 + h * C::WM;   // first row of this half
@@ -123,54 +150,48 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
         const int dl = threadIdx.x;
         const int dr = rb + dl, dc = rb + (dl & ~7);
         const bool dkeep = diag && dl < C::WM && dr < n && dc < ld;
-        half8v cdg{};
-        if (dkeep && csym) cdg = ldg<half8v>(csym + (int64_t)dr * ld + dc);
+        const half8v cdg = buf_load8(crs, sym_off(dkeep, dr, dc, ld));
         stage_rows<C>(acc, smem, h);
         each_row_chunk<C>(
-            smem,
-            [&](int lr, int c8) {
-                const int r = rb + lr, c = n0 + c8;
-                return r < n && c < ld && !(diag && c < (r & ~7) + 8);
-            },
+            smem, [](int, int) { return true; },
             [&](int it, int lr, int c8, float (&v)[8]) {
                 const int r = rb + lr, c = n0 + c8;
+                const bool keep = r < n && c < ld && !(diag && c < (r & ~7) + 8);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     float t = alpha * v[e];
-                    if (csym) t += beta * static_cast<float>(crow[it][e]);
+                    if (has_c) t += beta * static_cast<float>(crow[it][e]);
                     if (r == c + e) t += gamma;
                     v[e] = t;
                 }
-                stg_nt<half8v>(out + (int64_t)r * ld + c, to_half8(v));
-                if (diag) {   // the final values, for the column pass
+                buf_store8<2>(ors, sym_off(keep, r, c, ld), to_half8(v));
+                if (diag && keep) {   // the final values, for the column pass
                     *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8) = floatx4{v[0], v[1], v[2], v[3]};
                     *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8 + 4) = floatx4{v[4], v[5], v[6], v[7]};
                 }
             });
-        if (h == 0 && csym) sym_prefetch<C>(crow, csym, ld, n, m0, n0, 1);
+        if (h == 0) sym_prefetch<C>(crow, crs, ld, n, m0, n0, 1);
         if (!diag) continue;
-        if (dkeep) {   // reads only diagonal blocks, which the row pass leaves as staged
+        {   // reads only diagonal blocks, which the row pass leaves as staged
             const int ri = dl & 7, lc = h * C::WM + (dl & ~7);   // tile-local column of dc
             float v[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = e >= ri ? N[E::row_base(dl) + lc + e] : N[E::row_base((dl & ~7) + e) + lc + ri];
+                const int dlr = dl < C::WM ? dl : 0;   // rows past the half: any staged row, not stored
+                const float x = e >= ri ? N[E::row_base(dlr) + lc + e] : N[E::row_base((dlr & ~7) + e) + lc + ri];
                 float t = alpha * x;
-                if (csym) t += beta * static_cast<float>(cdg[e]);
+                if (has_c) t += beta * static_cast<float>(cdg[e]);
                 if (e == ri) t += gamma;
                 v[e] = t;
             }
-            stg<half8v>(out + (int64_t)dr * ld + dc, to_half8(v));
+            buf_store8(ors, sym_off(dkeep, dr, dc, ld), to_half8(v));
         }
         lds_barrier();   // the row pass's final values are in the staging
         each_col_chunk<C>(
-            smem,
-            [&](int cl, int lr8) {
-                const int c = n0 + cl, r8 = rb + lr8;
-                return c < n && r8 < ld && c > r8 + 7;
-            },
+            smem, [](int, int) { return true; },
             [&](int, int cl, int lr8, float (&v)[8]) {   // v[e] is (r8 + e, c), stored at (c, r8 + e)
-                stg<half8v>(out + (int64_t)(n0 + cl) * ld + rb + lr8, to_half8(v));
+                const int c = n0 + cl, r8 = rb + lr8;
+                buf_store8(ors, sym_off(c < n && r8 < ld && c > r8 + 7, c, r8, ld), to_half8(v));
             });
     }
 }
@@ -397,19 +418,20 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     // the C term of a symmetric product is requested before the main loop (it arrives with the
     // first operand tiles and waits in registers)
     const _Float16* csym = op.kind == kOpSym && op.csel >= 0 && op.beta != 0.f ? sym_buf(M, op.csel) : nullptr;
+    const __amdgpu_buffer_rsrc_t crs = sym_rsrc(csym, M.lds, M.s);
     half8v c0[Epi<NsCfg>::ROW_CHUNKS];
-    if (csym) sym_prefetch<NsCfg>(c0, csym, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, 0);
+    sym_prefetch<NsCfg>(c0, crs, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, 0);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
     gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero);
     if (op.kind == kOpUpdate) {
         update_finish(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
         const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
-        sym_store<NsCfg>(acc, smem, M.gram, nullptr, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, osc * osc, 0.f,
+        sym_store<NsCfg>(acc, smem, M.gram, crs, false, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, osc * osc, 0.f,
                          0.f, c0);
     } else {
-        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), csym, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, op.alpha,
-                         op.beta, op.gamma, c0);
+        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), crs, csym != nullptr, M.lds, M.s, ti * NsCfg::BM,
+                         tj * NsCfg::BN, op.alpha, op.beta, op.gamma, c0);
     }
 }
 
