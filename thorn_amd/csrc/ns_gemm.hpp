@@ -11,6 +11,8 @@
 // transposing reads), so no matrix is ever transposed in memory.
 #pragma once
 
+#include <type_traits>
+
 #include "thorn_common.hpp"
 
 namespace thorn {
@@ -178,6 +180,50 @@ __device__ __forceinline__ void read_frag(const char* st, int ks, int q, int wm,
     else ra[q - C::TN] = frag<C::BM, AK>(st, wm + 32 * (q - C::TN), ks, lane);
 }
 
+// Work split of a tile between its four waves. A diagonal tile of a symmetric result is only
+// stored as its upper block triangle (the epilogue mirrors it), so of its 8 x 8 grid of 32 x 32
+// blocks only the 36 with j >= i are computed: waves 0 and 3 take the blocks of their diagonal
+// quadrants with j >= i (10 each), waves 1 and 2 split the upper-right quadrant (rows 0-63 and
+// 64-127, 8 blocks each), and nobody computes the lower-left quadrant. The slowest wave then
+// issues 10 MFMAs per k16 step instead of 16.
+enum TileRole : int { kRoleFull = 0, kRoleTri = 1, kRoleHalf = 2 };
+
+template <int ROLE, int TM, int TN>
+struct RoleMap {
+    static constexpr int N = ROLE == kRoleFull ? TM * TN : ROLE == kRoleTri ? TM * (TM + 1) / 2 : 2 * TN;
+    // (i, j) of this wave's q-th MFMA block, rows before columns
+    static constexpr int i(int q) {
+        if (ROLE == kRoleFull) return q / TN;
+        if (ROLE == kRoleHalf) return q / TN;
+        int r = 0;
+        while (q >= TN - r) {
+            q -= TN - r;
+            ++r;
+        }
+        return r;
+    }
+    static constexpr int j(int q) {
+        if (ROLE != kRoleTri) return q % TN;
+        int r = 0;
+        while (q >= TN - r) {
+            q -= TN - r;
+            ++r;
+        }
+        return r + q;
+    }
+    // fragments read per k16 step: A0, B0 .. B(TN-1), A1 .. A(rows-1)
+    static constexpr int NF = (ROLE == kRoleHalf ? 2 : TM) + TN;
+};
+
+// f(std::integral_constant<int, Q>) for Q = B .. E-1, as straight-line code with Q a constant.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // The K tiles [lo, hi) of gemm_tile in one operand layout (AK / BK). On entry the stages hold
 // tiles lo .. lo+S-2 (tile lo visible to every wave); on exit they hold hi .. hi+S-2 likewise.
 // Each iteration is one basic block of two k16 sub-steps of TM * TN MFMAs, the order of every
@@ -189,16 +235,19 @@ __device__ __forceinline__ void read_frag(const char* st, int ks, int q, int wm,
 // reads stage (kt-1) % S any more, which then receives tile kt+S-1. Tiles past the end of K are
 // loaded (zeros or in-bounds data) and read but never used, which keeps the loop body free of
 // branches.
-template <class C, bool AK, bool BK>
+template <class C, bool AK, bool BK, int ROLE = kRoleFull>
 __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM>& da, const DmaPair<C::BN>& db,
                                              floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
                                              half8 (&fb)[2][C::TN], char* smem, const void* zero) {
     if (lo >= hi) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
+    // kRoleHalf: wave 1 takes rows 0-63, wave 2 rows 64-127 of the upper-right quadrant
+    const int wm = ROLE == kRoleHalf ? (wave >> 1) * (C::WM / 2) : (wave >> 1) * C::WM;
+    const int wn = ROLE == kRoleHalf ? C::WN : (wave & 1) * C::WN;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-    constexpr int NM = C::TM * C::TN;   // MFMAs per sub-step
-    constexpr int NF = C::TM + C::TN;   // fragments per sub-step
+    using R = RoleMap<ROLE, C::TM, C::TN>;
+    constexpr int NM = R::N;    // MFMAs per sub-step
+    constexpr int NF = R::NF;   // fragments per sub-step
     constexpr int NA = DmaPair<C::BM>::PER_WAVE, NB = DmaPair<C::BN>::PER_WAVE;
     static_assert(NF <= NM && NA + NB <= NM, "one fragment and one direct load per MFMA at most");
     {
@@ -208,29 +257,27 @@ __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM
     }
     for (int kt = lo; kt < hi; ++kt) {
         const char* sa = smem + (kt % C::S) * C::STAGE_BYTES;
-#pragma unroll
-        for (int q = 0; q < NM; ++q) {
-            const int i = q / C::TN, j = q % C::TN;
+        static_for<0, NM>([&](auto qc) {
+            constexpr int q = decltype(qc)::value, i = R::i(q), j = R::j(q);
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (q < NF) read_frag<C, AK, BK>(sa, 1, q, wm, wn, lane, fa[1], fb[1]);
+            if constexpr (q < NF) read_frag<C, AK, BK>(sa, 1, q, wm, wn, lane, fa[1], fb[1]);
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
         lds_wait_barrier<(C::S - 3) * C::LOADS_PER_STAGE>();
         __builtin_amdgcn_sched_barrier(0);
         const int tn = kt + C::S - 1;
         const uint32_t st_new = lds0 + (tn % C::S) * C::STAGE_BYTES;
         const char* na = smem + ((kt + 1) % C::S) * C::STAGE_BYTES;
-#pragma unroll
-        for (int q = 0; q < NM; ++q) {
-            const int i = q / C::TN, j = q % C::TN;
+        static_for<0, NM>([&](auto qc) {
+            constexpr int q = decltype(qc)::value, i = R::i(q), j = R::j(q);
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (q < NF) read_frag<C, AK, BK>(na, 0, q, wm, wn, lane, fa[0], fb[0]);
-            if (q < NA) da.issue_one(tn, q, st_new + wave * NA * 1024, zero);
-            else if (q < NA + NB) db.issue_one(tn, q - NA, st_new + C::A_BYTES + wave * NB * 1024, zero);
+            if constexpr (q < NF) read_frag<C, AK, BK>(na, 0, q, wm, wn, lane, fa[0], fb[0]);
+            if constexpr (q < NA) da.issue_one(tn, q, st_new + wave * NA * 1024, zero);
+            else if constexpr (q < NA + NB) db.issue_one(tn, q - NA, st_new + C::A_BYTES + wave * NB * 1024, zero);
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
     }
 }
 
@@ -241,9 +288,21 @@ __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM
 // transposed: lane l holds row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3
 // in registers r..r+3, which the epilogue writes to LDS as one 16-byte store. Ends with every
 // load and LDS read complete and a block barrier, so the stages are free for the epilogue.
+template <class C, int ROLE>
+__device__ __forceinline__ void gemm_segments(int KT, int k1, int k2, const DmaPair<C::BM>& da,
+                                              const DmaPair<C::BN>& db, floatx16 (&acc)[C::TM][C::TN], char* smem,
+                                              const void* zero) {
+    half8 fa[2][C::TM], fb[2][C::TN];
+    gemm_segment<C, false, false, ROLE>(0, k1, da, db, acc, fa, fb, smem, zero);
+    gemm_segment<C, true, false, ROLE>(k1, k2, da, db, acc, fa, fb, smem, zero);
+    gemm_segment<C, true, true, ROLE>(k2, KT, da, db, acc, fa, fb, smem, zero);
+}
+
+// `diag`: the tile is a diagonal tile of a symmetric result (m0 == n0), split by TileRole.
 template <class C>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0, int KT, int a_k0,
-                                          int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem, const void* zero) {
+                                          int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem, const void* zero,
+                                          bool diag = false) {
     static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -265,12 +324,12 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
         for (int q = 0; q < NB; ++q) db.issue_one(t, q, st + C::A_BYTES + wave * NB * 1024, zero);
     }
     lds_wait_barrier<(C::S - 2) * C::LOADS_PER_STAGE>();   // tile 0 visible
-    half8 fa[2][C::TM], fb[2][C::TN];
     const int k1 = a_k0 < KT ? a_k0 : KT;
     const int k2 = b_k0 < k1 ? k1 : (b_k0 < KT ? b_k0 : KT);
-    gemm_segment<C, false, false>(0, k1, da, db, acc, fa, fb, smem, zero);
-    gemm_segment<C, true, false>(k1, k2, da, db, acc, fa, fb, smem, zero);
-    gemm_segment<C, true, true>(k2, KT, da, db, acc, fa, fb, smem, zero);
+    // every role passes the same barriers: one per K tile, and the final one below
+    if (!diag) gemm_segments<C, kRoleFull>(KT, k1, k2, da, db, acc, smem, zero);
+    else if (wave == 0 || wave == 3) gemm_segments<C, kRoleTri>(KT, k1, k2, da, db, acc, smem, zero);
+    else gemm_segments<C, kRoleHalf>(KT, k1, k2, da, db, acc, smem, zero);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -313,13 +372,31 @@ __device__ __forceinline__ void col_chunk(int it, int& c, int& r8) {
 
 // Writes rows [half * WM, half * WM + WM) of the tile to the staging N, between two block
 // barriers (the previous user of smem, the main loop or another pass, is done before).
+// On a diagonal tile (gemm_tile's `diag`) the blocks sit where TileRole put them: half 0 gets
+// wave 0's quadrant and the upper-right quadrant from waves 1 (rows 0-63) and 2 (rows 64-127),
+// half 1 gets wave 3's quadrant; the lower-left quadrant is not staged (never read).
 template <class C>
-__device__ __forceinline__ void stage_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half) {
+__device__ __forceinline__ void stage_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, bool diag = false) {
     using E = Epi<C>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* N = reinterpret_cast<float*>(smem);
     lds_barrier();
-    if ((wave >> 1) == half) {
+    if (diag && (wave == 1 || wave == 2)) {
+        if (half == 0) {
+            const int r0 = (wave >> 1) * (C::WM / 2);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int r = r0 + 32 * i + (lane & 31);
+                        const int c = C::WN + 32 * j + 8 * q + 4 * (lane >> 5);
+                        *reinterpret_cast<floatx4*>(N + E::row_base(r) + c) = floatx4{
+                            acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    }
+        }
+    } else if ((wave >> 1) == half) {
         const int wn = (wave & 1) * C::WN;
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
@@ -386,7 +463,7 @@ __device__ __forceinline__ void each_col_chunk(const char* smem, Keep keep, Fn f
 // each_row_chunk), row = half * WM + local_row.
 template <class C, class Fn>
 __device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
-    stage_rows<C>(acc, smem, half);
+    stage_rows<C>(acc, smem, half, false);
     each_row_chunk<C>(smem, [](int, int) { return true; },
                       [&](int it, int r, int c8, float (&v)[8]) { fn(it, half, r, c8, v); });
 }

@@ -151,7 +151,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
         const int dr = rb + dl, dc = rb + (dl & ~7);
         const bool dkeep = diag && dl < C::WM && dr < n && dc < ld;
         const half8v cdg = buf_load8(crs, sym_off(dkeep, dr, dc, ld));
-        stage_rows<C>(acc, smem, h);
+        stage_rows<C>(acc, smem, h, diag);
         each_row_chunk<C>(
             smem, [](int, int) { return true; },
             [&](int it, int lr, int c8, float (&v)[8]) {
@@ -422,7 +422,8 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     half8v c0[Epi<NsCfg>::ROW_CHUNKS];
     sym_prefetch<NsCfg>(c0, crs, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, 0);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero);
+    gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero,
+                     op.kind != kOpUpdate && ti == tj);
     if (op.kind == kOpUpdate) {
         update_finish(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
