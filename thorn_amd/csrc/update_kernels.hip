@@ -62,11 +62,11 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
         if (vec) {
             if (cok[0]) {
                 const int c = c0 + 4 * lane;
-                const float4 g4 = ldg<float4>(M.g + rbase + c), m4 = ldg<float4>(M.m + rbase + c);
+                const float4 g4 = ldg_nt<float4>(M.g + rbase + c), m4 = ldg_nt<float4>(M.m + rbase + c);
                 gv[rr][0] = g4.x; gv[rr][1] = g4.y; gv[rr][2] = g4.z; gv[rr][3] = g4.w;
                 mv[rr][0] = m4.x; mv[rr][1] = m4.y; mv[rr][2] = m4.z; mv[rr][3] = m4.w;
                 if (md || mds) {
-                    const float4 p4 = ldg<float4>(M.p + rbase + c);
+                    const float4 p4 = ldg_nt<float4>(M.p + rbase + c);
                     pv[rr][0] = p4.x; pv[rr][1] = p4.y; pv[rr][2] = p4.z; pv[rr][3] = p4.w;
                 }
             }
@@ -312,8 +312,8 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             sv[rr] = 0.f;
             if (rr >= nrows || !ok) continue;
             const int row = r0 + rr;
-            pv[rr] = ldg<float4>(M.p + (int64_t)row * M.cols + c);
-            uv[rr] = ldg<half4>(M.uout + (int64_t)row * M.ldx + c);
+            pv[rr] = ldg_nt<float4>(M.p + (int64_t)row * M.cols + c);
+            uv[rr] = ldg_nt<half4>(M.uout + (int64_t)row * M.ldx + c);
             sv[rr] = ldg<float>(M.rowscale + row);
         }
 #pragma unroll
@@ -427,10 +427,10 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamTensor* __restrict_
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int64_t i = base + (int64_t)(q * 256 + threadIdx.x) * 4;
-            p4[q] = s.apply ? ldg<float4>(T.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            g4[q] = ldg<float4>(T.g + i);
-            m4[q] = ldg<float4>(T.m + i);
-            v4[q] = ldg<float4>(T.v + i);
+            p4[q] = s.apply ? ldg_nt<float4>(T.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            g4[q] = ldg_nt<float4>(T.g + i);
+            m4[q] = ldg_nt<float4>(T.m + i);
+            v4[q] = ldg_nt<float4>(T.v + i);
         }
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
