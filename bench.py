@@ -364,7 +364,84 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
                     tot += sum(v) / len(v) * 1024.0 * s
             if upd and len(scale) == 2:
                 lines.append(f'\nns_phase_kernel HBM bytes per launch: {tot:.6g}')
+        lines += mfma_lines(found)
     return '\n'.join(lines)
+
+
+def mfma_lines(found) -> list:
+    """ns_phase_kernel's MFMA utilisation, clock and executed MFMA flops from the counter passes
+    SQ_VALU_MFMA_BUSY_CYCLES + GRBM_GUI_ACTIVE and SQ_INSTS_VALU_MFMA_MOPS_F16 (one 512-flop op
+    each), per dispatch, with the dispatch's own start/end timestamps. GRBM_GUI_ACTIVE comes summed
+    over the XCDs, so a dispatch's cycles are it / Num_Xcc; MfmaUtil = busy / (cycles * Simd_Count),
+    as rocprofv3's derived metric defines it."""
+    import csv
+    agent = [r for f in found('*agent_info.csv') for r in csv.DictReader(open(f)) if r['Agent_Type'] == 'GPU']
+    if not agent:
+        return []
+    xcc, simds = int(agent[0]['Num_Xcc']), int(agent[0]['Simd_Count'])
+    fmax = float(agent[0]['Max_Engine_Clk_Fcompute'])
+    per: dict = {}
+    for f in found('*counter_collection.csv'):
+        for r in csv.DictReader(open(f)):
+            if 'ns_phase_kernel' not in r['Kernel_Name']:
+                continue
+            d = per.setdefault((f, r['Dispatch_Id']), {})
+            d[r['Counter_Name']] = float(r['Counter_Value'])
+            d['ns'] = int(r['End_Timestamp']) - int(r['Start_Timestamp'])
+    util, clk, rate = [], [], []
+    for d in per.values():
+        if 'SQ_VALU_MFMA_BUSY_CYCLES' in d and 'GRBM_GUI_ACTIVE' in d:
+            cyc = d['GRBM_GUI_ACTIVE'] / xcc
+            util.append(d['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * simds))
+            clk.append(cyc / d['ns'])
+        if 'SQ_INSTS_VALU_MFMA_MOPS_F16' in d:
+            rate.append(d['SQ_INSTS_VALU_MFMA_MOPS_F16'] * 512 / d['ns'] / 1e3)   # TFLOP/s
+    if not (util or rate):
+        return []
+    avg = lambda v: sum(v) / len(v)
+    out = ['', f'ns_phase_kernel MFMA counters ({max(len(util), len(rate))} dispatches; {simds} SIMDs, '
+               f'{xcc} XCDs, max engine clock {fmax:.0f} MHz):']
+    if util:
+        out.append(f'- MFMA busy (MfmaUtil): {100 * avg(util):.1f}% (min {100 * min(util):.1f}%, '
+                   f'max {100 * max(util):.1f}%); shader clock while busy {avg(clk):.2f} GHz')
+    if rate:
+        out.append(f'- executed f16 MFMA flops: {avg(rate):.0f} TFLOP/s per dispatch on average')
+    return out
+
+
+def vendor_gemm() -> int:
+    """The vendor library on the same products as full (unsymmetric) GEMMs: torch.bmm in f16 over
+    the config-2 shapes (hipBLASLt/rocBLAS), and two square GEMMs for scale. One JSON line."""
+    import torch
+    dev = torch.device('cuda:0')
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, dtype=torch.float16, generator=g)
+
+    def t(fn, flops, iters=20):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / iters
+        return {'ms': round(dt * 1e3, 4), 'tflops': round(flops / dt / 1e12, 1)}
+
+    res = {}
+    for n in (4096, 8192):
+        a, b = rnd(n, n), rnd(n, n)
+        res[f'mm_{n}'] = t(lambda: a @ b, 2.0 * n ** 3)
+        del a, b
+    a, b = rnd(140, 1024, 1024), rnd(140, 1024, 1024)
+    res['bmm_140x1024^3'] = t(lambda: torch.bmm(a, b), 140 * 2.0 * 1024 ** 3)
+    x = rnd(60, 1024, 3072)
+    xt = x.transpose(1, 2).contiguous()
+    res['bmm_60x(1024x3072)(3072x1024)'] = t(lambda: torch.bmm(x, xt), 60 * 2.0 * 1024 * 1024 * 3072)
+    res['bmm_60x(1024x1024)(1024x3072)'] = t(lambda: torch.bmm(a[:60], x), 60 * 2.0 * 1024 * 1024 * 3072)
+    print(json.dumps({'vendor_gemm_f16': res, 'peak_tflops': MFMA_PEAK_TFLOPS}), flush=True)
+    return 0
 
 
 def traffic_from_profile() -> float | None:
@@ -394,12 +471,16 @@ def main() -> int:
     ap.add_argument('--cpu-budget', type=float, default=20.0)
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
+    ap.add_argument('--vendor-gemm', action='store_true',
+                    help='time torch (hipBLASLt) f16 GEMMs of the Newton-Schulz shapes for comparison and exit')
     ap.add_argument('--rocprof-summary', metavar='DIR', nargs='+',
                     help='print a markdown summary of rocprofv3 CSV output directories and exit')
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib))
         return 0
+    if args.vendor_gemm:
+        return vendor_gemm()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: this build has no multi-GPU path (each matrix\'s step '
               'is independent; the sharding design is in DESIGN.md). Run with --gpus 1.', file=sys.stderr)
