@@ -38,6 +38,8 @@ HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E
 
 def config_shapes(config: int):
     """(ortho matrix shapes, non-ortho groups [(shape list, wd)], group overrides)."""
+    if config == 1:
+        return [(512, 256)], []
     if config in (2, 3):
         layer = [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (3072, 1024), (1024, 3072)]
         return layer * 20, [([(151936, 1024)], 0.1), ([(1024,)] * 41, 0.0)]
@@ -571,7 +573,7 @@ def main() -> int:
         'vs_baseline': None,
         'dtype': 'f16',
         'data': 'synthetic',
-        'config': {'workload': {2: 'qwen3-300m (BASELINE config 2)', 3: 'qwen3-300m decouple_md (config 3)',
+        'config': {'workload': {1: 'one 512x256 Linear (config 1)', 2: 'qwen3-300m (BASELINE config 2)', 3: 'qwen3-300m decouple_md (config 3)',
                                 4: 'earshot conv VAD (config 4)', 5: 'qwen3-1.7b matrices (config 5)'}[args.config]
                    + (' + Magma momentum_align' if args.momentum_align else ''),
                    'matrices': n_m, 'adam_tensors': len(params) - n_m,
