@@ -554,7 +554,8 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
 
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
-    THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel, dim3(n), dim3(256), 0, st, mats, n);
+    THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel,
+                 dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n);
     if (iters == 0) {   // momentum only (no update is due): the decouple_md round trip and done
         if (plan->md.n > 0) {   // p *= softplus(gains), the gains unchanged
             const thorn::TaskList md = task_list(dev, plan->md);

@@ -177,9 +177,14 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
 // steps of the gains from d softplus (thorn.py:910-967). The gains' updates only read p*g from
 // before the parameter update, so they run here, before Newton-Schulz.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats) {
-    __shared__ float scratch[12];
-    const OrthoMat& M = mats[blockIdx.x];
+// Grid: one column of blocks per matrix, kNormSlices deep. Block (i, 0) takes sigma, Magma, the
+// row gains and the scalar gain; block (i, g) takes slice g of the column gains (each column's sum
+// runs over rows / 16 partials, the long part).
+constexpr int kNormSlices = 8;
+
+// sigma = 1 / (||u||_F + 1e-8), the first-iterate scales and Magma's s of one matrix.
+__device__ __forceinline__ void norm_sigma_magma(const OrthoMat* __restrict__ mats, int n_mats, const OrthoMat& M,
+                                                 float* scratch) {
     const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
     float s = 0.f;
     for (int t = threadIdx.x; t < ntiles; t += 256) s += M.normpart[t];
@@ -219,6 +224,13 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
         t = block_sum(t, scratch);
         if (threadIdx.x == 0) magma_update(t, M.magma_s);
     }
+}
+
+__global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats) {
+    __shared__ float scratch[12];
+    const OrthoMat& M = mats[blockIdx.x];
+    const int slice = blockIdx.y;
+    if (slice == 0) norm_sigma_magma(mats, n_mats, M, scratch);
 
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
     if (!(md || mds) || !(M.flags & kFlagApply)) return;
@@ -227,7 +239,7 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
     a.bc1 = M.gain_bc1; a.bc2 = M.gain_bc2; a.eps = M.gain_eps;
     a.apply = true; a.degenerate = false; a.atan2_mode = M.gain_eps == 0.f;
     if (md) {
-        for (int i = threadIdx.x; i < M.rows; i += 256) {
+        for (int i = threadIdx.x; i < M.rows && slice == 0; i += 256) {
             float t = 0.f;
             for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpart[(int64_t)c * M.rows + i];
             float gain = M.rg[i], mo = M.rgm[i], va = M.rgv[i];
@@ -235,7 +247,9 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
             adam_elem(gain, grad, mo, va, a);
             M.rg[i] = gain; M.rgm[i] = mo; M.rgv[i] = va;
         }
-        for (int j = threadIdx.x; j < M.cols; j += 256) {
+        const int per = (M.cols + kNormSlices - 1) / kNormSlices;
+        const int j1 = min(M.cols, (slice + 1) * per);
+        for (int j = slice * per + threadIdx.x; j < j1; j += 256) {
             float t = 0.f;
             for (int r = 0; r < M.mom_tiles_r; ++r) t += M.colpart[(int64_t)r * M.cols + j];
             float gain = M.cg[j], mo = M.cgm[j], va = M.cgv[j];
@@ -243,7 +257,7 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
             adam_elem(gain, grad, mo, va, a);
             M.cg[j] = gain; M.cgm[j] = mo; M.cgv[j] = va;
         }
-    } else {
+    } else if (slice == 0) {
         float t = 0.f;
         for (int i = threadIdx.x; i < M.rows; i += 256)
             for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpart[(int64_t)c * M.rows + i];
@@ -376,28 +390,57 @@ __global__ __launch_bounds__(256) void ortho_md_rescale_kernel(const OrthoMat* _
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     const bool md = M.flags & kFlagMD;
     const bool apply = M.flags & kFlagApply;
+    const bool vec = M.flags & kFlagVec4;
     const float f = M.scal[kScalMDFactor];
     float spc[4];
+    bool cok[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int c = c0 + lane + 64 * e;
-        spc[e] = (md && c < M.cols) ? softplus_f(M.cg[c]) : 1.f;
+        const int c = tile_col(c0, lane, e, vec);
+        cok[e] = c < M.cols;
+        spc[e] = (md && cok[e]) ? softplus_f(M.cg[c]) : 1.f;
     }
     const float sp_scalar = md ? 1.f : softplus_f(M.rg[0]);
+    const int nrows = M.rows - r0;
+    // the wave's 4 rows are loaded first, so their loads are in flight together
+    float pv[4][4];
+#pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pv[rr][e] = 0.f;
+        if (rr >= nrows) continue;
+        const int64_t rbase = (int64_t)(r0 + rr) * M.cols;
+        if (vec) {
+            if (cok[0]) {
+                const float4 p4 = ldg_nt<float4>(M.p + rbase + c0 + 4 * lane);
+                pv[rr][0] = p4.x; pv[rr][1] = p4.y; pv[rr][2] = p4.z; pv[rr][3] = p4.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (cok[e]) pv[rr][e] = ldg<float>(M.p + rbase + tile_col(c0, lane, e, false));
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        if (rr >= nrows) break;
         const int row = r0 + rr;
-        if (row >= M.rows) break;
         const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
         const int64_t rbase = (int64_t)row * M.cols;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int c = c0 + lane + 64 * e;
-            if (c >= M.cols) continue;
-            float p = M.p[rbase + c];
+            float p = pv[rr][e];
             if (apply) p = p * f;
             p = p * spr;
             if (md) p = p * spc[e];
-            M.p[rbase + c] = p;
+            pv[rr][e] = p;
+        }
+        if (vec) {
+            if (cok[0]) stg_nt<float4>(M.p + rbase + c0 + 4 * lane, make_float4(pv[rr][0], pv[rr][1], pv[rr][2], pv[rr][3]));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (cok[e]) M.p[rbase + tile_col(c0, lane, e, false)] = pv[rr][e];
         }
     }
 }
