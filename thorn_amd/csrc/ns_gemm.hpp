@@ -333,142 +333,103 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Epilogue: the tile is streamed through LDS (reusing the pipeline stages) in two halves of
-// WM = BM/2 rows, the rows owned by one row of waves. stage_rows writes a half to the row-major
-// staging N (fp32; row r starts at row_base(r)); then
-//   each_row_chunk gives each thread 8 consecutive columns of one row, so global traffic is
-//     16-byte chunks with BN/8 lanes on one row;
-//   each_col_chunk gives each thread 8 consecutive rows of one column (the mirrored part of a
-//     symmetric tile), WM/8 lanes on one column taking its WM/8 row chunks, so each output row
-//     of the mirror gets 2*WM contiguous bytes.
-// Rows are NS floats apart plus 4 more after every 8 rows: the 64 lanes of a column read (16
-// row chunks x 4 columns, for WM = 128) then hit 64 distinct banks, and 16-byte row accesses
-// stay aligned.
+// Epilogue: every output of these GEMMs is f16, so the tile's final values are computed in
+// registers from the accumulators and staged once, as f16, in LDS (reusing the pipeline stages).
+// Row r of the staging starts at half rowoff(r) = r * SH + (r / 8) * PAD: rows are BN + 8 halves
+// (16-byte aligned) and every 8 rows add 8 more, so that the 16 lanes reading one column's row
+// chunks (each_col_chunk_h) and the 64 lanes writing an accumulator block (stage_f16) spread
+// over the banks. All four waves stage at once and one pass of 16-byte row chunks (32 lanes per
+// row) reads the tile back: half the LDS traffic of fp32 staging. Diagonal tiles of symmetric
+// results mirror staged f16 values, which keeps them exactly symmetric.
 template <class C>
-struct Epi {
-    static constexpr int NS = C::BN + 4;
-    static constexpr int N_BYTES = (C::WM * NS + (C::WM / 8) * 4) * 4;
-    static constexpr int SMEM = N_BYTES > C::LDS_BYTES ? N_BYTES : C::LDS_BYTES;
-    static constexpr int ROW_CHUNKS = C::WM * (C::BN / 8) / 256;   // per thread per half
-    static constexpr int COL_CHUNKS = C::BN * (C::WM / 8) / 256;
-    static constexpr int RC = C::WM / 8;                           // row chunks per column in a half
-    __device__ static __forceinline__ int row_base(int r) { return r * NS + (r >> 3) * 4; }
+struct EpiH {
+    static constexpr int SH = C::BN + 8;
+    static constexpr int PAD = 8;
+    static constexpr int BYTES = (C::BM * SH + (C::BM / 8) * PAD) * 2;
+    static constexpr int SMEM = BYTES > C::LDS_BYTES ? BYTES : C::LDS_BYTES;
+    static constexpr int ROW_ITERS = C::BM * (C::BN / 8) / 256;   // row chunks per thread
+    static constexpr int ROW_STEP = 8 * SH + PAD;                  // halves between chunks it, it+1
+    static_assert(C::BN / 8 == 32 && C::BM == 256, "256 x 256 tiles: one row per 32 lanes");
+    __device__ static __forceinline__ int rowoff(int r) { return r * SH + (r >> 3) * PAD; }
 };
 
-// Chunk `it` of this thread in a half: BN/8 lanes of a wave share one row (row passes); WM/8
-// lanes share one column and take its WM/8 row chunks (column passes).
-template <class C>
-__device__ __forceinline__ void row_chunk(int it, int& r, int& c8) {
-    const int idx = it * 256 + threadIdx.x;
-    r = idx / (C::BN / 8);
-    c8 = (idx % (C::BN / 8)) * 8;
-}
-template <class C>
-__device__ __forceinline__ void col_chunk(int it, int& c, int& r8) {
-    const int idx = it * 256 + threadIdx.x;
-    c = idx / Epi<C>::RC;
-    r8 = (idx % Epi<C>::RC) * 8;
-}
-
-// Writes rows [half * WM, half * WM + WM) of the tile to the staging N, between two block
-// barriers (the previous user of smem, the main loop or another pass, is done before).
-// On a diagonal tile (gemm_tile's `diag`) the blocks sit where TileRole put them: half 0 gets
-// wave 0's quadrant and the upper-right quadrant from waves 1 (rows 0-63) and 2 (rows 64-127),
-// half 1 gets wave 3's quadrant; the lower-left quadrant is not staged (never read).
-template <class C>
-__device__ __forceinline__ void stage_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, bool diag = false) {
-    using E = Epi<C>;
+// Stages f16(val(r, c, a)) for the accumulators this wave owns: val gives the final values of
+// tile-local row r, columns c .. c+3 from their 4 accumulators a. On a diagonal tile (gemm_tile's
+// `diag`) the blocks sit where TileRole put them (waves 1 and 2: rows 0-63 and 64-127 of the
+// upper-right quadrant); the lower-left quadrant is not staged. The caller separates this from
+// the previous use of smem and from the reads that follow with barriers.
+template <class C, class Val>
+__device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* smem, bool diag, Val val) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* N = reinterpret_cast<float*>(smem);
-    lds_barrier();
+    _Float16* S = reinterpret_cast<_Float16*>(smem);
+    auto put = [&](int r, int c, const floatx4& a) {
+        const floatx4 v = val(r, c, a);
+        *reinterpret_cast<half4*>(S + EpiH<C>::rowoff(r) + c) =
+            half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    };
     if (diag && (wave == 1 || wave == 2)) {
-        if (half == 0) {
-            const int r0 = (wave >> 1) * (C::WM / 2);
+        const int r0 = (wave >> 1) * (C::WM / 2);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < C::TN; ++j)
+            for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int r = r0 + 32 * i + (lane & 31);
-                        const int c = C::WN + 32 * j + 8 * q + 4 * (lane >> 5);
-                        *reinterpret_cast<floatx4*>(N + E::row_base(r) + c) = floatx4{
-                            acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    }
-        }
-    } else if ((wave >> 1) == half) {
-        const int wn = (wave & 1) * C::WN;
+                for (int q = 0; q < 4; ++q)
+                    put(r0 + 32 * i + (lane & 31), C::WN + 32 * j + 8 * q + 4 * (lane >> 5),
+                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+    } else {
+        const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = 32 * i + (lane & 31);
-                    const int c = wn + 32 * j + 8 * q + 4 * (lane >> 5);
-                    *reinterpret_cast<floatx4*>(N + E::row_base(r) + c) =
-                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                }
+                for (int q = 0; q < 4; ++q)
+                    put(wm + 32 * i + (lane & 31), wn + 32 * j + 8 * q + 4 * (lane >> 5),
+                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
     }
-    lds_barrier();
-}
-
-// fn(it, local_row, col8, float (&v)[8]): v = staged[local_row][col8 .. col8+7] for the chunks
-// with keep(local_row, col8); `it` numbers this thread's chunks 0 .. ROW_CHUNKS-1, in the order
-// given by row_chunk().
-// Chunk `it` is row 8*it + tid/(BN/8) (256 threads cover 8 rows per chunk), so its staging
-// address is one per-thread base plus the constant it * (8 * NS + 4) floats (row_base adds 4 every
-// 8 rows): no per-chunk address stays live in registers.
-template <class C, class Keep, class Fn>
-__device__ __forceinline__ void each_row_chunk(const char* smem, Keep keep, Fn fn) {
-    using E = Epi<C>;
-    static_assert(256 / (C::BN / 8) == 8, "8 rows per chunk");
-    const int tr = threadIdx.x / (C::BN / 8), c8 = (threadIdx.x % (C::BN / 8)) * 8;
-    int off = tr * E::NS + c8;
-    // opaque per pass: the compiler would otherwise keep every chunk address of the first half
-    // live for the second (same staging offsets) instead of recomputing it
-    asm volatile("" : "+v"(off));
-    const float* base = reinterpret_cast<const float*>(smem) + off;
-#pragma unroll
-    for (int it = 0; it < E::ROW_CHUNKS; ++it) {
-        const int r = 8 * it + tr;
-        if (!keep(r, c8)) continue;
-        const float* q = base + it * (8 * E::NS + 4);
-        const floatx4 a = *reinterpret_cast<const floatx4*>(q);
-        const floatx4 b = *reinterpret_cast<const floatx4*>(q + 4);
-        float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        fn(it, r, c8, v);
-    }
-}
-
-// fn(it, col, local_row8, float (&v)[8]): v = staged[local_row8 .. local_row8+7][col] for the
-// chunks with keep(col, local_row8); chunk order given by col_chunk().
-template <class C, class Keep, class Fn>
-__device__ __forceinline__ void each_col_chunk(const char* smem, Keep keep, Fn fn) {
-    using E = Epi<C>;
-    const float* N = reinterpret_cast<const float*>(smem);
-#pragma unroll
-    for (int it = 0; it < E::COL_CHUNKS; ++it) {
-        int c, r8;
-        col_chunk<C>(it, c, r8);
-        if (!keep(c, r8)) continue;
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = N[E::row_base(r8 + e) + c];
-        fn(it, c, r8, v);
-    }
-}
-
-// fn(it, half, local_row, col8, float (&v)[8]) over the row chunks of one half (see
-// each_row_chunk), row = half * WM + local_row.
-template <class C, class Fn>
-__device__ __forceinline__ void for_rows(floatx16 (&acc)[C::TM][C::TN], char* smem, int half, Fn fn) {
-    stage_rows<C>(acc, smem, half, false);
-    each_row_chunk<C>(smem, [](int, int) { return true; },
-                      [&](int it, int r, int c8, float (&v)[8]) { fn(it, half, r, c8, v); });
 }
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+
+// Chunk `it` (0 .. ROW_ITERS-1) of this thread in row order: tile-local row 8 * it + tid / 32,
+// columns c8 = 8 * (tid % 32) .. c8 + 7; its staging address is one per-thread base plus
+// it * ROW_STEP halves.
+__device__ __forceinline__ int row_chunk_base() {
+    return (threadIdx.x >> 5) * (256 + 8) + (threadIdx.x & 31) * 8;
+}
+
+// fn(it, r, c8, h): h = staged row r, columns c8 .. c8+7, over this thread's row chunks. The base
+// is opaque to the compiler, which then recomputes each chunk's address rather than keep 32 live.
+template <class C, class Fn>
+__device__ __forceinline__ void each_row_chunk_h(const char* smem, Fn fn) {
+    static_assert(EpiH<C>::SH == 256 + 8, "row_chunk_base");
+    const int tr = threadIdx.x >> 5, c8 = (threadIdx.x & 31) * 8;
+    int off = row_chunk_base();
+    asm volatile("" : "+v"(off));
+    const _Float16* base = reinterpret_cast<const _Float16*>(smem) + off;
+#pragma unroll
+    for (int it = 0; it < EpiH<C>::ROW_ITERS; ++it)
+        fn(it, 8 * it + tr, c8, *reinterpret_cast<const half8v*>(base + it * EpiH<C>::ROW_STEP));
+}
+
+// fn(c, r8, h): h[e] = staged (r8 + e, c), 8 rows of one column, over this thread's column
+// chunks: 16 lanes of a wave take 16 consecutive row chunks of one column (4 columns per wave
+// instruction), so the mirror of a column part is 256 contiguous bytes of an output row.
+template <class C, class Fn>
+__device__ __forceinline__ void each_col_chunk_h(const char* smem, Fn fn) {
+    const _Float16* S = reinterpret_cast<const _Float16*>(smem);
+#pragma unroll 4
+    for (int it = 0; it < EpiH<C>::ROW_ITERS; ++it) {
+        const int idx = it * 256 + threadIdx.x;
+        const int c = 4 * (idx >> 7) + ((idx >> 4) & 3);
+        const int r8 = 8 * (16 * ((idx >> 6) & 1) + (idx & 15));
+        half8v h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = S[EpiH<C>::rowoff(r8 + e) + c];
+        fn(c, r8, h);
+    }
+}
 
 __device__ __forceinline__ half8v to_half8(const float (&v)[8]) {
     return half8v{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3],

@@ -107,16 +107,17 @@ __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t rs, uint32_t o
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, static_cast<int>(off), 0, AUX);
 }
 
-// The beta * Csym chunks of half h of a tile, in row_chunk() order (zeros outside the matrix).
-template <class C>
-__device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS], __amdgpu_buffer_rsrc_t crs,
-                                             int64_t ld, int n, int m0, int n0, int h) {
+constexpr int kRowChunks = EpiH<NsCfg>::ROW_ITERS;   // row chunks of a tile per thread
+
+// Csym row chunks first .. first + N - 1 of this thread (zeros outside the matrix).
+template <int N>
+__device__ __forceinline__ void sym_load(half8v (&cv)[N], __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0,
+                                         int n0, int first) {
+    const int tr = threadIdx.x >> 5, c8 = (threadIdx.x & 31) * 8;
 #pragma unroll
-    for (int it = 0; it < Epi<C>::ROW_CHUNKS; ++it) {
-        int lr, c8;
-        row_chunk<C>(it, lr, c8);
-        const int r = m0 + h * C::WM + lr, c = n0 + c8;
-        cpre[it] = buf_load8(crs, sym_off(r < n && c < ld, r, c, ld));
+    for (int it = 0; it < N; ++it) {
+        const int r = m0 + 8 * (first + it) + tr, c = n0 + c8;
+        cv[it] = buf_load8(crs, sym_off(r < n && c < ld, r, c, ld));
     }
 }
 
@@ -124,76 +125,66 @@ __device__ __forceinline__ void sym_prefetch(half8v (&cpre)[Epi<C>::ROW_CHUNKS],
 // matrix (Csym optional: crs of size 0). Only the upper block triangle is stored: consumers read
 // a block below the diagonal as the transpose of its mirror above it, and a diagonal block either
 // way, so a diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the
-// Gram iteration): its upper triangle is computed and its lower triangle is the mirror. A
-// diagonal tile is written in three parts per half:
-//   the row pass stores the 8-column chunks right of each 8 x 8 diagonal block and writes their
-//     final fp32 values back into the staging;
-//   one thread per row assembles its row of the diagonal block: upper elements computed, lower
-//     ones computed from the mirrored accumulator with Csym's own row (Csym's diagonal tile is
-//     exactly symmetric), so they equal their mirrors bit for bit;
-//   the column pass stores the chunks left of the diagonal blocks from the staged final values.
-// crow holds half 0's row-pass Csym chunks on entry (sym_prefetch, issued by the caller ahead of
-// the main loop) and receives half 1's once half 0's row pass is done.
+// Gram iteration): its upper triangle is computed and its lower triangle is the mirror.
+// With Csym, its tile is first copied into the staging as is; each value is then replaced in
+// place by the final value computed from it (the same lane reads and writes each position). The
+// staged final values are stored in up to three passes:
+//   the row pass: row chunks (of a diagonal tile: those right of its 8 x 8 diagonal blocks);
+//   diagonal tiles: one thread per row assembles its row of the diagonal block, the elements left
+//     of the diagonal read from the column above it;
+//   diagonal tiles: the column pass stores the chunks left of the diagonal blocks, read down the
+//     staged columns above the diagonal.
+// Every output element is stored once.
 template <class C>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
                                           __amdgpu_buffer_rsrc_t crs, bool has_c, int64_t ld, int n, int m0, int n0,
-                                          float alpha, float beta, float gamma,
-                                          half8v (&crow)[Epi<C>::ROW_CHUNKS]) {
-    using E = Epi<C>;
-    float* N = reinterpret_cast<float*>(smem);
+                                          float alpha, float beta, float gamma) {
+    using E = EpiH<C>;
+    _Float16* const S = reinterpret_cast<_Float16*>(smem);
     const bool diag = m0 == n0;
     const __amdgpu_buffer_rsrc_t ors = sym_rsrc(out, ld, n);
+    if (has_c) {
+        // requested once the main loop is done: held through it, even a part of them would be
+        // spilled to scratch memory by the register allocator
+        half8v cv[kRowChunks];
+        sym_load(cv, crs, ld, n, m0, n0, 0);
+        _Float16* const base = S + row_chunk_base();
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int rb = m0 + h * C::WM;   // first row of this half
-        // diagonal-block pass (diagonal tiles): local row dl, columns dc .. dc+7
-        const int dl = threadIdx.x;
-        const int dr = rb + dl, dc = rb + (dl & ~7);
-        const bool dkeep = diag && dl < C::WM && dr < n && dc < ld;
-        const half8v cdg = buf_load8(crs, sym_off(dkeep, dr, dc, ld));
-        stage_rows<C>(acc, smem, h, diag);
-        each_row_chunk<C>(
-            smem, [](int, int) { return true; },
-            [&](int it, int lr, int c8, float (&v)[8]) {
-                const int r = rb + lr, c = n0 + c8;
-                const bool keep = r < n && c < ld && !(diag && c < (r & ~7) + 8);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    float t = alpha * v[e];
-                    if (has_c) t += beta * static_cast<float>(crow[it][e]);
-                    if (r == c + e) t += gamma;
-                    v[e] = t;
-                }
-                buf_store8<2>(ors, sym_off(keep, r, c, ld), to_half8(v));
-                if (diag && keep) {   // the final values, for the column pass
-                    *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8) = floatx4{v[0], v[1], v[2], v[3]};
-                    *reinterpret_cast<floatx4*>(N + E::row_base(lr) + c8 + 4) = floatx4{v[4], v[5], v[6], v[7]};
-                }
-            });
-        if (h == 0) sym_prefetch<C>(crow, crs, ld, n, m0, n0, 1);
-        if (!diag) continue;
-        {   // reads only diagonal blocks, which the row pass leaves as staged
-            const int ri = dl & 7, lc = h * C::WM + (dl & ~7);   // tile-local column of dc
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int dlr = dl < C::WM ? dl : 0;   // rows past the half: any staged row, not stored
-                const float x = e >= ri ? N[E::row_base(dlr) + lc + e] : N[E::row_base((dlr & ~7) + e) + lc + ri];
-                float t = alpha * x;
-                if (has_c) t += beta * static_cast<float>(cdg[e]);
-                if (e == ri) t += gamma;
-                v[e] = t;
-            }
-            buf_store8(ors, sym_off(dkeep, dr, dc, ld), to_half8(v));
-        }
-        lds_barrier();   // the row pass's final values are in the staging
-        each_col_chunk<C>(
-            smem, [](int, int) { return true; },
-            [&](int, int cl, int lr8, float (&v)[8]) {   // v[e] is (r8 + e, c), stored at (c, r8 + e)
-                const int c = n0 + cl, r8 = rb + lr8;
-                buf_store8(ors, sym_off(c < n && r8 < ld && c > r8 + 7, c, r8, ld), to_half8(v));
-            });
+        for (int it = 0; it < kRowChunks; ++it) *reinterpret_cast<half8v*>(base + it * E::ROW_STEP) = cv[it];
+        lds_barrier();
     }
+    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a) {
+        half4 cv = {};
+        if (has_c) cv = *reinterpret_cast<const half4*>(S + E::rowoff(r) + c);
+        floatx4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float x = alpha * a[e];
+            if (has_c) x += beta * static_cast<float>(cv[e]);
+            if (diag && r == c + e) x += gamma;
+            t[e] = x;
+        }
+        return t;
+    });
+    lds_barrier();
+    each_row_chunk_h<C>(smem, [&](int, int lr, int c8, const half8v& h) {
+        const int r = m0 + lr, c = n0 + c8;
+        const bool keep = r < n && c < ld && !(diag && c8 < (lr & ~7) + 8);
+        buf_store8<2>(ors, sym_off(keep, r, c, ld), h);
+    });
+    if (!diag) return;
+    {
+        const int lr = threadIdx.x, cb = lr & ~7;
+        half8v h = *reinterpret_cast<const half8v*>(S + E::rowoff(lr) + cb);
+#pragma unroll
+        for (int e = 0; e < 7; ++e)
+            if (e < (lr & 7)) h[e] = S[E::rowoff(cb + e) + lr];
+        buf_store8(ors, sym_off(m0 + lr < n && m0 + cb < ld, m0 + lr, m0 + cb, ld), h);
+    }
+    each_col_chunk_h<C>(smem, [&](int cl, int r8, const half8v& h) {   // h[e] is (r8 + e, cl), stored at (cl, r8 + e)
+        const int c = m0 + cl, r = m0 + r8;
+        buf_store8(ors, sym_off(c < n && r < ld && r8 + 8 <= cl, c, r, ld), h);
+    });
 }
 
 // One Newton-Schulz operation of a phase launch (see ns_phase_kernel).
@@ -213,20 +204,21 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int rows = M.rows, cols = M.cols, ldx = M.ldx, flags = M.flags;
-    // the stored first iterate is sigma * u up to the factor x0scale; applied per output chunk
-    // (x * 1 is exact), so the accumulators stay in their registers
+    // the stored first iterate is sigma * u up to the factor x0scale, applied as the tile is
+    // staged (x * 1 is exact); every output of the update is the f16 rounding of acc * osc
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
+
+    stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a) {
+        return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
+    });
+    lds_barrier();
 
     if (!op.final_iter) {
         _Float16* const dst = op.xsel == kXA ? M.xb : M.xa;
-#pragma unroll 1
-        for (int h = 0; h < 2; ++h)
-            for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
-                const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] *= osc;
-                if (r < rows && c < ldx) stg_nt<half8v>(dst + (int64_t)r * ldx + c, to_half8(v));
-            });
+        each_row_chunk_h<NsCfg>(smem, [&](int, int lr, int c8, const half8v& h) {
+            const int r = m0 + lr, c = n0 + c8;
+            if (r < rows && c < ldx) stg_nt<half8v>(dst + (int64_t)r * ldx + c, h);
+        });
         return;
     }
 
@@ -235,26 +227,21 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
         _Float16* const uout = M.uout;
         float* const rowsq = M.rowsqpart + (int64_t)tj * rows;
-#pragma unroll 1
-        for (int h = 0; h < 2; ++h)
-            for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
-                const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
+        each_row_chunk_h<NsCfg>(smem, [&](int, int lr, int c8, const half8v& h) {
+            const int r = m0 + lr, c = n0 + c8;
+            float sq = 0.f;
+            if (r < rows && c < ldx) {
+                stg_nt<half8v>(uout + (int64_t)r * ldx + c, h);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] *= osc;
-                const half8v hv = to_half8(v);
-                float sq = 0.f;
-                if (r < rows && c < ldx) {
-                    stg_nt<half8v>(uout + (int64_t)r * ldx + c, hv);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float f = static_cast<float>(hv[e]);
-                        sq += f * f;
-                    }
+                for (int e = 0; e < 8; ++e) {
+                    const float f = static_cast<float>(h[e]);
+                    sq += f * f;
                 }
-                static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
-                sq = sum32_upper(sq);
-                if ((threadIdx.x & 31) == 31 && r < rows) stg<float>(rowsq + r, sq);
-            });
+            }
+            static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
+            sq = sum32_upper(sq);
+            if ((threadIdx.x & 31) == 31 && r < rows) stg<float>(rowsq + r, sq);
+        });
         return;
     }
 
@@ -267,31 +254,29 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const float eta = (flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta, wd = M.wd;
     float* const p = M.p;
     float psq = 0.f;
-    auto step8 = [&](float (&pv)[8], const float (&v)[8]) {
+    auto step8 = [&](float (&pv)[8], const half8v& h) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float q = cautious_step(pv[e], (float)(_Float16)(v[e] * osc), eta, wd);
+            const float q = cautious_step(pv[e], static_cast<float>(h[e]), eta, wd);
             pv[e] = apply ? q : pv[e];
             psq += pv[e] * pv[e];
         }
     };
-    using E = Epi<NsCfg>;
+    constexpr int NC = EpiH<NsCfg>::ROW_ITERS;
     if (vec && m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols) {
         // Whole tile inside the matrix (every tile of a matrix with 256-multiple sides). Chunk
-        // `it` of half h is row m0 + h*WM + 8*it + tid/32, columns n0 + 8*(tid%32) .. +7 (the
-        // row_chunk() order); numbered L = h * ROW_CHUNKS + it, chunk L is requested into ring
-        // slot L % D as soon as chunk L - D has been used (the first D before half 0 is staged).
-        // Buffer instructions address it as one resource over the tile's rows (scalar
-        // registers), a per-lane offset shared by every chunk and a wave-uniform row offset, so
-        // no per-chunk address occupies vector registers. No memory operation in the pass is
-        // conditional, so each wait covers exactly the load it needs.
-        static_assert(NsCfg::BN / 8 == 32, "32 lanes per row chunk");
+        // L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32) .. +7, requested into ring slot
+        // L % D as soon as chunk L - D has been used (the first D once the tile is staged). Buffer
+        // instructions address it as one resource over the tile's rows (scalar registers), a
+        // per-lane offset shared by every chunk and a wave-uniform row offset, so no per-chunk
+        // address occupies vector registers. No memory operation in the pass is conditional, so
+        // each wait covers exactly the load it needs.
         constexpr int D = 2;
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
             p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
         const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
-        auto soff = [&](int L) { return ((L / E::ROW_CHUNKS) * NsCfg::WM + 8 * (L % E::ROW_CHUNKS)) * cols * 4; };
+        auto soff = [&](int L) { return 8 * L * cols * 4; };
         float4 ring[D][2];
         auto fetch = [&](int L) {
             ring[L % D][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, soff(L), 0));
@@ -299,49 +284,44 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         };
 #pragma unroll
         for (int L = 0; L < D; ++L) fetch(L);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            for_rows<NsCfg>(acc, smem, h, [&](int it, int half, int, int, float (&v)[8]) {
-                const int L = half * E::ROW_CHUNKS + it;
-                const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
-                float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                step8(pv, v);
-                // Stored whether or not the matrix is applied (the launch's task lists hold only
-                // applied matrices; otherwise p is written back unchanged). Each of the two
-                // stores covers every other 16 bytes: plain stores, which L2 merges into lines.
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[0], pv[1], pv[2], pv[3])),
-                                                       prs, voff, soff(L), 0);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[4], pv[5], pv[6], pv[7])),
-                                                       prs, voff + 16, soff(L), 0);
-                if (L + D < 2 * E::ROW_CHUNKS) fetch(L + D);
-                __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: no hoisted LDS reads
-            });
+        each_row_chunk_h<NsCfg>(smem, [&](int L, int, int, const half8v& h) {
+            const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
+            float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            step8(pv, h);
+            // Stored whether or not the matrix is applied (the launch's task lists hold only
+            // applied matrices; otherwise p is written back unchanged). Each of the two stores
+            // covers every other 16 bytes: plain stores, which L2 merges into lines.
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[0], pv[1], pv[2], pv[3])),
+                                                   prs, voff, soff(L), 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[4], pv[5], pv[6], pv[7])),
+                                                   prs, voff + 16, soff(L), 0);
+            if (L + D < NC) fetch(L + D);
+            __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: no hoisted LDS reads
+        });
     } else {   // edge tiles: each chunk loaded where it is used
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            for_rows<NsCfg>(acc, smem, h, [&](int, int half, int lr, int c8, float (&v)[8]) {
-                const int r = m0 + half * NsCfg::WM + lr, c = n0 + c8;
-                if (r >= rows || c >= cols) return;
-                float* pp = p + (int64_t)r * cols + c;
-                if (vec && c + 8 <= cols) {
-                    const float4 p0 = ldg<float4>(pp), p1 = ldg<float4>(pp + 4);
-                    float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                    step8(pv, v);
-                    if (apply) {
-                        stg<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
-                        stg<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
-                    }
-                } else {
-                    for (int e = 0; e < 8 && c + e < cols; ++e) {
-                        float x = ldg<float>(pp + e);
-                        if (apply) {
-                            x = cautious_step(x, (float)(_Float16)(v[e] * osc), eta, wd);
-                            stg<float>(pp + e, x);
-                        }
-                        psq += x * x;
-                    }
+        each_row_chunk_h<NsCfg>(smem, [&](int, int lr, int c8, const half8v& h) {
+            const int r = m0 + lr, c = n0 + c8;
+            if (r >= rows || c >= cols) return;
+            float* pp = p + (int64_t)r * cols + c;
+            if (vec && c + 8 <= cols) {
+                const float4 p0 = ldg<float4>(pp), p1 = ldg<float4>(pp + 4);
+                float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                step8(pv, h);
+                if (apply) {
+                    stg<float4>(pp, make_float4(pv[0], pv[1], pv[2], pv[3]));
+                    stg<float4>(pp + 4, make_float4(pv[4], pv[5], pv[6], pv[7]));
                 }
-            });
+            } else {
+                for (int e = 0; e < 8 && c + e < cols; ++e) {
+                    float x = ldg<float>(pp + e);
+                    if (apply) {
+                        x = cautious_step(x, static_cast<float>(h[e]), eta, wd);
+                        stg<float>(pp + e, x);
+                    }
+                    psq += x * x;
+                }
+            }
+        });
     }
     if (md) {
         const float t = block_sum(psq, scratch);
@@ -369,7 +349,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 // All three run the same main loop (gemm_tile) with per-operation operands and layouts.
 __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
                                                        TaskList t1, NsOp op1) {
-    __shared__ __attribute__((aligned(16))) char smem[Epi<NsCfg>::SMEM];
+    __shared__ __attribute__((aligned(16))) char smem[EpiH<NsCfg>::SMEM];
     __shared__ float scratch[4];
     int b = xcd_remap(blockIdx.x, gridDim.x);
     const bool second = b >= t0.total;
@@ -415,12 +395,6 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
             b_k0 = tj * KB;
         }
     }
-    // the C term of a symmetric product is requested before the main loop (it arrives with the
-    // first operand tiles and waits in registers)
-    const _Float16* csym = op.kind == kOpSym && op.csel >= 0 && op.beta != 0.f ? sym_buf(M, op.csel) : nullptr;
-    const __amdgpu_buffer_rsrc_t crs = sym_rsrc(csym, M.lds, M.s);
-    half8v c0[Epi<NsCfg>::ROW_CHUNKS];
-    sym_prefetch<NsCfg>(c0, crs, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, 0);
     floatx16 acc[NsCfg::TM][NsCfg::TN];
     gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero,
                      op.kind != kOpUpdate && ti == tj);
@@ -428,11 +402,12 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
         update_finish(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
         const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
-        sym_store<NsCfg>(acc, smem, M.gram, crs, false, M.lds, M.s, ti * NsCfg::BM, tj * NsCfg::BN, osc * osc, 0.f,
-                         0.f, c0);
+        sym_store<NsCfg>(acc, smem, M.gram, sym_rsrc(nullptr, 0, 0), false, M.lds, M.s, ti * NsCfg::BM,
+                         tj * NsCfg::BN, osc * osc, 0.f, 0.f);
     } else {
-        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), crs, csym != nullptr, M.lds, M.s, ti * NsCfg::BM,
-                         tj * NsCfg::BN, op.alpha, op.beta, op.gamma, c0);
+        const _Float16* csym = op.csel >= 0 && op.beta != 0.f ? sym_buf(M, op.csel) : nullptr;
+        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), sym_rsrc(csym, M.lds, M.s), csym != nullptr, M.lds, M.s,
+                         ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.beta, op.gamma);
     }
 }
 
