@@ -353,8 +353,10 @@ struct EpiH {
     __device__ static __forceinline__ int rowoff(int r) { return r * SH + (r >> 3) * PAD; }
 };
 
-// Stages f16(val(r, c, a)) for the accumulators this wave owns: val gives the final values of
-// tile-local row r, columns c .. c+3 from their 4 accumulators a. On a diagonal tile (gemm_tile's
+// Stages f16(val(r, c, a, dblk)) for the accumulators this wave owns: val gives the final values
+// of tile-local row r, columns c .. c+3 from their 4 accumulators a; dblk (wave-uniform) says that
+// the 32 x 32 block holds elements of the tile's diagonal, r == c + e for some e, which only the
+// diagonal blocks of waves 0 and 3 on a diagonal tile do. On a diagonal tile (gemm_tile's
 // `diag`) the blocks sit where TileRole put them (waves 1 and 2: rows 0-63 and 64-127 of the
 // upper-right quadrant); the lower-left quadrant is not staged. The caller separates this from
 // the previous use of smem and from the reads that follow with barriers.
@@ -362,8 +364,8 @@ template <class C, class Val>
 __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* smem, bool diag, Val val) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     _Float16* S = reinterpret_cast<_Float16*>(smem);
-    auto put = [&](int r, int c, const floatx4& a) {
-        const floatx4 v = val(r, c, a);
+    auto put = [&](int r, int c, const floatx4& a, bool dblk) {
+        const floatx4 v = val(r, c, a, dblk);
         *reinterpret_cast<half4*>(S + EpiH<C>::rowoff(r) + c) =
             half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
     };
@@ -376,9 +378,11 @@ __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* s
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     put(r0 + 32 * i + (lane & 31), C::WN + 32 * j + 8 * q + 4 * (lane >> 5),
-                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
+                        false);
     } else {
         const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
+        const bool dwave = diag && wm == wn;
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -386,7 +390,8 @@ __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* s
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     put(wm + 32 * i + (lane & 31), wn + 32 * j + 8 * q + 4 * (lane >> 5),
-                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
+                        i == j && dwave);
     }
 }
 

@@ -134,16 +134,16 @@ __device__ __forceinline__ void sym_load(half8v (&cv)[N], __amdgpu_buffer_rsrc_t
 //     of the diagonal read from the column above it;
 //   diagonal tiles: the column pass stores the chunks left of the diagonal blocks, read down the
 //     staged columns above the diagonal.
-// Every output element is stored once.
-template <class C>
+// Every output element is stored once. HAS_C: the Csym term is present (else crs and beta are
+// unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1 would leave as is).
+template <class C, bool HAS_C, bool SCALE>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
-                                          __amdgpu_buffer_rsrc_t crs, bool has_c, int64_t ld, int n, int m0, int n0,
+                                          __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0, int n0,
                                           float alpha, float beta, float gamma) {
     using E = EpiH<C>;
     _Float16* const S = reinterpret_cast<_Float16*>(smem);
     const bool diag = m0 == n0;
-    const __amdgpu_buffer_rsrc_t ors = sym_rsrc(out, ld, n);
-    if (has_c) {
+    if constexpr (HAS_C) {
         // requested once the main loop is done: held through it, even a part of them would be
         // spilled to scratch memory by the register allocator
         half8v cv[kRowChunks];
@@ -153,26 +153,40 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
         for (int it = 0; it < kRowChunks; ++it) *reinterpret_cast<half8v*>(base + it * E::ROW_STEP) = cv[it];
         lds_barrier();
     }
-    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a) {
-        half4 cv = {};
-        if (has_c) cv = *reinterpret_cast<const half4*>(S + E::rowoff(r) + c);
+    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a, bool dblk) {
         floatx4 t;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float x = alpha * a[e];
-            if (has_c) x += beta * static_cast<float>(cv[e]);
-            if (diag && r == c + e) x += gamma;
-            t[e] = x;
+        for (int e = 0; e < 4; ++e) t[e] = SCALE ? alpha * a[e] : a[e];
+        if constexpr (HAS_C) {
+            const half4 cv = *reinterpret_cast<const half4*>(S + E::rowoff(r) + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] += beta * static_cast<float>(cv[e]);
+        }
+        if (dblk) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (r == c + e) t[e] += gamma;
         }
         return t;
     });
     lds_barrier();
-    each_row_chunk_h<C>(smem, [&](int, int lr, int c8, const half8v& h) {
-        const int r = m0 + lr, c = n0 + c8;
-        const bool keep = r < n && c < ld && !(diag && c8 < (lr & ~7) + 8);
-        buf_store8<2>(ors, sym_off(keep, r, c, ld), h);
-    });
+    {
+        // Row pass through a resource over the tile's rows below n: the row offset of a chunk is
+        // an add to one per-lane offset, and a lane whose columns lie past ld stores nothing.
+        const int rows = n - m0 < C::BM ? n - m0 : C::BM;
+        const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+            out + int64_t(m0) * ld, 0, static_cast<int>(rows * ld * 2), 0x00020000);
+        const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
+        const uint32_t vbase = n0 + 8 * ck < ld ? static_cast<uint32_t>((tr * ld + n0 + 8 * ck) * 2) : kOutOfRange;
+        const uint32_t rstep = static_cast<uint32_t>(16 * ld);   // bytes of 8 rows
+        each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) {
+            // a diagonal tile stores the chunks right of its 8 x 8 diagonal blocks: ck > it
+            const uint32_t off = diag && ck <= it ? kOutOfRange : vbase + it * rstep;
+            buf_store8<2>(trs, off, h);
+        });
+    }
     if (!diag) return;
+    const __amdgpu_buffer_rsrc_t ors = sym_rsrc(out, ld, n);
     {
         const int lr = threadIdx.x, cb = lr & ~7;
         half8v h = *reinterpret_cast<const half8v*>(S + E::rowoff(lr) + cb);
@@ -204,13 +218,16 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int rows = M.rows, cols = M.cols, ldx = M.ldx, flags = M.flags;
-    // the stored first iterate is sigma * u up to the factor x0scale, applied as the tile is
-    // staged (x * 1 is exact); every output of the update is the f16 rounding of acc * osc
+    // the stored first iterate is sigma * u up to the factor x0scale, applied as the first
+    // update's tile is staged; every output of the update is the f16 rounding of acc * osc
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
 
-    stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a) {
-        return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
-    });
+    if (op.first)
+        stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a, bool) {
+            return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
+        });
+    else
+        stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) { return a; });
     lds_barrier();
 
     if (!op.final_iter) {
@@ -401,13 +418,27 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     if (op.kind == kOpUpdate) {
         update_finish(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
-        const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
-        sym_store<NsCfg>(acc, smem, M.gram, sym_rsrc(nullptr, 0, 0), false, M.lds, M.s, ti * NsCfg::BM,
-                         tj * NsCfg::BN, osc * osc, 0.f, 0.f);
+        const __amdgpu_buffer_rsrc_t none = sym_rsrc(nullptr, 0, 0);
+        const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
+        if (op.first) {
+            const float osc = M.scal[kScalX0Scale];
+            sym_store<NsCfg, false, true>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
+        } else {
+            sym_store<NsCfg, false, false>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, 1.f, 0.f, 0.f);
+        }
     } else {
-        const _Float16* csym = op.csel >= 0 && op.beta != 0.f ? sym_buf(M, op.csel) : nullptr;
-        sym_store<NsCfg>(acc, smem, sym_buf(M, op.osel), sym_rsrc(csym, M.lds, M.s), csym != nullptr, M.lds, M.s,
-                         ti * NsCfg::BM, tj * NsCfg::BN, op.alpha, op.beta, op.gamma);
+        const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
+        _Float16* const out = sym_buf(M, op.osel);
+        if (op.csel >= 0 && op.beta != 0.f) {
+            sym_store<NsCfg, true, true>(acc, smem, out, sym_rsrc(sym_buf(M, op.csel), M.lds, M.s), M.lds, M.s, m0,
+                                         n0, op.alpha, op.beta, op.gamma);
+        } else if (op.alpha != 1.f) {
+            sym_store<NsCfg, false, true>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, op.alpha, 0.f,
+                                          op.gamma);
+        } else {
+            sym_store<NsCfg, false, false>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, 1.f, 0.f,
+                                           op.gamma);
+        }
     }
 }
 
