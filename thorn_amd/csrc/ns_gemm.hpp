@@ -356,19 +356,32 @@ struct EpiH {
 // Stages f16(val(r, c, a, dblk)) for the accumulators this wave owns: val gives the final values
 // of tile-local row r, columns c .. c+3 from their 4 accumulators a; dblk (wave-uniform) says that
 // the 32 x 32 block holds elements of the tile's diagonal, r == c + e for some e, which only the
-// diagonal blocks of waves 0 and 3 on a diagonal tile do. On a diagonal tile (gemm_tile's
-// `diag`) the blocks sit where TileRole put them (waves 1 and 2: rows 0-63 and 64-127 of the
-// upper-right quadrant); the lower-left quadrant is not staged. The caller separates this from
-// the previous use of smem and from the reads that follow with barriers.
+// diagonal blocks of waves 0 and 3 on a diagonal tile do. The caller separates this from the
+// previous use of smem and from the reads that follow with barriers.
+// On a diagonal tile (gemm_tile's `diag`, symmetric results only) the blocks sit where TileRole
+// put them (waves 1 and 2: rows 0-63 and 64-127 of the upper-right quadrant; waves 0 and 3: the
+// blocks on and above the diagonal of their quadrants) and every value above the tile's diagonal
+// is also written at its transposed position, so the staged tile is exactly symmetric: the
+// diagonal blocks of waves 0 and 3 are written whole first, then the transposes of their upper
+// elements replace the lower ones (a wave's LDS writes complete in program order).
 template <class C, class Val>
 __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* smem, bool diag, Val val) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     _Float16* S = reinterpret_cast<_Float16*>(smem);
-    auto put = [&](int r, int c, const floatx4& a, bool dblk) {
-        const floatx4 v = val(r, c, a, dblk);
-        *reinterpret_cast<half4*>(S + EpiH<C>::rowoff(r) + c) =
-            half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    auto quad = [&](int i, int j, int q) {
+        return floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     };
+    auto put = [&](int r, int c, const half4& h) { *reinterpret_cast<half4*>(S + EpiH<C>::rowoff(r) + c) = h; };
+    auto put_t = [&](int r, int c, const half4& h, bool upper_only) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (!upper_only || c + e > r) S[EpiH<C>::rowoff(c + e) + r] = h[e];
+    };
+    auto final4 = [&](int r, int c, const floatx4& a, bool dblk) {
+        const floatx4 v = val(r, c, a, dblk);
+        return half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    };
+    const int lr = lane & 31, lc = 4 * (lane >> 5);
     if (diag && (wave == 1 || wave == 2)) {
         const int r0 = (wave >> 1) * (C::WM / 2);
 #pragma unroll
@@ -376,22 +389,43 @@ __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* s
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    put(r0 + 32 * i + (lane & 31), C::WN + 32 * j + 8 * q + 4 * (lane >> 5),
-                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
-                        false);
+                for (int q = 0; q < 4; ++q) {
+                    const int r = r0 + 32 * i + lr, c = C::WN + 32 * j + 8 * q + lc;
+                    const half4 h = final4(r, c, quad(i, j, q), false);
+                    put(r, c, h);
+                    put_t(r, c, h, false);
+                }
+    } else if (diag) {
+        const int wm = (wave >> 1) * C::WM;
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+            for (int j = i; j < C::TN; ++j) {
+                half4 h[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = wm + 32 * i + lr, c = wm + 32 * j + 8 * q + lc;
+                    h[q] = final4(r, c, quad(i, j, q), i == j);
+                    put(r, c, h[q]);
+                    if (j > i) put_t(r, c, h[q], false);
+                }
+                if (j == i) {
+                    __builtin_amdgcn_sched_barrier(0);   // the whole block first
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) put_t(wm + 32 * i + lr, wm + 32 * j + 8 * q + lc, h[q], true);
+                }
+            }
     } else {
         const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
-        const bool dwave = diag && wm == wn;
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
 #pragma unroll
             for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    put(wm + 32 * i + (lane & 31), wn + 32 * j + 8 * q + 4 * (lane >> 5),
-                        floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
-                        i == j && dwave);
+                for (int q = 0; q < 4; ++q) {
+                    const int r = wm + 32 * i + lr, c = wn + 32 * j + 8 * q + lc;
+                    put(r, c, final4(r, c, quad(i, j, q), false));
+                }
     }
 }
 
@@ -416,24 +450,6 @@ __device__ __forceinline__ void each_row_chunk_h(const char* smem, Fn fn) {
 #pragma unroll
     for (int it = 0; it < EpiH<C>::ROW_ITERS; ++it)
         fn(it, 8 * it + tr, c8, *reinterpret_cast<const half8v*>(base + it * EpiH<C>::ROW_STEP));
-}
-
-// fn(c, r8, h): h[e] = staged (r8 + e, c), 8 rows of one column, over this thread's column
-// chunks: 16 lanes of a wave take 16 consecutive row chunks of one column (4 columns per wave
-// instruction), so the mirror of a column part is 256 contiguous bytes of an output row.
-template <class C, class Fn>
-__device__ __forceinline__ void each_col_chunk_h(const char* smem, Fn fn) {
-    const _Float16* S = reinterpret_cast<const _Float16*>(smem);
-#pragma unroll 4
-    for (int it = 0; it < EpiH<C>::ROW_ITERS; ++it) {
-        const int idx = it * 256 + threadIdx.x;
-        const int c = 4 * (idx >> 7) + ((idx >> 4) & 3);
-        const int r8 = 8 * (16 * ((idx >> 6) & 1) + (idx & 15));
-        half8v h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = S[EpiH<C>::rowoff(r8 + e) + c];
-        fn(c, r8, h);
-    }
 }
 
 __device__ __forceinline__ half8v to_half8(const float (&v)[8]) {

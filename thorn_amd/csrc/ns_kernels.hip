@@ -127,14 +127,9 @@ __device__ __forceinline__ void sym_load(half8v (&cv)[N], __amdgpu_buffer_rsrc_t
 // way, so a diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the
 // Gram iteration): its upper triangle is computed and its lower triangle is the mirror.
 // With Csym, its tile is first copied into the staging as is; each value is then replaced in
-// place by the final value computed from it (the same lane reads and writes each position). The
-// staged final values are stored in up to three passes:
-//   the row pass: row chunks (of a diagonal tile: those right of its 8 x 8 diagonal blocks);
-//   diagonal tiles: one thread per row assembles its row of the diagonal block, the elements left
-//     of the diagonal read from the column above it;
-//   diagonal tiles: the column pass stores the chunks left of the diagonal blocks, read down the
-//     staged columns above the diagonal.
-// Every output element is stored once. HAS_C: the Csym term is present (else crs and beta are
+// place by the final value computed from it (the same lane reads and writes each position). On a
+// diagonal tile the staging also receives the transposes of the values above the diagonal
+// (stage_f16), so one pass of row chunks stores every tile. HAS_C: the Csym term is present (else crs and beta are
 // unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1 would leave as is).
 template <class C, bool HAS_C, bool SCALE>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
@@ -180,25 +175,9 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
         const uint32_t vbase = n0 + 8 * ck < ld ? static_cast<uint32_t>((tr * ld + n0 + 8 * ck) * 2) : kOutOfRange;
         const uint32_t rstep = static_cast<uint32_t>(16 * ld);   // bytes of 8 rows
         each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) {
-            // a diagonal tile stores the chunks right of its 8 x 8 diagonal blocks: ck > it
-            const uint32_t off = diag && ck <= it ? kOutOfRange : vbase + it * rstep;
-            buf_store8<2>(trs, off, h);
+            buf_store8<2>(trs, vbase + it * rstep, h);
         });
     }
-    if (!diag) return;
-    const __amdgpu_buffer_rsrc_t ors = sym_rsrc(out, ld, n);
-    {
-        const int lr = threadIdx.x, cb = lr & ~7;
-        half8v h = *reinterpret_cast<const half8v*>(S + E::rowoff(lr) + cb);
-#pragma unroll
-        for (int e = 0; e < 7; ++e)
-            if (e < (lr & 7)) h[e] = S[E::rowoff(cb + e) + lr];
-        buf_store8(ors, sym_off(m0 + lr < n && m0 + cb < ld, m0 + lr, m0 + cb, ld), h);
-    }
-    each_col_chunk_h<C>(smem, [&](int cl, int r8, const half8v& h) {   // h[e] is (r8 + e, cl), stored at (cl, r8 + e)
-        const int c = m0 + cl, r = m0 + r8;
-        buf_store8(ors, sym_off(c < n && r < ld && r8 + 8 <= cl, c, r, ld), h);
-    });
 }
 
 // One Newton-Schulz operation of a phase launch (see ns_phase_kernel).
