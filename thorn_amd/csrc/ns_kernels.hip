@@ -325,8 +325,9 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     }
 }
 
-// A Newton-Schulz phase launch: blocks [0, t0.total) run op0 over the tiles of task list t0, the
-// next t1.total blocks run op1 over t1. The two operations belong to disjoint sets of matrices
+// A Newton-Schulz phase launch: t0.total blocks run op0 over the tiles of task list t0, the other
+// t1.total blocks run op1 over t1, each XCD taking its eighth of the list with the longer tiles
+// first (t1_first: t1's; see xcd_split). The two operations belong to disjoint sets of matrices
 // (the square ones, on the plain quintic, and the others, on Gram Newton-Schulz), so one launch
 // carries a step of each schedule. Each block computes one 256 x 256 tile:
 //   Gram (kOpGram): R = X X^T (wide) or X^T X (tall) of the iterate in buffer `xsel`, rows of X
@@ -344,14 +345,15 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 //     epilogue.
 // All three run the same main loop (gemm_tile) with per-operation operands and layouts.
 __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
-                                                       TaskList t1, NsOp op1) {
+                                                       TaskList t1, NsOp op1, int t1_first) {
     __shared__ __attribute__((aligned(16))) char smem[EpiH<NsCfg>::SMEM];
     __shared__ float scratch[4];
-    int b = xcd_remap(blockIdx.x, gridDim.x);
-    const bool second = b >= t0.total;
+    int b;
+    const bool later = t1_first ? xcd_split(blockIdx.x, t1.total, t0.total, b)
+                                : xcd_split(blockIdx.x, t0.total, t1.total, b);
+    const bool second = t1_first ? !later : later;
     const TaskList& tl = second ? t1 : t0;
     const NsOp& op = second ? op1 : op0;
-    if (second) b -= t0.total;
     if (op.kind == kOpNone) return;
     const int k = find_task(tl.starts, tl.n, b);
     const OrthoMat& M = mats[tl.order[k]];

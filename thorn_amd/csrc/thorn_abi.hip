@@ -125,6 +125,9 @@ struct thorn_ortho_plan {
     // matrices applied this step (the reference skips the polar factor of the others,
     // thorn.py:1395-1396, 1436-1441). Same table offsets, fewer entries.
     TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{};
+    // mean short and long side of each set's matrices: the contraction lengths of its GEMM tiles
+    // (long side: Gram matrices; short side: the other products), to run longer tiles first
+    double mean_s[2]{}, mean_l[2]{};
     LaunchTimer timer;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
@@ -368,6 +371,16 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     std::vector<int32_t> sets[2];
     for (int i = 0; i < n; ++i) sets[plan->mats[i].l >= 2 * plan->mats[i].s ? 1 : 0].push_back(i);
     for (int q = 0; q < 2; ++q) {
+        for (int i : sets[q]) {
+            plan->mean_s[q] += plan->mats[i].s;
+            plan->mean_l[q] += plan->mats[i].l;
+        }
+        if (!sets[q].empty()) {
+            plan->mean_s[q] /= double(sets[q].size());
+            plan->mean_l[q] /= double(sets[q].size());
+        }
+    }
+    for (int q = 0; q < 2; ++q) {
         plan->sym_order[q] = snake(sets[q], [&](int i) { return double(plan->mats[i].sym_tiles) * plan->mats[i].l; });
         plan->g3_order[q] = snake(sets[q], [&](int i) {
             return double(plan->mats[i].g3_tiles_m) * plan->mats[i].g3_tiles_n * plan->mats[i].s;
@@ -594,8 +607,12 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         }
         const int total = tl[1].total + tl[0].total;
         if (total == 0) continue;
+        auto klen = [&](int q) {
+            return op[q].kind == thorn::kOpNone ? 0.0 : op[q].kind == thorn::kOpGram ? plan->mean_l[q] : plan->mean_s[q];
+        };
+        const int square_first = klen(0) > klen(1) ? 1 : 0;
         THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(256), 0, st, mats, tl[1],
-                     op[1], tl[0], op[0]);
+                     op[1], tl[0], op[0], square_first);
     }
     if (plan->pnn_live.n > 0) {
         const thorn::TaskList pnn = task_list(dev, plan->pnn_live);

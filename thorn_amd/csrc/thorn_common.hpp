@@ -143,13 +143,23 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 }
 
 // Workgroups of a launch are dispatched to the 8 XCDs round-robin (block b runs on XCD b % 8),
-// and each XCD has its own L2. Remapping makes XCD x run the contiguous range
-// [x*per + min(x, rem), ...) of logical tiles, so tiles that share operand panels share an L2.
-// A bijection on [0, total).
-__device__ __forceinline__ int xcd_remap(int b, int total) {
+// and each XCD has its own L2. A launch over two tile lists P and Q (np and nq tiles) makes XCD x
+// run a contiguous eighth of P, then a contiguous eighth of Q: tiles that share operand panels
+// share an L2, and every XCD gets the same mix of both lists. P's eighths go to XCDs 0..7 (the
+// np % 8 larger ones first); Q's continue where P's remainder stopped, so each XCD's share of the
+// two adds up to its share of the blocks, ceil((np + nq - x) / 8). Returns whether block b is a
+// tile of Q, and its tile index in its list; a bijection from [0, np + nq).
+__device__ __forceinline__ bool xcd_split(int b, int np, int nq, int& idx) {
     const int x = b & 7, i = b >> 3;
-    const int per = total >> 3, rem = total & 7;
-    return x * per + (x < rem ? x : rem) + i;
+    const int pp = np >> 3, rp = np & 7;
+    const int cp = pp + (x < rp ? 1 : 0);   // this XCD's tiles of P
+    if (i < cp) {
+        idx = x * pp + (x < rp ? x : rp) + i;
+        return false;
+    }
+    const int pq = nq >> 3, rq = nq & 7, xq = (x - rp) & 7;
+    idx = xq * pq + (xq < rq ? xq : rq) + (i - cp);
+    return true;
 }
 
 // Finds the task k with starts[k] <= b < starts[k+1] (starts has n+1 entries, ascending).
