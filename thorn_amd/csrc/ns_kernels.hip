@@ -201,6 +201,30 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     // update's tile is staged; every output of the update is the f16 rounding of acc * osc
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
 
+    // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) streams p
+    // through a ring of D row chunks: chunk L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32)
+    // .. +7, requested into slot L % D as soon as chunk L - D has been used, the first D before
+    // the tile is staged. Buffer instructions address it as one resource over the tile's rows
+    // (scalar registers), a per-lane offset shared by every chunk and a wave-uniform row offset,
+    // so no per-chunk address occupies vector registers.
+    const bool apply_full = op.final_iter && !(flags & kFlagPNN) && (flags & kFlagVec4) &&
+                            m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols;
+    constexpr int D = 8;
+    constexpr int NC = EpiH<NsCfg>::ROW_ITERS;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        M.p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
+    const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
+    auto soff = [&](int L) { return 8 * L * cols * 4; };
+    float4 ring[D][2];
+    auto fetch = [&](int L) {
+        ring[L % D][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, soff(L), 0));
+        ring[L % D][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff + 16, soff(L), 0));
+    };
+    if (apply_full) {
+#pragma unroll
+        for (int L = 0; L < D; ++L) fetch(L);
+    }
+
     if (op.first)
         stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a, bool) {
             return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
@@ -258,28 +282,10 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
             psq += pv[e] * pv[e];
         }
     };
-    constexpr int NC = EpiH<NsCfg>::ROW_ITERS;
-    if (vec && m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols) {
-        // Whole tile inside the matrix (every tile of a matrix with 256-multiple sides). Chunk
-        // L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32) .. +7, requested into ring slot
-        // L % D as soon as chunk L - D has been used (the first D once the tile is staged). Buffer
-        // instructions address it as one resource over the tile's rows (scalar registers), a
-        // per-lane offset shared by every chunk and a wave-uniform row offset, so no per-chunk
-        // address occupies vector registers. No memory operation in the pass is conditional, so
-        // each wait covers exactly the load it needs.
-        constexpr int D = 2;
+    if (apply_full) {
+        // No memory operation in the pass is conditional, so each wait covers exactly the load
+        // it needs.
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-            p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
-        const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
-        auto soff = [&](int L) { return 8 * L * cols * 4; };
-        float4 ring[D][2];
-        auto fetch = [&](int L) {
-            ring[L % D][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, soff(L), 0));
-            ring[L % D][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff + 16, soff(L), 0));
-        };
-#pragma unroll
-        for (int L = 0; L < D; ++L) fetch(L);
         each_row_chunk_h<NsCfg>(smem, [&](int L, int, int, const half8v& h) {
             const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
             float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
