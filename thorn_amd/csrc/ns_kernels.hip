@@ -233,11 +233,22 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) { return a; });
     lds_barrier();
 
+    // The f16 row passes (next iterate, u'): one buffer resource over the tile's rows below
+    // `rows`, so a chunk's offset is one per-lane offset plus a uniform row step; a lane whose
+    // columns lie past ldx stores nothing.
+    const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
+    const bool col_ok = n0 + 8 * ck < ldx;
+    const uint32_t vbase = col_ok ? static_cast<uint32_t>((tr * ldx + n0 + 8 * ck) * 2) : kOutOfRange;
+    const uint32_t rstep = static_cast<uint32_t>(16 * ldx);   // bytes of 8 rows
+    auto tile_rsrc = [&](_Float16* base) {
+        const int trows = rows - m0 < NsCfg::BM ? rows - m0 : NsCfg::BM;
+        return __builtin_amdgcn_make_buffer_rsrc(base + int64_t(m0) * ldx, 0, trows * ldx * 2, 0x00020000);
+    };
+
     if (!op.final_iter) {
-        _Float16* const dst = op.xsel == kXA ? M.xb : M.xa;
-        each_row_chunk_h<NsCfg>(smem, [&](int, int lr, int c8, const half8v& h) {
-            const int r = m0 + lr, c = n0 + c8;
-            if (r < rows && c < ldx) stg_nt<half8v>(dst + (int64_t)r * ldx + c, h);
+        const __amdgpu_buffer_rsrc_t drs = tile_rsrc(op.xsel == kXA ? M.xb : M.xa);
+        each_row_chunk_h<NsCfg>(smem, [&](int it, int, int, const half8v& h) {
+            buf_store8<2>(drs, vbase + it * rstep, h);
         });
         return;
     }
@@ -245,19 +256,18 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     if (flags & kFlagPNN) {
         // u' in f16 (the reference's polar factor is f16 rounded, thorn.py:635, 662) and per-row
         // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
-        _Float16* const uout = M.uout;
+        const __amdgpu_buffer_rsrc_t urs = tile_rsrc(M.uout);
         float* const rowsq = M.rowsqpart + (int64_t)tj * rows;
-        each_row_chunk_h<NsCfg>(smem, [&](int, int lr, int c8, const half8v& h) {
-            const int r = m0 + lr, c = n0 + c8;
+        each_row_chunk_h<NsCfg>(smem, [&](int it, int lr, int, const half8v& h) {
+            const int r = m0 + lr;
+            buf_store8<2>(urs, vbase + it * rstep, h);
             float sq = 0.f;
-            if (r < rows && c < ldx) {
-                stg_nt<half8v>(uout + (int64_t)r * ldx + c, h);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float f = static_cast<float>(h[e]);
-                    sq += f * f;
-                }
+            for (int e = 0; e < 8; ++e) {
+                const float f = static_cast<float>(h[e]);
+                sq += f * f;
             }
+            sq = r < rows && col_ok ? sq : 0.f;
             static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
             sq = sum32_upper(sq);
             if ((threadIdx.x & 31) == 31 && r < rows) stg<float>(rowsq + r, sq);
