@@ -336,11 +336,11 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // Epilogue: every output of these GEMMs is f16, so the tile's final values are computed in
 // registers from the accumulators and staged once, as f16, in LDS (reusing the pipeline stages).
 // Row r of the staging starts at half rowoff(r) = r * SH + (r / 8) * PAD: rows are BN + 8 halves
-// (16-byte aligned) and every 8 rows add 8 more, so that the 16 lanes reading one column's row
-// chunks (each_col_chunk_h) and the 64 lanes writing an accumulator block (stage_f16) spread
-// over the banks. All four waves stage at once and one pass of 16-byte row chunks (32 lanes per
-// row) reads the tile back: half the LDS traffic of fp32 staging. Diagonal tiles of symmetric
-// results mirror staged f16 values, which keeps them exactly symmetric.
+// (16-byte aligned) and every 8 rows add 8 more, so that the 64 lanes writing an accumulator
+// block (stage_f16: 32 consecutive rows, 8 bytes each) spread over the banks. All four waves
+// stage at once and one pass of 16-byte row chunks (32 lanes per row) reads the tile back: half
+// the LDS traffic of fp32 staging. Diagonal tiles of symmetric results also stage the transposes
+// of their upper values, which keeps them exactly symmetric.
 template <class C>
 struct EpiH {
     static constexpr int SH = C::BN + 8;
