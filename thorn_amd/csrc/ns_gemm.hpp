@@ -452,11 +452,6 @@ __device__ __forceinline__ void each_row_chunk_h(const char* smem, Fn fn) {
         fn(it, 8 * it + tr, c8, *reinterpret_cast<const half8v*>(base + it * EpiH<C>::ROW_STEP));
 }
 
-__device__ __forceinline__ half8v to_half8(const float (&v)[8]) {
-    return half8v{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3],
-                  (_Float16)v[4], (_Float16)v[5], (_Float16)v[6], (_Float16)v[7]};
-}
-
 // Upper-triangle tile (ti <= tj) number q of a T x T tile grid, row by row.
 __device__ __forceinline__ void tri_decode(int q, int T, int& ti, int& tj) {
     int row = 0, rem = q;

@@ -295,7 +295,6 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     if (apply_full) {
         // No memory operation in the pass is conditional, so each wait covers exactly the load
         // it needs.
-        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         each_row_chunk_h<NsCfg>(smem, [&](int L, int, int, const half8v& h) {
             const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
             float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
