@@ -208,6 +208,39 @@ def test_single_matrix_update(shape, wd):
     _log(f'[gpu]   {w}')
 
 
+MANY = [(512, 1536), (1536, 512), (768, 768), (1024, 256), (640, 640), (300, 900), (512, 512), (96, 200)]
+
+
+def test_many_matrices_share_launches():
+    """One group of mixed shapes: every launch carries tiles of both Newton-Schulz schedules
+    (the Gram set and the square-ish set), each XCD taking its share of both lists, with tile
+    counts that are not multiples of the XCD count. Each matrix's step must match the oracle's
+    one-matrix step."""
+    _log(f'[gpu] many matrices {MANY}')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(1234)
+    p0 = [torch.randn(sh, generator=g) * 0.02 for sh in MANY]
+    grads = [torch.randn(sh, generator=g) * 1e-3 for sh in MANY]
+    grp = dict(orthogonalize=True, lr=1e-2, weight_decay=0.1)
+    pg = [torch.nn.Parameter(p.clone().to(DEV)) for p in p0]
+    gpu = thorn_amd.THORN([dict(grp, params=pg)])
+    for p, gr in zip(pg, grads):
+        p.grad = gr.clone().to(DEV)
+    gpu.step()
+    torch.cuda.synchronize()
+    w = {}
+    for i, sh in enumerate(MANY):
+        pc = torch.nn.Parameter(p0[i].clone())
+        cpu = O.OracleTHORN([dict(grp, params=[pc])])
+        pc.grad = grads[i].clone()
+        cpu.step()
+        dpg = pg[i].detach().cpu() - p0[i]
+        dpc = pc.detach() - p0[i]
+        dpe = exact_dp(p0[i], grads[i], torch.zeros_like(p0[i]), grp)
+        check_ortho_dp(dpg, dpc, dpe, w, f'{sh}')
+    _log(f'[gpu]   {w}')
+
+
 def test_ns_against_closed_form():
     """lr=1, wd=0, square matrix: delta p = -scale * u', compared with U phi(S) V^T in f64."""
     thorn_amd = _thorn()
