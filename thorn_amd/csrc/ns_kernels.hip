@@ -258,19 +258,23 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
         const __amdgpu_buffer_rsrc_t urs = tile_rsrc(M.uout);
         float* const rowsq = M.rowsqpart + (int64_t)tj * rows;
+        // The row sums go through a buffer resource with an out-of-range offset for every lane
+        // but a row's last: a conditional store per chunk split the pass into a block per
+        // chunk, each a dependent chain of adds and lane moves.
+        const __amdgpu_buffer_rsrc_t qrs =
+            __builtin_amdgcn_make_buffer_rsrc(rowsq + m0, 0, (rows - m0) * 4, 0x00020000);
+        const uint32_t qoff = ck == 31 ? static_cast<uint32_t>(tr * 4) : kOutOfRange;
         each_row_chunk_h<NsCfg>(smem, [&](int it, int lr, int, const half8v& h) {
-            const int r = m0 + lr;
             buf_store8<2>(urs, vbase + it * rstep, h);
-            float sq = 0.f;
+            float t = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float f = static_cast<float>(h[e]);
-                sq += f * f;
+                t += f * f;
             }
-            sq = r < rows && col_ok ? sq : 0.f;
             static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
-            sq = sum32_upper(sq);
-            if ((threadIdx.x & 31) == 31 && r < rows) stg<float>(rowsq + r, sq);
+            t = sum32_upper(m0 + lr < rows && col_ok ? t : 0.f);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, t), qrs, qoff + it * 32, 0, 0);
         });
         return;
     }
