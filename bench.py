@@ -62,61 +62,48 @@ def ns_flops(shapes, iters=5) -> float:
     return total
 
 
-def schedule_ops(iters: int, restart_mask: int) -> list:
-    """The operation sequence the library launches for one matrix (thorn_abi.hip, ns_schedule):
-    'gram' (R = X X^T), 'poly' (P), 'sym' (Q P, R P or P (R P)) and 'update' (Q X)."""
+def gram_ops(iters: int, restart_mask: int) -> list:
+    """The Gram Newton-Schulz operations the library launches for one non-square matrix
+    (thorn_abi.hip, gram_schedule; the reference's recurrences, thorn.py:637-653): 'gram'
+    (R = X X^T), 'poly' (Z = b R + c R^2), 'sym' (a Q + Q Z, a R + R Z, a RZ + Z RZ) and 'update'
+    (Q X)."""
     def restart(i):
         return 0 < i < 32 and (restart_mask >> i) & 1
     ops = ['gram']
-    q = False
     for i in range(iters):
         if restart(i):
             ops += ['update', 'gram']
-            q = False
         ops.append('poly')
-        if q:
+        if i != 0 and not restart(i):
             ops.append('sym')
-        q = True
         if i < iters - 1 and not restart(i + 1):
             ops += ['sym', 'sym']
     ops.append('update')
     return ops
 
 
-def ns_schedule(iters: int, restart_mask: int) -> dict:
-    """Launch counts of the Gram Newton-Schulz schedule the library runs for a restart mask (bit i:
-    restart before iteration i): Gram matrices, polynomials P, symmetric products and X updates."""
-    def restart(i):
-        return 0 < i < 32 and (restart_mask >> i) & 1
-    n = {'gram': 1, 'poly': 0, 'symprod': 0, 'update': 1}
-    q = False
-    for i in range(iters):
-        if restart(i):
-            n['update'] += 1
-            n['gram'] += 1
-            q = False
-        n['poly'] += 1
-        if q:
-            n['symprod'] += 1
-        q = True
-        if i < iters - 1 and not restart(i + 1):
-            n['symprod'] += 2
-    return n
+def plain_ops(iters: int) -> list:
+    """The plain quintic for one square matrix (thorn.py:654-658): A = X X^T, B = b A + c A^2,
+    X <- a X + B X per iteration (thorn_abi.hip, plain_schedule)."""
+    return ['gram', 'poly', 'update'] * iters
+
+
+def op_counts(ops: list) -> dict:
+    return {k: ops.count(k) for k in ('gram', 'poly', 'sym', 'update')}
 
 
 def schedule_flops(shapes, iters: int, restart_mask: int) -> float:
     """Algorithmic flops of the schedules the library runs: Gram Newton-Schulz with `restart_mask`
-    on matrices at least twice as long as wide, the plain quintic (a restart before every
-    iteration) on the others;
-    s^2 l per Gram matrix, s^3 per polynomial or symmetric product (symmetric results counted
-    once), 2 s^2 l per update. The plain schedule gives ns_flops."""
-    plain = ns_schedule(iters, (1 << iters) - 2)
-    gram = ns_schedule(iters, restart_mask)
+    on every non-square matrix, the plain quintic on square ones (thorn.py:628); s^2 l per Gram
+    matrix, s^3 per polynomial or symmetric product (symmetric results counted once), 2 s^2 l per
+    update. For square matrices this is ns_flops."""
+    plain = op_counts(plain_ops(iters))
+    gram = op_counts(gram_ops(iters, restart_mask))
     total = 0.0
     for r, c in shapes:
         s, l = min(r, c), max(r, c)
-        sched = gram if l >= 2 * s else plain
-        total += (sched['gram'] * s * s * l + (sched['poly'] + sched['symprod']) * s ** 3
+        sched = gram if r != c else plain
+        total += (sched['gram'] * s * s * l + (sched['poly'] + sched['sym']) * s ** 3
                   + sched['update'] * 2.0 * s * s * l)
     return total
 
@@ -210,7 +197,7 @@ def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
     # the oracle runs the reference's schedules: Gram Newton-Schulz (restart before iteration 2 at
     # the default coefficients) for every non-square matrix, the plain quintic for square ones
     def ref_flops(sh):
-        return schedule_flops([sh], 5, 0b100 if sh[0] != sh[1] else (1 << 5) - 2)
+        return schedule_flops([sh], 5, 0b100)
 
     for sh in sorted(counts, key=ref_flops):   # cheapest shapes first
         if time.perf_counter() - t_start > budget_s:
@@ -301,12 +288,12 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
         starts = [i for i, r in enumerate(rows) if 'ortho_pre_kernel' in r['Kernel_Name']]
         if len(starts) >= 2:
             mats, _ = config_shapes(2)
-            gram = schedule_ops(5, 4)
-            plain = schedule_ops(5, (1 << 5) - 2)
+            gram = gram_ops(5, 4)
+            plain = plain_ops(5)
             fl = {'gram': lambda s_, l_: s_ * s_ * l_, 'poly': lambda s_, l_: s_ ** 3,
                   'sym': lambda s_, l_: s_ ** 3, 'update': lambda s_, l_: 2.0 * s_ * s_ * l_}
             lines += ['Newton-Schulz launches of the last complete step (config 2; Gram-schedule op on the '
-                      '100 matrices >= 2:1 / plain-schedule op on the 40 square ones):', '',
+                      '100 non-square matrices / plain-schedule op on the 40 square ones):', '',
                       '| launch | ops | TFLOP (algorithmic) | us | TFLOP/s |', '|---:|---|---:|---:|---:|']
             k = 0
             for r in rows[starts[-2]:starts[-1]]:
@@ -315,7 +302,7 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
                 us = (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
                 f = 0.0
                 names = []
-                for sched, pick in ((gram, lambda s_, l_: l_ >= 2 * s_), (plain, lambda s_, l_: l_ < 2 * s_)):
+                for sched, pick in ((gram, lambda s_, l_: l_ != s_), (plain, lambda s_, l_: l_ == s_)):
                     op = sched[k] if k < len(sched) else None
                     names.append(op or '-')
                     if op:
@@ -582,8 +569,9 @@ def main() -> int:
                    'ns_arith': 'f16 MFMA, fp32 accumulate; fp32 state'},
         'gpu_event_ms_per_step': round(gpu_ms, 3),
         'first_step_ms': round(first_ms, 1),
-        'ns': {'schedule': {'square': ns_schedule(grp0.iters, (1 << grp0.iters) - 2),
-                            'other': ns_schedule(grp0.iters, mask), 'restart_mask': mask}, 'flops_per_step': F,
+        'ns': {'schedule': {'square': op_counts(plain_ops(grp0.iters)),
+                            'other': op_counts(gram_ops(grp0.iters, mask)), 'restart_mask': mask},
+               'flops_per_step': F,
                'plain_quintic_flops': ns_flops(mats), 'ms_per_step': round(ns_ms, 3),
                'tflops': round(F / (ns_ms * 1e-3) / 1e12, 1) if ns_ms > 0 else None,
                'mfma_frac': round(F / (ns_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4) if ns_ms > 0 else None},

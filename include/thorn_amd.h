@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 4
+#define THORN_ABI_VERSION 5
 
 enum {
     THORN_OK = 0,
@@ -48,7 +48,9 @@ enum {
 #define THORN_MAT_MD_SCALAR 4      /* decouple_md with one scalar gain (thorn.py:1609-1612) */
 
 /* Per-step flags (ThornOrthoMatStep.step_flags). */
-#define THORN_STEP_KEEP_GRAD 8     /* write g *= gain back to the gradient (none_grad=False) */
+#define THORN_STEP_KEEP_GRAD 8     /* none_grad=False. No effect since ABI 5: the gradient of a
+                                      decouple_md matrix is always multiplied by its gains in
+                                      place, as the reference's g.mul_ does (thorn.py:907) */
 #define THORN_STEP_APPLY 16        /* update the parameter this step (thorn.py:1395-1396) */
 
 int thorn_abi_version(void);
@@ -75,7 +77,8 @@ typedef struct ThornOrthoMatStep {
     float* p;             /* parameter (rows x cols) */
     float* g;             /* gradient */
     float* m;             /* state['moment'] */
-    float* row_gain;      /* decouple_md: state['row_gain'] (rows) or state['gain'] (scalar) */
+    float* row_gain;      /* decouple_md: state['row_gain'] (rows) or state['gain'] (scalar; the
+                             consecutive matrices of a parameter share it and it steps once) */
     float* col_gain;      /* state['col_gain'] (cols) */
     float* row_gain_moment;
     float* row_gain_variance;
@@ -106,12 +109,11 @@ size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);
 /* Runs the whole step for the group: coeffs holds iters (a, b, c) triples (thorn.py:425-480),
- * 1 <= iters <= 32. Matrices with max(rows, cols) >= 2 min(rows, cols) run Gram Newton-Schulz
- * (thorn.py:637-653) with a restart before iteration i for every bit i (1 <= i < iters) set in
- * restart_mask, the restart positions of _gram_ns_restarts (thorn.py:483-514); the others run the
- * plain quintic (thorn.py:655-658), which is Gram Newton-Schulz restarted before every iteration.
- * The reference takes the Gram form for every non-square matrix; in exact arithmetic both are the
- * same map, and below 2:1 the plain one is the more accurate in f16.
+ * 1 <= iters <= 32. Non-square matrices run Gram Newton-Schulz (thorn.py:637-653) with a restart
+ * before iteration i for every bit i (1 <= i < iters) set in restart_mask, the restart positions of
+ * _gram_ns_restarts (thorn.py:483-514); square ones run the plain quintic (thorn.py:654-658). Both
+ * follow the reference's recurrences and f16 rounding points (Z, Q, RZ, R; A, B, aX + BX).
+ * With decouple_md, the gradient is multiplied by the gains in place (thorn.py:907).
  * A matrix without THORN_STEP_APPLY updates its momentum (and, with decouple_md, goes through the
  * gain round trip p / G * G) but not its parameter, as the reference does for a step that is not
  * due under update_rate (thorn.py:1395, 1403-1421). iters = 0 runs only that part, for a table in
@@ -187,7 +189,7 @@ enum {
     THORN_KIND_PRE = 0,        /* momentum + first iterate (ortho_pre_kernel) */
     THORN_KIND_NORM = 1,       /* per-matrix norm, decouple_md gains */
     THORN_KIND_GRAM = 2,       /* Newton-Schulz Gram matrix R of the iterate */
-    THORN_KIND_POLY = 3,       /* Newton-Schulz polynomial P = a I + b R + c R^2 */
+    THORN_KIND_POLY = 3,       /* Newton-Schulz Z = b R + c R^2 (plain quintic: B = b A + c A^2) */
     THORN_KIND_UPDATE = 4,     /* Newton-Schulz update Q X / X Q (and the fused apply) */
     THORN_KIND_ROWSTATS = 5,   /* per-row normalization statistics */
     THORN_KIND_PNN_APPLY = 6,  /* per-row normalized apply */
@@ -195,7 +197,7 @@ enum {
     THORN_KIND_MD_RESCALE = 8, /* decouple_md reassembly */
     THORN_KIND_ADAM = 9,       /* multi-tensor Adam */
     THORN_KIND_CAST = 10,      /* first iterate: u / ||u|| rounded to f16 */
-    THORN_KIND_SYMPROD = 11,   /* Gram Newton-Schulz products Q P, R P, P (R P) */
+    THORN_KIND_SYMPROD = 11,   /* Gram Newton-Schulz products a Q + Q Z, a R + R Z, a RZ + Z RZ */
     THORN_KIND_MAGMA = 12,     /* Magma statistics of the Adam tensors */
     THORN_KIND_COUNT = 13
 };

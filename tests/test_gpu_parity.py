@@ -3,13 +3,12 @@
 Tolerances:
   * fp32 optimizer state (moment, variance, gain moments): relative Frobenius <= 1e-5;
   * the update delta p_new - p_old of orthogonalized matrices: relative Frobenius <= 2e-2 against
-    the oracle (the reference's float16 Gram Newton-Schulz; the HIP path runs the f16 plain
-    quintic on MFMA). Both are also compared with the exact update (the same step with the f64
-    closed-form polar map U phi(S) V^T), and the oracle-parity bound is widened by the
-    reference's own measured error against it. The widening only matters for tiny or skinny
-    matrices, where any float16 iteration with these coefficients is ~1-3e-2 off (a=8, b=-22,
-    c=15 cancel catastrophically near sigma=1; e.g. 2x2, 32x5); at the benchmark shapes the
-    reference's own error is ~1e-3;
+    the oracle (the reference's float16 Newton-Schulz: Gram Newton-Schulz for non-square matrices,
+    the plain quintic for square ones). The HIP path runs the same recurrences with the same f16
+    rounding points on MFMA, so it tracks the oracle even where both are 1-3e-2 away from the exact
+    polar map (tiny and skinny matrices such as 2x2 or 32x5, where a=8, b=-22, c=15 cancel near
+    sigma=1). The distance of both to the exact update (the same step with the f64 closed-form polar
+    map U phi(S) V^T) is logged;
   * Adam-only tensors: delta p relative Frobenius <= 1e-4 (elementwise fp32 arithmetic).
 Inputs are generated on the CPU and copied bit for bit to the GPU.
 """
@@ -98,16 +97,18 @@ def exact_dp(p_old, g, m_prev, group: dict):
     return p64 - p_old.double()
 
 
+DP_TOL = 2e-2   # north star: post-Newton-Schulz update and new parameters, relative Frobenius
+
+
 def check_ortho_dp(dpg, dpc, dpe, worst: dict, where: str) -> None:
     """dpg: HIP update, dpc: oracle update, dpe: exact update (see the module docstring)."""
     r, r_ex, ref_ex = rel(dpg, dpc), rel(dpg, dpe), rel(dpc, dpe)
     worst['dp'] = max(worst.get('dp', 0.0), r)
     worst['dp_exact'] = max(worst.get('dp_exact', 0.0), r_ex)
     worst['ref_exact'] = max(worst.get('ref_exact', 0.0), ref_ex)
-    if r > 2e-2:
-        worst['widened'] = worst.get('widened', 0) + 1
+    if r > DP_TOL / 4:
         _log(f'[gpu]   {where}: vs oracle {r:.2e}, vs exact {r_ex:.2e}, oracle vs exact {ref_ex:.2e}')
-    assert r <= 2e-2 + ref_ex, (where, r, r_ex, ref_ex)
+    assert r <= DP_TOL, (where, r, r_ex, ref_ex)
 
 
 def _run_pair(build, steps, teacher_forced):
@@ -118,7 +119,7 @@ def _run_pair(build, steps, teacher_forced):
     ggroups = _clone_groups(groups, gparams)
     cpu = O.OracleTHORN(groups)
     gpu = thorn_amd.THORN(ggroups)
-    worst = {'state': 0.0, 'dp': 0.0, 'dp_adam': 0.0, 'dp_exact': 0.0, 'ref_exact': 0.0, 'widened': 0}
+    worst = {'state': 0.0, 'dp': 0.0, 'dp_adam': 0.0, 'dp_exact': 0.0, 'ref_exact': 0.0}
     group_of = {id(p): g for g in groups for p in g['params']}
     for s in range(1, steps + 1):
         if teacher_forced and s > 1:
@@ -176,8 +177,19 @@ def test_trajectory_teacher_forced(name):
     assert w['dp_adam'] <= 1e-4, w
 
 
-SHAPES = [(1, 17), (17, 1), (2, 2), (5, 3), (3, 5), (129, 130), (130, 129), (300, 7), (8, 520),
-          (256, 256), (1024, 64), (64, 1000), (257, 255), (4, 33, 17)]
+# ragged and extreme shapes, then the conv kernels and the Linear of config 4 (flattened to
+# out x (in * k)), whose Newton-Schulz runs the Gram form at s = 5 .. 256
+SHAPES = [(1, 17), (17, 1), (2, 2), (5, 3), (3, 5), (300, 7), (8, 520),
+          (256, 256), (1024, 64), (64, 1000), (4, 33, 17),
+          (32, 5), (64, 96), (64, 192), (128, 192), (128, 384), (256, 640), (256, 128)]
+
+# Non-square but nearly square: the reference's f16 Gram Newton-Schulz is chaotic here. Perturbing
+# its fp32 input by one part in 2^22 moves its own output by up to 2.7e-2 (128 x 129) and 2.2e-2
+# (512 x 520), and it lies 2-3e-2 from the exact polar map, so two executions of the reference
+# with different fp32 summation orders already differ by more than 2e-2. These shapes are held to
+# NEAR_SQUARE_TOL against the oracle and against the exact update.
+NEAR_SQUARE = [(129, 130), (130, 129), (257, 255)]
+NEAR_SQUARE_TOL = 5e-2
 
 
 @pytest.mark.parametrize('shape', SHAPES)
@@ -208,12 +220,43 @@ def test_single_matrix_update(shape, wd):
     _log(f'[gpu]   {w}')
 
 
+@pytest.mark.parametrize('shape', NEAR_SQUARE)
+def test_near_square_matrix_update(shape):
+    """Nearly square non-square matrices (see NEAR_SQUARE): the update is within NEAR_SQUARE_TOL of
+    the oracle's and of the exact one, and the oracle's own sensitivity to a 2^-22 relative
+    perturbation of its input is logged beside it."""
+    _log(f'[gpu] near-square matrix {shape}')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(sum(shape) * 7 + 1)
+    p0 = torch.randn(shape, generator=g) * 0.02
+    grad = torch.randn(shape, generator=g) * 1e-3
+    grp = dict(orthogonalize=True, lr=1e-2, weight_decay=0.1)
+    dps = []
+    for gr in (grad, grad * (1 + 2 ** -22)):
+        pc = torch.nn.Parameter(p0.clone())
+        cpu = O.OracleTHORN([dict(grp, params=[pc])])
+        pc.grad = gr.clone()
+        cpu.step()
+        dps.append(pc.detach() - p0)
+    pg = torch.nn.Parameter(p0.clone().to(DEV))
+    gpu = thorn_amd.THORN([dict(grp, params=[pg])])
+    pg.grad = grad.clone().to(DEV)
+    gpu.step()
+    torch.cuda.synchronize()
+    dpg = pg.detach().cpu() - p0
+    dpe = exact_dp(p0, grad, torch.zeros_like(p0), grp)
+    r, r_ex, ref_ex, ref_self = rel(dpg, dps[0]), rel(dpg, dpe), rel(dps[0], dpe), rel(dps[1], dps[0])
+    _log(f'[gpu]   vs oracle {r:.2e}, vs exact {r_ex:.2e}, oracle vs exact {ref_ex:.2e}, '
+         f'oracle vs perturbed oracle {ref_self:.2e}')
+    assert r <= NEAR_SQUARE_TOL and r_ex <= NEAR_SQUARE_TOL, (r, r_ex, ref_ex, ref_self)
+
+
 MANY = [(512, 1536), (1536, 512), (768, 768), (1024, 256), (640, 640), (300, 900), (512, 512), (96, 200)]
 
 
 def test_many_matrices_share_launches():
     """One group of mixed shapes: every launch carries tiles of both Newton-Schulz schedules
-    (the Gram set and the square-ish set), each XCD taking its share of both lists, with tile
+    (the Gram set and the square set), each XCD taking its share of both lists, with tile
     counts that are not multiples of the XCD count. Each matrix's step must match the oracle's
     one-matrix step."""
     _log(f'[gpu] many matrices {MANY}')
@@ -322,15 +365,16 @@ def test_state_dict_roundtrip_and_layout():
 
 
 def test_gradient_scale_jumps():
-    """The first Newton-Schulz iterate of a step is written in f16 with the previous step's power-of-
-    two scale; when the gradient scale jumps by more than 16x either way the kernels rebuild it
-    exactly. Steps with 1.5x, 1000x and 1e-4x jumps, with and without momentum, against the oracle."""
+    """The first Newton-Schulz iterate of a large matrix (2^20 elements or more) is written in f16
+    with the previous step's power-of-two scale; when the gradient scale jumps by more than 16x
+    either way the kernels rebuild it exactly. Steps with 1.5x, 1000x and 1e-4x jumps, with and
+    without momentum, against the oracle; the small matrices take the exact path every step."""
     _log('[gpu] gradient scale jumps')
     scales = [1.0, 1.5, 1000.0, 1200.0, 0.1, 1e-4, 1e-4]
 
     def build():
         g = torch.Generator().manual_seed(77)
-        shapes = [(256, 256), (300, 7), (1024, 64), (64, 1000), (130, 129)]
+        shapes = [(1024, 1024), (300, 7), (2048, 512), (64, 1000), (512, 2048), (130, 97)]
         params = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in shapes]
         groups = [dict(orthogonalize=True, params=params[:3], lr=1e-2, weight_decay=0.1),
                   dict(orthogonalize=True, params=params[3:], lr=1e-2, weight_decay=0.0, betas=(0.0, 0.95))]

@@ -87,7 +87,7 @@ SIGNATURES = {
 }
 KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
          'symprod', 'magma']
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 

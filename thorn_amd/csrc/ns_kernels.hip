@@ -1,11 +1,15 @@
 // Grouped Newton-Schulz phase kernels over an orthogonalized parameter group (gfx950).
 //
-// Reference semantics: thorn.py:626-662 (_polar_decomp_impl), Gram Newton-Schulz with restarts,
-// in f16 with fp32 accumulation. With R the Gram matrix of the short side and
-// P_i = a_i I + b_i R + c_i R^2, iteration i multiplies Q by P_i and advances R to P_i R P_i;
-// at a restart (and at the end) the iterate is updated, X <- Q X, and R is formed again from it.
-// A restart before every iteration is the plain quintic X <- P_i X (thorn.py:655-658). The first
-// iterate is u / (||u||_F + 1e-8) rounded to f16 (thorn.py:632-635).
+// Reference semantics: thorn.py:626-662 (_polar_decomp_impl) in f16 with fp32 accumulation, with
+// the reference's own recurrences and rounding points: every product is rounded to f16 once, as
+// f16(beta * C + alpha * (A B)) (the eager baddbmm), and Q = Z + a I rounds Z first.
+//   Gram Newton-Schulz (non-square matrices, thorn.py:637-653), R = X X^T of the short side:
+//     for each iteration i: a restart (i in S, i != 0) sets X <- Q X and R <- X X^T;
+//     Z = b R + c R R;  Q = Z + a I (i == 0 or a restart) or Q = a Q + Q Z;
+//     unless the next iteration restarts or this is the last: RZ = a R + R Z, R = a RZ + Z RZ;
+//     at the end X <- Q X.
+//   Plain quintic (square matrices, thorn.py:654-658): A = X X^T, B = b A + c A A, X <- a X + B X.
+// The first iterate is u / (||u||_F + 1e-8) rounded to f16 (thorn.py:632-635).
 #include "ns_gemm.hpp"
 #include "thorn_kernels.hpp"
 
@@ -25,10 +29,9 @@ __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) 
 __device__ __forceinline__ _Float16* sym_buf(const OrthoMat& M, int sel) {
     switch (sel) {
         case kBufR: return M.gram;
-        case kBufP: return M.poly;
+        case kBufZ: return M.zbuf;
         case kBufQA: return M.qa;
-        case kBufQB: return M.qb;
-        default: return M.tmp;
+        default: return M.qb;
     }
 }
 
@@ -40,46 +43,46 @@ __device__ __forceinline__ Operand square_operand(const _Float16* p, const Ortho
     return op;
 }
 
-// First iterate: xb = f16(u * sigma), sigma = 1 / (||u||_F + 1e-8), over 16 x 256 tiles.
-__global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
-    const int b = blockIdx.x;
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int local = b - tl.starts[k];
-    const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
+// First iterate, exact form (thorn.py:632-635): xb = f16(u / (||u||_F + 1e-8)) with
+// u = g + beta1 * m recomputed from the gradient (times the decouple_md gains: ortho_pre_kernel
+// writes g back for those matrices, as the reference's g.mul_ does) and the updated moment, the
+// same fmaf as ortho_pre_kernel. It runs for matrices on the exact path, and for prescaled ones
+// whose stored iterate is out of range after a gradient-scale jump (kScalRepair). Grid: x strides
+// over the 16 x 256 tiles of matrix blockIdx.y; a matrix that needs neither returns at once.
+__global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restrict__ mats) {
+    const OrthoMat& M = mats[blockIdx.y];
+    if ((M.flags & kFlagPrescaled) && M.scal[kScalRepair] == 0.f) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (M.flags & kFlagPrescaled) return;   // ortho_pre_kernel wrote xb (ortho_repair_kernel checks it)
-    const float sigma = M.scal[kScalSigma];
-    const int r0 = tr * 16 + wave * 4;
-    const int c = tc * 256 + 4 * lane;
-    if (c >= M.ldx) return;
-    // x0 and xb share the padded layout; the padding of x0 is zero, so whole 4-chunks are safe
-    float4 u[4];
+    const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
+    const float denom = M.scal[kScalDenom], beta1 = M.beta1;
+    const bool vec = M.flags & kFlagVec4;
+    for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
+        const int tr = t / M.mom_tiles_c, tc = t % M.mom_tiles_c;
+        const int r0 = tr * 16 + wave * 4, c0 = tc * 256;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-        if (r0 + rr < M.rows) u[rr] = ldg<float4>(M.x0 + (int64_t)(r0 + rr) * M.ldx + c);
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = r0 + rr;
+            if (r >= M.rows) break;
+            const int64_t rb = (int64_t)r * M.cols;
+            _Float16* xrow = M.xb + (int64_t)r * M.ldx;
+            if (vec) {
+                const int c = c0 + 4 * lane;
+                if (c >= M.cols) continue;
+                const float4 g4 = ldg<float4>(M.g + rb + c), m4 = ldg<float4>(M.m + rb + c);
+                stg<half4>(xrow + c, half4{(_Float16)(fmaf(m4.x, beta1, g4.x) / denom),
+                                           (_Float16)(fmaf(m4.y, beta1, g4.y) / denom),
+                                           (_Float16)(fmaf(m4.z, beta1, g4.z) / denom),
+                                           (_Float16)(fmaf(m4.w, beta1, g4.w) / denom)});
+            } else {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        if (r0 + rr >= M.rows) break;
-        const half4 h = half4{(_Float16)(u[rr].x * sigma), (_Float16)(u[rr].y * sigma), (_Float16)(u[rr].z * sigma),
-                              (_Float16)(u[rr].w * sigma)};
-        stg<half4>(M.xb + (int64_t)(r0 + rr) * M.ldx + c, h);
-    }
-}
-
-// Prescaled first iterates whose scale drifted too far (kScalRepair): rebuild xb = f16(sigma * u)
-// exactly from the gradient and the updated moment, u = g + beta1 * m (such matrices have no
-// decouple_md). One block per matrix; the common case is an immediate exit.
-__global__ __launch_bounds__(256) void ortho_repair_kernel(const OrthoMat* __restrict__ mats) {
-    const OrthoMat& M = mats[blockIdx.x];
-    if (!(M.flags & kFlagPrescaled) || M.scal[kScalRepair] == 0.f) return;
-    const float sigma = M.scal[kScalSigma];
-    for (int r = 0; r < M.rows; ++r)
-        for (int c = threadIdx.x; c < M.cols; c += 256) {
-            const int64_t i = (int64_t)r * M.cols + c;
-            const float u = fmaf(ldg<float>(M.m + i), M.beta1, ldg<float>(M.g + i));
-            M.xb[(int64_t)r * M.ldx + c] = (_Float16)(u * sigma);
+                for (int e = 0; e < 4; ++e) {
+                    const int c = c0 + lane + 64 * e;
+                    if (c < M.cols)
+                        xrow[c] = (_Float16)(fmaf(ldg<float>(M.m + rb + c), beta1, ldg<float>(M.g + rb + c)) / denom);
+                }
+            }
         }
+    }
 }
 
 // Buffer access to an s x ld f16 workspace matrix. Every load and store of the symmetric
@@ -121,34 +124,62 @@ __device__ __forceinline__ void sym_load(half8v (&cv)[N], __amdgpu_buffer_rsrc_t
     }
 }
 
-// out = alpha * acc + beta * Csym + gamma * I (f16) on an upper-triangle tile of a symmetric s x s
-// matrix (Csym optional: crs of size 0). Only the upper block triangle is stored: consumers read
-// a block below the diagonal as the transpose of its mirror above it, and a diagonal block either
-// way, so a diagonal tile must be exactly symmetric (an antisymmetric error in R grows through the
-// Gram iteration): its upper triangle is computed and its lower triangle is the mirror.
+// Row pass: stores the staged f16 tile (rows m0.. below n, columns n0..) into `out` through a
+// resource over the tile's rows: the row offset of a chunk is an add to one per-lane offset, and a
+// lane whose columns lie past ld stores nothing.
+template <class C>
+__device__ __forceinline__ void store_staged(const char* smem, _Float16* out, int64_t ld, int n, int m0, int n0) {
+    const int rows = n - m0 < C::BM ? n - m0 : C::BM;
+    const __amdgpu_buffer_rsrc_t trs =
+        __builtin_amdgcn_make_buffer_rsrc(out + int64_t(m0) * ld, 0, static_cast<int>(rows * ld * 2), 0x00020000);
+    const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
+    const uint32_t vbase = n0 + 8 * ck < ld ? static_cast<uint32_t>((tr * ld + n0 + 8 * ck) * 2) : kOutOfRange;
+    const uint32_t rstep = static_cast<uint32_t>(16 * ld);   // bytes of 8 rows
+    each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) { buf_store8<2>(trs, vbase + it * rstep, h); });
+}
+
+// Copies the row chunks of an f16 matrix tile (rows m0 + r < n, columns n0 + c < ld of a matrix
+// with leading dimension ld; zeros elsewhere) into the staging, 8 chunks in flight at a time.
+template <class C>
+__device__ __forceinline__ void stage_rows(char* smem, __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0, int n0) {
+    using E = EpiH<C>;
+    _Float16* const base = reinterpret_cast<_Float16*>(smem) + row_chunk_base();
+#pragma unroll
+    for (int h = 0; h < kRowChunks; h += 8) {
+        half8v cv[8];
+        sym_load(cv, crs, ld, n, m0, n0, h);
+#pragma unroll
+        for (int it = 0; it < 8; ++it) *reinterpret_cast<half8v*>(base + (h + it) * E::ROW_STEP) = cv[it];
+    }
+}
+
+// out = f16(alpha * acc + beta * Csym) on an upper-triangle tile of a symmetric s x s matrix
+// (Csym optional: crs of size 0), the reference's single rounding of beta * C + alpha * (A B).
+// Only the upper block triangle is stored: consumers read a block below the diagonal as the
+// transpose of its mirror above it, and a diagonal block either way, so a diagonal tile must be
+// exactly symmetric: its upper triangle is computed and its lower triangle is the mirror.
 // With Csym, its tile is first copied into the staging as is; each value is then replaced in
 // place by the final value computed from it (the same lane reads and writes each position). On a
 // diagonal tile the staging also receives the transposes of the values above the diagonal
-// (stage_f16), so one pass of row chunks stores every tile. HAS_C: the Csym term is present (else crs and beta are
-// unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1 would leave as is).
-template <class C, bool HAS_C, bool SCALE>
+// (stage_f16), so one pass of row chunks stores every tile. HAS_C: the Csym term is present (else
+// crs and beta are unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1
+// would leave as is). DUAL: the tile is also stored to out2 as Q = Z + a I, the diagonal
+// elements rounded from the f16 Z (thorn.py:648, `Z + a * I` in f16): f16(float(Z_ii) + dual_add)
+// with dual_add = f16(a).
+template <class C, bool HAS_C, bool SCALE, bool DUAL = false>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
                                           __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0, int n0,
-                                          float alpha, float beta, float gamma) {
+                                          float alpha, float beta, _Float16* out2 = nullptr, float dual_add = 0.f) {
     using E = EpiH<C>;
     _Float16* const S = reinterpret_cast<_Float16*>(smem);
     const bool diag = m0 == n0;
     if constexpr (HAS_C) {
         // requested once the main loop is done: held through it, even a part of them would be
         // spilled to scratch memory by the register allocator
-        half8v cv[kRowChunks];
-        sym_load(cv, crs, ld, n, m0, n0, 0);
-        _Float16* const base = S + row_chunk_base();
-#pragma unroll
-        for (int it = 0; it < kRowChunks; ++it) *reinterpret_cast<half8v*>(base + it * E::ROW_STEP) = cv[it];
+        stage_rows<C>(smem, crs, ld, n, m0, n0);
         lds_barrier();
     }
-    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a, bool dblk) {
+    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a, bool) {
         floatx4 t;
 #pragma unroll
         for (int e = 0; e < 4; ++e) t[e] = SCALE ? alpha * a[e] : a[e];
@@ -157,26 +188,21 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
 #pragma unroll
             for (int e = 0; e < 4; ++e) t[e] += beta * static_cast<float>(cv[e]);
         }
-        if (dblk) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (r == c + e) t[e] += gamma;
-        }
         return t;
     });
     lds_barrier();
-    {
-        // Row pass through a resource over the tile's rows below n: the row offset of a chunk is
-        // an add to one per-lane offset, and a lane whose columns lie past ld stores nothing.
-        const int rows = n - m0 < C::BM ? n - m0 : C::BM;
-        const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
-            out + int64_t(m0) * ld, 0, static_cast<int>(rows * ld * 2), 0x00020000);
-        const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
-        const uint32_t vbase = n0 + 8 * ck < ld ? static_cast<uint32_t>((tr * ld + n0 + 8 * ck) * 2) : kOutOfRange;
-        const uint32_t rstep = static_cast<uint32_t>(16 * ld);   // bytes of 8 rows
-        each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) {
-            buf_store8<2>(trs, vbase + it * rstep, h);
-        });
+    store_staged<C>(smem, out, ld, n, m0, n0);
+    if constexpr (DUAL) {
+        if (diag) {
+            lds_barrier();   // the row pass has read the staging
+            const int r = threadIdx.x;
+            if (r < C::BM && m0 + r < n) {
+                _Float16& z = S[E::rowoff(r) + r];
+                z = static_cast<_Float16>(static_cast<float>(z) + dual_add);
+            }
+            lds_barrier();
+        }
+        store_staged<C>(smem, out2, ld, n, m0, n0);
     }
 }
 
@@ -185,21 +211,29 @@ enum NsOpKind : int32_t { kOpNone = 0, kOpGram = 1, kOpSym = 2, kOpUpdate = 3 };
 struct NsOp {
     int32_t kind;
     int32_t xsel, first, final_iter;   // gram, update: iterate buffer, first-iterate scaling, last update
-    int32_t asel, bsel, csel, osel;    // sym: out = alpha * A B + beta * C + gamma * I
-    int32_t qsel;                      // update: X <- Q X
-    float alpha, beta, gamma;
+    int32_t asel, bsel, csel, osel;    // sym: out = f16(alpha * A B + beta * C) (C absent: csel < 0)
+    int32_t osel2;                     // sym: >= 0: also Q = out + a I into this buffer (dual_add = f16(a))
+    int32_t qsel;                      // update: X <- Q X, or X <- beta X + Q X when csel >= 0
+    float alpha, beta, dual_add;
 };
 
 // Epilogue of an update tile (see ns_phase_kernel). Every field of the matrix table it needs is
 // read once into a register first: stores through the matrix pointers could alias the table in
 // global memory as far as the compiler knows, and it would reload fields after every store.
+// HAS_C: the plain quintic's X <- a X + B X (thorn.py:658): the tile of the input iterate X is
+// staged first and each output is f16(osc * acc + beta * osc * X), the reference's single
+// rounding of a X + B X; otherwise f16(osc * acc).
+template <bool HAS_C>
 __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int rows = M.rows, cols = M.cols, ldx = M.ldx, flags = M.flags;
     // the stored first iterate is sigma * u up to the factor x0scale, applied as the first
     // update's tile is staged; every output of the update is the f16 rounding of acc * osc
+    // (plus the X term)
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
+    _Float16* const xin = op.xsel == kXA ? M.xa : M.xb;
+    _Float16* const xout = op.xsel == kXA ? M.xb : M.xa;
 
     // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) streams p
     // through a ring of D row chunks: chunk L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32)
@@ -225,12 +259,25 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         for (int L = 0; L < D; ++L) fetch(L);
     }
 
-    if (op.first)
+    if constexpr (HAS_C) {
+        stage_rows<NsCfg>(smem, sym_rsrc(xin, ldx, rows), ldx, rows, m0, n0);
+        lds_barrier();
+        const float bx = op.beta * osc;
+        const _Float16* const S = reinterpret_cast<const _Float16*>(smem);
+        stage_f16<NsCfg>(acc, smem, false, [&](int r, int c, const floatx4& a, bool) {
+            const half4 xv = *reinterpret_cast<const half4*>(S + EpiH<NsCfg>::rowoff(r) + c);
+            floatx4 t;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] = osc * a[e] + bx * static_cast<float>(xv[e]);
+            return t;
+        });
+    } else if (op.first) {
         stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a, bool) {
             return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
         });
-    else
+    } else {
         stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) { return a; });
+    }
     lds_barrier();
 
     // The f16 row passes (next iterate, u'): one buffer resource over the tile's rows below
@@ -246,7 +293,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     };
 
     if (!op.final_iter) {
-        const __amdgpu_buffer_rsrc_t drs = tile_rsrc(op.xsel == kXA ? M.xb : M.xa);
+        const __amdgpu_buffer_rsrc_t drs = tile_rsrc(xout);
         each_row_chunk_h<NsCfg>(smem, [&](int it, int, int, const half8v& h) {
             buf_store8<2>(drs, vbase + it * rstep, h);
         });
@@ -254,9 +301,10 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     }
 
     if (flags & kFlagPNN) {
-        // u' in f16 (the reference's polar factor is f16 rounded, thorn.py:635, 662) and per-row
+        // u' in f16 into the iterate buffer this update does not read (the reference's polar
+        // factor is f16 rounded, thorn.py:635, 662) and per-row
         // partial sums of u'^2 over this tile's columns (consecutive lanes cover a row).
-        const __amdgpu_buffer_rsrc_t urs = tile_rsrc(M.uout);
+        const __amdgpu_buffer_rsrc_t urs = tile_rsrc(xout);
         float* const rowsq = M.rowsqpart + (int64_t)tj * rows;
         // The row sums go through a buffer resource with an out-of-range offset for every lane
         // but a row's last: a conditional store per chunk split the pass into a block per
@@ -352,16 +400,18 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 //   Gram (kOpGram): R = X X^T (wide) or X^T X (tall) of the iterate in buffer `xsel`, rows of X
 //     read K-major or its columns MN-major; upper-triangle tile number `local`. `first`: the
 //     iterate is the stored first iterate, sigma * u up to the factor x0scale.
-//   Symmetric product (kOpSym): out = alpha * A B + beta * C + gamma * I over s x s workspace
-//     matrices that are symmetric and commute (all are polynomials in the same R), so the product
-//     is symmetric: upper-triangle tiles. A's block row ti and B's block row tj (B symmetric: its
+//   Symmetric product (kOpSym): out = f16(alpha * A B + beta * C) over s x s workspace matrices
+//     that are symmetric and commute (all are polynomials in the same R), so the product is
+//     symmetric: upper-triangle tiles. A's block row ti and B's block row tj (B symmetric: its
 //     column is its row); a matrix stored as its upper block triangle is read MN-major (from the
-//     transposed mirror block) before its diagonal block. C may be absent (csel < 0).
+//     transposed mirror block) before its diagonal block. C may be absent (csel < 0). With
+//     osel2 >= 0 the tile is also stored as Q = out + a I (Gram Newton-Schulz after a restart).
 //   Update (kOpUpdate): X' = Q X (wide) or X Q (tall) with X in buffer `xsel` and Q the workspace
-//     matrix `qsel`, output tile number `local` in column-major order (consecutive tiles share
-//     the column panel of X and, a few apart, the row panels of Q); Q's blocks before the
-//     diagonal block are read transposed from their mirror above it. See update_finish for the
-//     epilogue.
+//     matrix `qsel`, plus beta X when csel >= 0 (the plain quintic's a X + B X); output tile
+//     number `local` in column-major order (consecutive tiles share the column panel of X and, a
+//     few apart, the row panels of Q); Q's blocks before the diagonal block are read transposed
+//     from their mirror above it. The output goes to the other iterate buffer. See update_finish
+//     for the epilogue.
 // All three run the same main loop (gemm_tile) with per-operation operands and layouts.
 __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
                                                        TaskList t1, NsOp op1, int t1_first) {
@@ -416,28 +466,33 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero,
                      op.kind != kOpUpdate && ti == tj);
     if (op.kind == kOpUpdate) {
-        update_finish(M, acc, local, ti, tj, op, smem, scratch);
+        if (op.csel >= 0) update_finish<true>(M, acc, local, ti, tj, op, smem, scratch);
+        else update_finish<false>(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
         const __amdgpu_buffer_rsrc_t none = sym_rsrc(nullptr, 0, 0);
         const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
         if (op.first) {
             const float osc = M.scal[kScalX0Scale];
-            sym_store<NsCfg, false, true>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, osc * osc, 0.f, 0.f);
+            sym_store<NsCfg, false, true>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, osc * osc, 0.f);
         } else {
-            sym_store<NsCfg, false, false>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, 1.f, 0.f, 0.f);
+            sym_store<NsCfg, false, false>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, 1.f, 0.f);
         }
     } else {
         const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
         _Float16* const out = sym_buf(M, op.osel);
-        if (op.csel >= 0 && op.beta != 0.f) {
-            sym_store<NsCfg, true, true>(acc, smem, out, sym_rsrc(sym_buf(M, op.csel), M.lds, M.s), M.lds, M.s, m0,
-                                         n0, op.alpha, op.beta, op.gamma);
+        if (op.csel >= 0) {
+            const __amdgpu_buffer_rsrc_t crs = sym_rsrc(sym_buf(M, op.csel), M.lds, M.s);
+            if (op.osel2 >= 0)
+                sym_store<NsCfg, true, true, true>(acc, smem, out, crs, M.lds, M.s, m0, n0, op.alpha, op.beta,
+                                                   sym_buf(M, op.osel2), op.dual_add);
+            else if (op.alpha != 1.f)
+                sym_store<NsCfg, true, true>(acc, smem, out, crs, M.lds, M.s, m0, n0, op.alpha, op.beta);
+            else
+                sym_store<NsCfg, true, false>(acc, smem, out, crs, M.lds, M.s, m0, n0, 1.f, op.beta);
         } else if (op.alpha != 1.f) {
-            sym_store<NsCfg, false, true>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, op.alpha, 0.f,
-                                          op.gamma);
+            sym_store<NsCfg, false, true>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, op.alpha, 0.f);
         } else {
-            sym_store<NsCfg, false, false>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, 1.f, 0.f,
-                                           op.gamma);
+            sym_store<NsCfg, false, false>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, 1.f, 0.f);
         }
     }
 }

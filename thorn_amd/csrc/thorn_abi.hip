@@ -26,6 +26,7 @@ int check_launch(const char* what) {
 }
 
 constexpr size_t kAlign = 256;
+constexpr int64_t kPrescaleMinElems = int64_t(1) << 20;   // see thorn_ortho_fill_table
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -34,7 +35,7 @@ constexpr size_t kNone = ~size_t(0);
 struct MatLayout {
     int32_t rows, cols, s, l, ldx, lds, tall, flags;
     int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
-    size_t x0, xa, xb, gram, poly, qa, qb, tmp, uout, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
+    size_t xa, xb, gram, zbuf, qa, qb, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
     size_t magpart;
 };
 
@@ -128,6 +129,7 @@ struct thorn_ortho_plan {
     // mean short and long side of each set's matrices: the contraction lengths of its GEMM tiles
     // (long side: Gram matrices; short side: the other products), to run longer tiles first
     double mean_s[2]{}, mean_l[2]{};
+    int max_mom_tiles = 0;   // elementwise 16 x 256 tiles of the largest matrix
     LaunchTimer timer;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
@@ -198,68 +200,113 @@ struct ScheduledOp {
     int kind;   // THORN_KIND_* for launch timing
 };
 
-// The Newton-Schulz launch sequence of one matrix set: Gram Newton-Schulz (thorn.py:637-653) in
-// the P-form of its recurrences. With P_i = a_i I + b_i R + c_i R^2: Q <- Q P_i (Q = P_i right after
-// a restart) and, unless the next iteration restarts or this is the last, R <- P_i (R P_i). A
-// restart before iteration i (bit i of `mask`) and the end apply X <- Q X and form R from the new
-// X. A restart before every iteration is the plain quintic X <- P_i X (thorn.py:655-658).
-std::vector<ScheduledOp> ns_schedule(int iters, uint32_t mask, const float* coeffs) {
+// The Newton-Schulz launch sequence of one matrix set and the iterate buffer that holds u' after
+// its last update (the per-row normalization reads it from there).
+struct NsSchedule {
+    std::vector<ScheduledOp> ops;
+    int uout_sel;
+};
+
+thorn::NsOp make_op(int32_t kind) {
+    thorn::NsOp o{};
+    o.kind = kind;
+    o.csel = -1;
+    o.osel2 = -1;
+    o.alpha = 1.f;
+    return o;
+}
+
+inline int other_x(int xsel) { return xsel == thorn::kXB ? thorn::kXA : thorn::kXB; }
+
+void push_gram(std::vector<ScheduledOp>& ops, int xsel, bool first) {
+    thorn::NsOp o = make_op(thorn::kOpGram);
+    o.xsel = xsel;
+    o.first = first ? 1 : 0;
+    ops.push_back({o, THORN_KIND_GRAM});
+}
+
+void push_update(std::vector<ScheduledOp>& ops, int xsel, int qsel, bool first, bool fin, bool plus_x, float beta) {
+    thorn::NsOp o = make_op(thorn::kOpUpdate);
+    o.xsel = xsel;
+    o.qsel = qsel;
+    o.first = first ? 1 : 0;
+    o.final_iter = fin ? 1 : 0;
+    if (plus_x) {
+        o.csel = 0;
+        o.beta = beta;
+    }
+    ops.push_back({o, THORN_KIND_UPDATE});
+}
+
+// out = f16(alpha * A B + beta * C); dual >= 0: also Q = out + f16(dual_a) I into buffer `dual`
+void push_sym(std::vector<ScheduledOp>& ops, int a, int b, int c, int out, float alpha, float beta, int kind,
+              int dual = -1, float dual_a = 0.f) {
+    thorn::NsOp o = make_op(thorn::kOpSym);
+    o.asel = a;
+    o.bsel = b;
+    o.csel = c;
+    o.osel = out;
+    o.alpha = alpha;
+    o.beta = beta;
+    o.osel2 = dual;
+    o.dual_add = static_cast<float>(static_cast<_Float16>(dual_a));   // `a * I` in f16
+    ops.push_back({o, kind});
+}
+
+// Gram Newton-Schulz with restarts, the reference's recurrences and rounding points
+// (thorn.py:637-653); bit i of `mask`: restart before iteration i. RZ lives in whichever Q buffer
+// does not hold Q.
+NsSchedule gram_schedule(int iters, uint32_t mask, const float* coeffs) {
     using namespace thorn;
     auto restarts_at = [&](int i) { return i > 0 && i < 32 && ((mask >> i) & 1u); };
-    auto make = [](int32_t kind) {
-        NsOp o{};
-        o.kind = kind;
-        o.csel = -1;
-        return o;
-    };
-    std::vector<ScheduledOp> ops;
-    auto gram = [&](int xsel, bool first) {
-        NsOp o = make(kOpGram);
-        o.xsel = xsel;
-        o.first = first ? 1 : 0;
-        ops.push_back({o, THORN_KIND_GRAM});
-    };
-    auto update = [&](int xsel, int qsel, bool first, bool fin) {
-        NsOp o = make(kOpUpdate);
-        o.xsel = xsel;
-        o.qsel = qsel;
-        o.first = first ? 1 : 0;
-        o.final_iter = fin ? 1 : 0;
-        ops.push_back({o, THORN_KIND_UPDATE});
-    };
-    auto sym = [&](int a, int b, int c, int out, float alpha, float beta, float gamma, int kind) {
-        NsOp o = make(kOpSym);
-        o.asel = a; o.bsel = b; o.csel = c; o.osel = out;
-        o.alpha = alpha; o.beta = beta; o.gamma = gamma;
-        ops.push_back({o, kind});
-    };
+    NsSchedule sc;
     int xsel = kXB;    // the first iterate
     bool first = true; // xsel still holds it
-    int qsel = -1;     // buffer of Q; -1 before the first P after a restart
-    gram(xsel, true);
+    int qsel = -1;
+    push_gram(sc.ops, xsel, true);
     for (int i = 0; i < iters; ++i) {
         const float a = coeffs[3 * i], b = coeffs[3 * i + 1], c = coeffs[3 * i + 2];
-        if (restarts_at(i)) {
-            update(xsel, qsel, first, false);
-            xsel = xsel == kXB ? kXA : kXB;
+        const bool restart = restarts_at(i);
+        if (restart) {   // X <- Q X, R <- X X^T (thorn.py:641-643)
+            push_update(sc.ops, xsel, qsel, first, false, false, 0.f);
+            xsel = other_x(xsel);
             first = false;
-            gram(xsel, false);
-            qsel = -1;
+            push_gram(sc.ops, xsel, false);
         }
-        const int psel = qsel < 0 ? (qsel = kBufQA) : kBufP;   // right after a restart P_i is Q
-        sym(kBufR, kBufR, kBufR, psel, c, b, a, THORN_KIND_POLY);
-        if (psel == kBufP) {
-            const int qnew = qsel == kBufQA ? kBufQB : kBufQA;
-            sym(qsel, kBufP, -1, qnew, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
-            qsel = qnew;
+        if (i == 0 || restart) {   // Z = b R + c R R; Q = Z + a I (thorn.py:647-648)
+            qsel = kBufQA;
+            push_sym(sc.ops, kBufR, kBufR, kBufR, kBufZ, c, b, THORN_KIND_POLY, qsel, a);
+        } else {                   // Z; Q = a Q + Q Z
+            push_sym(sc.ops, kBufR, kBufR, kBufR, kBufZ, c, b, THORN_KIND_POLY);
+            const int qn = qsel == kBufQA ? kBufQB : kBufQA;
+            push_sym(sc.ops, qsel, kBufZ, qsel, qn, 1.f, a, THORN_KIND_SYMPROD);
+            qsel = qn;
         }
-        if (i < iters - 1 && !restarts_at(i + 1)) {
-            sym(kBufR, psel, -1, kBufT, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
-            sym(psel, kBufT, -1, kBufR, 1.f, 0.f, 0.f, THORN_KIND_SYMPROD);
+        if (i < iters - 1 && !restarts_at(i + 1)) {   // RZ = a R + R Z; R = a RZ + Z RZ (thorn.py:649-651)
+            const int rz = qsel == kBufQA ? kBufQB : kBufQA;
+            push_sym(sc.ops, kBufR, kBufZ, kBufR, rz, 1.f, a, THORN_KIND_SYMPROD);
+            push_sym(sc.ops, kBufZ, rz, rz, kBufR, 1.f, a, THORN_KIND_SYMPROD);
         }
     }
-    update(xsel, qsel, first, true);
-    return ops;
+    push_update(sc.ops, xsel, qsel, first, true, false, 0.f);   // X <- Q X (thorn.py:653)
+    sc.uout_sel = other_x(xsel);
+    return sc;
+}
+
+// The plain quintic (thorn.py:654-658): A = X X^T; B = b A + c A A; X <- a X + B X.
+NsSchedule plain_schedule(int iters, const float* coeffs) {
+    using namespace thorn;
+    NsSchedule sc;
+    int xsel = kXB;
+    for (int i = 0; i < iters; ++i) {
+        const float a = coeffs[3 * i], b = coeffs[3 * i + 1], c = coeffs[3 * i + 2];
+        push_gram(sc.ops, xsel, i == 0);
+        push_sym(sc.ops, kBufR, kBufR, kBufR, kBufZ, c, b, THORN_KIND_POLY);
+        push_update(sc.ops, xsel, kBufZ, i == 0, i == iters - 1, true, a);
+        xsel = other_x(xsel);
+    }
+    sc.uout_sel = xsel;   // the buffer the last update wrote
+    return sc;
 }
 
 }  // namespace
@@ -326,15 +373,13 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.n_psq = md ? static_cast<int32_t>(pnn ? mom_tiles : int64_t(L.g3_tiles_m) * L.g3_tiles_n) : 0;
         const size_t xbytes = size_t(L.rows) * L.ldx * 2;
         const size_t sbytes = size_t(L.s) * L.lds * 2;
-        L.x0 = take(2 * xbytes);   // fp32
+        const bool square = L.rows == L.cols;   // the plain quintic needs no Q (thorn.py:654-658)
         L.xa = take(xbytes);
         L.xb = take(xbytes);
         L.gram = take(sbytes);
-        L.poly = take(sbytes);
-        L.qa = take(sbytes);
-        L.qb = take(sbytes);
-        L.tmp = take(sbytes);
-        L.uout = pnn ? take(xbytes) : kNone;
+        L.zbuf = take(sbytes);
+        L.qa = square ? kNone : take(sbytes);
+        L.qb = square ? kNone : take(sbytes);
         L.normpart = take(sizeof(float) * mom_tiles);
         L.rowpart = md ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
         L.colpart = (L.flags & THORN_MAT_MD) ? take(sizeof(float) * size_t(L.mom_tiles_r) * L.cols) : kNone;
@@ -365,11 +410,10 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         for (auto& bin : bins) out.insert(out.end(), bin.begin(), bin.end());
         return out;
     };
-    // Gram Newton-Schulz for matrices at least twice as long as they are wide; the others (square
-    // ones included) take the plain quintic: below 2:1 the Gram schedule saves few flops and its
-    // f16 error grows (it is the same map in exact arithmetic).
+    // Gram Newton-Schulz for every non-square matrix, the plain quintic for square ones
+    // (thorn.py:628, 637-658).
     std::vector<int32_t> sets[2];
-    for (int i = 0; i < n; ++i) sets[plan->mats[i].l >= 2 * plan->mats[i].s ? 1 : 0].push_back(i);
+    for (int i = 0; i < n; ++i) sets[plan->mats[i].rows != plan->mats[i].cols ? 1 : 0].push_back(i);
     for (int q = 0; q < 2; ++q) {
         for (int i : sets[q]) {
             plan->mean_s[q] += plan->mats[i].s;
@@ -396,6 +440,11 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
         sym_blocks[i] = L.sym_tiles;
         g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
+        plan->max_mom_tiles = std::max<int64_t>(plan->max_mom_tiles, mom_blocks[i]);
+    }
+    if (n > 65535) {
+        delete plan;
+        return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: more than 65535 matrices in one plan");
     }
     size_t off = 0;
     plan->mats_off = 0;
@@ -464,15 +513,12 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.cgm = S.col_gain_moment; M.cgv = S.col_gain_variance;
         M.target = S.target_norm;
         M.zero = ws;
-        M.x0 = static_cast<float*>(at(L.x0));
         M.xa = static_cast<_Float16*>(at(L.xa));
         M.xb = static_cast<_Float16*>(at(L.xb));
         M.gram = static_cast<_Float16*>(at(L.gram));
-        M.poly = static_cast<_Float16*>(at(L.poly));
+        M.zbuf = static_cast<_Float16*>(at(L.zbuf));
         M.qa = static_cast<_Float16*>(at(L.qa));
         M.qb = static_cast<_Float16*>(at(L.qb));
-        M.tmp = static_cast<_Float16*>(at(L.tmp));
-        M.uout = static_cast<_Float16*>(at(L.uout));
         M.normpart = static_cast<float*>(at(L.normpart));
         M.rowpart = static_cast<float*>(at(L.rowpart));
         M.colpart = static_cast<float*>(at(L.colpart));
@@ -488,11 +534,21 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
             while (i + cnt < n && steps[i + cnt].magma_s == S.magma_s) ++cnt;
             M.magma_n = cnt;
         }
+        M.gain_n = 0;
+        if (mds && (i == 0 || steps[i - 1].row_gain != S.row_gain)) {   // first matrix of a parameter
+            int cnt = 1;
+            while (i + cnt < n && steps[i + cnt].row_gain == S.row_gain) ++cnt;
+            M.gain_n = cnt;
+        }
         M.rows = L.rows; M.cols = L.cols; M.s = L.s; M.l = L.l;
         M.ldx = L.ldx; M.lds = L.lds; M.tall = L.tall;
         int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
         if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m)) flags |= thorn::kFlagVec4;
-        if (workspace == plan->stepped_ws && !md && !mds) flags |= thorn::kFlagPrescaled;
+        // The first iterate of a large matrix is written directly in f16 with the previous step's
+        // power-of-two scale (one pass less over u); small matrices, whose Newton-Schulz rounding
+        // is not averaged out, and decouple_md ones take the exact form of thorn.py:632-635.
+        if (workspace == plan->stepped_ws && !md && !mds && int64_t(L.rows) * L.cols >= kPrescaleMinElems)
+            flags |= thorn::kFlagPrescaled;
         else any_exact = true;
         if (S.magma_s) {
             if (reinterpret_cast<uintptr_t>(S.magma_s) & 3u)
@@ -578,32 +634,29 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         plan->stepped_ws = plan->filled_ws;
         return THORN_OK;
     }
-    if (plan->any_exact) {
-        THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(plan->pre.total),
-                     dim3(256), 0, st, mats, task_list(dev, plan->pre));
+    // The exact first iterate (and the rebuild of prescaled ones out of range): one row of blocks
+    // per matrix, a tile per block when some matrix is on the exact path, else 64 blocks per
+    // matrix that return at once unless a gradient scale jumped.
+    {
+        const int gx = plan->any_exact ? std::max(plan->max_mom_tiles, 1) : std::min(plan->max_mom_tiles, 64);
+        THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(std::max(gx, 1), n),
+                     dim3(256), 0, st, mats);
     }
-    if (plan->filled_ws == plan->stepped_ws) {
-        THORN_LAUNCH(THORN_KIND_CAST, "ortho_repair_kernel", thorn::ortho_repair_kernel, dim3(n), dim3(256), 0, st,
-                     mats);
-    }
-    // Newton-Schulz: matrices of aspect ratio below 2 on the plain quintic, the others on Gram
-    // Newton-Schulz with the given restarts (thorn.py:628, 637-658); step k of both schedules
-    // shares launch k.
-    const uint32_t plain = iters >= 32 ? 0xFFFFFFFEu : ((1u << iters) - 2u);
-    const std::vector<ScheduledOp> sched[2] = {ns_schedule(iters, plain, coeffs),
-                                               ns_schedule(iters, restart_mask, coeffs)};
+    // Newton-Schulz: square matrices on the plain quintic, the others on Gram Newton-Schulz with
+    // the given restarts (thorn.py:628, 637-658); step k of both schedules shares launch k.
+    const NsSchedule sched[2] = {plain_schedule(iters, coeffs), gram_schedule(iters, restart_mask, coeffs)};
     const thorn::TaskList sym[2] = {task_list(dev, plan->sym_live[0]), task_list(dev, plan->sym_live[1])};
     const thorn::TaskList g3[2] = {task_list(dev, plan->g3_live[0]), task_list(dev, plan->g3_live[1])};
-    const size_t steps = std::max(sched[0].size(), sched[1].size());
+    const size_t steps = std::max(sched[0].ops.size(), sched[1].ops.size());
     for (size_t k = 0; k < steps; ++k) {
         thorn::NsOp op[2]{};
         thorn::TaskList tl[2]{};
         int kind = -1;
         for (int q = 1; q >= 0; --q) {   // the Gram set first: it names the launch for timing
-            if (k >= sched[q].size() || sym[q].n == 0) continue;
-            op[q] = sched[q][k].op;
+            if (k >= sched[q].ops.size() || sym[q].n == 0) continue;
+            op[q] = sched[q].ops[k].op;
             tl[q] = op[q].kind == thorn::kOpUpdate ? g3[q] : sym[q];
-            if (kind < 0) kind = sched[q][k].kind;
+            if (kind < 0) kind = sched[q].ops[k].kind;
         }
         const int total = tl[1].total + tl[0].total;
         if (total == 0) continue;
@@ -620,8 +673,11 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         const thorn::TaskList pnn = task_list(dev, plan->pnn_live);
         THORN_LAUNCH(THORN_KIND_ROWSTATS, "ortho_rowstats_kernel", thorn::ortho_rowstats_kernel, dim3(pnn.n),
                      dim3(256), 0, st, mats, pnn.order);
+        thorn::UoutSel usel;
+        usel.sel[0] = sched[0].uout_sel;
+        usel.sel[1] = sched[1].uout_sel;
         THORN_LAUNCH(THORN_KIND_PNN_APPLY, "ortho_pnn_apply_kernel", thorn::ortho_pnn_apply_kernel, dim3(pnn.total),
-                     dim3(256), 0, st, mats, pnn);
+                     dim3(256), 0, st, mats, pnn, usel);
     }
     if (plan->md.n > 0) {
         const thorn::TaskList md = task_list(dev, plan->md);

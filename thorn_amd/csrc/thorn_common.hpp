@@ -202,15 +202,13 @@ struct OrthoMat {
     const float* target;   // decoupled-magnitude target norm (0-d)
     const void* zero;      // 256 bytes of zeros in the workspace (source of out-of-range tile chunks)
 
-    float* x0;         // rows x ldx, u = g + beta1*m (fp32, unnormalized)
     _Float16* xa;      // rows x ldx, Newton-Schulz iterate (ping)
-    _Float16* xb;      // rows x ldx, Newton-Schulz iterate (pong)
-    _Float16* gram;    // s x lds: R, the Gram matrix of the short side
-    _Float16* poly;    // s x lds: P = a I + b R + c R^2 of the current iteration
-    _Float16* qa;      // s x lds: Q, the accumulated product of the P's since the last restart
-    _Float16* qb;      // s x lds: (ping-pong with qa)
-    _Float16* tmp;     // s x lds: R P while R is advanced to P R P
-    _Float16* uout;    // rows x ldx, final update (per-row-normalized matrices only)
+    _Float16* xb;      // rows x ldx, Newton-Schulz iterate (pong); the final u' of per-row-normalized
+                       // matrices goes to whichever of the two the last update does not read
+    _Float16* gram;    // s x lds: R, the Gram matrix of the short side (plain quintic: A = X X^T)
+    _Float16* zbuf;    // s x lds: Z = b R + c R^2 (plain quintic: B = b A + c A^2)
+    _Float16* qa;      // s x lds: Q, the accumulated polynomial since the last restart, or R Z
+    _Float16* qb;      // s x lds: (ping-pong with qa; non-square matrices only)
     float* normpart;   // [mom_tiles] partial sums of u^2
     float* rowpart;    // [mom_tiles_c][rows] partial row sums of p*g*softplus(cg)
     float* colpart;    // [mom_tiles_r][cols] partial column sums of p*g*softplus(rg)
@@ -235,10 +233,13 @@ struct OrthoMat {
     int32_t n_psq;
     int32_t apply_tiles;   // elementwise tiles of the per-row-normalized apply kernel
     int32_t magma_n;       // Magma: matrices of the parameter when this is its first one, else 0
+    int32_t gain_n;        // scalar decouple_md gain: matrices of the parameter when this is its
+                           // first one, else 0 (one gain for the whole parameter, thorn.py:1609-1612)
 };
 
 enum ScalSlot : int {
     kScalSigma = 0,    // 1 / (||u||_F + 1e-8)
+    kScalDenom = 6,    // ||u||_F + 1e-8, the divisor of the exact first iterate (thorn.py:633)
     kScalGamma = 1,    // per-row-normalization Frobenius rescale
     kScalMDFactor = 2, // target / (||p||_F + 1e-8)
     kScalX0Scale = 3,  // factor from the stored f16 first iterate to sigma * u (1 when exact)
@@ -247,7 +248,7 @@ enum ScalSlot : int {
 };
 
 // Selectors of the s x s workspace matrices and of the two iterate buffers.
-enum SymBuf : int { kBufR = 0, kBufP = 1, kBufQA = 2, kBufQB = 3, kBufT = 4 };
+enum SymBuf : int { kBufR = 0, kBufZ = 1, kBufQA = 2, kBufQB = 3 };
 enum XBuf : int { kXB = 0, kXA = 1 };   // the first iterate is written to xb
 
 // A grouped launch: task k covers blocks [starts[k], starts[k+1]) and works on matrix order[k].

@@ -21,7 +21,9 @@ __device__ __forceinline__ int tile_col(int c0, int lane, int e, bool vec) {
 //   md:   G = softplus(rg_i) * softplus(cg_j); p /= G; pg = p * g; g *= G
 //         rowpart += pg * softplus(cg_j); colpart += pg * softplus(rg_i)
 //   magma: magpart += (g*m, g*g, m*m) with the moment before the update (thorn.py:1390-1392)
-//   m = m * beta1 + g;  u = g + beta1 * m;  x0 = u (fp32);  normpart += u^2
+//   m = m * beta1 + g;  u = g + beta1 * m;  normpart += u^2;  prescaled: xb = f16(u * 2^k)
+// With decouple_md, g * G is written back into the gradient (the reference's in-place g.mul_,
+// thorn.py:907), which ortho_cast_kernel then reads to rebuild u.
 __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
     __shared__ float colred[4][kTileC];
     __shared__ float scratch[12];
@@ -34,7 +36,6 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
     const bool vec = M.flags & kFlagVec4;
-    const bool keep_grad = M.flags & kFlagKeepGrad;
     const bool presc = M.flags & kFlagPrescaled;   // never combined with md
     const bool magma = M.flags & kFlagMagma;
     const float prescale = presc ? M.scal[kScalPrescale] : 1.f;
@@ -118,9 +119,8 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
             rowacc = wave_sum(rowacc);
             if (lane == 0) M.rowpart[(int64_t)tc * M.rows + row] = rowacc;
         }
-        // first iterate: exact fp32 u (scaled and rounded by ortho_cast_kernel once sigma is
-        // known), or directly f16(u * 2^k) with the previous step's power of two
-        float* xrow = M.x0 + (int64_t)row * M.ldx;
+        // first iterate: directly f16(u * 2^k) with the previous step's power of two, or later
+        // by ortho_cast_kernel (exact path) once ||u|| is known
         _Float16* hrow = M.xb + (int64_t)row * M.ldx;
         if (vec) {
             if (cok[0]) {
@@ -128,14 +128,11 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                 stg_nt<float4>(M.m + rbase + c, make_float4(mv[rr][0], mv[rr][1], mv[rr][2], mv[rr][3]));
                 if (md || mds) {
                     stg_nt<float4>(M.p + rbase + c, make_float4(pv[rr][0], pv[rr][1], pv[rr][2], pv[rr][3]));
-                    if (keep_grad)
-                        stg_nt<float4>(M.g + rbase + c, make_float4(gv[rr][0], gv[rr][1], gv[rr][2], gv[rr][3]));
+                    stg<float4>(M.g + rbase + c, make_float4(gv[rr][0], gv[rr][1], gv[rr][2], gv[rr][3]));
                 }
                 if (presc)
                     stg<half4>(hrow + c, half4{(_Float16)(xv[0] * prescale), (_Float16)(xv[1] * prescale),
                                                (_Float16)(xv[2] * prescale), (_Float16)(xv[3] * prescale)});
-                else
-                    stg<float4>(xrow + c, make_float4(xv[0], xv[1], xv[2], xv[3]));
             }
         } else {
 #pragma unroll
@@ -145,10 +142,9 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                 stg_nt<float>(M.m + rbase + c, mv[rr][e]);
                 if (md || mds) {
                     stg_nt<float>(M.p + rbase + c, pv[rr][e]);
-                    if (keep_grad) stg_nt<float>(M.g + rbase + c, gv[rr][e]);
+                    stg<float>(M.g + rbase + c, gv[rr][e]);
                 }
                 if (presc) hrow[c] = (_Float16)(xv[e] * prescale);
-                else stg<float>(xrow + c, xv[e]);
             }
         }
     }
@@ -191,7 +187,8 @@ __device__ __forceinline__ void norm_sigma_magma(const OrthoMat* __restrict__ ma
     s = block_sum(s, scratch);
     if (threadIdx.x == 0) {
         const float nrm = sqrtf(s);
-        const float sigma = 1.f / (nrm + 1e-8f);
+        const float denom = nrm + 1e-8f;
+        const float sigma = 1.f / denom;
         float x0scale = 1.f, repair = 0.f;
         if (M.flags & kFlagPrescaled) {
             // the stored iterate is u * 2^k; it matches the exact f16(sigma * u) range while 2^k
@@ -201,6 +198,7 @@ __device__ __forceinline__ void norm_sigma_magma(const OrthoMat* __restrict__ ma
             else x0scale = sigma / M.scal[kScalPrescale];
         }
         M.scal[kScalSigma] = sigma;
+        M.scal[kScalDenom] = denom;
         M.scal[kScalX0Scale] = x0scale;
         M.scal[kScalRepair] = repair;
         // next step's prescale: the power of two nearest sigma (kept when sigma is not finite)
@@ -257,10 +255,15 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
             adam_elem(gain, grad, mo, va, a);
             M.cg[j] = gain; M.cgm[j] = mo; M.cgv[j] = va;
         }
-    } else if (slice == 0) {
+    } else if (slice == 0 && M.gain_n > 0) {
+        // one scalar gain per parameter: its first matrix sums the partials of all of them
+        // (p_g.sum() over the whole tensor, thorn.py:920) and steps the gain once
         float t = 0.f;
-        for (int i = threadIdx.x; i < M.rows; i += 256)
-            for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpart[(int64_t)c * M.rows + i];
+        for (int q = 0; q < M.gain_n && (int)blockIdx.x + q < n_mats; ++q) {
+            const OrthoMat& Q = mats[blockIdx.x + q];
+            for (int i = threadIdx.x; i < Q.rows; i += 256)
+                for (int c = 0; c < Q.mom_tiles_c; ++c) t += Q.rowpart[(int64_t)c * Q.rows + i];
+        }
         t = block_sum(t, scratch);
         if (threadIdx.x == 0) {
             float gain = M.rg[0], mo = M.rgm[0], va = M.rgv[0];
@@ -275,6 +278,15 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
 // Per-row normalization (thorn.py:709-766): s_i = rsqrt(max(mean_j u'_ij^2, eps)),
 // gamma = ||u'||_F / max(||s * u'||_F, eps); one block per matrix.
 // ---------------------------------------------------------------------------------------------
+// The last Newton-Schulz update leaves u' (f16) in one of the two iterate buffers, which one
+// depending on the schedule: usel[0] for square matrices (plain quintic), usel[1] for the others.
+struct UoutSel {
+    int32_t sel[2];
+};
+__device__ __forceinline__ const _Float16* uout_of(const OrthoMat& M, const UoutSel& u) {
+    return u.sel[M.s == M.l ? 0 : 1] == kXA ? M.xa : M.xb;
+}
+
 __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __restrict__ mats,
                                                              const int32_t* __restrict__ idx) {
     __shared__ float scratch[4];
@@ -296,7 +308,8 @@ __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __r
 }
 
 // p <- p - eta * cwd((u' * s_i) * gamma) over per-row-normalized matrices, plus p^2 partials for md.
-__global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
+__global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
+                                                              UoutSel usel) {
     __shared__ float scratch[4];
     const int b = blockIdx.x;
     const int k = find_task(tl.starts, tl.n, b);
@@ -308,6 +321,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
     if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
     const float gamma = M.scal[kScalGamma];
     const float eta = (M.flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta;   // thorn.py:1405
+    const _Float16* const uout = uout_of(M, usel);
     const bool md = M.flags & (kFlagMD | kFlagMDScalar);
     const bool vec = M.flags & kFlagVec4;
     const int nrows = M.rows - r0;
@@ -327,7 +341,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             if (rr >= nrows || !ok) continue;
             const int row = r0 + rr;
             pv[rr] = ldg_nt<float4>(M.p + (int64_t)row * M.cols + c);
-            uv[rr] = ldg_nt<half4>(M.uout + (int64_t)row * M.ldx + c);
+            uv[rr] = ldg_nt<half4>(uout + (int64_t)row * M.ldx + c);
             sv[rr] = ldg<float>(M.rowscale + row);
         }
 #pragma unroll
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             if (row >= M.rows) break;
             const float s = M.rowscale[row];
             const int64_t rbase = (int64_t)row * M.cols;
-            const _Float16* urow = M.uout + (int64_t)row * M.ldx;
+            const _Float16* urow = uout + (int64_t)row * M.ldx;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int c = c0 + lane + 64 * e;

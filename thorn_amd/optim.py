@@ -332,8 +332,8 @@ class _OrthoRunner:
     @staticmethod
     def restart_mask(group: _Group, iters: int) -> int:
         """Gram Newton-Schulz restart positions (thorn.py:582, 637-653) as a bit mask for the
-        library, which runs Gram Newton-Schulz on matrices at least twice as long as wide and the
-        plain quintic on the others (thorn.py:628, 655-658)."""
+        library, which runs Gram Newton-Schulz on every non-square matrix and the plain quintic on
+        square ones (thorn.py:628, 654-658)."""
         return sum(1 << i for i in group.restarts if 0 < i < iters)
 
 
