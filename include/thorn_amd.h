@@ -46,6 +46,12 @@ enum {
 #define THORN_MAT_PER_ROW_NORM 1   /* per-row normalization (thorn.py:704-707, 709-766) */
 #define THORN_MAT_MD 2             /* decouple_md with row and column gains (thorn.py:1603-1608) */
 #define THORN_MAT_MD_SCALAR 4      /* decouple_md with one scalar gain (thorn.py:1609-1612) */
+#define THORN_MAT_ADAM 8           /* a decouple_md tensor of a non-orthogonalized group: the update
+                                      is the Adam step (thorn.py:1702-1721), no Newton-Schulz; needs
+                                      THORN_MAT_MD or THORN_MAT_MD_SCALAR. A 1-D tensor is 1 x n. */
+#define THORN_MAT_NORM_ROWS 16     /* with THORN_MAT_ADAM: the renormalization runs per row
+                                      (norm_axis = -1, thorn.py:594-595, 1717); target_norm then
+                                      points at `rows` values */
 
 /* Per-step flags (ThornOrthoMatStep.step_flags). */
 #define THORN_STEP_KEEP_GRAD 8     /* none_grad=False. No effect since ABI 5: the gradient of a
@@ -94,6 +100,12 @@ typedef struct ThornOrthoMatStep {
     int32_t reserved;
     float* magma_s;       /* Magma: state['s'] (0-d) or null. Consecutive matrices with the same
                              magma_s are one parameter: the cosine similarity spans them all. */
+    /* THORN_MAT_ADAM only (thorn.py:838-888 with lr = eta, the group lr * rect * magma): */
+    float* v;             /* state['variance'] */
+    float adam_beta2, adam_w1, adam_w2;    /* beta2, 1 - beta1, 1 - beta2 */
+    float adam_bc1, adam_bc2, adam_eps;    /* bias corrections; eps 0 selects Adam-atan2 */
+    int32_t adam_degenerate;               /* rect == 0: u = m (thorn.py:883-885) */
+    int32_t reserved2;
 } ThornOrthoMatStep;
 
 typedef struct thorn_ortho_plan* thorn_ortho_plan_t;

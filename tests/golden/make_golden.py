@@ -19,7 +19,10 @@ What the fixtures pin, and why they need the reference itself (closed forms cove
   * traj_md.npz       - 20 steps with decouple_md on the orthogonalized group (config-3 branch);
   * magma.npz         - _w1rand sequences and _momentum_aligned_mask outputs (Magma);
   * traj_magma*.npz   - Magma trajectories: the mixed and decouple_md sets with momentum_align on
-    every group, and row-sparse embedding gradients with and without it.
+    every group, and row-sparse embedding gradients with and without it;
+  * traj_md_adam.npz  - 20 steps with decouple_md on orthogonalized and Adam groups (row/column
+    gains, scalar gains shared by batched matrices, rectification, a per-row norm axis);
+  * traj_md_module.npz - 10 steps of THORN(module, decouple_md=True) (the nn.Module overload).
 
 Usage: python tests/golden/make_golden.py [fixture ...]   (e.g. `magma traj_magma`; default: all)
 """
@@ -167,7 +170,10 @@ def magma_fixtures(ref) -> None:
 def run_trajectory(ref, name: str, build, steps: int, snapshot_every: int) -> None:
     torch.manual_seed(0)
     params, groups, grads = build()
-    opt = ref.THORN(groups)
+    if isinstance(groups, dict):   # the nn.Module overload
+        opt = ref.THORN(groups['module'], **groups['kwargs'])
+    else:
+        opt = ref.THORN(groups)
     out = {}
     for i, p in enumerate(params):
         out[f'init_p{i}'] = p.detach().clone()
@@ -203,6 +209,8 @@ def main(only: list[str]) -> None:
         ('traj_sparse', lambda: run_trajectory(ref, 'traj_sparse.npz', workloads.sparse_small, 12, 4)),
         ('traj_magma_sparse', lambda: run_trajectory(ref, 'traj_magma_sparse.npz', workloads.magma_sparse_small,
                                                      12, 4)),
+        ('traj_md_adam', lambda: run_trajectory(ref, 'traj_md_adam.npz', workloads.md_adam_small, 20, 10)),
+        ('traj_md_module', lambda: run_trajectory(ref, 'traj_md_module.npz', workloads.md_module, 10, 5)),
     ]
     for name, job in jobs:
         if not only or name in only:

@@ -134,3 +134,62 @@ def sparse_small(steps: int = 12, momentum_align: bool = False):
 
 def magma_sparse_small(steps: int = 12):
     return sparse_small(steps, momentum_align=True)
+
+
+def md_adam_small(steps: int = 20):
+    """decouple_md on every kind of group: orthogonalized matrices with row/column gains,
+    batched (3-D, 4-D) orthogonalized parameters sharing one scalar gain (split_gain=False), and
+    non-orthogonalized (Adam) tensors with row/column gains, a scalar gain, rectification, and a
+    per-row norm axis with the default 'init' target norm (thorn.py:594-608, 1704-1721)."""
+    gen = torch.Generator().manual_seed(31)
+    ortho_split = [(40, 24), (2, 12, 20)]
+    ortho_scalar = [(3, 20, 28), (2, 2, 16, 12)]
+    adam_split = [(60, 16), (32,), (2, 8, 12)]
+    adam_scalar = [(20, 12), (16,)]
+    adam_rows = [(30, 10)]
+    sets = [ortho_split, ortho_scalar, adam_split, adam_scalar, adam_rows]
+    shapes = [sh for st in sets for sh in st]
+    params = [_leaf(torch.ones(sh) + 0.1 * torch.randn(sh, generator=gen) if len(sh) == 1
+                    else torch.randn(sh, generator=gen) * 0.02) for sh in shapes]
+    grads = _grads(gen, shapes, steps, 1e-3, outlier_rows=0.05)
+    bounds = [0]
+    for st in sets:
+        bounds.append(bounds[-1] + len(st))
+    ps = [params[bounds[k]:bounds[k + 1]] for k in range(len(sets))]
+    groups = [
+        {'orthogonalize': True, 'params': ps[0], 'lr': 8e-3, 'weight_decay': 0.0, 'decouple_md': True},
+        {'orthogonalize': True, 'params': ps[1], 'lr': 4e-3, 'weight_decay': 0.05, 'decouple_md': True,
+         'split_gain': False, 'gain_lr': 2e-3},
+        {'orthogonalize': False, 'params': ps[2], 'lr': 2e-3, 'weight_decay': 0.1, 'decouple_md': True},
+        {'orthogonalize': False, 'params': ps[3], 'lr': 2e-3, 'weight_decay': 0.0, 'decouple_md': True,
+         'split_gain': False, 'rectify': True, 'eps': 1e-8, 'gain_betas': (0.8, 0.9)},
+        {'orthogonalize': False, 'params': ps[4], 'lr': 1e-3, 'weight_decay': 0.1, 'decouple_md': True,
+         'norm_axis': -1},
+    ]
+    return params, groups, lambda s, i, prm: grads[(s, i)]
+
+
+class _MdNet(torch.nn.Module):
+    def __init__(self, gen):
+        super().__init__()
+        self.embed = torch.nn.Embedding(40, 12)
+        self.proj = torch.nn.Linear(12, 24)
+        self.conv = torch.nn.Conv1d(3, 8, 5)
+        self.norm = torch.nn.LayerNorm(24)
+        self.lm_head = torch.nn.Linear(24, 40, bias=False)
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.05 + (1.0 if p.ndim == 1 else 0.0))
+
+
+def md_module(steps: int = 10):
+    """The nn.Module overload with decouple_md=True, as README.md:109 uses it: _auto_assign puts the
+    flag into both the orthogonalized group (Linear and conv weights) and the Adam group
+    (embedding, lm_head, biases, norm) (thorn.py:1302-1331). `groups` is the module and the
+    constructor's keyword arguments."""
+    gen = torch.Generator().manual_seed(41)
+    net = _MdNet(gen)
+    params = list(net.parameters())
+    shapes = [tuple(p.shape) for p in params]
+    grads = _grads(gen, shapes, steps, 1e-3, outlier_rows=0.05)
+    return params, {'module': net, 'kwargs': {'lr': 3e-3, 'decouple_md': True}}, lambda s, i, prm: grads[(s, i)]

@@ -56,10 +56,13 @@ def test_invalid_hyperparameters_raise_value_error_at_step(bad, msg):
 
 
 def test_unsupported_features_raise_not_implemented():
-    p = nn.Parameter(torch.zeros(3, 3))
-    opt = thorn_amd.THORN([{'orthogonalize': False, 'params': [p], 'lr': 1e-3, 'decouple_md': True}])
-    p.grad = torch.zeros(3, 3)
-    with pytest.raises(NotImplementedError, match='decouple_md on a non-orthogonalized group'):
+    """decouple_md runs on Adam groups too; a norm axis other than the trailing matrix or the last
+    dim is refused before anything is computed."""
+    p = nn.Parameter(torch.zeros(2, 3, 3))
+    opt = thorn_amd.THORN([{'orthogonalize': False, 'params': [p], 'lr': 1e-3, 'decouple_md': True,
+                            'norm_axis': 0}])
+    p.grad = torch.zeros(2, 3, 3)
+    with pytest.raises(NotImplementedError, match='norm_axis=0'):
         opt.step()
 
 
@@ -85,3 +88,12 @@ def test_coefficients_match_reference_goldens_exactly():
         np.testing.assert_array_equal(a, z['coeffs'][off:off + it])
         off += it
         assert list(_coeffs.gram_restarts(tuple(map(tuple, a)))) == [int(x) for x in z['restarts'][k] if x >= 0]
+
+
+def test_reference_import_path():
+    """``from thorn import THORN`` (the reference's thorn/__init__.py:1) gives this build's class."""
+    import thorn
+    from thorn import THORN
+    assert THORN is thorn_amd.THORN
+    assert thorn.__all__ == ['THORN', 'THORNOrthoGroup', 'THORNNonOrthoGroup', 'THORNGroup']
+    assert thorn.THORNOrthoGroup is thorn_amd.THORNOrthoGroup

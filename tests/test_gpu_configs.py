@@ -1,0 +1,208 @@
+"""GPU parity at the BASELINE workloads (configs 2-5), each against the oracle.
+
+Configs 2, 3 and 5 are too large for the CPU oracle on the GPU box's host (its fp16 GEMMs take
+hours), so the checker there is the oracle itself run on CUDA tensors: the reference's eager
+PyTorch path (thorn.py with Triton and compile off) executing on the GPU's vendor GEMMs, on the
+same inputs. Config 4 is small and uses the CPU oracle.
+
+Bars: fp32 state (moment, variance, gains and their moments) relative
+Frobenius <= 1e-5; each orthogonalized matrix's update p_new - p_old within 2e-2; Adam tensors'
+update within 1e-4. Gradients are drawn once per step and handed to both sides bit for bit.
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+import bench  # noqa: E402  (the BASELINE workload generators)
+from oracle import thorn_oracle as O  # noqa: E402
+from tests.test_gpu_parity import DP_TOL, _clone_groups, rel  # noqa: E402
+
+DEV = 'cuda:0'
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _pair(params, groups):
+    """GPU THORN over `params` and the oracle over device copies of them (same groups)."""
+    import thorn_amd
+    oparams = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    return thorn_amd.THORN(groups), O.OracleTHORN(_clone_groups(groups, oparams)), oparams
+
+
+def _teacher_force(gpu, params, ora, oparams):
+    with torch.no_grad():
+        for p, q in zip(params, oparams):
+            p.copy_(q)
+            for k, v in ora.state[q].items():
+                if torch.is_tensor(v):
+                    gpu.state[p][k].copy_(v)
+                else:
+                    gpu.state[p][k] = v
+
+
+def _step_and_check(gpu, params, ora, oparams, grads, ortho_ids, worst, where, since=None):
+    """One step on both sides; per-tensor update and state checks. `since`: parameter values to
+    measure the update from (default: the values before this step)."""
+    before = since if since is not None else [p.detach().clone() for p in params]
+    obefore = since if since is not None else [q.detach().clone() for q in oparams]
+    for p, q, g in zip(params, oparams, grads):
+        p.grad = g.clone()
+        q.grad = g.clone()
+    gpu.step()
+    ora.step()
+    torch.cuda.synchronize()
+    return _check(gpu, params, ora, oparams, before, obefore, ortho_ids, worst, where)
+
+
+def _check(gpu, params, ora, oparams, before, obefore, ortho_ids, worst, where):
+    for i, (p, q) in enumerate(zip(params, oparams)):
+        dp, dq = p.detach() - before[i], q.detach() - obefore[i]
+        r = rel(dp, dq)
+        if id(p) in ortho_ids:
+            worst['dp'] = max(worst.get('dp', 0.0), r)
+            assert r <= DP_TOL, (where, i, tuple(p.shape), r)
+        else:
+            worst['dp_adam'] = max(worst.get('dp_adam', 0.0), r)
+            assert r <= 1e-4, (where, i, tuple(p.shape), r)
+        for k, v in ora.state[q].items():
+            if torch.is_tensor(v) and k != 'target_norm':
+                sr = rel(gpu.state[p][k], v)
+                worst['state'] = max(worst.get('state', 0.0), sr)
+                assert sr <= 1e-5, (where, i, k, sr)
+            elif not torch.is_tensor(v):
+                assert gpu.state[p][k] == v, (where, i, k)
+    return worst
+
+
+def _draw(params, gen, scale=1e-3, student_t=False):
+    out = []
+    for p in params:
+        z = torch.randn(p.shape, generator=gen, device=DEV)
+        if student_t:
+            chi = sum(torch.randn(p.shape, generator=gen, device=DEV) ** 2 for _ in range(3))
+            z = z / torch.sqrt(chi / 3)
+        out.append(z * scale)
+    return out
+
+
+def test_config2_full_step():
+    """BASELINE config 2 (140 Qwen3 matrices, 41 RMSNorm vectors, the 151936 x 1024 embedding), two
+    whole steps: the exact first iterate, then the prescaled one."""
+    _log('[gpu] config 2: two full steps against the oracle on the GPU')
+    params, grads, groups, mats = bench.build_workload(2, DEV)
+    gpu, ora, oparams = _pair(params, groups)
+    ortho = {id(p) for p in groups[0]['params']}
+    gen = torch.Generator(device=DEV).manual_seed(12)
+    worst = {}
+    _step_and_check(gpu, params, ora, oparams, grads, ortho, worst, 'step 1')
+    _step_and_check(gpu, params, ora, oparams, _draw(params, gen), ortho, worst, 'step 2')
+    _log(f'[gpu]   config 2: {worst}')
+
+
+def _state_drift(gpu, params, ora, oparams) -> float:
+    worst = 0.0
+    for p, q in zip(params, oparams):
+        for k, v in ora.state[q].items():
+            if torch.is_tensor(v) and k != 'target_norm':
+                worst = max(worst, rel(gpu.state[p][k], v))
+    return worst
+
+
+CONFIG3_CARRIED_DRIFT = 1e-3   # bound on the state drift after 9 free-running decouple_md steps
+
+
+def test_config3_decouple_md_50_steps():
+    """the config-2 shapes with decouple_md (md scaling, lr 8e-3, wd 0) for 50
+    steps, checked every 10. Free running, the f16 Newton-Schulz difference (~2e-3 of each update)
+    enters the row and column gains through p * g and the gains scale the gradient, so the two
+    sides' states drift apart: 2.8e-5 of the gain moments after 10 steps, above the 1e-5 state
+    bar. Every 10th step therefore starts from the oracle's state (teacher forcing) and is checked
+    at the full bars; the carried drift of the 9 free steps before it is logged and held to
+    CONFIG3_CARRIED_DRIFT."""
+    _log('[gpu] config 3: 50 decouple_md steps, checked every 10')
+    params, _, groups, mats = bench.build_workload(3, DEV)
+    gpu, ora, oparams = _pair(params, groups)
+    ortho = {id(p) for p in groups[0]['params']}
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    worst = {}
+    for step in range(1, 51):
+        grads = _draw(params, gen)
+        if step % 10:
+            for p, q, g in zip(params, oparams, grads):
+                p.grad = g.clone()
+                q.grad = g.clone()
+            gpu.step()
+            ora.step()
+            continue
+        torch.cuda.synchronize()
+        drift = _state_drift(gpu, params, ora, oparams)
+        worst['carried_drift'] = max(worst.get('carried_drift', 0.0), drift)
+        assert drift <= CONFIG3_CARRIED_DRIFT, (step, drift)
+        _teacher_force(gpu, params, ora, oparams)
+        _step_and_check(gpu, params, ora, oparams, grads, ortho, worst, f'step {step}')
+        _log(f'[gpu]   step {step}: carried drift over 9 steps {drift:.2e}; {worst}')
+
+
+def test_config4_conv_vad_10_steps():
+    """BASELINE config 4 (Earshot-like conv VAD: six conv kernels flattened to out x (in k), a
+    256 x 128 Linear, 12 vectors), 10 free-running steps against the CPU oracle."""
+    import thorn_amd
+    _log('[gpu] config 4: 10 free-running steps against the CPU oracle')
+    params_cpu, _, groups_cpu, mats = bench.build_workload(4, 'cpu')
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params_cpu]
+    gpu = thorn_amd.THORN(_clone_groups(groups_cpu, gparams))
+    ora = O.OracleTHORN(groups_cpu)
+    ortho = {id(p) for p in groups_cpu[0]['params']}
+    gen = torch.Generator().manual_seed(14)
+    worst = {}
+    for step in range(1, 11):
+        before = [p.detach().clone() for p in params_cpu]
+        gbefore = [p.detach().clone() for p in gparams]
+        grads = [torch.randn(p.shape, generator=gen) * 1e-2 for p in params_cpu]
+        for p, q, g in zip(gparams, params_cpu, grads):
+            p.grad = g.to(DEV)
+            q.grad = g.clone()
+        gpu.step()
+        ora.step()
+        torch.cuda.synchronize()
+        for i, (p, q) in enumerate(zip(gparams, params_cpu)):
+            r = rel(p.detach().cpu() - gbefore[i].cpu(), q.detach() - before[i])
+            key, bar = ('dp', DP_TOL) if id(q) in ortho else ('dp_adam', 1e-4)
+            worst[key] = max(worst.get(key, 0.0), r)
+            assert r <= bar, (step, i, tuple(q.shape), r)
+            for k, v in ora.state[q].items():
+                if torch.is_tensor(v):
+                    sr = rel(gpu.state[p][k], v)
+                    worst['state'] = max(worst.get('state', 0.0), sr)
+                    assert sr <= 1e-5, (step, i, k, sr)
+    _log(f'[gpu]   config 4: {worst}')
+
+
+def test_config5_every_shape():
+    """BASELINE config 5 (Qwen3 ~1.7B-scale: 28 layers of 2048^2, 1024 x 2048, 6144 x 2048 and
+    2048 x 6144 matrices, plus 8192^2 and 16384 x 1024), Student-t(3) gradients, two whole steps
+    against the oracle on the GPU. Drawn on the GPU (1.49e9 elements)."""
+    _log('[gpu] config 5: two full steps against the oracle on the GPU')
+    mats, _ = bench.config_shapes(5)
+    gen = torch.Generator(device=DEV).manual_seed(3407)
+    params = [torch.nn.Parameter(torch.randn(sh, generator=gen, device=DEV) * 0.02) for sh in mats]
+    groups = [{'orthogonalize': True, 'params': params, 'lr': 1e-3, 'betas': (0.9, 0.95), 'weight_decay': 0.1,
+               'scaling_mode': 'moonlight'}]
+    gpu, ora, oparams = _pair(params, groups)
+    ortho = {id(p) for p in params}
+    worst = {}
+    for step in (1, 2):
+        grads = _draw(params, gen, student_t=True)
+        _step_and_check(gpu, params, ora, oparams, grads, ortho, worst, f'step {step}')
+        del grads
+    _log(f'[gpu]   config 5: {worst}')
+    assert math.isfinite(worst['dp'])

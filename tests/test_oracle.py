@@ -161,7 +161,10 @@ def test_cautious_weight_decay_closed_form():
 def _run_oracle(build, steps, snap):
     torch.manual_seed(0)
     params, groups, grads = build()
-    opt = O.OracleTHORN(groups)
+    if isinstance(groups, dict):   # the nn.Module overload
+        opt = O.OracleTHORN(groups['module'], **groups['kwargs'])
+    else:
+        opt = O.OracleTHORN(groups)
     got = {}
     for s in range(1, steps + 1):
         for i, p in enumerate(params):
@@ -181,7 +184,9 @@ def _run_oracle(build, steps, snap):
                                                    ('traj_magma.npz', workloads.magma_small, 20, 10),
                                                    ('traj_magma_md.npz', workloads.magma_md_small, 20, 10),
                                                    ('traj_sparse.npz', workloads.sparse_small, 12, 4),
-                                                   ('traj_magma_sparse.npz', workloads.magma_sparse_small, 12, 4)])
+                                                   ('traj_magma_sparse.npz', workloads.magma_sparse_small, 12, 4),
+                                                   ('traj_md_adam.npz', workloads.md_adam_small, 20, 10),
+                                                   ('traj_md_module.npz', workloads.md_module, 10, 5)])
 def test_trajectories_match_reference(name, build, steps, snap):
     z = np.load(GOLD / name)
     got = _run_oracle(build, steps, snap)

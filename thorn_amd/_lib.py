@@ -24,6 +24,8 @@ THORN_ERR_UNSUPPORTED = 3
 MAT_PER_ROW_NORM = 1
 MAT_MD = 2
 MAT_MD_SCALAR = 4
+MAT_ADAM = 8
+MAT_NORM_ROWS = 16
 STEP_KEEP_GRAD = 8
 STEP_APPLY = 16
 
@@ -42,6 +44,10 @@ ORTHO_MAT_STEP = np.dtype([
     ('gain_bc1', np.float32), ('gain_bc2', np.float32),
     ('step_flags', np.int32), ('reserved', np.int32),
     ('magma_s', np.uint64),
+    ('v', np.uint64),
+    ('adam_beta2', np.float32), ('adam_w1', np.float32), ('adam_w2', np.float32),
+    ('adam_bc1', np.float32), ('adam_bc2', np.float32), ('adam_eps', np.float32),
+    ('adam_degenerate', np.int32), ('reserved2', np.int32),
 ], align=True)
 ADAM_TENSOR_STEP = np.dtype([
     ('p', np.uint64), ('g', np.uint64), ('m', np.uint64), ('v', np.uint64),

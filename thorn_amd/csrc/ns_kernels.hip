@@ -46,11 +46,13 @@ __device__ __forceinline__ Operand square_operand(const _Float16* p, const Ortho
 // First iterate, exact form (thorn.py:632-635): xb = f16(u / (||u||_F + 1e-8)) with
 // u = g + beta1 * m recomputed from the gradient (times the decouple_md gains: ortho_pre_kernel
 // writes g back for those matrices, as the reference's g.mul_ does) and the updated moment, the
-// same fmaf as ortho_pre_kernel. It runs for matrices on the exact path, and for prescaled ones
-// whose stored iterate is out of range after a gradient-scale jump (kScalRepair). Grid: x strides
+// same fmaf as ortho_pre_kernel. It runs for the matrices applied this step on the exact path, and
+// for prescaled ones whose stored iterate is out of range after a gradient-scale jump
+// (kScalRepair). Grid: x strides
 // over the 16 x 256 tiles of matrix blockIdx.y; a matrix that needs neither returns at once.
 __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restrict__ mats) {
     const OrthoMat& M = mats[blockIdx.y];
+    if ((M.flags & (kFlagAdam | kFlagApply)) != kFlagApply) return;   // no Newton-Schulz this step
     if ((M.flags & kFlagPrescaled) && M.scal[kScalRepair] == 0.f) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntiles = M.mom_tiles_r * M.mom_tiles_c;

@@ -36,7 +36,8 @@ struct MatLayout {
     int32_t rows, cols, s, l, ldx, lds, tall, flags;
     int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
     size_t xa, xb, gram, zbuf, qa, qb, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
-    size_t magpart;
+    size_t magpart, rowpsq;
+    bool adam, norm_rows;   // THORN_MAT_ADAM, THORN_MAT_NORM_ROWS
 };
 
 struct TaskOffsets {
@@ -120,12 +121,12 @@ struct thorn_ortho_plan {
     size_t mats_off = 0;
     // Newton-Schulz task lists per matrix set: [0] square matrices (plain quintic), [1] the others
     // (Gram Newton-Schulz); sym = upper-triangle tiles of s x s products, g3 = tiles of X updates.
-    TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, md{};
-    std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, md_order;
+    TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, md{}, adam{};
+    std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, md_order, adam_order;
     // The Newton-Schulz and per-row-normalization lists of the last filled table: only the
     // matrices applied this step (the reference skips the polar factor of the others,
     // thorn.py:1395-1396, 1436-1441). Same table offsets, fewer entries.
-    TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{};
+    TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{}, adam_live{};
     // mean short and long side of each set's matrices: the contraction lengths of its GEMM tiles
     // (long side: Gram matrices; short side: the other products), to run longer tiles first
     double mean_s[2]{}, mean_l[2]{};
@@ -137,6 +138,7 @@ struct thorn_ortho_plan {
     const void* stepped_ws = nullptr;  // workspace of the last completed thorn_ortho_step
     bool any_exact = true;             // the last filled table has matrices on the exact path
     bool any_apply = true;             // the last filled table has matrices flagged THORN_STEP_APPLY
+    bool any_adam_apply = true;        // ... among its THORN_MAT_ADAM ones
 };
 
 struct thorn_adam_plan {
@@ -352,6 +354,15 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
             delete plan;
             return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: MD and MD_SCALAR are exclusive");
         }
+        if ((d.flags & THORN_MAT_ADAM) &&
+            (!(d.flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) || (d.flags & THORN_MAT_PER_ROW_NORM))) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: ADAM needs MD or MD_SCALAR and no PER_ROW_NORM");
+        }
+        if ((d.flags & THORN_MAT_NORM_ROWS) && !(d.flags & THORN_MAT_ADAM)) {
+            delete plan;
+            return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: NORM_ROWS needs ADAM");
+        }
         MatLayout L{};
         L.rows = static_cast<int32_t>(d.rows);
         L.cols = static_cast<int32_t>(d.cols);
@@ -361,6 +372,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.ldx = static_cast<int32_t>(align_up(L.cols, 8));
         L.lds = static_cast<int32_t>(align_up(L.s, 8));
         L.flags = d.flags & (THORN_MAT_PER_ROW_NORM | THORN_MAT_MD | THORN_MAT_MD_SCALAR);
+        L.adam = (d.flags & THORN_MAT_ADAM) != 0;
+        L.norm_rows = (d.flags & THORN_MAT_NORM_ROWS) != 0;
         L.mom_tiles_r = static_cast<int32_t>(cdiv(L.rows, thorn::kTileR));
         L.mom_tiles_c = static_cast<int32_t>(cdiv(L.cols, thorn::kTileC));
         L.g3_tiles_m = static_cast<int32_t>(cdiv(L.rows, NsCfg::BM));
@@ -370,9 +383,10 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         const bool pnn = L.flags & THORN_MAT_PER_ROW_NORM;
         const bool md = L.flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR);
         const int64_t mom_tiles = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
-        L.n_psq = md ? static_cast<int32_t>(pnn ? mom_tiles : int64_t(L.g3_tiles_m) * L.g3_tiles_n) : 0;
-        const size_t xbytes = size_t(L.rows) * L.ldx * 2;
-        const size_t sbytes = size_t(L.s) * L.lds * 2;
+        L.n_psq = md ? static_cast<int32_t>(pnn || L.adam ? mom_tiles : int64_t(L.g3_tiles_m) * L.g3_tiles_n) : 0;
+        // an Adam-group tensor runs no Newton-Schulz: no iterate or s x s buffers
+        const size_t xbytes = L.adam ? 0 : size_t(L.rows) * L.ldx * 2;
+        const size_t sbytes = L.adam ? 0 : size_t(L.s) * L.lds * 2;
         const bool square = L.rows == L.cols;   // the plain quintic needs no Q (thorn.py:654-658)
         L.xa = take(xbytes);
         L.xb = take(xbytes);
@@ -380,11 +394,12 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.zbuf = take(sbytes);
         L.qa = square ? kNone : take(sbytes);
         L.qb = square ? kNone : take(sbytes);
+        L.rowpsq = L.norm_rows ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
         L.normpart = take(sizeof(float) * mom_tiles);
         L.rowpart = md ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
         L.colpart = (L.flags & THORN_MAT_MD) ? take(sizeof(float) * size_t(L.mom_tiles_r) * L.cols) : kNone;
         L.rowsqpart = pnn ? take(sizeof(float) * size_t(L.g3_tiles_n) * L.rows) : kNone;
-        L.rowscale = pnn ? take(sizeof(float) * L.rows) : kNone;
+        L.rowscale = pnn || L.norm_rows ? take(sizeof(float) * L.rows) : kNone;
         L.scal = take(sizeof(float) * 8);
         L.psqpart = md ? take(sizeof(float) * L.n_psq) : kNone;
         L.magpart = take(sizeof(float4) * mom_tiles);
@@ -413,7 +428,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     // Gram Newton-Schulz for every non-square matrix, the plain quintic for square ones
     // (thorn.py:628, 637-658).
     std::vector<int32_t> sets[2];
-    for (int i = 0; i < n; ++i) sets[plan->mats[i].rows != plan->mats[i].cols ? 1 : 0].push_back(i);
+    for (int i = 0; i < n; ++i)
+        if (!plan->mats[i].adam) sets[plan->mats[i].rows != plan->mats[i].cols ? 1 : 0].push_back(i);
     for (int q = 0; q < 2; ++q) {
         for (int i : sets[q]) {
             plan->mean_s[q] += plan->mats[i].s;
@@ -433,6 +449,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     for (int i = 0; i < n; ++i) {
         if (plan->mats[i].flags & THORN_MAT_PER_ROW_NORM) plan->pnn_order.push_back(i);
         if (plan->mats[i].flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
+        if (plan->mats[i].adam) plan->adam_order.push_back(i);
     }
     std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n);
     for (int i = 0; i < n; ++i) {
@@ -456,6 +473,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     }
     plan->pnn = add_tasks(off, plan->pnn_order, mom_blocks);
     plan->md = add_tasks(off, plan->md_order, mom_blocks);
+    plan->adam = add_tasks(off, plan->adam_order, mom_blocks);
     plan->table_bytes = off;
     if (int64_t(plan->sym[0].total) + plan->sym[1].total + plan->g3[0].total + plan->g3[1].total >=
         (int64_t(1) << 31) - 1) {
@@ -491,14 +509,15 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     std::memset(host, 0, plan->table_bytes);
     char* ws = static_cast<char*>(workspace);
     auto at = [ws](size_t o) -> void* { return o == kNone ? nullptr : ws + o; };
-    bool any_exact = false, any_apply = false;
+    bool any_exact = false, any_apply = false, any_adam_apply = false;
     auto* mats = reinterpret_cast<thorn::OrthoMat*>(host + plan->mats_off);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
         const ThornOrthoMatStep& S = steps[i];
         const bool md = L.flags & THORN_MAT_MD, mds = L.flags & THORN_MAT_MD_SCALAR;
-        if (!S.p || !S.g || !S.m)
-            return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: matrix " + std::to_string(i) + " has a null p/g/m");
+        if (!S.p || !S.g || !S.m || (L.adam && !S.v))
+            return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: matrix " + std::to_string(i) +
+                                               " has a null p/g/m (or v)");
         if ((md && (!S.row_gain || !S.col_gain || !S.row_gain_moment || !S.row_gain_variance ||
                     !S.col_gain_moment || !S.col_gain_variance || !S.target_norm)) ||
             (mds && (!S.row_gain || !S.row_gain_moment || !S.row_gain_variance || !S.target_norm)))
@@ -527,6 +546,10 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.scal = static_cast<float*>(at(L.scal));
         M.psqpart = static_cast<float*>(at(L.psqpart));
         M.magpart = static_cast<float4*>(at(L.magpart));
+        M.rowpsq = static_cast<float*>(at(L.rowpsq));
+        M.v = S.v;
+        M.adam_beta2 = S.adam_beta2; M.adam_w1 = S.adam_w1; M.adam_w2 = S.adam_w2;
+        M.adam_bc1 = S.adam_bc1; M.adam_bc2 = S.adam_bc2; M.adam_eps = S.adam_eps;
         M.magma_s = S.magma_s;
         M.magma_n = 0;
         if (S.magma_s && (i == 0 || steps[i - 1].magma_s != S.magma_s)) {   // first matrix of a parameter
@@ -543,20 +566,24 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.rows = L.rows; M.cols = L.cols; M.s = L.s; M.l = L.l;
         M.ldx = L.ldx; M.lds = L.lds; M.tall = L.tall;
         int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
-        if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m)) flags |= thorn::kFlagVec4;
+        if (L.adam) flags |= thorn::kFlagAdam | (S.adam_degenerate ? thorn::kFlagAdamDegen : 0);
+        if (L.norm_rows) flags |= thorn::kFlagNormRows;
+        if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m) && (!L.adam || aligned16(S.v)))
+            flags |= thorn::kFlagVec4;
         // The first iterate of a large matrix is written directly in f16 with the previous step's
         // power-of-two scale (one pass less over u); small matrices, whose Newton-Schulz rounding
         // is not averaged out, and decouple_md ones take the exact form of thorn.py:632-635.
         if (workspace == plan->stepped_ws && !md && !mds && int64_t(L.rows) * L.cols >= kPrescaleMinElems)
             flags |= thorn::kFlagPrescaled;
-        else any_exact = true;
+        else if (!L.adam) any_exact = true;
         if (S.magma_s) {
             if (reinterpret_cast<uintptr_t>(S.magma_s) & 3u)
                 return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: magma_s must be 4-byte aligned");
             flags |= thorn::kFlagMagma;
         }
         M.flags = flags;
-        any_apply = any_apply || (flags & thorn::kFlagApply);
+        if (L.adam) any_adam_apply = any_adam_apply || (flags & thorn::kFlagApply);
+        else any_apply = any_apply || (flags & thorn::kFlagApply);
         M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
         M.gain_lr = S.gain_lr; M.gain_beta2 = S.gain_beta2; M.gain_w1 = S.gain_w1; M.gain_w2 = S.gain_w2;
         M.gain_eps = S.gain_eps; M.gain_bc1 = S.gain_bc1; M.gain_bc2 = S.gain_bc2;
@@ -593,10 +620,12 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         applied_only(plan->g3_order[q], plan->g3[q], g3_blocks, plan->g3_live[q]);
     }
     applied_only(plan->pnn_order, plan->pnn, mom_blocks, plan->pnn_live);
+    applied_only(plan->adam_order, plan->adam, mom_blocks, plan->adam_live);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
     plan->any_exact = any_exact;
     plan->any_apply = any_apply;
+    plan->any_adam_apply = any_adam_apply;
     return THORN_OK;
 }
 
@@ -625,9 +654,18 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel,
                  dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n);
-    if (iters == 0) {   // momentum only (no update is due): the decouple_md round trip and done
-        if (plan->md.n > 0) {   // p *= softplus(gains), the gains unchanged
+    if (plan->adam_live.n > 0) {   // the Adam step of the decouple_md tensors of an Adam group
+        const thorn::TaskList ad = task_list(dev, plan->adam_live);
+        THORN_LAUNCH(THORN_KIND_ADAM, "ortho_adam_apply_kernel", thorn::ortho_adam_apply_kernel, dim3(ad.total),
+                     dim3(256), 0, st, mats, ad);
+    }
+    if (iters == 0) {   // no Newton-Schulz update is due: the decouple_md tail and done
+        if (plan->md.n > 0) {   // p *= target / ||p|| where applied, then p *= softplus(gains)
             const thorn::TaskList md = task_list(dev, plan->md);
+            if (plan->any_adam_apply) {
+                THORN_LAUNCH(THORN_KIND_MD_FACTOR, "ortho_md_factor_kernel", thorn::ortho_md_factor_kernel,
+                             dim3(md.n), dim3(256), 0, st, mats, md.order);
+            }
             THORN_LAUNCH(THORN_KIND_MD_RESCALE, "ortho_md_rescale_kernel", thorn::ortho_md_rescale_kernel,
                          dim3(md.total), dim3(256), 0, st, mats, md);
         }

@@ -185,6 +185,9 @@ enum OrthoFlags : int32_t {
     kFlagVec4 = 32,      // p, g, m 16-byte aligned and cols % 4 == 0: float4 path
     kFlagPrescaled = 64, // first iterate written in f16 as u * 2^k, 2^k from the previous step
     kFlagMagma = 128,    // Magma: statistics into magpart, eta scaled by *magma_s
+    kFlagAdam = 256,     // decouple_md tensor of an Adam group: Adam step instead of Newton-Schulz
+    kFlagNormRows = 512, // kFlagAdam: renormalize per row (norm_axis = -1)
+    kFlagAdamDegen = 1024, // kFlagAdam: rectification says rho <= 4, u = m
 };
 
 // One matrix of an orthogonalized group. All user tensors are fp32, row-major rows x cols,
@@ -235,6 +238,10 @@ struct OrthoMat {
     int32_t magma_n;       // Magma: matrices of the parameter when this is its first one, else 0
     int32_t gain_n;        // scalar decouple_md gain: matrices of the parameter when this is its
                            // first one, else 0 (one gain for the whole parameter, thorn.py:1609-1612)
+    // kFlagAdam: state['variance'] and the Adam scalars (lr is eta, wd is wd)
+    float* v;
+    float* rowpsq;    // kFlagNormRows: [mom_tiles_c][rows] partial row sums of p^2 after the update
+    float adam_beta2, adam_w1, adam_w2, adam_bc1, adam_bc2, adam_eps;
 };
 
 enum ScalSlot : int {

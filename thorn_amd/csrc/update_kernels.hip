@@ -24,6 +24,9 @@ __device__ __forceinline__ int tile_col(int c0, int lane, int e, bool vec) {
 //   m = m * beta1 + g;  u = g + beta1 * m;  normpart += u^2;  prescaled: xb = f16(u * 2^k)
 // With decouple_md, g * G is written back into the gradient (the reference's in-place g.mul_,
 // thorn.py:907), which ortho_cast_kernel then reads to rebuild u.
+// kFlagAdam (a decouple_md tensor of an Adam group, thorn.py:1702-1711): the Magma statistics use
+// the gradient before the gains (the mask comes first there), and the moments take the Adam step,
+// m = lerp(m, g, 1 - beta1), v = beta2 v + (1 - beta2) g^2; ortho_adam_apply_kernel moves p.
 __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
     __shared__ float colred[4][kTileC];
     __shared__ float scratch[12];
@@ -41,6 +44,8 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const float prescale = presc ? M.scal[kScalPrescale] : 1.f;
     const float beta1 = M.beta1;
     const int nrows = M.rows - r0;   // rows of this wave's 4 that exist (may be <= 0)
+    const bool adam = M.flags & kFlagAdam;
+    const float a_w1 = M.adam_w1, a_beta2 = M.adam_beta2, a_w2 = M.adam_w2;
 
     float spc[4] = {1.f, 1.f, 1.f, 1.f};
     bool cok[4];
@@ -53,12 +58,12 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const float sp_scalar = mds ? softplus_f(M.rg[0]) : 1.f;
 
     // all loads of the wave's 4 rows first, so they are in flight together
-    float gv[4][4], mv[4][4], pv[4][4];
+    float gv[4][4], mv[4][4], pv[4][4], vv[4][4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         const int64_t rbase = (int64_t)(r0 + rr) * M.cols;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) gv[rr][e] = mv[rr][e] = pv[rr][e] = 0.f;
+        for (int e = 0; e < 4; ++e) gv[rr][e] = mv[rr][e] = pv[rr][e] = vv[rr][e] = 0.f;
         if (rr >= nrows) continue;
         if (vec) {
             if (cok[0]) {
@@ -70,6 +75,10 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                     const float4 p4 = ldg_nt<float4>(M.p + rbase + c);
                     pv[rr][0] = p4.x; pv[rr][1] = p4.y; pv[rr][2] = p4.z; pv[rr][3] = p4.w;
                 }
+                if (adam) {
+                    const float4 v4 = ldg_nt<float4>(M.v + rbase + c);
+                    vv[rr][0] = v4.x; vv[rr][1] = v4.y; vv[rr][2] = v4.z; vv[rr][3] = v4.w;
+                }
             }
         } else {
 #pragma unroll
@@ -79,6 +88,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                 gv[rr][e] = ldg<float>(M.g + rbase + c);
                 mv[rr][e] = ldg<float>(M.m + rbase + c);
                 if (md || mds) pv[rr][e] = ldg<float>(M.p + rbase + c);
+                if (adam) vv[rr][e] = ldg<float>(M.v + rbase + c);
             }
         }
     }
@@ -98,6 +108,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
         for (int e = 0; e < 4; ++e) {
             if (!cok[e]) { xv[e] = 0.f; continue; }
             float g = gv[rr][e];
+            if (adam && magma) ms.add(g, mv[rr][e]);   // thorn.py:1702, before the gains
             if (md || mds) {
                 const float G = md ? spr * spc[e] : sp_scalar;
                 const float p = pv[rr][e] / G;
@@ -107,6 +118,12 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                 gv[rr][e] = g;
                 rowacc += md ? pg * spc[e] : pg;
                 colacc[e] += pg * spr;
+            }
+            if (adam) {   // thorn.py:876-877
+                mv[rr][e] = lerp_torch(mv[rr][e], g, a_w1);
+                vv[rr][e] = vv[rr][e] * a_beta2 + a_w2 * g * g;
+                xv[e] = 0.f;
+                continue;
             }
             if (magma) ms.add(g, mv[rr][e]);
             const float m = mv[rr][e] * beta1 + g;
@@ -130,6 +147,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                     stg_nt<float4>(M.p + rbase + c, make_float4(pv[rr][0], pv[rr][1], pv[rr][2], pv[rr][3]));
                     stg<float4>(M.g + rbase + c, make_float4(gv[rr][0], gv[rr][1], gv[rr][2], gv[rr][3]));
                 }
+                if (adam) stg_nt<float4>(M.v + rbase + c, make_float4(vv[rr][0], vv[rr][1], vv[rr][2], vv[rr][3]));
                 if (presc)
                     stg<half4>(hrow + c, half4{(_Float16)(xv[0] * prescale), (_Float16)(xv[1] * prescale),
                                                (_Float16)(xv[2] * prescale), (_Float16)(xv[3] * prescale)});
@@ -144,6 +162,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
                     stg_nt<float>(M.p + rbase + c, pv[rr][e]);
                     stg<float>(M.g + rbase + c, gv[rr][e]);
                 }
+                if (adam) stg_nt<float>(M.v + rbase + c, vv[rr][e]);
                 if (presc) hrow[c] = (_Float16)(xv[e] * prescale);
             }
         }
@@ -381,13 +400,76 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
 }
 
 // ---------------------------------------------------------------------------------------------
-// decouple_md tail (thorn.py:1414-1421, 969-977): p *= target / (||p||_F + 1e-8), then
-// p *= softplus(rg_i), p *= softplus(cg_j) with the gains already updated.
+// Adam step of the decouple_md tensors of an Adam group (thorn.py:1704-1714, 878-888), after
+// ortho_pre_kernel moved m and v and ortho_norm_kernel moved Magma's s: p <- p - lr * cwd(u) with
+// u = atan2(m bc1, sqrt(v bc2)) (eps = 0), m bc1 / (sqrt(v bc2) + eps), or m when degenerate;
+// p^2 partials for the renormalization (per tile, or per row and column tile with kFlagNormRows).
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ortho_adam_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl) {
+    __shared__ float scratch[4];
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    const bool rows_norm = M.flags & kFlagNormRows;
+    AdamScalars a;
+    a.lr = (M.flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta;   // thorn.py:1712
+    a.wd = M.wd; a.beta2 = M.adam_beta2; a.w1 = M.adam_w1; a.w2 = M.adam_w2;
+    a.bc1 = M.adam_bc1; a.bc2 = M.adam_bc2; a.eps = M.adam_eps;
+    a.apply = true;
+    a.degenerate = M.flags & kFlagAdamDegen;
+    a.atan2_mode = M.adam_eps == 0.f;
+    float psq = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = r0 + rr;
+        if (row >= M.rows) break;   // uniform over the wave
+        const int64_t rbase = (int64_t)row * M.cols;
+        float rsq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + lane + 64 * e;
+            if (c >= M.cols) continue;
+            float pe = ldg<float>(M.p + rbase + c);
+            const float me = ldg<float>(M.m + rbase + c), ve = ldg<float>(M.v + rbase + c);
+            float u;
+            if (a.degenerate) u = me;
+            else if (a.atan2_mode) u = atan2f(me * a.bc1, sqrtf(ve * a.bc2));
+            else u = (me * a.bc1) / (sqrtf(ve * a.bc2) + a.eps);
+            pe = cautious_step(pe, u, a.lr, a.wd);
+            stg<float>(M.p + rbase + c, pe);
+            rsq += pe * pe;
+        }
+        if (rows_norm) {
+            const float t = wave_sum(rsq);
+            if (lane == 0) M.rowpsq[(int64_t)tc * M.rows + row] = t;
+        }
+        psq += rsq;
+    }
+    const float t = block_sum(psq, scratch);
+    if (threadIdx.x == 0) M.psqpart[local] = t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// decouple_md tail (thorn.py:1414-1421, 1716-1721, 969-977): p *= target / (||p|| + 1e-8), then
+// p *= softplus(rg_i), p *= softplus(cg_j) with the gains already updated. The norm is the
+// matrix's Frobenius norm, or each row's with kFlagNormRows (its factor in rowscale).
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void ortho_md_factor_kernel(const OrthoMat* __restrict__ mats,
                                                               const int32_t* __restrict__ idx) {
     __shared__ float scratch[4];
     const OrthoMat& M = mats[idx[blockIdx.x]];
+    if (M.flags & kFlagNormRows) {
+        for (int r = threadIdx.x; r < M.rows; r += 256) {
+            float t = 0.f;
+            for (int c = 0; c < M.mom_tiles_c; ++c) t += M.rowpsq[(int64_t)c * M.rows + r];
+            M.rowscale[r] = M.target[r] / (sqrtf(t) + 1e-8f);
+        }
+        return;
+    }
     float s = 0.f;
     for (int t = threadIdx.x; t < M.n_psq; t += 256) s += M.psqpart[t];
     s = block_sum(s, scratch);
@@ -405,6 +487,7 @@ __global__ __launch_bounds__(256) void ortho_md_rescale_kernel(const OrthoMat* _
     const bool md = M.flags & kFlagMD;
     const bool apply = M.flags & kFlagApply;
     const bool vec = M.flags & kFlagVec4;
+    const bool rows_norm = M.flags & kFlagNormRows;
     const float f = M.scal[kScalMDFactor];
     float spc[4];
     bool cok[4];
@@ -441,10 +524,11 @@ __global__ __launch_bounds__(256) void ortho_md_rescale_kernel(const OrthoMat* _
         const int row = r0 + rr;
         const float spr = md ? softplus_f(M.rg[row]) : sp_scalar;
         const int64_t rbase = (int64_t)row * M.cols;
+        const float fr = rows_norm ? M.rowscale[row] : f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float p = pv[rr][e];
-            if (apply) p = p * f;
+            if (apply) p = p * fr;
             p = p * spr;
             if (md) p = p * spc[e];
             pv[rr][e] = p;

@@ -11,9 +11,12 @@ the random mask comes from the per-parameter PRNG state, a host integer as in th
 the cosine-similarity EMA ``s`` stays on the device, where the kernels read it as a learning-rate
 factor.
 
+``decouple_md`` runs on orthogonalized and non-orthogonalized groups alike: the tensors of an Adam
+group with it take the Adam step inside the same gain round trip as the matrices (thorn.py:1704-1721).
+
 Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
-behaviour): DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), ``decouple_md`` on
-non-orthogonalized groups or with sparse gradients, and non-fp32 parameters.
+behaviour): DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), a ``decouple_md`` norm axis
+other than the last two dims or the last dim, and non-fp32 parameters.
 """
 from __future__ import annotations
 
@@ -227,21 +230,48 @@ def _check_tensor(t: torch.Tensor, what: str) -> None:
         raise NotImplementedError(f'THORN on MI355X needs contiguous tensors; {what} is not')
 
 
-class _OrthoRunner:
-    """One orthogonalized parameter set: plan, workspace and the per-step table."""
+def _matrix_view(p: torch.Tensor) -> tuple:
+    """(rows, cols, batch): a parameter as a batch of rows x cols matrices over its last two dims
+    (thorn.py:629, 707, 777); a vector or scalar is one 1 x n matrix."""
+    if p.ndim >= 2:
+        return p.shape[-2], p.shape[-1], math.prod(p.shape[:-2])
+    return 1, max(1, p.numel()), 1
 
-    def __init__(self, params: list, group: _Group, device: torch.device):
+
+def _md_norm_rows(p: torch.Tensor, group: _Group) -> bool:
+    """decouple_md renormalization axis of a non-orthogonalized tensor (thorn.py:594-595, 1717):
+    False for a norm over each trailing matrix (the default; a vector's whole length), True for a
+    norm over each row (norm_axis = -1 on ndim >= 2). Other axes are not implemented."""
+    ax = group.norm_axis_(p)
+    nd = max(p.ndim, 1)
+    dims = sorted({(a % nd) for a in (ax if isinstance(ax, (tuple, list)) else (ax,))})
+    if p.ndim <= 1 or dims == [nd - 2, nd - 1]:
+        return False
+    if dims == [nd - 1]:
+        return True
+    raise NotImplementedError(f'decouple_md with norm_axis={ax!r} on a {p.ndim}-d tensor is not implemented '
+                              'on the MI355X path (supported: the last two dims, or the last dim)')
+
+
+class _OrthoRunner:
+    """One orthogonalized parameter set (or, with adam=True, the decouple_md tensors of a
+    non-orthogonalized group, whose update is the Adam step): plan, workspace and the per-step
+    table."""
+
+    def __init__(self, params: list, group: _Group, device: torch.device, adam: bool = False):
         self.params = params
         self.device = device
+        self.adam = adam
         rows, cols, flags, owner, sub = [], [], [], [], []
         for i, p in enumerate(params):
-            r, c = p.shape[-2], p.shape[-1]
-            batch = math.prod(p.shape[:-2])
+            r, c, batch = _matrix_view(p)
             f = 0
-            if _needs_neuron_norm(p.shape, group):
+            if adam:
+                f |= _lib.MAT_ADAM | (_lib.MAT_NORM_ROWS if _md_norm_rows(p, group) else 0)
+            elif _needs_neuron_norm(p.shape, group):
                 f |= _lib.MAT_PER_ROW_NORM
             if group.decouple_md:
-                f |= _lib.MAT_MD if group.split_gain else _lib.MAT_MD_SCALAR
+                f |= _lib.MAT_MD if (group.split_gain and p.ndim > 1) else _lib.MAT_MD_SCALAR
             for b in range(batch):
                 rows.append(r)
                 cols.append(c)
@@ -256,15 +286,13 @@ class _OrthoRunner:
         self.workspace = torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
-        self.scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)
         self.md = group.decouple_md
-        self.split_gain = group.split_gain
 
     def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None) -> None:
         """unmasked: id(p) -> False for a parameter whose Magma mask skips this step."""
         params, steps = self.params, self.steps
         n = len(self.owner)
-        elem = np.asarray([p.shape[-2] * p.shape[-1] for p in params], dtype=np.int64)[self.owner]
+        elem = (self.rows * self.cols).astype(np.int64)
         bytes_off = self.sub * elem * 4
         own = self.owner
         p_ptr = np.asarray([p.data_ptr() for p in params], dtype=np.uint64)[own]
@@ -274,7 +302,25 @@ class _OrthoRunner:
         steps['p'] = p_ptr + bytes_off.astype(np.uint64)
         steps['g'] = g_ptr + bytes_off.astype(np.uint64)
         steps['m'] = m_ptr + bytes_off.astype(np.uint64)
-        steps['eta'] = (group.lr * self.scale)[own]
+        if self.adam:   # thorn.py:1704-1714: lr * rect, the Adam moments' scalars
+            beta1, beta2 = group.betas
+            st = np.asarray([s['step'] for s in states], dtype=np.float64)
+            rect = np.asarray([_compute_rect(group, s['step']) for s in states], dtype=np.float64)
+            steps['eta'] = (group.lr * rect)[own]
+            steps['v'] = (np.asarray([s['variance'].data_ptr() for s in states], dtype=np.uint64)[own]
+                          + bytes_off.astype(np.uint64))
+            steps['adam_beta2'] = beta2
+            steps['adam_w1'] = 1 - beta1
+            steps['adam_w2'] = 1 - beta2
+            steps['adam_bc1'] = (1 / (1 - beta1 ** st))[own]
+            steps['adam_bc2'] = (1 / (1 - beta2 ** st))[own]
+            steps['adam_eps'] = group.eps
+            steps['adam_degenerate'] = (rect == 0.0).astype(np.int32)[own]
+        else:
+            # the group is rebuilt every step, so scaling_mode and target_rms edits take effect as
+            # in the reference (thorn.py:1405)
+            scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)
+            steps['eta'] = (group.lr * scale)[own]
         steps['weight_decay'] = group.weight_decay
         steps['beta1'] = group.betas[0]
         # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
@@ -300,31 +346,34 @@ class _OrthoRunner:
             cols = self.cols
             sub = self.sub
 
+            # row/column gains, or one scalar gain for vectors and split_gain=False (thorn.py:1603-1612)
+            split = np.asarray(['row_gain' in s for s in states], dtype=bool)[own]
+
             def ptrs(key, per):
-                base = np.asarray([s[key].data_ptr() for s in states], dtype=np.uint64)[own]
+                base = np.asarray([s[key].data_ptr() if key in s else 0 for s in states], dtype=np.uint64)[own]
                 return base + (sub * per * 4).astype(np.uint64)
 
-            if self.split_gain:
-                steps['row_gain'] = ptrs('row_gain', rows)
-                steps['row_gain_moment'] = ptrs('row_gain_moment', rows)
-                steps['row_gain_variance'] = ptrs('row_gain_variance', rows)
-                steps['col_gain'] = ptrs('col_gain', cols)
-                steps['col_gain_moment'] = ptrs('col_gain_moment', cols)
-                steps['col_gain_variance'] = ptrs('col_gain_variance', cols)
-            else:
-                steps['row_gain'] = ptrs('gain', 0)
-                steps['row_gain_moment'] = ptrs('gain_moment', 0)
-                steps['row_gain_variance'] = ptrs('gain_variance', 0)
+            for name, key, per in (('row_gain', 'row_gain', rows), ('row_gain_moment', 'row_gain_moment', rows),
+                                   ('row_gain_variance', 'row_gain_variance', rows),
+                                   ('col_gain', 'col_gain', cols), ('col_gain_moment', 'col_gain_moment', cols),
+                                   ('col_gain_variance', 'col_gain_variance', cols)):
+                steps[name] = np.where(split, ptrs(key, per), np.uint64(0))
+            for name, key in (('row_gain', 'gain'), ('row_gain_moment', 'gain_moment'),
+                              ('row_gain_variance', 'gain_variance')):
+                steps[name] = np.where(split, steps[name], ptrs(key, 0))
+            # target norm: one value per matrix, or per row of each matrix (norm_axis = -1)
             tn = np.empty(n, dtype=np.uint64)
+            batch = np.bincount(np.asarray(own), minlength=len(params))
             for k, (i, b) in enumerate(zip(own, sub)):
                 t = states[i]['target_norm']
-                tn[k] = t.data_ptr() + (int(b) * 4 if t.numel() > 1 else 0)
+                per = t.numel() // batch[i] if t.numel() > 1 else 0
+                tn[k] = t.data_ptr() + int(b) * per * 4
             steps['target_norm'] = tn
         host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
-        if not due.any():   # no polar factor this step: momentum (gains round trip, Magma s) only
+        if self.adam or not due.any():   # no polar factor this step: momentum (gains, Magma s) only
             coeffs = coeffs[:0]
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
                        torch.cuda.current_stream(self.device).cuda_stream)
@@ -470,15 +519,12 @@ class THORN(Optimizer):
 
     def _validate(self, p: torch.Tensor, group: _Group) -> None:
         g = p.grad
-        if not group.orthogonalize and group.decouple_md:
-            raise NotImplementedError('decouple_md on a non-orthogonalized group is not implemented '
-                                      'on the MI355X path')
+        if group.decouple_md and not group.orthogonalize:
+            _md_norm_rows(p, group)   # raises for an unsupported norm axis
         if g.is_sparse and group.orthogonalize:
             # the reference's momentum step g + beta1 * m (thorn.py:1381) fails the same way
             raise RuntimeError('add(sparse, dense) is not supported: an orthogonalized parameter needs a '
                                'dense gradient')
-        if g.is_sparse and group.decouple_md:
-            raise NotImplementedError('sparse gradients with decouple_md are not implemented on the MI355X path')
         if type(p.data).__name__ == 'DTensor' or type(g).__name__ == 'DTensor':
             raise NotImplementedError('DTensor / FSDP2 parameters are not implemented on the MI355X path')
         if g.shape != p.shape:
@@ -538,11 +584,20 @@ class THORN(Optimizer):
             self._magma_scratch[dev] = w
         return w
 
+    # Runners (plan + workspace) kept per group and device: a new set of live parameters (some
+    # without a gradient this step) builds a new runner, and the least recently used one beyond
+    # this many is dropped with its workspace, so memory stays bounded when the set changes.
+    _RUNNERS_PER_GROUP = 2
+
     def _runner(self, key, factory):
-        r = self._runners.get(key)
+        r = self._runners.pop(key, None)
         if r is None:
+            slot = key[:3]   # (kind, group index, device)
+            same = [k for k in self._runners if k[:3] == slot]
+            for k in same[:max(0, len(same) - self._RUNNERS_PER_GROUP + 1)]:
+                del self._runners[k]
             r = factory()
-            self._runners[key] = r
+        self._runners[key] = r   # most recently used last
         return r
 
     # -- step (thorn.py:1583-1753) ---------------------------------------------------------------
@@ -556,7 +611,7 @@ class THORN(Optimizer):
             self._init_state(p, group)
             g = p.grad
             if g.is_sparse and not group.orthogonalize:
-                if g.sparse_dim() != 1:   # thorn.py:1671-1672
+                if group.decouple_md or g.sparse_dim() != 1:   # thorn.py:1671-1672
                     p.grad = g.to_dense()
                 else:
                     g = g.coalesce()
@@ -587,6 +642,11 @@ class THORN(Optimizer):
                            group.decouple_md, group.split_gain, group.force_per_neuron_norm,
                            group.betas[1] > 0)
                     runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev))
+                    runner.run(self, group, unmasked)
+                elif group.decouple_md:   # Adam step inside the decouple_md round trip (thorn.py:1704-1721)
+                    key = ('mdadam', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
+                           group.split_gain, tuple(_md_norm_rows(p, group) for p in ps))
+                    runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev, adam=True))
                     runner.run(self, group, unmasked)
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
