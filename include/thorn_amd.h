@@ -117,6 +117,10 @@ void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan);
  * in f16, prescaled by a power of two the previous step stored there (rebuilt exactly when the
  * gradient scale moved by more than 16x); the first step on a workspace takes the exact path. */
 size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
+/* The int32 at this byte offset of the workspace is nonzero after a step in which a cluster of
+ * workgroups of the small-matrix Newton-Schulz launch did not all become resident (its bounded
+ * barrier wait expired; that step's small-matrix updates are then not valid). */
+#define THORN_WS_STATUS_OFFSET 256
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);
@@ -211,7 +215,8 @@ enum {
     THORN_KIND_CAST = 10,      /* first iterate: u / ||u|| rounded to f16 */
     THORN_KIND_SYMPROD = 11,   /* Gram Newton-Schulz products a Q + Q Z, a R + R Z, a RZ + Z RZ */
     THORN_KIND_MAGMA = 12,     /* Magma statistics of the Adam tensors */
-    THORN_KIND_COUNT = 13
+    THORN_KIND_SMALL = 13,     /* the whole Newton-Schulz of the small matrices (one launch) */
+    THORN_KIND_COUNT = 14
 };
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
 int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);

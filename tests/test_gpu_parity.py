@@ -34,6 +34,11 @@ def _thorn():
     return thorn_amd
 
 
+def _lib():
+    from thorn_amd import _lib as lib
+    return lib
+
+
 def rel(a, b) -> float:
     a = a.detach().double().cpu()
     b = b.detach().double().cpu()
@@ -111,10 +116,16 @@ def check_ortho_dp(dpg, dpc, dpe, worst: dict, where: str) -> None:
     assert r <= DP_TOL, (where, r, r_ex, ref_ex)
 
 
-def _run_pair(build, steps, teacher_forced):
+def _run_pair(build, steps, teacher_forced, oracle_dev='cpu'):
+    """oracle_dev='cuda' runs the oracle on device copies (its large f16 products on the host CPU
+    would take minutes)."""
     thorn_amd = _thorn()
     torch.manual_seed(0)
     params, groups, grads = build()
+    if oracle_dev != 'cpu':
+        moved = [torch.nn.Parameter(p.detach().clone().to(oracle_dev)) for p in params]
+        groups = _clone_groups(groups, moved)
+        params = moved
     if isinstance(groups, dict):   # the nn.Module overload: the same module on the GPU
         gmod = copy.deepcopy(groups['module']).to(DEV)
         gparams = list(gmod.parameters())
@@ -137,13 +148,13 @@ def _run_pair(build, steps, teacher_forced):
                   for p in params]
         for i, (pc, pg) in enumerate(zip(params, gparams)):
             g = grads(s, i, pc)
-            pc.grad = g.clone()
+            pc.grad = g.clone().to(pc.device)
             pg.grad = g.clone().to(DEV)
         cpu.step()
         gpu.step()
         torch.cuda.synchronize()
         for i, (pc, pg) in enumerate(zip(params, gparams)):
-            dpc = pc.detach() - before_c[i]
+            dpc = (pc.detach() - before_c[i]).cpu()
             dpg = pg.detach().cpu() - before_g[i].cpu()
             r = rel(dpg, dpc)
             grp = group_of[id(pc)]
@@ -157,7 +168,7 @@ def _run_pair(build, steps, teacher_forced):
                 worst['dp'] = max(worst['dp'], r)
                 assert r <= 2e-2, (s, i, r)
             else:
-                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp)
+                dpe = exact_dp(before_c[i].cpu(), grads(s, i, pc).cpu(), m_prev[i].cpu(), grp)
                 check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
             for k, v in cpu.state[pc].items():
                 if torch.is_tensor(v) and k != 'target_norm':
@@ -293,6 +304,10 @@ def test_many_matrices_share_launches():
         dpe = exact_dp(p0[i], grads[i], torch.zeros_like(p0[i]), grp)
         check_ortho_dp(dpg, dpc, dpe, w, f'{sh}')
     _log(f'[gpu]   {w}')
+    # the small-matrix launch's cluster barriers all completed
+    for r in gpu._runners.values():
+        status = r.workspace[_lib().WS_STATUS_OFFSET:_lib().WS_STATUS_OFFSET + 4].view(torch.int32).item()
+        assert status == 0, status
 
 
 def test_ns_against_closed_form():
@@ -398,7 +413,7 @@ def test_gradient_scale_jumps():
             return draws[(s, i)]
         return params, groups, grads
 
-    w = _run_pair(build, len(scales), teacher_forced=False)
+    w = _run_pair(build, len(scales), teacher_forced=False, oracle_dev=DEV)
     _log(f'[gpu]   {w}')
     assert w['state'] <= 1e-5, w
 
@@ -487,7 +502,7 @@ def test_update_rate(name, rate):
                 worst['dp'] = max(worst['dp'], r)
                 assert r <= 2e-2, (s, i, r)
             else:
-                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp)
+                dpe = exact_dp(before_c[i].cpu(), grads(s, i, pc).cpu(), m_prev[i].cpu(), grp)
                 check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
     _log(f'[gpu]   {worst}')
     assert worst['state'] <= 1e-5, worst
@@ -574,7 +589,7 @@ def test_magma(name, rate, monkeypatch):
                 worst['dp'] = max(worst['dp'], r)
                 assert r <= 2e-2, (s, i, r)
             else:
-                dpe = exact_dp(before_c[i], grads(s, i, pc), m_prev[i], grp) * float(cst['s'])
+                dpe = exact_dp(before_c[i].cpu(), grads(s, i, pc).cpu(), m_prev[i].cpu(), grp) * float(cst['s'])
                 check_ortho_dp(dpg, dpc, dpe, worst, f'step {s} param {i} {tuple(pc.shape)}')
     _log(f'[gpu]   {worst}')
     assert worst['masked'] > 0 and worst['applied'] > 0, worst

@@ -7,9 +7,9 @@ Same mathematics as thorn.py:425-514 (Polar Express, arXiv:2505.16932):
   * every iteration but the last is divided by the safety factor (x -> x/(1+eps));
   * the interval then maps to [p(l), 2 - p(l)].
 The Gram restart search simulates scalar Gram Newton-Schulz on a log-spaced singular-value grid
-and picks the restart set with the smallest worst-case dynamic range (thorn.py:482-514). The
-build iterates the plain quintic on the short-side Gram matrix, so the restarts are computed only
-to raise the same ValueError as the reference for settings with no stable schedule.
+and picks the restart set with the smallest worst-case dynamic range (thorn.py:482-514); the
+library runs Gram Newton-Schulz with these restarts on every non-square matrix, and settings with
+no stable schedule raise the reference's ValueError.
 """
 from __future__ import annotations
 

@@ -92,7 +92,8 @@ SIGNATURES = {
     'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
 KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
-         'symprod', 'magma']
+         'symprod', 'magma', 'small']
+WS_STATUS_OFFSET = 256
 ABI_VERSION = 5
 
 _lib = None

@@ -1,0 +1,321 @@
+// Newton-Schulz for small matrices (short side s <= 256): one launch runs the whole schedule of
+// every small matrix of a group (gfx950).
+//
+// The grouped 256 x 256-tile launches of ns_kernels.hip give a small matrix one tile per phase, so
+// its 18 phases cost 18 launch latencies. Here each small matrix gets a cluster of 1024-thread
+// workgroups (one for s <= 128, four for s <= 256) that runs every operation of the schedule in
+// turn, 32 x 32 output tiles dealt to its 16 * C waves, with a barrier between operations. The
+// operands stay in the L2-resident workspace, each s x s result and each iterate also stored
+// transposed, so that every MFMA fragment, of A or of B, is one 16-byte load of a K-contiguous row.
+// Products are computed whole (no mirroring of a symmetric result), and every output is rounded to
+// f16 once from f16(beta C + alpha A B), as the reference's eager baddbmm does (thorn.py:338-343),
+// so on small matrices the iteration tracks the reference's f16 trajectory closely.
+//
+// Workspace of a small matrix (all f16, padded to multiples of 32 with zeros that stay zero):
+//   xw[2], xwt[2]: the iterate in the wide orientation (s_p x l_p) and transposed (l_p x s_p),
+//     two slots; the iterate of a tall parameter is the transpose of its rows (thorn.py:629-630);
+//   sq[4], sqt[4]: R, Z, QA, QB (s_p x s_p) and their transposes.
+// The first iterate comes from xb (the parameter's orientation, written by ortho_cast_kernel);
+// u' goes to xa in the parameter's orientation, with the per-row partial sums of u'^2 that the
+// per-row normalization needs.
+#include "ns_kernels.hip"
+
+namespace thorn {
+
+constexpr int kSmallMaxS = 256;        // short side of the matrices this path takes
+constexpr int kSmallMaxOps = 64;       // operations per schedule
+constexpr int kSmallThreads = 1024;    // 16 waves per workgroup
+constexpr int kSmallWaves = kSmallThreads / 64;
+
+struct SmallOp {
+    int8_t kind;     // kOpGram, kOpSym, kOpUpdate
+    int8_t a, b, c;  // sym: A, B, C buffers (c < 0: none); update: a = Q buffer, c >= 0: + beta X
+    int8_t o, o2;    // sym: output buffer, dual output (Q = out + dual I) or -1
+    int8_t xsel;     // gram, update: iterate slot read (the update writes the other one)
+    int8_t fin;      // update: the last one (writes u')
+    float alpha, beta, dual;
+};
+
+struct SmallSchedule {
+    SmallOp op[2][kSmallMaxOps];   // [0] square matrices (plain quintic), [1] the others (Gram)
+    int32_t n[2];
+};
+
+// Small-matrix buffers inside OrthoMat (see the plan): sq[i] at M.small + i * sqe, their
+// transposes after them, then xw[2], xwt[2]; sizes in elements.
+struct SmallView {
+    _Float16* base;
+    int sp, lp;          // s and l rounded up to 32
+    int64_t sqe, xe;     // elements of an s_p x s_p and of an s_p x l_p buffer
+    __device__ __forceinline__ _Float16* sq(int i) const { return base + i * sqe; }
+    __device__ __forceinline__ _Float16* sqt(int i) const { return base + (4 + i) * sqe; }
+    __device__ __forceinline__ _Float16* xw(int i) const { return base + 8 * sqe + i * xe; }
+    __device__ __forceinline__ _Float16* xwt(int i) const { return base + 8 * sqe + (2 + i) * xe; }
+};
+
+__device__ __forceinline__ SmallView small_view(const OrthoMat& M) {
+    SmallView v;
+    v.base = M.small;
+    v.sp = (M.s + 31) & ~31;
+    v.lp = (M.l + 31) & ~31;
+    v.sqe = int64_t(v.sp) * v.sp;
+    v.xe = int64_t(v.sp) * v.lp;
+    return v;
+}
+
+// Barrier of the C workgroups of one matrix: sense-reversing (count, generation) in the
+// workspace, agent-scope release on arrival and acquire on departure. The wait is bounded: a
+// cluster whose members are not all resident cannot hang the GPU; it sets *err and goes on.
+__device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err) {
+    __syncthreads();
+    if (C > 1 && threadIdx.x == 0) {
+        int* cnt = bar;
+        int* gen = bar + 1;
+        const int g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int a = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (a == C - 1) {
+            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(gen, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            int it = 0;
+            while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++it > (1 << 24)) {
+                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+    }
+    __syncthreads();
+}
+
+// Operand panels in LDS: a super-tile of up to 128 x 128 outputs (up to 16 tiles of 32 x 32, one
+// per wave) is computed from K chunks of 64: rows [M0, M0+SM) of A and [N0, N0+SN) of BT, 64 halves
+// each, loaded by the whole workgroup with 16-byte loads (8 consecutive lanes per 128-byte row)
+// into one of two buffers while the other is consumed. Rows are 72 halves apart (16 bytes of
+// padding spread the fragment reads over the banks).
+constexpr int kPanelK = 64;
+constexpr int kPanelLd = kPanelK + 8;
+constexpr int kPanelRows = 256;                      // A rows then BT rows, 128 each at most
+constexpr int kPanelHalves = kPanelRows * kPanelLd;  // one buffer
+
+// Loads chunk [k0, min(k0+64, K)) of the panels into buffer `buf` (rows past SM / SN and columns
+// past K are not loaded).
+__device__ __forceinline__ void panel_load(_Float16* buf, const _Float16* A, int64_t lda, const _Float16* BT,
+                                           int64_t ldb, int M0, int N0, int SM, int SN, int k0, int K) {
+    const int nch = (SM + SN) * (kPanelK / 8);
+    for (int ch = threadIdx.x; ch < nch; ch += kSmallThreads) {
+        const int r = ch >> 3, c8 = (ch & 7) * 8;
+        if (k0 + c8 >= K) continue;
+        const _Float16* src = r < SM ? A + int64_t(M0 + r) * lda + k0 + c8 : BT + int64_t(N0 + r - SM) * ldb + k0 + c8;
+        const int lr = r < SM ? r : 128 + (r - SM);
+        *reinterpret_cast<half8*>(buf + lr * kPanelLd + c8) = ldg<half8>(src);
+    }
+}
+
+// acc (this wave's tile of the super-tile, if it has one) = A[M0.., 0:K] * B[0:K, N0..] with A
+// row-major (lda) and B given by its transpose BT row-major (ldb), K a multiple of 16 (chunks of
+// 64, the last one possibly shorter: its unused columns are neither loaded nor read). The whole
+// workgroup calls it (barriers inside); `panels` holds two buffers.
+__device__ __forceinline__ floatx16 small_block(_Float16* panels, const _Float16* A, int64_t lda, const _Float16* BT,
+                                                int64_t ldb, int M0, int N0, int SM, int SN, int K, int wave,
+                                                int lane, bool has_tile, int ti, int tj) {
+    floatx16 acc = {};
+    const int nk = (K + kPanelK - 1) / kPanelK;
+    panel_load(panels, A, lda, BT, ldb, M0, N0, SM, SN, 0, K);
+    for (int c = 0; c < nk; ++c) {
+        __syncthreads();   // chunk c is in buffer c & 1; buffer (c + 1) & 1 is free
+        if (c + 1 < nk) panel_load(panels + ((c + 1) & 1) * kPanelHalves, A, lda, BT, ldb, M0, N0, SM, SN,
+                                   (c + 1) * kPanelK, K);
+        if (has_tile) {
+            const _Float16* buf = panels + (c & 1) * kPanelHalves;
+            const _Float16* pa = buf + (32 * ti + (lane & 31)) * kPanelLd + 8 * (lane >> 5);
+            const _Float16* pb = buf + (128 + 32 * tj + (lane & 31)) * kPanelLd + 8 * (lane >> 5);
+            const int kc = min(kPanelK, K - c * kPanelK);
+            for (int k = 0; k < kc; k += 16) {
+                const half8 a = *reinterpret_cast<const half8*>(pa + k);
+                const half8 b = *reinterpret_cast<const half8*>(pb + k);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();   // every wave is done with the panels
+    return acc;
+}
+
+// The wave's 32 x 32 f16 staging tile: row-major, rows of 34 halves.
+constexpr int kStageLd = 34;
+
+// Lanes of one wave hand values to each other through the staging tile: every LDS access before
+// this point is complete, and (a compiler memory barrier) none is moved across it or served from
+// a value loaded before it. Without it the compiler may reuse a value it already loaded, since a
+// write by another lane is not visible to a single thread's program order.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Stages f16(alpha * acc + beta * C) of tile (m0, n0); C is read through its transpose CT
+// (4 contiguous halves per load).
+__device__ __forceinline__ void small_stage(const floatx16& acc, _Float16* stage, float alpha, float beta,
+                                            const _Float16* CT, int64_t ldc, int m0, int n0, int lane) {
+    const int j = lane & 31;
+    wave_lds_sync();   // the previous tile's reads of the staging are done
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int i0 = 8 * g + 4 * (lane >> 5);
+        float cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (CT) {
+            const half4 c4 = ldg<half4>(CT + int64_t(n0 + j) * ldc + m0 + i0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[e] = static_cast<float>(c4[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = alpha * acc[4 * g + e];
+            if (CT) t += beta * cv[e];
+            stage[(i0 + e) * kStageLd + j] = static_cast<_Float16>(t);
+        }
+    }
+    wave_lds_sync();   // the whole tile is staged before any lane reads it
+}
+
+// Stores the staged tile to out (row-major, ld) at (m0, n0) and its transpose to outT (ldt) at
+// (n0, m0): 16-byte chunks, 2 + 2 per lane. Tiles lie inside the padded buffers.
+__device__ __forceinline__ void small_store(const _Float16* stage, _Float16* out, int64_t ld, _Float16* outT,
+                                            int64_t ldt, int m0, int n0, int lane) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int ch = lane + 64 * q, r = ch >> 2, c8 = (ch & 3) * 8;
+        half8 h, t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h[e] = stage[r * kStageLd + c8 + e];
+            t[e] = stage[(c8 + e) * kStageLd + r];
+        }
+        stg<half8>(out + int64_t(m0 + r) * ld + n0 + c8, h);
+        stg<half8>(outT + int64_t(n0 + r) * ldt + m0 + c8, t);
+    }
+}
+
+// u' (f16) in the parameter's orientation into xa, from the staged tile (m0, n0) of the wide
+// iterate (s_p x l_p); per-row partial sums of u'^2 into rowsqpart[tile column][row] for
+// per-row-normalized matrices. Element (i, j) of the wide iterate is parameter element (i, j)
+// (wide or square) or (j, i) (tall).
+__device__ __forceinline__ void small_store_final(const _Float16* stage, const OrthoMat& M, int m0, int n0, int lane) {
+    const bool tall = M.tall;
+    const int prow0 = tall ? n0 : m0, pcol0 = tall ? m0 : n0;   // the tile in the parameter's orientation
+    auto at = [&](int pr, int pc) { return tall ? stage[pc * kStageLd + pr] : stage[pr * kStageLd + pc]; };
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int ch = lane + 64 * q, r = ch >> 2, c8 = (ch & 3) * 8;
+        if (prow0 + r < M.rows && pcol0 + c8 < M.ldx) {
+            half8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = at(r, c8 + e);
+            stg<half8>(M.xa + int64_t(prow0 + r) * M.ldx + pcol0 + c8, h);
+        }
+    }
+    if ((M.flags & kFlagPNN) && lane < 32 && prow0 + lane < M.rows) {
+        float t = 0.f;
+        for (int c = 0; c < 32; ++c) {
+            const float f = static_cast<float>(at(lane, c));
+            t += f * f;
+        }
+        M.rowsqpart[int64_t(pcol0 >> 5) * M.rows + prow0 + lane] = t;
+    }
+}
+
+// One launch: the schedule of every small matrix in the task list (blocks starts[k] ..
+// starts[k+1]-1 are the cluster of matrix order[k]). err: set when a cluster barrier times out.
+// Each operation's output is cut into super-tiles of up to 128 x 128 dealt to the cluster's
+// workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
+__global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
+                                                                 SmallSchedule sc, int* err) {
+    __shared__ __attribute__((aligned(16))) _Float16 panels[2 * kPanelHalves];
+    __shared__ _Float16 stage_all[kSmallWaves][32 * kStageLd];
+    const int k = find_task(tl.starts, tl.n, blockIdx.x);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int member = blockIdx.x - tl.starts[k];
+    const int C = tl.starts[k + 1] - tl.starts[k];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    _Float16* const stage = stage_all[wave];
+    const SmallView V = small_view(M);
+    int* const bar = M.small_bar;
+    const int set = M.rows == M.cols ? 0 : 1;
+
+    // the first iterate in both orientations of the wide form
+    {
+        const int64_t n = int64_t(M.s) * M.l;
+        for (int64_t e = int64_t(member) * kSmallThreads + threadIdx.x; e < n; e += int64_t(C) * kSmallThreads) {
+            const int i = static_cast<int>(e / M.l), j = static_cast<int>(e % M.l);   // wide (s x l) index
+            const _Float16 x = M.tall ? M.xb[int64_t(j) * M.ldx + i] : M.xb[int64_t(i) * M.ldx + j];
+            V.xw(0)[int64_t(i) * V.lp + j] = x;
+            V.xwt(0)[int64_t(j) * V.sp + i] = x;
+        }
+    }
+    cluster_barrier(bar, C, err);
+
+    const int nops = sc.n[set];
+    for (int q = 0; q < nops; ++q) {
+        const SmallOp op = sc.op[set][q];
+        // output rows x cols and the operands of this operation
+        const int orows = V.sp, ocols = op.kind == kOpUpdate ? V.lp : V.sp;
+        const _Float16 *A, *BT, *CT = nullptr;
+        int64_t lda, ldb;
+        int K;
+        if (op.kind == kOpGram) {          // R = X X^T, K = l
+            A = BT = V.xw(op.xsel);
+            lda = ldb = V.lp;
+            K = V.lp;
+        } else if (op.kind == kOpSym) {    // out = alpha A B + beta C
+            A = V.sq(op.a);
+            BT = V.sqt(op.b);
+            lda = ldb = V.sp;
+            K = V.sp;
+            if (op.c >= 0) CT = V.sqt(op.c);
+        } else {                           // X' = Q X (+ beta X), K = s
+            A = V.sq(op.a);
+            BT = V.xwt(op.xsel);
+            lda = ldb = V.sp;
+            K = V.sp;
+            if (op.c >= 0) CT = V.xwt(op.xsel);
+        }
+        const int SM = min(orows, 128), SN = min(ocols, 128);
+        const int SR = (orows + 127) / 128, SC = (ocols + 127) / 128;
+        const int tm = SM / 32;
+        const bool has_tile = wave < tm * (SN / 32);
+        const int ti = has_tile ? wave % tm : 0, tj = has_tile ? wave / tm : 0;
+        for (int st = member; st < SR * SC; st += C) {
+            const int M0 = 128 * (st % SR), N0 = 128 * (st / SR);
+            const int sm = min(SM, orows - M0), sn = min(SN, ocols - N0);
+            const bool mine = has_tile && 32 * ti < sm && 32 * tj < sn;
+            const floatx16 acc = small_block(panels, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine, ti, tj);
+            if (!mine) continue;
+            const int m0 = M0 + 32 * ti, n0 = N0 + 32 * tj;
+            const float alpha = op.kind == kOpSym ? op.alpha : 1.f;
+            small_stage(acc, stage, alpha, op.beta, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
+            if (op.kind == kOpGram) {
+                small_store(stage, V.sq(kBufR), V.sp, V.sqt(kBufR), V.sp, m0, n0, lane);
+            } else if (op.kind == kOpSym) {
+                small_store(stage, V.sq(op.o), V.sp, V.sqt(op.o), V.sp, m0, n0, lane);
+                if (op.o2 >= 0) {
+                    wave_lds_sync();
+                    if (m0 == n0 && lane < 32 && m0 + lane < M.s) {
+                        _Float16& z = stage[lane * kStageLd + lane];
+                        z = static_cast<_Float16>(static_cast<float>(z) + op.dual);
+                    }
+                    wave_lds_sync();
+                    small_store(stage, V.sq(op.o2), V.sp, V.sqt(op.o2), V.sp, m0, n0, lane);
+                }
+            } else if (op.fin) {
+                small_store_final(stage, M, m0, n0, lane);
+            } else {
+                const int xo = 1 - op.xsel;
+                small_store(stage, V.xw(xo), V.lp, V.xwt(xo), V.sp, m0, n0, lane);
+            }
+        }
+        cluster_barrier(bar, C, err);
+    }
+}
+
+}  // namespace thorn

@@ -1,7 +1,7 @@
 // C ABI of the THORN step (declared in include/thorn_amd.h): host-side plans, device tables and
 // the launch sequence. One translation unit: the kernel sources are included below.
 #include "../../include/thorn_amd.h"
-#include "ns_kernels.hip"
+#include "ns_small.hip"
 #include "update_kernels.hip"
 
 #include <algorithm>
@@ -36,8 +36,11 @@ struct MatLayout {
     int32_t rows, cols, s, l, ldx, lds, tall, flags;
     int32_t mom_tiles_r, mom_tiles_c, g3_tiles_m, g3_tiles_n, sym_tiles, n_psq;
     size_t xa, xb, gram, zbuf, qa, qb, normpart, rowpart, colpart, rowsqpart, rowscale, scal, psqpart;
-    size_t magpart, rowpsq;
+    size_t magpart, rowpsq, small, small_bar;
     bool adam, norm_rows;   // THORN_MAT_ADAM, THORN_MAT_NORM_ROWS
+    bool is_small;          // Newton-Schulz in ns_small_kernel
+    int32_t cluster;        // its workgroups
+    int32_t rowsq_tiles;
 };
 
 struct TaskOffsets {
@@ -121,12 +124,14 @@ struct thorn_ortho_plan {
     size_t mats_off = 0;
     // Newton-Schulz task lists per matrix set: [0] square matrices (plain quintic), [1] the others
     // (Gram Newton-Schulz); sym = upper-triangle tiles of s x s products, g3 = tiles of X updates.
-    TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, md{}, adam{};
-    std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, md_order, adam_order;
+    TaskOffsets pre{}, sym[2]{}, g3[2]{}, pnn{}, rs{}, md{}, adam{}, small{};
+    // pnn: matrices applied by ortho_pnn_apply_kernel (per-row-normalized or small); rs: the
+    // per-row-normalized ones (ortho_rowstats_kernel); small: ns_small_kernel's clusters
+    std::vector<int32_t> pre_order, sym_order[2], g3_order[2], pnn_order, rs_order, md_order, adam_order, small_order;
     // The Newton-Schulz and per-row-normalization lists of the last filled table: only the
     // matrices applied this step (the reference skips the polar factor of the others,
     // thorn.py:1395-1396, 1436-1441). Same table offsets, fewer entries.
-    TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{}, adam_live{};
+    TaskOffsets sym_live[2]{}, g3_live[2]{}, pnn_live{}, rs_live{}, adam_live{}, small_live{};
     // mean short and long side of each set's matrices: the contraction lengths of its GEMM tiles
     // (long side: Gram matrices; short side: the other products), to run longer tiles first
     double mean_s[2]{}, mean_l[2]{};
@@ -311,6 +316,35 @@ NsSchedule plain_schedule(int iters, const float* coeffs) {
     return sc;
 }
 
+// The compact form of a schedule for ns_small_kernel's kernel arguments; false if it is too long.
+bool small_encode(const NsSchedule& sc, thorn::SmallOp* out, int32_t& n) {
+    n = 0;
+    if (sc.ops.size() > static_cast<size_t>(thorn::kSmallMaxOps)) return false;
+    for (const ScheduledOp& so : sc.ops) {
+        const thorn::NsOp& o = so.op;
+        thorn::SmallOp s{};
+        s.kind = static_cast<int8_t>(o.kind);
+        s.xsel = static_cast<int8_t>(o.xsel);
+        s.fin = static_cast<int8_t>(o.final_iter);
+        s.alpha = o.alpha;
+        s.beta = o.beta;
+        s.dual = o.dual_add;
+        s.o2 = -1;
+        if (o.kind == thorn::kOpSym) {
+            s.a = static_cast<int8_t>(o.asel);
+            s.b = static_cast<int8_t>(o.bsel);
+            s.c = static_cast<int8_t>(o.csel);
+            s.o = static_cast<int8_t>(o.osel);
+            s.o2 = static_cast<int8_t>(o.osel2);
+        } else if (o.kind == thorn::kOpUpdate) {
+            s.a = static_cast<int8_t>(o.qsel);
+            s.c = static_cast<int8_t>(o.csel);
+        }
+        out[n++] = s;
+    }
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -335,6 +369,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     if (n < 0 || (n > 0 && !descs)) return fail(THORN_ERR_INVALID, "thorn_ortho_plan_create: bad matrix list");
     auto* plan = new thorn_ortho_plan();
     size_t ws = kAlign;   // [0, 256): zeros, never written (source of out-of-range GEMM tile chunks)
+    ws += kAlign;         // [256, 512): status words (THORN_WS_STATUS_OFFSET)
     auto take = [&ws](size_t bytes) {
         if (bytes == 0) return kNone;
         const size_t o = ws;
@@ -383,11 +418,25 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         const bool pnn = L.flags & THORN_MAT_PER_ROW_NORM;
         const bool md = L.flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR);
         const int64_t mom_tiles = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
-        L.n_psq = md ? static_cast<int32_t>(pnn || L.adam ? mom_tiles : int64_t(L.g3_tiles_m) * L.g3_tiles_n) : 0;
+        // small matrices run their whole Newton-Schulz in ns_small_kernel and are applied by
+        // ortho_pnn_apply_kernel (u' in xa); they always take the exact first iterate
+        L.is_small = !L.adam && L.s <= thorn::kSmallMaxS && int64_t(L.rows) * L.cols < kPrescaleMinElems;
+        L.cluster = L.s <= 128 ? 1 : 4;
+        L.rowsq_tiles = static_cast<int32_t>(L.is_small ? cdiv(L.cols, 32) : L.g3_tiles_n);
+        L.n_psq = md ? static_cast<int32_t>(pnn || L.adam || L.is_small ? mom_tiles
+                                                                         : int64_t(L.g3_tiles_m) * L.g3_tiles_n)
+                     : 0;
         // an Adam-group tensor runs no Newton-Schulz: no iterate or s x s buffers
         const size_t xbytes = L.adam ? 0 : size_t(L.rows) * L.ldx * 2;
-        const size_t sbytes = L.adam ? 0 : size_t(L.s) * L.lds * 2;
+        const size_t sbytes = L.adam || L.is_small ? 0 : size_t(L.s) * L.lds * 2;
         const bool square = L.rows == L.cols;   // the plain quintic needs no Q (thorn.py:654-658)
+        if (L.is_small) {
+            const size_t sp = align_up(L.s, 32), lp = align_up(L.l, 32);
+            L.small = take((8 * sp * sp + 4 * sp * lp) * 2);
+            L.small_bar = take(2 * sizeof(int));
+        } else {
+            L.small = L.small_bar = kNone;
+        }
         L.xa = take(xbytes);
         L.xb = take(xbytes);
         L.gram = take(sbytes);
@@ -398,7 +447,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.normpart = take(sizeof(float) * mom_tiles);
         L.rowpart = md ? take(sizeof(float) * size_t(L.mom_tiles_c) * L.rows) : kNone;
         L.colpart = (L.flags & THORN_MAT_MD) ? take(sizeof(float) * size_t(L.mom_tiles_r) * L.cols) : kNone;
-        L.rowsqpart = pnn ? take(sizeof(float) * size_t(L.g3_tiles_n) * L.rows) : kNone;
+        L.rowsqpart = pnn ? take(sizeof(float) * size_t(L.rowsq_tiles) * L.rows) : kNone;
         L.rowscale = pnn || L.norm_rows ? take(sizeof(float) * L.rows) : kNone;
         L.scal = take(sizeof(float) * 8);
         L.psqpart = md ? take(sizeof(float) * L.n_psq) : kNone;
@@ -429,7 +478,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     // (thorn.py:628, 637-658).
     std::vector<int32_t> sets[2];
     for (int i = 0; i < n; ++i)
-        if (!plan->mats[i].adam) sets[plan->mats[i].rows != plan->mats[i].cols ? 1 : 0].push_back(i);
+        if (!plan->mats[i].adam && !plan->mats[i].is_small)
+            sets[plan->mats[i].rows != plan->mats[i].cols ? 1 : 0].push_back(i);
     for (int q = 0; q < 2; ++q) {
         for (int i : sets[q]) {
             plan->mean_s[q] += plan->mats[i].s;
@@ -447,16 +497,20 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         });
     }
     for (int i = 0; i < n; ++i) {
-        if (plan->mats[i].flags & THORN_MAT_PER_ROW_NORM) plan->pnn_order.push_back(i);
-        if (plan->mats[i].flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
-        if (plan->mats[i].adam) plan->adam_order.push_back(i);
+        const MatLayout& L = plan->mats[i];
+        if (L.flags & THORN_MAT_PER_ROW_NORM) plan->rs_order.push_back(i);
+        if ((L.flags & THORN_MAT_PER_ROW_NORM) || L.is_small) plan->pnn_order.push_back(i);
+        if (L.flags & (THORN_MAT_MD | THORN_MAT_MD_SCALAR)) plan->md_order.push_back(i);
+        if (L.adam) plan->adam_order.push_back(i);
+        if (L.is_small) plan->small_order.push_back(i);
     }
-    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n);
+    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n), small_blocks(n), one_block(n, 1);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
         mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
         sym_blocks[i] = L.sym_tiles;
         g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
+        small_blocks[i] = L.cluster;
         plan->max_mom_tiles = std::max<int64_t>(plan->max_mom_tiles, mom_blocks[i]);
     }
     if (n > 65535) {
@@ -472,8 +526,10 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         plan->g3[q] = add_tasks(off, plan->g3_order[q], g3_blocks);
     }
     plan->pnn = add_tasks(off, plan->pnn_order, mom_blocks);
+    plan->rs = add_tasks(off, plan->rs_order, one_block);
     plan->md = add_tasks(off, plan->md_order, mom_blocks);
     plan->adam = add_tasks(off, plan->adam_order, mom_blocks);
+    plan->small = add_tasks(off, plan->small_order, small_blocks);
     plan->table_bytes = off;
     if (int64_t(plan->sym[0].total) + plan->sym[1].total + plan->g3[0].total + plan->g3[1].total >=
         (int64_t(1) << 31) - 1) {
@@ -547,6 +603,9 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.psqpart = static_cast<float*>(at(L.psqpart));
         M.magpart = static_cast<float4*>(at(L.magpart));
         M.rowpsq = static_cast<float*>(at(L.rowpsq));
+        M.small = static_cast<_Float16*>(at(L.small));
+        M.small_bar = static_cast<int*>(at(L.small_bar));
+        M.rowsq_tiles = L.rowsq_tiles;
         M.v = S.v;
         M.adam_beta2 = S.adam_beta2; M.adam_w1 = S.adam_w1; M.adam_w2 = S.adam_w2;
         M.adam_bc1 = S.adam_bc1; M.adam_bc2 = S.adam_bc2; M.adam_eps = S.adam_eps;
@@ -568,6 +627,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         int32_t flags = L.flags | (S.step_flags & (THORN_STEP_KEEP_GRAD | THORN_STEP_APPLY));
         if (L.adam) flags |= thorn::kFlagAdam | (S.adam_degenerate ? thorn::kFlagAdamDegen : 0);
         if (L.norm_rows) flags |= thorn::kFlagNormRows;
+        if (L.is_small) flags |= thorn::kFlagSmall;
         if (L.cols % 4 == 0 && aligned16(S.p) && aligned16(S.g) && aligned16(S.m) && (!L.adam || aligned16(S.v)))
             flags |= thorn::kFlagVec4;
         // The first iterate of a large matrix is written directly in f16 with the previous step's
@@ -592,12 +652,13 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.n_psq = L.n_psq;
         M.apply_tiles = L.mom_tiles_r * L.mom_tiles_c;
     }
-    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n);
+    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n), small_blocks(n), one_block(n, 1);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
         mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
         sym_blocks[i] = L.sym_tiles;
         g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
+        small_blocks[i] = L.cluster;
     }
     auto applied_only = [&](const std::vector<int32_t>& order, const TaskOffsets& full,
                             const std::vector<int64_t>& blocks_of, TaskOffsets& live) {
@@ -620,7 +681,9 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         applied_only(plan->g3_order[q], plan->g3[q], g3_blocks, plan->g3_live[q]);
     }
     applied_only(plan->pnn_order, plan->pnn, mom_blocks, plan->pnn_live);
+    applied_only(plan->rs_order, plan->rs, one_block, plan->rs_live);
     applied_only(plan->adam_order, plan->adam, mom_blocks, plan->adam_live);
+    applied_only(plan->small_order, plan->small, small_blocks, plan->small_live);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
     plan->any_exact = any_exact;
@@ -707,10 +770,26 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(256), 0, st, mats, tl[1],
                      op[1], tl[0], op[0], square_first);
     }
+    if (plan->small_live.n > 0) {   // every small matrix's whole schedule in one launch
+        thorn::SmallSchedule ss{};
+        for (int q = 0; q < 2; ++q) {
+            if (!small_encode(sched[q], ss.op[q], ss.n[q]))
+                return fail(THORN_ERR_UNSUPPORTED, "thorn_ortho_step: more than " +
+                                                       std::to_string(thorn::kSmallMaxOps) +
+                                                       " Newton-Schulz operations for the small-matrix path");
+        }
+        int* status = reinterpret_cast<int*>(static_cast<char*>(const_cast<void*>(plan->filled_ws)) +
+                                             THORN_WS_STATUS_OFFSET);
+        THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel, dim3(plan->small_live.total),
+                     dim3(thorn::kSmallThreads), 0, st, mats, task_list(dev, plan->small_live), ss, status);
+    }
+    if (plan->rs_live.n > 0) {
+        const thorn::TaskList rs = task_list(dev, plan->rs_live);
+        THORN_LAUNCH(THORN_KIND_ROWSTATS, "ortho_rowstats_kernel", thorn::ortho_rowstats_kernel, dim3(rs.n),
+                     dim3(256), 0, st, mats, rs.order);
+    }
     if (plan->pnn_live.n > 0) {
         const thorn::TaskList pnn = task_list(dev, plan->pnn_live);
-        THORN_LAUNCH(THORN_KIND_ROWSTATS, "ortho_rowstats_kernel", thorn::ortho_rowstats_kernel, dim3(pnn.n),
-                     dim3(256), 0, st, mats, pnn.order);
         thorn::UoutSel usel;
         usel.sel[0] = sched[0].uout_sel;
         usel.sel[1] = sched[1].uout_sel;

@@ -188,6 +188,7 @@ enum OrthoFlags : int32_t {
     kFlagAdam = 256,     // decouple_md tensor of an Adam group: Adam step instead of Newton-Schulz
     kFlagNormRows = 512, // kFlagAdam: renormalize per row (norm_axis = -1)
     kFlagAdamDegen = 1024, // kFlagAdam: rectification says rho <= 4, u = m
+    kFlagSmall = 2048,   // Newton-Schulz in ns_small_kernel; u' in xa, applied by ortho_pnn_apply_kernel
 };
 
 // One matrix of an orthogonalized group. All user tensors are fp32, row-major rows x cols,
@@ -242,6 +243,9 @@ struct OrthoMat {
     float* v;
     float* rowpsq;    // kFlagNormRows: [mom_tiles_c][rows] partial row sums of p^2 after the update
     float adam_beta2, adam_w1, adam_w2, adam_bc1, adam_bc2, adam_eps;
+    _Float16* small;     // kFlagSmall: the small-matrix iterates and s x s buffers (ns_small.hip)
+    int* small_bar;      // kFlagSmall: the cluster barrier (count, generation)
+    int32_t rowsq_tiles; // partial sums per row in rowsqpart (column tiles of the last update)
 };
 
 enum ScalSlot : int {

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __r
     float tot = 0.f, nw = 0.f;
     for (int i = threadIdx.x; i < M.rows; i += 256) {
         float rs = 0.f;
-        for (int t = 0; t < M.g3_tiles_n; ++t) rs += M.rowsqpart[(int64_t)t * M.rows + i];
+        for (int t = 0; t < M.rowsq_tiles; ++t) rs += M.rowsqpart[(int64_t)t * M.rows + i];
         const float mean = rs / (float)M.cols;
         const float s = 1.f / sqrtf(fmaxf(mean, eps));
         M.rowscale[i] = s;
@@ -326,7 +326,9 @@ __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __r
     if (threadIdx.x == 0) M.scal[kScalGamma] = sqrtf(tot) / fmaxf(sqrtf(nw), eps);
 }
 
-// p <- p - eta * cwd((u' * s_i) * gamma) over per-row-normalized matrices, plus p^2 partials for md.
+// p <- p - eta * cwd((u' * s_i) * gamma) over per-row-normalized matrices, p <- p - eta * cwd(u')
+// over the other small-path matrices (whose u' ns_small_kernel leaves in xa), plus p^2 partials
+// for md.
 __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
                                                               UoutSel usel) {
     __shared__ float scratch[4];
@@ -338,9 +340,10 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
-    const float gamma = M.scal[kScalGamma];
+    const bool pnn = M.flags & kFlagPNN;
+    const float gamma = pnn ? M.scal[kScalGamma] : 1.f;
     const float eta = (M.flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta;   // thorn.py:1405
-    const _Float16* const uout = uout_of(M, usel);
+    const _Float16* const uout = (M.flags & kFlagSmall) ? M.xa : uout_of(M, usel);
     const bool md = M.flags & (kFlagMD | kFlagMDScalar);
     const bool vec = M.flags & kFlagVec4;
     const int nrows = M.rows - r0;
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             const int row = r0 + rr;
             pv[rr] = ldg_nt<float4>(M.p + (int64_t)row * M.cols + c);
             uv[rr] = ldg_nt<half4>(uout + (int64_t)row * M.ldx + c);
-            sv[rr] = ldg<float>(M.rowscale + row);
+            sv[rr] = pnn ? ldg<float>(M.rowscale + row) : 1.f;
         }
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
         for (int rr = 0; rr < 4; ++rr) {
             const int row = r0 + rr;
             if (row >= M.rows) break;
-            const float s = M.rowscale[row];
+            const float s = pnn ? M.rowscale[row] : 1.f;
             const int64_t rbase = (int64_t)row * M.cols;
             const _Float16* urow = uout + (int64_t)row * M.ldx;
 #pragma unroll
