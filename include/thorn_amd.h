@@ -137,6 +137,20 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
                      uint32_t restart_mask, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): thorn_ortho_fill_table
+ * and thorn_ortho_step in one call, with the workspace and the device table in a file-scope
+ * device array of THORN_NOALLOC_SCRATCH_BYTES per GPU instead of caller memory. It calls no
+ * hipMalloc or hipFree; the plan (thorn_ortho_plan_create, made beforehand) holds the host side
+ * of the table. Every call clears the workspace part of the array with a kernel and takes the
+ * exact first iterate (nothing is carried between calls). Plans whose workspace and table exceed
+ * the array are refused with THORN_ERR_INVALID. All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (other streams, other threads) race and must be serialized by the
+ * caller. The results equal thorn_ortho_step's on a fresh workspace. */
+#define THORN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, const float* coeffs,
+                             int iters, uint32_t restart_mask, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Non-orthogonalized group: Adam / Adam-atan2 / rectified Adam with cautious weight decay, all
  * tensors of all such groups in one launch. Replaces the per-parameter loop of _step_params

@@ -79,6 +79,7 @@ SIGNATURES = {
     'thorn_ortho_table_bytes': (_sz, [_vp]),
     'thorn_ortho_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
     'thorn_ortho_step': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp]),
+    'thorn_ortho_step_noalloc': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp]),
     'thorn_adam_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
     'thorn_adam_plan_destroy': (None, [_vp]),
     'thorn_adam_table_bytes': (_sz, [_vp]),
@@ -94,6 +95,7 @@ SIGNATURES = {
 KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_factor', 'md_rescale', 'adam', 'cast',
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
+NOALLOC_SCRATCH_BYTES = 32 << 20
 ABI_VERSION = 5
 
 _lib = None
@@ -168,6 +170,12 @@ class OrthoPlan:
         iters = coeffs.shape[0]
         check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, restart_mask, stream),
               'thorn_ortho_step')
+
+    def step_noalloc(self, steps: np.ndarray, coeffs: np.ndarray, restart_mask: int, stream: int) -> None:
+        """fill_table + step with the library's static device workspace (no allocation)."""
+        iters = coeffs.shape[0]
+        check(self._lib.thorn_ortho_step_noalloc(self.handle, steps.ctypes.data, coeffs.ctypes.data, iters,
+                                                 restart_mask, stream), 'thorn_ortho_step_noalloc')
 
     def timing_enable(self, max_launches: int) -> None:
         check(self._lib.thorn_ortho_timing_enable(self.handle, max_launches), 'thorn_ortho_timing_enable')

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -136,6 +137,11 @@ struct thorn_ortho_plan {
     // (long side: Gram matrices; short side: the other products), to run longer tiles first
     double mean_s[2]{}, mean_l[2]{};
     int max_mom_tiles = 0;   // elementwise 16 x 256 tiles of the largest matrix
+    // per-matrix block counts of the task lists, and room for one filtered list: fill_table runs
+    // every step and allocates nothing
+    std::vector<int64_t> mom_blocks, sym_blocks, g3_blocks, small_blocks, one_block;
+    std::vector<int32_t> kept;
+    std::vector<char> host_table;   // host side of the table for thorn_ortho_step_noalloc
     LaunchTimer timer;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
@@ -207,10 +213,27 @@ struct ScheduledOp {
     int kind;   // THORN_KIND_* for launch timing
 };
 
+// A fixed-capacity list of operations (the schedules are built on every step, without touching
+// the heap): iters <= 32 takes at most 6 per iteration and 2 more.
+struct OpList {
+    static constexpr int kCap = 200;
+    ScheduledOp v[kCap];
+    int n = 0;
+    void push_back(const ScheduledOp& o) {
+        if (n < kCap) v[n] = o;
+        ++n;   // n > kCap marks an overflow, which the caller reports
+    }
+    size_t size() const { return static_cast<size_t>(n); }
+    bool overflow() const { return n > kCap; }
+    const ScheduledOp& operator[](size_t i) const { return v[i]; }
+    const ScheduledOp* begin() const { return v; }
+    const ScheduledOp* end() const { return v + (n < kCap ? n : kCap); }
+};
+
 // The Newton-Schulz launch sequence of one matrix set and the iterate buffer that holds u' after
 // its last update (the per-row normalization reads it from there).
 struct NsSchedule {
-    std::vector<ScheduledOp> ops;
+    OpList ops;
     int uout_sel;
 };
 
@@ -225,14 +248,14 @@ thorn::NsOp make_op(int32_t kind) {
 
 inline int other_x(int xsel) { return xsel == thorn::kXB ? thorn::kXA : thorn::kXB; }
 
-void push_gram(std::vector<ScheduledOp>& ops, int xsel, bool first) {
+void push_gram(OpList& ops, int xsel, bool first) {
     thorn::NsOp o = make_op(thorn::kOpGram);
     o.xsel = xsel;
     o.first = first ? 1 : 0;
     ops.push_back({o, THORN_KIND_GRAM});
 }
 
-void push_update(std::vector<ScheduledOp>& ops, int xsel, int qsel, bool first, bool fin, bool plus_x, float beta) {
+void push_update(OpList& ops, int xsel, int qsel, bool first, bool fin, bool plus_x, float beta) {
     thorn::NsOp o = make_op(thorn::kOpUpdate);
     o.xsel = xsel;
     o.qsel = qsel;
@@ -246,7 +269,7 @@ void push_update(std::vector<ScheduledOp>& ops, int xsel, int qsel, bool first, 
 }
 
 // out = f16(alpha * A B + beta * C); dual >= 0: also Q = out + f16(dual_a) I into buffer `dual`
-void push_sym(std::vector<ScheduledOp>& ops, int a, int b, int c, int out, float alpha, float beta, int kind,
+void push_sym(OpList& ops, int a, int b, int c, int out, float alpha, float beta, int kind,
               int dual = -1, float dual_a = 0.f) {
     thorn::NsOp o = make_op(thorn::kOpSym);
     o.asel = a;
@@ -345,7 +368,51 @@ bool small_encode(const NsSchedule& sc, thorn::SmallOp* out, int32_t& n) {
     return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Workspace of thorn_ortho_step_noalloc: a file-scope device array (one copy per GPU the library
+// runs on, held until the process ends). Host code never uses the array's name as an address: its
+// per-device address comes from hipGetSymbolAddress, taken once per device with that device
+// current.
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(THORN_NOALLOC_SCRATCH_BYTES);
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
+
+static __device__ __align__(256) unsigned char scratch[THORN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+int scratch_of_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(THORN_ERR_HIP, std::string("thorn_ortho_step_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(THORN_ERR_UNSUPPORTED, "thorn_ortho_step_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(THORN_ERR_HIP, std::string("thorn_ortho_step_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return THORN_OK;
+}
+
+}  // namespace
+
+namespace thorn {
+// Clears n16 16-byte words (the no-alloc workspace must start at zero: its padding and the zero
+// page are read by the Newton-Schulz kernels). A fill kernel rather than a memset, so that a
+// caller may capture the step in a graph.
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint4* __restrict__ p, int64_t n16) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n16; i += int64_t(gridDim.x) * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+}  // namespace thorn
 
 extern "C" {
 
@@ -504,7 +571,17 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         if (L.adam) plan->adam_order.push_back(i);
         if (L.is_small) plan->small_order.push_back(i);
     }
-    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n), small_blocks(n), one_block(n, 1);
+    plan->mom_blocks.assign(n, 0);
+    plan->sym_blocks.assign(n, 0);
+    plan->g3_blocks.assign(n, 0);
+    plan->small_blocks.assign(n, 0);
+    plan->one_block.assign(n, 1);
+    plan->kept.reserve(n);
+    std::vector<int64_t>& mom_blocks = plan->mom_blocks;
+    std::vector<int64_t>& sym_blocks = plan->sym_blocks;
+    std::vector<int64_t>& g3_blocks = plan->g3_blocks;
+    std::vector<int64_t>& small_blocks = plan->small_blocks;
+    std::vector<int64_t>& one_block = plan->one_block;
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
         mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
@@ -531,6 +608,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     plan->adam = add_tasks(off, plan->adam_order, mom_blocks);
     plan->small = add_tasks(off, plan->small_order, small_blocks);
     plan->table_bytes = off;
+    plan->host_table.assign(plan->table_bytes, 0);
     if (int64_t(plan->sym[0].total) + plan->sym[1].total + plan->g3[0].total + plan->g3[1].total >=
         (int64_t(1) << 31) - 1) {
         delete plan;
@@ -652,18 +730,15 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.n_psq = L.n_psq;
         M.apply_tiles = L.mom_tiles_r * L.mom_tiles_c;
     }
-    std::vector<int64_t> mom_blocks(n), sym_blocks(n), g3_blocks(n), small_blocks(n), one_block(n, 1);
-    for (int i = 0; i < n; ++i) {
-        const MatLayout& L = plan->mats[i];
-        mom_blocks[i] = int64_t(L.mom_tiles_r) * L.mom_tiles_c;
-        sym_blocks[i] = L.sym_tiles;
-        g3_blocks[i] = int64_t(L.g3_tiles_m) * L.g3_tiles_n;
-        small_blocks[i] = L.cluster;
-    }
+    const std::vector<int64_t>& mom_blocks = plan->mom_blocks;
+    const std::vector<int64_t>& sym_blocks = plan->sym_blocks;
+    const std::vector<int64_t>& g3_blocks = plan->g3_blocks;
+    const std::vector<int64_t>& small_blocks = plan->small_blocks;
+    const std::vector<int64_t>& one_block = plan->one_block;
     auto applied_only = [&](const std::vector<int32_t>& order, const TaskOffsets& full,
                             const std::vector<int64_t>& blocks_of, TaskOffsets& live) {
-        std::vector<int32_t> kept;
-        kept.reserve(order.size());
+        std::vector<int32_t>& kept = plan->kept;   // capacity n since plan creation
+        kept.clear();
         int64_t total = 0;
         for (int32_t i : order) {
             if (!(mats[i].flags & thorn::kFlagApply)) continue;
@@ -746,6 +821,8 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     // Newton-Schulz: square matrices on the plain quintic, the others on Gram Newton-Schulz with
     // the given restarts (thorn.py:628, 637-658); step k of both schedules shares launch k.
     const NsSchedule sched[2] = {plain_schedule(iters, coeffs), gram_schedule(iters, restart_mask, coeffs)};
+    if (sched[0].ops.overflow() || sched[1].ops.overflow())
+        return fail(THORN_ERR_INVALID, "thorn_ortho_step: too many Newton-Schulz operations");
     const thorn::TaskList sym[2] = {task_list(dev, plan->sym_live[0]), task_list(dev, plan->sym_live[1])};
     const thorn::TaskList g3[2] = {task_list(dev, plan->g3_live[0]), task_list(dev, plan->g3_live[1])};
     const size_t steps = std::max(sched[0].ops.size(), sched[1].ops.size());
@@ -806,6 +883,39 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
 #undef THORN_LAUNCH
     plan->stepped_ws = plan->filled_ws;
     return THORN_OK;
+}
+
+int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, const float* coeffs,
+                             int iters, uint32_t restart_mask, void* stream) {
+    if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_step_noalloc: null plan");
+    const size_t ws_bytes = align_up(plan->ws_bytes, kAlign);
+    const size_t need = ws_bytes + align_up(plan->table_bytes, kAlign);
+    if (need > kNoAllocScratchBytes)
+        return fail(THORN_ERR_INVALID, "thorn_ortho_step_noalloc: the plan needs " + std::to_string(need) +
+                                           " bytes of workspace and table; the no-alloc limit is " +
+                                           std::to_string(kNoAllocScratchBytes) + " bytes (THORN_NOALLOC_SCRATCH_BYTES)");
+    void* base = nullptr;
+    if (int rc = scratch_of_current_device(&base)) return rc;
+    char* ws = static_cast<char*>(base);
+    char* table_dev = ws + ws_bytes;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // the array is shared by every call on this GPU: start from zeros and the exact first iterate
+    plan->stepped_ws = nullptr;
+    if (int rc = thorn_ortho_fill_table(plan, steps, ws, table_dev, plan->host_table.data())) return rc;
+    const int64_t n16 = static_cast<int64_t>(ws_bytes / 16);
+    const int grid = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 2048));
+    hipLaunchKernelGGL(thorn::zero_fill_kernel, dim3(std::max(grid, 1)), dim3(256), 0, st,
+                       reinterpret_cast<uint4*>(ws), n16);
+    if (int rc = check_launch("zero_fill_kernel")) return rc;
+    if (plan->table_bytes > 0) {
+        const hipError_t e = hipMemcpyAsync(table_dev, plan->host_table.data(), plan->table_bytes,
+                                            hipMemcpyHostToDevice, st);
+        if (e != hipSuccess)
+            return fail(THORN_ERR_HIP, std::string("thorn_ortho_step_noalloc: table copy: ") + hipGetErrorString(e));
+    }
+    const int rc = thorn_ortho_step(plan, table_dev, coeffs, iters, restart_mask, stream);
+    plan->stepped_ws = nullptr;   // the next call may find another plan's data in the array
+    return rc;
 }
 
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches) {
