@@ -30,6 +30,9 @@ sys.path.insert(0, ROOT)
 
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense f16/bf16 MFMA
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E
+# Plan kinds of the Newton-Schulz launches, and the small-matrix path's limits (thorn_abi.hip)
+NS_KINDS = ('gram', 'poly', 'symprod', 'update', 'small')
+SMALL_MAX_S, SMALL_MAX_ELEMS = 256, 1 << 20
 
 
 # ---------------------------------------------------------------------------------------------
@@ -240,8 +243,7 @@ def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
 # rocprofv3 summaries and the HBM-traffic calibration
 # ---------------------------------------------------------------------------------------------
 
-TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'ns_phase_traffic_qwen3_300m.md')
-_TRAFFIC_RE = r'ns_phase_kernel HBM bytes per launch: ([0-9.eE+]+)'
+TRAFFIC_PROFILES = {'ns_phase_kernel': 'ns_phase_traffic_qwen3_300m.md'}
 
 
 def copy_calibration(mib: int, device) -> None:
@@ -433,13 +435,16 @@ def vendor_gemm() -> int:
     return 0
 
 
-def traffic_from_profile() -> float | None:
-    """HBM bytes per ns_phase_kernel launch from the committed counter summary, if present."""
+def traffic_from_profile(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` from its committed counter summary, if present."""
     import re
+    if kernel not in TRAFFIC_PROFILES:
+        return None
     try:
-        m = re.search(_TRAFFIC_RE, open(TRAFFIC_PROFILE).read())
+        text = open(os.path.join(ROOT, 'profiles', TRAFFIC_PROFILES[kernel])).read()
     except OSError:
         return None
+    m = re.search(kernel + r' HBM bytes per launch: ([0-9.eE+]+)', text)
     return float(m.group(1)) if m else None
 
 
@@ -533,14 +538,24 @@ def main() -> int:
     grp0 = thorn_amd.optim._Group.from_kwargs(**opt.param_groups[0])
     mask = thorn_amd.optim._OrthoRunner.restart_mask(grp0, grp0.iters)
     F = schedule_flops(mats, grp0.iters, mask)
-    ns_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('gram', 'poly', 'symprod', 'update')) / args.steps
+    small = [sh for sh in mats if min(sh) <= SMALL_MAX_S and sh[0] * sh[1] < SMALL_MAX_ELEMS]
+    F_small = schedule_flops(small, grp0.iters, mask)
+    ns_ms = sum(kinds.get(k, (0.0, 0))[0] for k in NS_KINDS) / args.steps
     upd_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('pre', 'norm', 'rowstats', 'pnn_apply', 'adam')) / args.steps
     cbytes = compulsory_bytes(mats, params, n_m)
-    # dominant kernel: ns_phase_kernel, which runs every Newton-Schulz GEMM (one launch per
-    # schedule step); its algorithmic flops per launch are the step's F over its launch count
-    ns_launches = sum(kinds.get(k, (0.0, 0))[1] for k in ('gram', 'poly', 'symprod', 'update')) / args.steps
-    ns_flops_per_launch = F / max(ns_launches, 1)
-    u_avg = ns_ms / max(ns_launches, 1)
+    # dominant kernel: ns_phase_kernel, which runs the Newton-Schulz products of the large
+    # matrices (one launch per schedule step); with no large matrix, ns_small_kernel. Its
+    # algorithmic flops per launch are its matrices' schedule flops over its launch count.
+    if F - F_small > 0:
+        dom_kinds = ('gram', 'poly', 'symprod', 'update')
+        dom_name, dom_flops = 'ns_phase_kernel', F - F_small
+    else:
+        dom_kinds, dom_name, dom_flops = ('small',), 'ns_small_kernel', F_small
+    ns_launches = sum(kinds.get(k, (0.0, 0))[1] for k in NS_KINDS) / args.steps
+    dom_launches = sum(kinds.get(k, (0.0, 0))[1] for k in dom_kinds) / args.steps
+    dom_ms = sum(kinds.get(k, (0.0, 0))[0] for k in dom_kinds) / args.steps
+    ns_flops_per_launch = dom_flops / max(dom_launches, 1)
+    u_avg = dom_ms / max(dom_launches, 1)
     achieved = ns_flops_per_launch / (u_avg * 1e-3) / 1e12 if u_avg > 0 else 0.0
     phases = {k: {'ms_per_launch': round(ms / n, 4), 'launches_per_step': n / args.steps}
               for k, (ms, n) in sorted(kinds.items())}
@@ -578,10 +593,12 @@ def main() -> int:
         'update': {'compulsory_bytes': cbytes, 'ms_per_step': round(upd_ms, 3),
                    'gbps': round(cbytes / (upd_ms * 1e-3) / 1e9, 1) if upd_ms > 0 else None,
                    'hbm_frac': round(cbytes / (upd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if upd_ms > 0 else None},
-        'roofline': {'kernel': 'ns_phase_kernel', 'bound': 'mfma', 'achieved': round(achieved, 1),
+        'roofline': {'kernel': dom_name, 'bound': 'mfma', 'achieved': round(achieved, 1),
                      'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_PEAK_TFLOPS, 4),
-                     'traffic': traffic_from_profile(), 'flops_per_launch': ns_flops_per_launch,
-                     'launches_per_step': ns_launches, 'avg_launch_ms': round(u_avg, 4)},
+                     'traffic': traffic_from_profile(dom_name), 'flops_per_launch': ns_flops_per_launch,
+                     'launches_per_step': dom_launches, 'avg_launch_ms': round(u_avg, 4)},
+        'launches_per_step': {'ns': ns_launches,
+                              'total': sum(n for _, n in kinds.values()) / args.steps},
         'phases': phases,
         'cpu_baseline': cpu,
         'workload_gen_s': round(gen_s, 1),

@@ -138,34 +138,68 @@ __device__ __forceinline__ void lds_barrier() {
 // from there on (k0 = 0: always K-major; k0 >= the tile count: always MN-major). A symmetric
 // matrix stored as its upper block triangle is read MN-major, from the transposed mirror block,
 // before its diagonal block and K-major from there on.
+//
+// The loads of consecutive K tiles are issued in order (t = 0, 1, 2, ...), so each lane keeps the
+// source of its chunks of the next tile (`cur`) and advances it by the layout's tile stride after
+// every load: a load costs a compare, a select and a 64-bit add of vector work, which the MFMA
+// it follows in the loop body covers. begin_tile switches the sources to the K-major layout when
+// the next tile is tile k0.
 template <int MN>
 struct DmaPair {
     static constexpr int PER_WAVE = MN / 64;
-    DmaSrc<MN, true> kmaj;
-    DmaSrc<MN, false> mnmaj;
+    DmaSrc<MN, true> kmaj;           // K-major sources of tile 0, for the switch at k0
+    const char* cur[PER_WAVE];       // this lane's chunk q of the next tile to issue
+    int lim[PER_WAVE];               // chunk q exists in tile t iff t * 32 < lim[q]
+    int64_t step;                    // bytes between consecutive K tiles in the current layout
     int k0;
 
     __device__ __forceinline__ void init(const Operand& op, int mn0, int wave, int lane, int k0_) {
         kmaj.init(op, mn0, wave, lane);
-        mnmaj.init(op, mn0, wave, lane);
         k0 = k0_;
+        if (k0 <= 0) {
+#pragma unroll
+            for (int q = 0; q < PER_WAVE; ++q) {
+                cur[q] = kmaj.src[q];
+                lim[q] = kmaj.lim[q];
+            }
+            step = kmaj.step;
+        } else {
+            DmaSrc<MN, false> mnmaj;
+            mnmaj.init(op, mn0, wave, lane);
+#pragma unroll
+            for (int q = 0; q < PER_WAVE; ++q) {
+                cur[q] = mnmaj.src[q];
+                lim[q] = mnmaj.lim[q];
+            }
+            step = mnmaj.step;
+        }
     }
 
-    // Direct load q of this wave for K tile t into the stage at `lds` (a wave-uniform LDS byte
-    // address of this operand's part of the stage). The layout is selected per lane, not by a
-    // branch, so the loads interleave with the MFMAs of the loop body. Every address is inside
-    // the operand (chunks past its end come from `zero`) for any t >= 0.
+    // Called before the first load of tile t, for t = 0, 1, 2, ... in order (t is wave-uniform,
+    // so this is a scalar branch taken at most once per tile).
+    __device__ __forceinline__ void begin_tile(int t) {
+        if (t == k0 && t > 0) {
+#pragma unroll
+            for (int q = 0; q < PER_WAVE; ++q) {
+                cur[q] = kmaj.src[q] + t * kmaj.step;
+                lim[q] = kmaj.lim[q];
+            }
+            step = kmaj.step;
+        }
+    }
+
+    // Direct load q of this wave for K tile t (the tile of the last begin_tile) into the stage at
+    // `lds` (a wave-uniform LDS byte address of this operand's part of the stage). Every address
+    // is inside the operand (chunks past its end come from `zero`) for any t >= 0.
     // The load is inline assembly so that the compiler does not track it as an LDS write: its
     // conservative aliasing would otherwise wait for every outstanding load before the next LDS
     // fragment read and serialize the pipeline. The main loop orders the loads explicitly
     // (lds_wait_barrier); the "memory" clobber keeps LDS accesses from moving across them.
-    __device__ __forceinline__ void issue_one(int t, int q, uint32_t lds, const void* zero) const {
-        const bool km = t >= k0;
-        const char* src = km ? kmaj.src[q] + t * kmaj.step : mnmaj.src[q] + t * mnmaj.step;
-        const int lim = km ? kmaj.lim[q] : mnmaj.lim[q];
-        const void* p = t * DmaSrc<MN, true>::BKC < lim ? static_cast<const void*>(src) : zero;
+    __device__ __forceinline__ void issue_one(int t, int q, uint32_t lds, const void* zero) {
+        const void* p = t * DmaSrc<MN, true>::BKC < lim[q] ? static_cast<const void*>(cur[q]) : zero;
         asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p), "{m0}"(lds + q * 1024)
                      : "memory");
+        cur[q] += step;
     }
 };
 
@@ -236,11 +270,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 // loaded (zeros or in-bounds data) and read but never used, which keeps the loop body free of
 // branches.
 template <class C, bool AK, bool BK, int ROLE = kRoleFull>
-__device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM>& da, const DmaPair<C::BN>& db,
+__device__ __forceinline__ void gemm_segment(int lo, int hi, DmaPair<C::BM>& da, DmaPair<C::BN>& db,
                                              floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
                                              half8 (&fb)[2][C::TN], char* smem, const void* zero) {
     if (lo >= hi) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // kRoleHalf: wave 1 takes rows 0-63, wave 2 rows 64-127 of the upper-right quadrant
     const int wm = ROLE == kRoleHalf ? (wave >> 1) * (C::WM / 2) : (wave >> 1) * C::WM;
     const int wn = ROLE == kRoleHalf ? C::WN : (wave & 1) * C::WN;
@@ -257,6 +291,8 @@ __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM
     }
     for (int kt = lo; kt < hi; ++kt) {
         const char* sa = smem + (kt % C::S) * C::STAGE_BYTES;
+        da.begin_tile(kt + C::S - 1);
+        db.begin_tile(kt + C::S - 1);
         static_for<0, NM>([&](auto qc) {
             constexpr int q = decltype(qc)::value, i = R::i(q), j = R::j(q);
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
@@ -289,8 +325,8 @@ __device__ __forceinline__ void gemm_segment(int lo, int hi, const DmaPair<C::BM
 // in registers r..r+3, which the epilogue writes to LDS as one 16-byte store. Ends with every
 // load and LDS read complete and a block barrier, so the stages are free for the epilogue.
 template <class C, int ROLE>
-__device__ __forceinline__ void gemm_segments(int KT, int k1, int k2, const DmaPair<C::BM>& da,
-                                              const DmaPair<C::BN>& db, floatx16 (&acc)[C::TM][C::TN], char* smem,
+__device__ __forceinline__ void gemm_segments(int KT, int k1, int k2, DmaPair<C::BM>& da,
+                                              DmaPair<C::BN>& db, floatx16 (&acc)[C::TM][C::TN], char* smem,
                                               const void* zero) {
     half8 fa[2][C::TM], fb[2][C::TN];
     gemm_segment<C, false, false, ROLE>(0, k1, da, db, acc, fa, fb, smem, zero);
@@ -304,7 +340,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
                                           int b_k0, floatx16 (&acc)[C::TM][C::TN], char* smem, const void* zero,
                                           bool diag = false) {
     static_assert(C::S >= 3 && C::S <= 5, "pipeline depth");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -318,6 +354,8 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 #pragma unroll
     for (int t = 0; t < C::S - 1; ++t) {
         const uint32_t st = lds0 + t * C::STAGE_BYTES;
+        da.begin_tile(t);
+        db.begin_tile(t);
 #pragma unroll
         for (int q = 0; q < NA; ++q) da.issue_one(t, q, st + wave * NA * 1024, zero);
 #pragma unroll
