@@ -43,6 +43,30 @@ __device__ __forceinline__ Operand square_operand(const _Float16* p, const Ortho
     return op;
 }
 
+// Buffers of a matrix on the small-matrix path (kFlagSmall; ns_small.hip) inside OrthoMat: sq[i]
+// (R, Z, QA, QB, s_p x s_p) at M.small + i * sqe, their transposes after them, then the iterate
+// slots xw[2] (s_p x l_p, the wide orientation) and xwt[2] (their transposes); sizes in elements,
+// every buffer padded to multiples of 32 with zeros that stay zero.
+struct SmallView {
+    _Float16* base;
+    int sp, lp;          // s and l rounded up to 32
+    int64_t sqe, xe;     // elements of an s_p x s_p and of an s_p x l_p buffer
+    __device__ __forceinline__ _Float16* sq(int i) const { return base + i * sqe; }
+    __device__ __forceinline__ _Float16* sqt(int i) const { return base + (4 + i) * sqe; }
+    __device__ __forceinline__ _Float16* xw(int i) const { return base + 8 * sqe + i * xe; }
+    __device__ __forceinline__ _Float16* xwt(int i) const { return base + 8 * sqe + (2 + i) * xe; }
+};
+
+__device__ __forceinline__ SmallView small_view(const OrthoMat& M) {
+    SmallView v;
+    v.base = M.small;
+    v.sp = (M.s + 31) & ~31;
+    v.lp = (M.l + 31) & ~31;
+    v.sqe = int64_t(v.sp) * v.sp;
+    v.xe = int64_t(v.sp) * v.lp;
+    return v;
+}
+
 // First iterate, exact form (thorn.py:632-635): xb = f16(u / (||u||_F + 1e-8)) with
 // u = g + beta1 * m recomputed from the gradient (times the decouple_md gains: ortho_pre_kernel
 // writes g back for those matrices, as the reference's g.mul_ does) and the updated moment, the
@@ -67,7 +91,19 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
             if (r >= M.rows) break;
             const int64_t rb = (int64_t)r * M.cols;
             _Float16* xrow = M.xb + (int64_t)r * M.ldx;
-            if (vec) {
+            if (M.flags & kFlagSmall) {   // straight into both wide orientations of iterate slot 0
+                const SmallView V = small_view(M);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int c = c0 + lane + 64 * e;
+                    if (c >= M.cols) continue;
+                    const _Float16 x =
+                        (_Float16)(fmaf(ldg<float>(M.m + rb + c), beta1, ldg<float>(M.g + rb + c)) / denom);
+                    const int i = M.tall ? c : r, j = M.tall ? r : c;   // wide (s x l) position
+                    V.xw(0)[int64_t(i) * V.lp + j] = x;
+                    V.xwt(0)[int64_t(j) * V.sp + i] = x;
+                }
+            } else if (vec) {
                 const int c = c0 + 4 * lane;
                 if (c >= M.cols) continue;
                 const float4 g4 = ldg<float4>(M.g + rb + c), m4 = ldg<float4>(M.m + rb + c);

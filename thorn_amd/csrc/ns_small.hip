@@ -15,7 +15,7 @@
 //   xw[2], xwt[2]: the iterate in the wide orientation (s_p x l_p) and transposed (l_p x s_p),
 //     two slots; the iterate of a tall parameter is the transpose of its rows (thorn.py:629-630);
 //   sq[4], sqt[4]: R, Z, QA, QB (s_p x s_p) and their transposes.
-// The first iterate comes from xb (the parameter's orientation, written by ortho_cast_kernel);
+// The first iterate is written into xw[0] and xwt[0] by ortho_cast_kernel;
 // u' goes to xa in the parameter's orientation, with the per-row partial sums of u'^2 that the
 // per-row normalization needs.
 #include "ns_kernels.hip"
@@ -40,28 +40,6 @@ struct SmallSchedule {
     SmallOp op[2][kSmallMaxOps];   // [0] square matrices (plain quintic), [1] the others (Gram)
     int32_t n[2];
 };
-
-// Small-matrix buffers inside OrthoMat (see the plan): sq[i] at M.small + i * sqe, their
-// transposes after them, then xw[2], xwt[2]; sizes in elements.
-struct SmallView {
-    _Float16* base;
-    int sp, lp;          // s and l rounded up to 32
-    int64_t sqe, xe;     // elements of an s_p x s_p and of an s_p x l_p buffer
-    __device__ __forceinline__ _Float16* sq(int i) const { return base + i * sqe; }
-    __device__ __forceinline__ _Float16* sqt(int i) const { return base + (4 + i) * sqe; }
-    __device__ __forceinline__ _Float16* xw(int i) const { return base + 8 * sqe + i * xe; }
-    __device__ __forceinline__ _Float16* xwt(int i) const { return base + 8 * sqe + (2 + i) * xe; }
-};
-
-__device__ __forceinline__ SmallView small_view(const OrthoMat& M) {
-    SmallView v;
-    v.base = M.small;
-    v.sp = (M.s + 31) & ~31;
-    v.lp = (M.l + 31) & ~31;
-    v.sqe = int64_t(v.sp) * v.sp;
-    v.xe = int64_t(v.sp) * v.lp;
-    return v;
-}
 
 // Barrier of the C workgroups of one matrix: sense-reversing (count, generation) in the
 // workspace, agent-scope release on arrival and acquire on departure. The wait is bounded: a
@@ -92,56 +70,69 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err) {
 }
 
 // Operand panels in LDS: a super-tile of up to 128 x 128 outputs (up to 16 tiles of 32 x 32, one
-// per wave) is computed from K chunks of 64: rows [M0, M0+SM) of A and [N0, N0+SN) of BT, 64 halves
-// each, loaded by the whole workgroup with 16-byte loads (8 consecutive lanes per 128-byte row)
-// into one of two buffers while the other is consumed. Rows are 72 halves apart (16 bytes of
-// padding spread the fragment reads over the banks).
-constexpr int kPanelK = 64;
-constexpr int kPanelLd = kPanelK + 8;
-constexpr int kPanelRows = 256;                      // A rows then BT rows, 128 each at most
-constexpr int kPanelHalves = kPanelRows * kPanelLd;  // one buffer
+// per wave) is computed from K chunks of 32: rows [M0, M0+SM) of A and [N0, N0+SN) of BT, 64
+// bytes each, in the K-major stage layout of the large-matrix GEMM (chunk c of row r at
+// r * 64 + (c ^ ((r >> 2) & 3)) * 16: 16 lanes reading rows r..r+15 at one chunk cover all banks).
+// A ring of kSmallStages stages is filled by direct global-to-LDS loads, one 1 KB load per wave
+// per chunk (its 64 lanes fill 64 consecutive 16-byte slots: lane slot s holds the chunk whose
+// swizzled position is s), kSmallStages - 1 chunks ahead of the MFMAs: the products here are too
+// short to cover a load's latency, so three chunks (a K of 96) are in flight. Between products the
+// ring holds the waves' epilogue staging tiles.
+constexpr int kSmallStages = 4;
+constexpr int kSmallStageBytes = 2 * 128 * 64;   // A rows [0, 128), then BT rows [0, 128)
 
-// Loads chunk [k0, min(k0+64, K)) of the panels into buffer `buf` (rows past SM / SN and columns
-// past K are not loaded).
-__device__ __forceinline__ void panel_load(_Float16* buf, const _Float16* A, int64_t lda, const _Float16* BT,
-                                           int64_t ldb, int M0, int N0, int SM, int SN, int k0, int K) {
-    const int nch = (SM + SN) * (kPanelK / 8);
-    for (int ch = threadIdx.x; ch < nch; ch += kSmallThreads) {
-        const int r = ch >> 3, c8 = (ch & 7) * 8;
-        if (k0 + c8 >= K) continue;
-        const _Float16* src = r < SM ? A + int64_t(M0 + r) * lda + k0 + c8 : BT + int64_t(N0 + r - SM) * ldb + k0 + c8;
-        const int lr = r < SM ? r : 128 + (r - SM);
-        *reinterpret_cast<half8*>(buf + lr * kPanelLd + c8) = ldg<half8>(src);
-    }
+// This wave's direct loads except the newest n (0 <= n <= kSmallStages - 2, wave-uniform) are
+// complete, then the block barrier.
+__device__ __forceinline__ void wait_loads_barrier(int n) {
+    if (n >= 2) asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 }
+static_assert(kSmallStages - 2 == 2, "wait_loads_barrier covers 0 .. kSmallStages - 2");
 
 // acc (this wave's tile of the super-tile, if it has one) = A[M0.., 0:K] * B[0:K, N0..] with A
-// row-major (lda) and B given by its transpose BT row-major (ldb), K a multiple of 16 (chunks of
-// 64, the last one possibly shorter: its unused columns are neither loaded nor read). The whole
-// workgroup calls it (barriers inside); `panels` holds two buffers.
-__device__ __forceinline__ floatx16 small_block(_Float16* panels, const _Float16* A, int64_t lda, const _Float16* BT,
-                                                int64_t ldb, int M0, int N0, int SM, int SN, int K, int wave,
-                                                int lane, bool has_tile, int ti, int tj) {
+// row-major (lda) and B given by its transpose BT row-major (ldb), K a multiple of 32, every
+// operand row inside the padded buffers (rows past sm / sn read `zero`). The whole workgroup
+// calls it (barriers inside; the first one orders it after every wave's use of the staging tiles
+// in the ring); on return every load has landed and the stages are free.
+__device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, const _Float16* A, int64_t lda,
+                                                const _Float16* BT, int64_t ldb, int M0, int N0, int sm, int sn,
+                                                int K, int wave, int lane, bool has_tile, int ti, int tj) {
     floatx16 acc = {};
-    const int nk = (K + kPanelK - 1) / kPanelK;
-    panel_load(panels, A, lda, BT, ldb, M0, N0, SM, SN, 0, K);
-    for (int c = 0; c < nk; ++c) {
-        __syncthreads();   // chunk c is in buffer c & 1; buffer (c + 1) & 1 is free
-        if (c + 1 < nk) panel_load(panels + ((c + 1) & 1) * kPanelHalves, A, lda, BT, ldb, M0, N0, SM, SN,
-                                   (c + 1) * kPanelK, K);
+    const int nk = K / 32;
+    const int slot = wave * 64 + lane, part = slot >> 9, r = (slot >> 2) & 127;
+    const int c = (slot & 3) ^ ((r >> 2) & 3);
+    const bool ok = part == 0 ? r < sm : r < sn;
+    const char* src = reinterpret_cast<const char*>(part == 0 ? A + int64_t(M0 + r) * lda : BT + int64_t(N0 + r) * ldb) +
+                      16 * c;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(stages)) + wave * 1024;
+    auto issue = [&](int t) {
+        const void* p = ok ? static_cast<const void*>(src + int64_t(t) * 64) : zero;
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p),
+                     "{m0}"(lds0 + (t % kSmallStages) * kSmallStageBytes)
+                     : "memory");
+    };
+    __syncthreads();
+    const int pre = nk < kSmallStages - 1 ? nk : kSmallStages - 1;
+    for (int t = 0; t < pre; ++t) issue(t);
+    for (int kc = 0; kc < nk; ++kc) {
+        // this wave's loads of chunk kc have landed (the ones issued after it may still be in
+        // flight); after the barrier every wave's have, and nobody reads stage (kc - 1) % S any
+        // more, which then receives chunk kc + S - 1
+        const int ahead = nk - 1 - kc < kSmallStages - 2 ? nk - 1 - kc : kSmallStages - 2;
+        wait_loads_barrier(ahead);
+        if (kc + kSmallStages - 1 < nk) issue(kc + kSmallStages - 1);
         if (has_tile) {
-            const _Float16* buf = panels + (c & 1) * kPanelHalves;
-            const _Float16* pa = buf + (32 * ti + (lane & 31)) * kPanelLd + 8 * (lane >> 5);
-            const _Float16* pb = buf + (128 + 32 * tj + (lane & 31)) * kPanelLd + 8 * (lane >> 5);
-            const int kc = min(kPanelK, K - c * kPanelK);
-            for (int k = 0; k < kc; k += 16) {
-                const half8 a = *reinterpret_cast<const half8*>(pa + k);
-                const half8 b = *reinterpret_cast<const half8*>(pb + k);
+            const char* st = stages + (kc % kSmallStages) * kSmallStageBytes;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const half8 a = frag<128, true>(st, 32 * ti, ks, lane);
+                const half8 b = frag<128, true>(st + kSmallStageBytes / 2, 32 * tj, ks, lane);
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
             }
         }
     }
-    __syncthreads();   // every wave is done with the panels
+    __syncthreads();   // every wave is done with the stages
     return acc;
 }
 
@@ -154,25 +145,29 @@ constexpr int kStageLd = 34;
 // write by another lane is not visible to a single thread's program order.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Stages f16(alpha * acc + beta * C) of tile (m0, n0); C is read through its transpose CT
-// (4 contiguous halves per load).
+// This lane's C values of tile (m0, n0), read through C's transpose CT (4 contiguous halves per
+// load), in the accumulator layout: cv[g][e] is C[m0 + 8g + 4(lane / 32) + e][n0 + lane % 32].
+// Requested before the tile's product, so that their latency overlaps it.
+__device__ __forceinline__ void small_load_c(half4 (&cv)[4], const _Float16* CT, int64_t ldc, int m0, int n0,
+                                             int lane) {
+    const int j = lane & 31;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) cv[g] = ldg<half4>(CT + int64_t(n0 + j) * ldc + m0 + 8 * g + 4 * (lane >> 5));
+}
+
+// Stages f16(alpha * acc + beta * C) of tile (m0, n0), C from small_load_c (HAS_C).
+template <bool HAS_C>
 __device__ __forceinline__ void small_stage(const floatx16& acc, _Float16* stage, float alpha, float beta,
-                                            const _Float16* CT, int64_t ldc, int m0, int n0, int lane) {
+                                            const half4 (&cv)[4], int lane) {
     const int j = lane & 31;
     wave_lds_sync();   // the previous tile's reads of the staging are done
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int i0 = 8 * g + 4 * (lane >> 5);
-        float cv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (CT) {
-            const half4 c4 = ldg<half4>(CT + int64_t(n0 + j) * ldc + m0 + i0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) cv[e] = static_cast<float>(c4[e]);
-        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float t = alpha * acc[4 * g + e];
-            if (CT) t += beta * cv[e];
+            if (HAS_C) t += beta * static_cast<float>(cv[g][e]);
             stage[(i0 + e) * kStageLd + j] = static_cast<_Float16>(t);
         }
     }
@@ -231,29 +226,17 @@ __device__ __forceinline__ void small_store_final(const _Float16* stage, const O
 // workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
 __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
                                                                  SmallSchedule sc, int* err) {
-    __shared__ __attribute__((aligned(16))) _Float16 panels[2 * kPanelHalves];
-    __shared__ _Float16 stage_all[kSmallWaves][32 * kStageLd];
+    __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
+    static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
     const int k = find_task(tl.starts, tl.n, blockIdx.x);
     const OrthoMat& M = mats[tl.order[k]];
     const int member = blockIdx.x - tl.starts[k];
     const int C = tl.starts[k + 1] - tl.starts[k];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    _Float16* const stage = stage_all[wave];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    _Float16* const stage = reinterpret_cast<_Float16*>(stages) + wave * 32 * kStageLd;
     const SmallView V = small_view(M);
     int* const bar = M.small_bar;
     const int set = M.rows == M.cols ? 0 : 1;
-
-    // the first iterate in both orientations of the wide form
-    {
-        const int64_t n = int64_t(M.s) * M.l;
-        for (int64_t e = int64_t(member) * kSmallThreads + threadIdx.x; e < n; e += int64_t(C) * kSmallThreads) {
-            const int i = static_cast<int>(e / M.l), j = static_cast<int>(e % M.l);   // wide (s x l) index
-            const _Float16 x = M.tall ? M.xb[int64_t(j) * M.ldx + i] : M.xb[int64_t(i) * M.ldx + j];
-            V.xw(0)[int64_t(i) * V.lp + j] = x;
-            V.xwt(0)[int64_t(j) * V.sp + i] = x;
-        }
-    }
-    cluster_barrier(bar, C, err);
 
     const int nops = sc.n[set];
     for (int q = 0; q < nops; ++q) {
@@ -289,11 +272,15 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             const int M0 = 128 * (st % SR), N0 = 128 * (st / SR);
             const int sm = min(SM, orows - M0), sn = min(SN, ocols - N0);
             const bool mine = has_tile && 32 * ti < sm && 32 * tj < sn;
-            const floatx16 acc = small_block(panels, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine, ti, tj);
-            if (!mine) continue;
             const int m0 = M0 + 32 * ti, n0 = N0 + 32 * tj;
+            half4 cv[4] = {};
+            if (mine && CT) small_load_c(cv, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
+            const floatx16 acc = small_block(stages, M.zero, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine,
+                                             ti, tj);
+            if (!mine) continue;
             const float alpha = op.kind == kOpSym ? op.alpha : 1.f;
-            small_stage(acc, stage, alpha, op.beta, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
+            if (CT) small_stage<true>(acc, stage, alpha, op.beta, cv, lane);
+            else small_stage<false>(acc, stage, alpha, op.beta, cv, lane);
             if (op.kind == kOpGram) {
                 small_store(stage, V.sq(kBufR), V.sp, V.sqt(kBufR), V.sp, m0, n0, lane);
             } else if (op.kind == kOpSym) {
