@@ -166,76 +166,120 @@ def compulsory_bytes(mats, params, n_m) -> float:
 # CPU baseline: the oracle (restated reference eager path) on a bounded sample
 # ---------------------------------------------------------------------------------------------
 
-def cpu_baseline(config: int, budget_s: float = 30.0) -> dict:
-    """Times the oracle on one matrix of every distinct shape and on a slice of the Adam tensors,
-    then scales each by its count in the full step. Stops adding shapes once `budget_s` is spent
-    (the remaining shapes are then scaled from the measured time per flop)."""
+def host_cpu() -> dict:
+    """The host's CPU model, the ISA flags that decide CPU f16 GEMM speed, and the threads used."""
+    info = {'model': 'unknown', 'flags': [], 'threads': len(os.sched_getaffinity(0))}
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name') and info['model'] == 'unknown':
+                info['model'] = line.split(':', 1)[1].strip()
+            elif line.startswith('flags'):
+                have = set(line.split(':', 1)[1].split())
+                info['flags'] = sorted(f for f in ('avx2', 'avx512f', 'avx512_bf16', 'avx512_fp16', 'amx_bf16',
+                                                   'amx_fp16', 'amx_tile') if f in have)
+                break
+    except OSError:
+        pass
+    return info
+
+
+def gemm_probe(m: int = 256, k: int = 768, n: int = 256) -> dict:
+    """torch.baddbmm GFLOP/s on the CPU in f16, bf16 and f32 at one (m x k) (k x n) product: the
+    rate of the GEMMs the oracle (the reference's eager path) runs, which the host ISA decides."""
+    import torch
+    out = {'shape': f'{m}x{k}x{n}'}
+    gen = torch.Generator().manual_seed(0)
+    for name, dt in (('f16', torch.float16), ('bf16', torch.bfloat16), ('f32', torch.float32)):
+        a = torch.randn(1, m, k, generator=gen).to(dt)
+        b = torch.randn(1, k, n, generator=gen).to(dt)
+        c = torch.zeros(1, m, n, dtype=dt)
+        torch.baddbmm(c, a, b)   # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or time.perf_counter() - t0 < 0.2:
+            torch.baddbmm(c, a, b)
+            reps += 1
+            if time.perf_counter() - t0 > 2.0:
+                break
+        out[name + '_gflops'] = round(2.0 * m * k * n * reps / (time.perf_counter() - t0) / 1e9, 2)
+    return out
+
+
+def cpu_baseline(config: int, budget_s: float = 20.0) -> dict:
+    """The oracle (the reference's eager algorithm, oracle/thorn_oracle.py) timed on this host.
+
+    Per distinct matrix shape of the workload, cheapest first: one oracle step on one matrix of
+    that shape, timed when the f16 GEMM probe predicts it fits the remaining budget ('measured');
+    otherwise its time is the shape's schedule flops at the probe's f16 rate, times the ratio of
+    measured to probe-predicted time of the measured shapes, or of a 256 x 768 proxy matrix when
+    none was measured ('probe-scaled'). Each shape's time is multiplied by its count. The Adam
+    tensors are timed on a slice (at least 1 Mi elements) and scaled by element count."""
     import torch
     from oracle import thorn_oracle as O
 
-    threads = len(os.sched_getaffinity(0))
+    host = host_cpu()
+    threads = host['threads']
     torch.set_num_threads(threads)
+    probe = gemm_probe()
+    rate = probe['f16_gflops'] * 1e9   # flop/s of the oracle's f16 products
     gen = torch.Generator().manual_seed(3407)
     mats, others = config_shapes(config)
     counts = {}
     for sh in mats:
         counts[sh] = counts.get(sh, 0) + 1
     t_start = time.perf_counter()
-    per_shape = {}
 
-    def timed_steps(opt, p, shape, reps):
-        """Median of up to `reps` steps, stopping early once the budget is spent. The first step
-        also allocates the zero state (a negligible share next to Newton-Schulz on the CPU)."""
-        times = []
-        for _ in range(reps):
-            p.grad = torch.randn(shape, generator=gen) * 1e-3
-            t0 = time.perf_counter()
-            opt.step()
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_start > budget_s:
-                break
-        times.sort()
-        return times[len(times) // 2]
-
-    # the oracle runs the reference's schedules: Gram Newton-Schulz (restart before iteration 2 at
-    # the default coefficients) for every non-square matrix, the plain quintic for square ones
-    def ref_flops(sh):
+    def ref_flops(sh):   # Gram NS (restart before iteration 2) if non-square, else the plain quintic
         return schedule_flops([sh], 5, 0b100)
 
-    for sh in sorted(counts, key=ref_flops):   # cheapest shapes first
-        if time.perf_counter() - t_start > budget_s:
-            break
+    def one_step(sh):
         p = torch.nn.Parameter(torch.randn(sh, generator=gen) * 0.02)
         opt = O.OracleTHORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3, 'weight_decay': 0.1,
                               'scaling_mode': 'moonlight'}])
-        per_shape[sh] = timed_steps(opt, p, sh, 3)
-    measured_flops = sum(ref_flops(sh) for sh in per_shape)
-    sec_per_flop = sum(per_shape.values()) / max(measured_flops, 1.0)
-    est = 0.0
-    for sh, n in counts.items():
-        est += n * per_shape.get(sh, ref_flops(sh) * sec_per_flop)
-    # Adam: a 1/10 slice of the non-orthogonalized elements (at least 1 Mi)
+        p.grad = torch.randn(sh, generator=gen) * 1e-3
+        t0 = time.perf_counter()
+        opt.step()
+        return time.perf_counter() - t0
+
+    per_shape, ratios = {}, []
+    for sh in sorted(counts, key=ref_flops):
+        predicted = ref_flops(sh) / rate
+        left = budget_s - (time.perf_counter() - t_start)
+        if predicted < left:
+            t = one_step(sh)
+            ratios.append(t / predicted)
+            per_shape[sh] = {'count': counts[sh], 'gflop': round(ref_flops(sh) / 1e9, 2), 's': round(t, 3),
+                             'how': 'measured'}
+    if not ratios:   # calibrate on a proxy with the workload's most common aspect ratio
+        proxy = (256, 768)
+        ratios.append(one_step(proxy) / (ref_flops(proxy) / rate))
+    ratio = sorted(ratios)[len(ratios) // 2]
+    for sh in counts:
+        if sh not in per_shape:
+            per_shape[sh] = {'count': counts[sh], 'gflop': round(ref_flops(sh) / 1e9, 2),
+                             's': round(ref_flops(sh) / rate * ratio, 3), 'how': 'probe-scaled'}
+    est = sum(v['count'] * v['s'] for v in per_shape.values())
     adam_total = sum(math.prod(sh) for shapes, _ in others for sh in shapes)
-    adam_time = 0.0
-    sample = ''
+    adam = None
     if adam_total:
         n_slice = min(max(1 << 20, adam_total // 10), adam_total)
         p = torch.nn.Parameter(torch.randn(n_slice, generator=gen) * 0.02)
         opt = O.OracleTHORN([{'orthogonalize': False, 'params': [p], 'lr': 1e-3, 'weight_decay': 0.1}])
-        adam_time = timed_steps(opt, p, (n_slice,), 3) * adam_total / n_slice
-        sample = f' + Adam on {n_slice} of {adam_total} elements'
-    est += adam_time
-    wall = time.perf_counter() - t_start
-    try:
-        model = next(l.split(':', 1)[1].strip() for l in open('/proc/cpuinfo') if l.startswith('model name'))
-    except (OSError, StopIteration):
-        model = 'unknown'
+        ts = []
+        for _ in range(3):
+            p.grad = torch.randn(n_slice, generator=gen) * 1e-3
+            t0 = time.perf_counter()
+            opt.step()
+            ts.append(time.perf_counter() - t0)
+        adam_s = sorted(ts)[1] * adam_total / n_slice
+        adam = {'elements': adam_total, 'sampled': n_slice, 's': round(adam_s, 3)}
+        est += adam_s
+    n_meas = sum(v['how'] == 'measured' for v in per_shape.values())
     return {
-        'value': round(est * 1000.0, 1), 'unit': 'ms per full step (extrapolated)', 'cores': threads,
-        'kind': 'port',
-        'sample': (f'oracle step (median of up to 3, within a {budget_s:.0f} s budget) on one matrix of '
-                   f'each of {len(per_shape)}/{len(counts)} distinct shapes (cheapest first, the rest '
-                   f'scaled by flops){sample}, scaled by count; {wall:.1f} s of CPU work; host {model}'),
+        'value': round(est * 1000.0, 1), 'unit': 'ms per full step', 'cores': threads, 'kind': 'port',
+        'sample': f'{n_meas}/{len(per_shape)} shapes measured, rest probe-scaled; Adam sliced; '
+                  f'{time.perf_counter() - t_start:.0f} s',
+        'host': host, 'gemm_probe': probe, 'probe_to_oracle_ratio': round(ratio, 3),
+        'per_shape': {f'{r}x{c}': v for (r, c), v in per_shape.items()}, 'adam': adam,
     }
 
 
