@@ -507,6 +507,9 @@ def main() -> int:
                          'matrices skip Newton-Schulz, so the per-launch flops vary and no roofline is given)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--cpu-budget', type=float, default=20.0)
+    ap.add_argument('--polar-decomp-batch-size', type=int, default=None,
+                    help="elements per Newton-Schulz batch (the optimizer's polar_decomp_batch_size; "
+                         "default: the library's, one batch per group)")
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
     ap.add_argument('--vendor-gemm', action='store_true',
@@ -539,6 +542,8 @@ def main() -> int:
     gen_s = time.perf_counter() - t0
     n_m = len(mats)
     opt = thorn_amd.THORN(groups)
+    if args.polar_decomp_batch_size is not None:
+        opt.polar_decomp_batch_size = args.polar_decomp_batch_size
 
     def one_step():
         for p, g in zip(params, grads):
@@ -566,18 +571,18 @@ def main() -> int:
     gpu_ms = ev0.elapsed_time(ev1) / args.steps
 
     # per-kernel breakdown: the same K steps again with a HIP event pair around every launch
-    runners = list(opt._runners.values())
-    for r in runners:
-        r.plan.timing_enable(64 * args.steps)
+    plans = [pl for r in opt._runners.values() for pl in r.plans]
+    for pl in plans:
+        pl.timing_enable(64 * args.steps)
     for _ in range(args.steps):
         one_step()
     torch.cuda.synchronize()
     kinds: dict = {}
-    for r in runners:
-        for k, (ms, n) in r.plan.timing_read().items():
+    for pl in plans:
+        for k, (ms, n) in pl.timing_read().items():
             tot, cnt = kinds.get(k, (0.0, 0))
             kinds[k] = (tot + ms, cnt + n)
-        r.plan.timing_enable(0)
+        pl.timing_enable(0)
 
     grp0 = thorn_amd.optim._Group.from_kwargs(**opt.param_groups[0])
     mask = thorn_amd.optim._OrthoRunner.restart_mask(grp0, grp0.iters)
@@ -625,6 +630,9 @@ def main() -> int:
                    'matrices': n_m, 'adam_tensors': len(params) - n_m,
                    'ortho_elements': sum(r * c for r, c in mats),
                    'adam_elements': sum(p.numel() for p in params[n_m:]), 'ns_iters': 5,
+                   'polar_decomp_batch_size': opt.polar_decomp_batch_size,
+                   'workspace_bytes': sum({ws.data_ptr(): ws.numel() for r in opt._runners.values()
+                                           for ws in r.workspaces}.values()),
                    'ns_arith': 'f16 MFMA, fp32 accumulate; fp32 state'},
         'gpu_event_ms_per_step': round(gpu_ms, 3),
         'first_step_ms': round(first_ms, 1),

@@ -97,3 +97,15 @@ def test_reference_import_path():
     assert THORN is thorn_amd.THORN
     assert thorn.__all__ == ['THORN', 'THORNOrthoGroup', 'THORNNonOrthoGroup', 'THORNGroup']
     assert thorn.THORNOrthoGroup is thorn_amd.THORNOrthoGroup
+
+
+def test_polar_decomp_batches():
+    """polar_decomp_batch_size (thorn.py:1237, 1440): consecutive parameters, at most the limit's
+    elements per batch, a larger parameter alone, and 0 = every parameter alone."""
+    from thorn_amd.optim import _batches
+    ps = [torch.zeros(n) for n in (5, 3, 4, 10, 1, 1)]
+    sizes = lambda bs: [[p.numel() for p in b] for b in bs]
+    assert sizes(_batches(ps, 8)) == [[5, 3], [4], [10], [1, 1]]
+    assert sizes(_batches(ps, 0)) == [[5], [3], [4], [10], [1], [1]]
+    assert sizes(_batches(ps, 1 << 31)) == [[5, 3, 4, 10, 1, 1]]
+    assert thorn_amd.THORN.polar_decomp_batch_size == 2 * 1024 ** 3

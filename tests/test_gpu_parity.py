@@ -306,8 +306,56 @@ def test_many_matrices_share_launches():
     _log(f'[gpu]   {w}')
     # the small-matrix launch's cluster barriers all completed
     for r in gpu._runners.values():
-        status = r.workspace[_lib().WS_STATUS_OFFSET:_lib().WS_STATUS_OFFSET + 4].view(torch.int32).item()
-        assert status == 0, status
+        for ws in r.workspaces:
+            status = ws[_lib().WS_STATUS_OFFSET:_lib().WS_STATUS_OFFSET + 4].view(torch.int32).item()
+            assert status == 0, status
+
+
+BATCHED = [(1024, 1024), (512, 1536), (2048, 512), (96, 200), (300, 700), (1024, 512)]
+
+
+def test_batches_share_one_workspace():
+    """polar_decomp_batch_size (thorn.py:1237, 1440) caps the elements planned in one batch: six
+    matrices at 1.2e6 elements per batch make four plans, run in turn on one workspace, so no
+    plan may trust the first-iterate prescale factors in it (another plan stepped in between).
+    Three steps (the second and third would take the prescaled first iterate on a workspace of
+    their own), each matrix against the oracle run on device copies, teacher-forced."""
+    _log(f'[gpu] batches {BATCHED}')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(4321)
+    p0 = [torch.randn(sh, generator=g) * 0.02 for sh in BATCHED]
+    grp = dict(orthogonalize=True, lr=1e-2, weight_decay=0.1)
+    pg = [torch.nn.Parameter(p.clone().to(DEV)) for p in p0]
+    pc = [torch.nn.Parameter(p.clone().to(DEV)) for p in p0]
+    gpu = thorn_amd.THORN([dict(grp, params=pg)])
+    gpu.polar_decomp_batch_size = 1_200_000
+    ora = O.OracleTHORN([dict(grp, params=pc)])
+    w = {'dp': 0.0, 'state': 0.0}
+    for step in range(1, 4):
+        if step > 1:
+            _copy_state_to(gpu, pg, ora, pc)
+        grads = [torch.randn(sh, generator=g).to(DEV) * 1e-3 for sh in BATCHED]
+        before_g = [p.detach().clone() for p in pg]
+        before_c = [p.detach().clone() for p in pc]
+        for a, b, gr in zip(pg, pc, grads):
+            a.grad = gr.clone()
+            b.grad = gr.clone()
+        gpu.step()
+        ora.step()
+        torch.cuda.synchronize()
+        for i, sh in enumerate(BATCHED):
+            r = rel(pg[i].detach() - before_g[i], pc[i].detach() - before_c[i])
+            w['dp'] = max(w['dp'], r)
+            assert r <= DP_TOL, (step, sh, r)
+            for k, v in ora.state[pc[i]].items():
+                if torch.is_tensor(v):
+                    sr = rel(gpu.state[pg[i]][k], v)
+                    w['state'] = max(w['state'], sr)
+                    assert sr <= 1e-5, (step, sh, k, sr)
+    runners = list(gpu._runners.values())
+    assert len(runners) == 1 and len(runners[0].plans) == 4
+    assert len({ws.data_ptr() for ws in runners[0].workspaces}) == 1
+    _log(f'[gpu]   {w}')
 
 
 def test_ns_against_closed_form():

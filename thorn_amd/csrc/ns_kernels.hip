@@ -82,6 +82,31 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
     const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
     const float denom = M.scal[kScalDenom], beta1 = M.beta1;
     const bool vec = M.flags & kFlagVec4;
+    // The Newton-Schulz products read padding (columns past the matrix up to ld, and for the
+    // small path rows and columns up to multiples of 32) and must find zeros there. Every later
+    // iterate and product writes its padding from zero-padded inputs, so the first iterate's
+    // padding is cleared here: the workspace may hold another plan's data (plans of one group
+    // that run in turn on one workspace).
+    if (blockIdx.x == 0) {
+        if (M.flags & kFlagSmall) {
+            const SmallView V = small_view(M);
+            for (int e = threadIdx.x; e < (V.sp - M.s) * V.lp; e += 256) {   // rows s .. s_p
+                const int i = M.s + e / V.lp, j = e % V.lp;
+                V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
+                V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
+            }
+            for (int e = threadIdx.x; e < M.s * (V.lp - M.l); e += 256) {     // columns l .. l_p
+                const int i = e / (V.lp - M.l), j = M.l + e % (V.lp - M.l);
+                V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
+                V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
+            }
+        } else if (M.ldx > M.cols) {
+            for (int e = threadIdx.x; e < M.rows * (M.ldx - M.cols); e += 256) {
+                const int r = e / (M.ldx - M.cols), c = M.cols + e % (M.ldx - M.cols);
+                M.xb[int64_t(r) * M.ldx + c] = _Float16(0.f);
+            }
+        }
+    }
     for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
         const int tr = t / M.mom_tiles_c, tc = t % M.mom_tiles_c;
         const int r0 = tr * 16 + wave * 4, c0 = tc * 256;

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <unordered_map>
 #include <string>
 #include <vector>
 
@@ -402,6 +403,29 @@ int scratch_of_current_device(void** out) {
     return THORN_OK;
 }
 
+// Plans may share one workspace (the optimizer's batches of a group run in turn on one). The
+// first iterate's prescale factors a step leaves in the workspace belong to the plan that ran it,
+// so each workspace remembers the last plan that stepped on it.
+std::mutex g_ws_mu;
+std::unordered_map<const void*, const thorn_ortho_plan*> g_ws_last;
+
+const thorn_ortho_plan* last_plan_on(const void* ws) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    const auto it = g_ws_last.find(ws);
+    return it == g_ws_last.end() ? nullptr : it->second;
+}
+
+void note_step(const thorn_ortho_plan* plan) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    g_ws_last[plan->filled_ws] = plan;
+}
+
+void forget_plan(const thorn_ortho_plan* plan) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (auto it = g_ws_last.begin(); it != g_ws_last.end();)
+        it = it->second == plan ? g_ws_last.erase(it) : std::next(it);
+}
+
 }  // namespace
 
 namespace thorn {
@@ -624,7 +648,10 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     return THORN_OK;
 }
 
-void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan) { delete plan; }
+void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan) {
+    if (plan) forget_plan(plan);
+    delete plan;
+}
 
 size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan) { return plan ? plan->ws_bytes : 0; }
 
@@ -633,6 +660,8 @@ size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan) { return plan ? plan->ta
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host) {
     if (!plan || !table_dev || !table_host) return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: null argument");
+    // the prescale factors in the workspace are this plan's only if no other plan stepped on it since
+    const bool own_workspace = last_plan_on(workspace) == plan;
     const int n = static_cast<int>(plan->mats.size());
     if (n > 0 && (!steps || !workspace)) return fail(THORN_ERR_INVALID, "thorn_ortho_fill_table: null steps/workspace");
     if ((reinterpret_cast<uintptr_t>(workspace) % kAlign) != 0)
@@ -711,7 +740,8 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         // The first iterate of a large matrix is written directly in f16 with the previous step's
         // power-of-two scale (one pass less over u); small matrices, whose Newton-Schulz rounding
         // is not averaged out, and decouple_md ones take the exact form of thorn.py:632-635.
-        if (workspace == plan->stepped_ws && !md && !mds && int64_t(L.rows) * L.cols >= kPrescaleMinElems)
+        if (workspace == plan->stepped_ws && own_workspace && !md && !mds &&
+            int64_t(L.rows) * L.cols >= kPrescaleMinElems)
             flags |= thorn::kFlagPrescaled;
         else if (!L.adam) any_exact = true;
         if (S.magma_s) {
@@ -808,6 +838,7 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
                          dim3(md.total), dim3(256), 0, st, mats, md);
         }
         plan->stepped_ws = plan->filled_ws;
+        note_step(plan);
         return THORN_OK;
     }
     // The exact first iterate (and the rebuild of prescaled ones out of range): one row of blocks
@@ -882,6 +913,7 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     }
 #undef THORN_LAUNCH
     plan->stepped_ws = plan->filled_ws;
+    note_step(plan);
     return THORN_OK;
 }
 

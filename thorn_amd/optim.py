@@ -253,37 +253,47 @@ def _md_norm_rows(p: torch.Tensor, group: _Group) -> bool:
                               'on the MI355X path (supported: the last two dims, or the last dim)')
 
 
+def _plan_shapes(params: list, group: _Group, adam: bool, with_owner: bool = False):
+    """rows, cols and library flags of every matrix of `params` (a parameter with ndim > 2 is one
+    matrix per leading index, thorn.py:629), and with_owner: each matrix's parameter index and
+    index within it."""
+    rows, cols, flags, owner, sub = [], [], [], [], []
+    for i, p in enumerate(params):
+        r, c, batch = _matrix_view(p)
+        f = 0
+        if adam:
+            f |= _lib.MAT_ADAM | (_lib.MAT_NORM_ROWS if _md_norm_rows(p, group) else 0)
+        elif _needs_neuron_norm(p.shape, group):
+            f |= _lib.MAT_PER_ROW_NORM
+        if group.decouple_md:
+            f |= _lib.MAT_MD if (group.split_gain and p.ndim > 1) else _lib.MAT_MD_SCALAR
+        for b in range(batch):
+            rows.append(r)
+            cols.append(c)
+            flags.append(f)
+            owner.append(i)
+            sub.append(b)
+    return (rows, cols, flags, owner, sub) if with_owner else (rows, cols, flags)
+
+
 class _OrthoRunner:
     """One orthogonalized parameter set (or, with adam=True, the decouple_md tensors of a
     non-orthogonalized group, whose update is the Adam step): plan, workspace and the per-step
     table."""
 
-    def __init__(self, params: list, group: _Group, device: torch.device, adam: bool = False):
+    def __init__(self, params: list, group: _Group, device: torch.device, adam: bool = False,
+                 workspace: Optional[torch.Tensor] = None):
         self.params = params
         self.device = device
         self.adam = adam
-        rows, cols, flags, owner, sub = [], [], [], [], []
-        for i, p in enumerate(params):
-            r, c, batch = _matrix_view(p)
-            f = 0
-            if adam:
-                f |= _lib.MAT_ADAM | (_lib.MAT_NORM_ROWS if _md_norm_rows(p, group) else 0)
-            elif _needs_neuron_norm(p.shape, group):
-                f |= _lib.MAT_PER_ROW_NORM
-            if group.decouple_md:
-                f |= _lib.MAT_MD if (group.split_gain and p.ndim > 1) else _lib.MAT_MD_SCALAR
-            for b in range(batch):
-                rows.append(r)
-                cols.append(c)
-                flags.append(f)
-                owner.append(i)
-                sub.append(b)
+        rows, cols, flags, owner, sub = _plan_shapes(params, group, adam, with_owner=True)
         self.rows = np.asarray(rows, dtype=np.int64)
         self.cols = np.asarray(cols, dtype=np.int64)
         self.owner = owner
         self.sub = np.asarray(sub, dtype=np.int64)
         self.plan = _lib.OrthoPlan(rows, cols, flags)
-        self.workspace = torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
+        self.workspace = (torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
+                          if workspace is None else workspace)
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
         self.md = group.decouple_md
@@ -386,6 +396,55 @@ class _OrthoRunner:
         return sum(1 << i for i in group.restarts if 0 < i < iters)
 
 
+def _batches(params: list, limit: int) -> list:
+    """Consecutive runs of parameters of at most `limit` elements each (one parameter alone when
+    it is larger; limit <= 0: every parameter alone), the reference's polar_decomp_batch_size
+    (thorn.py:1237, 1440) applied to a plan's parameters."""
+    out, cur, n = [], [], 0
+    for p in params:
+        k = p.numel()
+        if cur and (limit <= 0 or n + k > limit):
+            out.append(cur)
+            cur, n = [], 0
+        cur.append(p)
+        n += k
+    if cur:
+        out.append(cur)
+    return out
+
+
+class _OrthoBatches:
+    """A group's orthogonalized parameters in batches of at most polar_decomp_batch_size elements
+    (thorn.py:1237, 1440): one plan per batch, run in turn on one workspace sized for the largest,
+    so the Newton-Schulz buffers of only one batch exist at a time. Plans that share a workspace
+    take the exact first iterate (the library keeps the cheaper prescaled one for a plan that
+    stepped last on its workspace)."""
+
+    def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False):
+        batches = _batches(params, limit)
+        self.runners = []
+        workspace = None
+        if len(batches) > 1:
+            sizes = [_lib.OrthoPlan(*_plan_shapes(b, group, adam)).workspace_bytes for b in batches]
+            workspace = torch.zeros(max(1, max(sizes)), dtype=torch.uint8, device=device)
+        for b in batches:
+            self.runners.append(_OrthoRunner(b, group, device, adam, workspace))
+        self.workspace_bytes = (workspace.numel() if workspace is not None
+                                else self.runners[0].workspace.numel())
+
+    @property
+    def plans(self) -> list:
+        return [r.plan for r in self.runners]
+
+    @property
+    def workspaces(self) -> list:
+        return [r.workspace for r in self.runners]
+
+    def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None) -> None:
+        for r in self.runners:
+            r.run(opt, group, unmasked)
+
+
 class _AdamRunner:
     """All tensors of the non-orthogonalized groups of one step: one multi-tensor launch."""
 
@@ -396,6 +455,14 @@ class _AdamRunner:
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
         self.workspace = torch.empty(max(256, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
+
+    @property
+    def plans(self) -> list:
+        return [self.plan]
+
+    @property
+    def workspaces(self) -> list:
+        return [self.workspace]
 
     def run(self, entries: list, update_rate: int = 1, unmasked: Optional[dict] = None) -> None:
         """entries: (p, state, group) per tensor, in plan order. A tensor's parameter is written
@@ -431,7 +498,12 @@ class THORN(Optimizer):
     """Drop-in for pykeio/THORN's ``THORN`` (thorn.py:1229-1776) on one MI355X."""
 
     param_groups: list
-    polar_decomp_batch_size: int = 32 * 1024 * 1024   # accepted for compatibility (thorn.py:1237)
+    # Elements of the parameters whose Newton-Schulz runs in one batch (thorn.py:1237, 1440): a
+    # group's orthogonalized parameters are planned in consecutive batches of at most this many
+    # elements (0: one parameter per batch), run in turn on one workspace. The reference's default
+    # is 32 Mi elements; here it is 2 Gi, so that a group is one batch on a 288 GB MI355X: the
+    # grouped launches over all of a group's matrices are what fills the GPU.
+    polar_decomp_batch_size: int = 2 * 1024 * 1024 * 1024
 
     @overload
     def __init__(self, params: nn.Module, *, lr: float, none_grad: bool = True, weight_decay: float = 0.1,
@@ -638,15 +710,17 @@ class THORN(Optimizer):
         for dev, ps in by_dev.items():
             with torch.cuda.device(dev):
                 if group.orthogonalize:
+                    limit = int(self.polar_decomp_batch_size)
                     key = ('ortho', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
                            group.decouple_md, group.split_gain, group.force_per_neuron_norm,
-                           group.betas[1] > 0)
-                    runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev))
+                           group.betas[1] > 0, limit)
+                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit))
                     runner.run(self, group, unmasked)
                 elif group.decouple_md:   # Adam step inside the decouple_md round trip (thorn.py:1704-1721)
+                    limit = int(self.polar_decomp_batch_size)
                     key = ('mdadam', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
-                           group.split_gain, tuple(_md_norm_rows(p, group) for p in ps))
-                    runner = self._runner(key, lambda: _OrthoRunner(ps, group, dev, adam=True))
+                           group.split_gain, tuple(_md_norm_rows(p, group) for p in ps), limit)
+                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, adam=True))
                     runner.run(self, group, unmasked)
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
