@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 5
+#define THORN_ABI_VERSION 6
 
 enum {
     THORN_OK = 0,
@@ -105,7 +105,8 @@ typedef struct ThornOrthoMatStep {
     float adam_beta2, adam_w1, adam_w2;    /* beta2, 1 - beta1, 1 - beta2 */
     float adam_bc1, adam_bc2, adam_eps;    /* bias corrections; eps 0 selects Adam-atan2 */
     int32_t adam_degenerate;               /* rect == 0: u = m (thorn.py:883-885) */
-    int32_t reserved2;
+    float pnn_eps;        /* per-row normalization's eps, torch.finfo(p.dtype).eps (thorn.py:720);
+                             0 selects float32's */
 } ThornOrthoMatStep;
 
 typedef struct thorn_ortho_plan* thorn_ortho_plan_t;

@@ -109,3 +109,13 @@ def test_polar_decomp_batches():
     assert sizes(_batches(ps, 0)) == [[5], [3], [4], [10], [1], [1]]
     assert sizes(_batches(ps, 1 << 31)) == [[5, 3, 4, 10, 1, 1]]
     assert thorn_amd.THORN.polar_decomp_batch_size == 2 * 1024 ** 3
+
+
+def test_fp16_and_fp64_parameters_are_refused():
+    """bf16 and fp32 parameters step; fp16 and fp64 raise before anything is computed."""
+    for dt in (torch.float16, torch.float64):
+        p = nn.Parameter(torch.zeros(3, 3, dtype=dt))
+        opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3}])
+        p.grad = torch.zeros(3, 3, dtype=dt)
+        with pytest.raises(NotImplementedError, match='fp32 and bf16'):
+            opt.step()

@@ -15,6 +15,7 @@ Inputs are generated on the CPU and copied bit for bit to the GPU.
 from __future__ import annotations
 
 import copy
+import math
 import sys
 
 import numpy as np
@@ -82,9 +83,10 @@ def _copy_state_to(gpu_opt, gpu_params, cpu_opt, cpu_params):
                     gst[k] = v
 
 
-def exact_dp(p_old, g, m_prev, group: dict):
+def exact_dp(p_old, g, m_prev, group: dict, eps: float = float(torch.finfo(torch.float32).eps)):
     """The reference's step for one non-md orthogonalized matrix in float64 with the exact polar
-    map (thorn.py:1376-1381, 626-662 closed form, 704-766, 669-702)."""
+    map (thorn.py:1376-1381, 626-662 closed form, 704-766, 669-702); eps: per-row normalization's,
+    torch.finfo(p.dtype).eps (:720)."""
     grp = O.Group.from_dict(dict(group, params=[]))
     b1 = grp.betas[0]
     g64, m64, p64 = g.double(), m_prev.double(), p_old.double().clone()
@@ -94,7 +96,6 @@ def exact_dp(p_old, g, m_prev, group: dict):
     up = O.polar_closed_form(u, coeffs)
     lr = grp.lr * O.lr_scale_ortho(up, grp)
     if O.needs_neuron_norm(p_old, grp):
-        eps = float(torch.finfo(torch.float32).eps)
         v_norm = up.norm(dim=(-2, -1), keepdim=True)
         up = up * up.square().mean(dim=-1, keepdim=True).clamp_min(eps).rsqrt()
         up = up * (v_norm / up.norm(dim=(-2, -1), keepdim=True).clamp_min(eps))
@@ -356,6 +357,85 @@ def test_batches_share_one_workspace():
     assert len(runners) == 1 and len(runners[0].plans) == 4
     assert len({ws.data_ptr() for ws in runners[0].workspaces}) == 1
     _log(f'[gpu]   {w}')
+
+
+def test_low_precision_and_strided_parameters():
+    """bf16 parameters (the reference's README trains a bf16 model, thorn.py:1404 casts the
+    update to p.dtype) and a non-contiguous fp32 parameter step through fp32 working copies;
+    the parameter and its state are rounded to their dtype once per step where the reference
+    rounds after every torch op, and per-row normalization takes the dtype's eps (thorn.py:720).
+    Three teacher-forced steps against the oracle on device copies (the reference's own
+    low-precision arithmetic). Bars: fp32 ones for the strided parameter; for bf16 the state
+    within 1e-2 relative, and each matrix's update, measured against the exact step from
+    the same low-precision inputs (float64, exact polar map, the dtype's eps), no farther from it
+    than 2e-2 or 1.5 times the reference's own distance, whichever is larger; the vectors' Adam
+    update within 5e-2 of the reference's (the reference rounds each of its ops to bf16)."""
+    _log('[gpu] bf16 / strided parameters')
+    thorn_amd = _thorn()
+    g = torch.Generator(device=DEV).manual_seed(777)
+    def mk(shape, dtype, transposed=False):
+        t = torch.randn(shape, generator=g, device=DEV) * 0.02
+        t = t.t() if transposed else t
+        return t.to(dtype)
+    specs = [((512, 256), torch.bfloat16, False), ((256, 768), torch.bfloat16, False),
+             ((384, 384), torch.bfloat16, False), ((96, 40), torch.bfloat16, False),
+             ((256, 512), torch.bfloat16, False), ((128, 320), torch.float32, True)]
+    vecs = [((1024,), torch.bfloat16), ((300,), torch.bfloat16)]
+    def build():
+        ps = [torch.nn.Parameter(mk(sh, dt, tr)) for sh, dt, tr in specs]
+        vs = [torch.nn.Parameter(torch.ones(sh, device=DEV, dtype=dt)) for sh, dt in vecs]
+        return ps, vs
+    pg, vg = build()
+    pc = [torch.nn.Parameter(p.detach().clone()) for p in pg]
+    vc = [torch.nn.Parameter(v.detach().clone()) for v in vg]
+    assert not pg[-1].is_contiguous()
+    grp = dict(lr=1e-2, weight_decay=0.1)
+    gpu = thorn_amd.THORN([dict(grp, orthogonalize=True, params=pg), dict(grp, orthogonalize=False, params=vg)])
+    ora = O.OracleTHORN([dict(grp, orthogonalize=True, params=pc), dict(grp, orthogonalize=False, params=vc)])
+    allg, allc = pg + vg, pc + vc
+    w = {'bf16_state': 0.0, 'bf16_dp': 0.0, 'fp32_dp': 0.0, 'fp32_state': 0.0}
+    for step in range(1, 4):
+        if step > 1:
+            _copy_state_to(gpu, allg, ora, allc)
+        before_g = [p.detach().clone() for p in allg]
+        before_c = [p.detach().clone() for p in allc]
+        m_prev = [ora.state[b]['moment'].clone() if 'moment' in ora.state[b] else torch.zeros_like(b)
+                  for b in allc]
+        grads = []
+        for a, b in zip(allg, allc):
+            gr = (torch.randn(a.shape, generator=g, device=DEV) * 1e-3).to(a.dtype)
+            grads.append(gr)
+            a.grad = gr.clone()
+            b.grad = gr.clone()
+        gpu.step()
+        ora.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(allg, allc)):
+            dpg, dpc = (a.detach() - before_g[i]).float(), (b.detach() - before_c[i]).float()
+            r = rel(dpg, dpc)
+            low = a.dtype != torch.float32
+            if low and i < len(pg):
+                dpe = exact_dp(before_c[i].cpu(), grads[i].cpu(), m_prev[i].cpu(), dict(grp, orthogonalize=True),
+                               eps=float(torch.finfo(a.dtype).eps)).float()
+                r_ex, ref_ex = rel(dpg.cpu(), dpe), rel(dpc.cpu(), dpe)
+                w['bf16_dp'] = max(w['bf16_dp'], r)
+                w['bf16_vs_exact'] = max(w.get('bf16_vs_exact', 0.0), r_ex)
+                w['bf16_ref_vs_exact'] = max(w.get('bf16_ref_vs_exact', 0.0), ref_ex)
+                assert r_ex <= max(DP_TOL, 1.5 * ref_ex), (step, i, tuple(a.shape), a.dtype, r, r_ex, ref_ex)
+            elif low:
+                w['bf16_dp'] = max(w['bf16_dp'], r)
+                assert r <= 5e-2, (step, i, tuple(a.shape), a.dtype, r)
+            else:
+                w['fp32_dp'] = max(w['fp32_dp'], r)
+                assert r <= DP_TOL, (step, i, r)
+            for k, v in ora.state[b].items():
+                if torch.is_tensor(v):
+                    sr = rel(gpu.state[a][k].float(), v.float())
+                    assert gpu.state[a][k].dtype == v.dtype, (k, gpu.state[a][k].dtype, v.dtype)
+                    key = 'bf16_state' if low else 'fp32_state'
+                    w[key] = max(w[key], sr)
+                    assert sr <= (1e-2 if low else 1e-5), (step, i, k, sr)
+        _log(f'[gpu]   step {step}: {w}')
 
 
 def test_ns_against_closed_form():

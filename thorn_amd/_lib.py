@@ -47,7 +47,7 @@ ORTHO_MAT_STEP = np.dtype([
     ('v', np.uint64),
     ('adam_beta2', np.float32), ('adam_w1', np.float32), ('adam_w2', np.float32),
     ('adam_bc1', np.float32), ('adam_bc2', np.float32), ('adam_eps', np.float32),
-    ('adam_degenerate', np.int32), ('reserved2', np.int32),
+    ('adam_degenerate', np.int32), ('pnn_eps', np.float32),
 ], align=True)
 ADAM_TENSOR_STEP = np.dtype([
     ('p', np.uint64), ('g', np.uint64), ('m', np.uint64), ('v', np.uint64),
@@ -96,7 +96,7 @@ KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_f
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
 NOALLOC_SCRATCH_BYTES = 32 << 20
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 

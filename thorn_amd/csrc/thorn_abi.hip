@@ -716,6 +716,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
         M.v = S.v;
         M.adam_beta2 = S.adam_beta2; M.adam_w1 = S.adam_w1; M.adam_w2 = S.adam_w2;
         M.adam_bc1 = S.adam_bc1; M.adam_bc2 = S.adam_bc2; M.adam_eps = S.adam_eps;
+        M.pnn_eps = S.pnn_eps > 0.f ? S.pnn_eps : 1.1920928955078125e-07f;   // torch.finfo(torch.float32).eps
         M.magma_s = S.magma_s;
         M.magma_n = 0;
         if (S.magma_s && (i == 0 || steps[i - 1].magma_s != S.magma_s)) {   // first matrix of a parameter

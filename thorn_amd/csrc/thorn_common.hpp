@@ -246,6 +246,7 @@ struct OrthoMat {
     _Float16* small;     // kFlagSmall: the small-matrix iterates and s x s buffers (ns_small.hip)
     int* small_bar;      // kFlagSmall: the cluster barrier (count, generation)
     int32_t rowsq_tiles; // partial sums per row in rowsqpart (column tiles of the last update)
+    float pnn_eps;       // per-row normalization's eps: torch.finfo(p.dtype).eps (thorn.py:720)
 };
 
 enum ScalSlot : int {

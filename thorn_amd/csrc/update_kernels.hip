@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __r
                                                              const int32_t* __restrict__ idx) {
     __shared__ float scratch[4];
     const OrthoMat& M = mats[idx[blockIdx.x]];
-    const float eps = 1.1920928955078125e-07f;   // torch.finfo(torch.float32).eps
+    const float eps = M.pnn_eps;   // torch.finfo(p.dtype).eps
     float tot = 0.f, nw = 0.f;
     for (int i = threadIdx.x; i < M.rows; i += 256) {
         float rs = 0.f;

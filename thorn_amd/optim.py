@@ -16,11 +16,13 @@ group with it take the Adam step inside the same gain round trip as the matrices
 
 Not implemented on this path (each raises ``NotImplementedError`` instead of silently changing
 behaviour): DTensor/FSDP2 parameters (thorn.py:979-1186, 1459-1581), a ``decouple_md`` norm axis
-other than the last two dims or the last dim, and non-fp32 parameters.
+other than the last two dims or the last dim, dtypes other than fp32 and bf16, and a sparse
+gradient on a parameter that is not contiguous fp32.
 """
 from __future__ import annotations
 
 import math
+import weakref
 from dataclasses import dataclass, field, fields, MISSING
 from functools import partial
 from typing import Any, Callable, Literal, Optional, Union, cast, overload
@@ -221,13 +223,59 @@ def _magma_unmasked(state: dict) -> bool:
     return draw % 2 == 0
 
 
+# Storage types of parameters, gradients and state. Others than contiguous fp32 step through fp32
+# working copies (_Shadow). fp16 is not among them: the reference's fp16 Adam underflows g^2
+# (1e-6 at a 1e-3 gradient) where fp32 arithmetic does not, so its trajectory is not one an fp32
+# computation can follow.
+_DTYPES = (torch.float32, torch.bfloat16)
+
+
 def _check_tensor(t: torch.Tensor, what: str) -> None:
-    if t.dtype != torch.float32:
-        raise NotImplementedError(f'THORN on MI355X supports fp32 tensors only; {what} is {t.dtype}')
+    if t.dtype not in _DTYPES:
+        raise NotImplementedError(f'THORN on MI355X supports fp32 and bf16 tensors; {what} is {t.dtype}')
     if not t.is_cuda:
         raise RuntimeError(f'THORN on MI355X needs device tensors; {what} is on {t.device}')
-    if not t.is_contiguous():
-        raise NotImplementedError(f'THORN on MI355X needs contiguous tensors; {what} is not')
+
+
+def _needs_shadow(p: torch.Tensor) -> bool:
+    g = p.grad
+    return (p.dtype != torch.float32 or not p.is_contiguous() or
+            (g is not None and not g.is_sparse and (g.dtype != torch.float32 or not g.is_contiguous())))
+
+
+class _Shadow:
+    """The fp32 working copy of a parameter that is not contiguous fp32 (a bf16 model, thorn.py
+    README's gradient-release example; a strided view): a contiguous fp32 parameter with a gradient
+    buffer and fp32 copies of the state tensors, loaded from the parameter and its state before
+    the step and written back after it. The kernels then run their fp32 arithmetic; the parameter
+    and its state are rounded to their own dtype once per step (the reference rounds after every
+    torch op, thorn.py:1381, 1404, 702), and per-row normalization uses the dtype's eps (:720)."""
+
+    def __init__(self, p: torch.Tensor):
+        self.param = torch.nn.Parameter(torch.empty(p.shape, dtype=torch.float32, device=p.device),
+                                        requires_grad=False)
+        self.param._thorn_dtype = p.dtype
+        self.grad = torch.empty(p.shape, dtype=torch.float32, device=p.device)
+        self.state: dict = {}
+
+    def load(self, p: torch.Tensor, state: dict) -> None:
+        self.param.data.copy_(p.detach())
+        self.grad.copy_(p.grad)
+        self.param.grad = self.grad
+        for k, v in state.items():
+            if torch.is_tensor(v):
+                if k not in self.state or self.state[k].shape != v.shape:
+                    self.state[k] = torch.empty(v.shape, dtype=torch.float32, device=v.device)
+                self.state[k].copy_(v)
+            else:
+                self.state[k] = v
+
+    def store(self, p: torch.Tensor, state: dict) -> None:
+        with torch.no_grad():
+            p.copy_(self.param.data)
+        for k, v in state.items():
+            if torch.is_tensor(v):
+                v.copy_(self.state[k])
 
 
 def _matrix_view(p: torch.Tensor) -> tuple:
@@ -307,7 +355,7 @@ class _OrthoRunner:
         own = self.owner
         p_ptr = np.asarray([p.data_ptr() for p in params], dtype=np.uint64)[own]
         g_ptr = np.asarray([p.grad.data_ptr() for p in params], dtype=np.uint64)[own]
-        states = [opt.state[p] for p in params]
+        states = [opt._state_of(p) for p in params]
         m_ptr = np.asarray([s['moment'].data_ptr() for s in states], dtype=np.uint64)[own]
         steps['p'] = p_ptr + bytes_off.astype(np.uint64)
         steps['g'] = g_ptr + bytes_off.astype(np.uint64)
@@ -333,6 +381,8 @@ class _OrthoRunner:
             steps['eta'] = (group.lr * scale)[own]
         steps['weight_decay'] = group.weight_decay
         steps['beta1'] = group.betas[0]
+        steps['pnn_eps'] = np.asarray([torch.finfo(getattr(p, '_thorn_dtype', p.dtype)).eps
+                                       for p in params], dtype=np.float32)[own]
         # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
         # momentum (and the decouple_md round trip) runs every step
         due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 and (unmasked is None or unmasked[id(p)])
@@ -520,6 +570,8 @@ class THORN(Optimizer):
     def __init__(self, params, *, backend=torch.cuda, **conf):
         _lib.load()   # fail at construction, not at the first step, when the library is missing
         self._update_rate = 1
+        self._shadows: dict = {}         # id(parameter) -> _Shadow, dropped with the parameter
+        self._shadow_state: dict = {}    # id(shadow parameter) -> its fp32 state
         self.backend = backend
         groups = THORN._auto_assign(params, **conf) if isinstance(params, nn.Module) else params
         for group in groups:
@@ -603,8 +655,9 @@ class THORN(Optimizer):
             raise AssertionError(f'gradient shape {tuple(g.shape)} != parameter shape {tuple(p.shape)}')
         _check_tensor(p, 'parameter')
         if g.is_sparse:
-            if g.dtype != torch.float32 or not g.is_cuda:
-                raise NotImplementedError('THORN on MI355X needs fp32 device gradients')
+            if g.dtype != torch.float32 or not g.is_cuda or p.dtype != torch.float32 or not p.is_contiguous():
+                raise NotImplementedError('THORN on MI355X needs a contiguous fp32 parameter and gradient '
+                                          'for a sparse gradient')
         else:
             _check_tensor(g, 'gradient')
         if g.device != p.device:
@@ -704,9 +757,25 @@ class THORN(Optimizer):
             self.state[p]['step'] += 1
         if not live:
             return
+        # parameters that are not contiguous fp32 step through their fp32 working copies
+        shadows = {}
+        for p in live:
+            if _needs_shadow(p):
+                sh = self._shadows.get(id(p))
+                if sh is None or sh.param.shape != p.shape:
+                    if sh is None:
+                        weakref.finalize(p, self._drop_shadow, id(p))
+                    else:
+                        self._shadow_state.pop(id(sh.param), None)
+                    sh = self._shadows[id(p)] = _Shadow(p)
+                    self._shadow_state[id(sh.param)] = sh.state
+                sh.load(p, self.state[p])
+                shadows[p] = sh
+                if unmasked is not None:
+                    unmasked[id(sh.param)] = unmasked[id(p)]
         by_dev: dict = {}
         for p in live:
-            by_dev.setdefault(p.device, []).append(p)
+            by_dev.setdefault(p.device, []).append(shadows[p].param if p in shadows else p)
         for dev, ps in by_dev.items():
             with torch.cuda.device(dev):
                 if group.orthogonalize:
@@ -725,11 +794,23 @@ class THORN(Optimizer):
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
                     runner = self._runner(key, lambda: _AdamRunner(ps, dev))
-                    runner.run([(p, self.state[p], group) for p in ps], self._update_rate, unmasked)
+                    runner.run([(p, self._state_of(p), group) for p in ps], self._update_rate, unmasked)
+        for p, sh in shadows.items():
+            sh.store(p, self.state[p])
         for p in live:
             if group.none_grad:
                 p.grad = None
             self.state[p]['step'] += 1
+
+    def _drop_shadow(self, key: int) -> None:
+        sh = self._shadows.pop(key, None)
+        if sh is not None:
+            self._shadow_state.pop(id(sh.param), None)
+
+    def _state_of(self, p: torch.Tensor) -> dict:
+        """The state a runner reads: a working copy's (_Shadow), or the parameter's own."""
+        st = self._shadow_state.get(id(p))
+        return st if st is not None else self.state[p]
 
     @overload
     def step(self, closure: None = None, *, param: Optional[torch.nn.Parameter] = None) -> None: ...
