@@ -148,43 +148,14 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
     }
 }
 
-// Buffer access to an s x ld f16 workspace matrix. Every load and store of the symmetric
-// epilogue is a buffer instruction issued unconditionally: a chunk outside the matrix, or one the
-// epilogue does not write, gets the offset kOutOfRange, past the resource's size, so the load
-// returns zeros and the store is dropped. With no conditional memory operation, the compiler's
-// waits count exactly the operations still needed (a conditional one made it wait for every
-// outstanding store before each chunk). A null matrix gets a resource of size 0: all zeros.
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t kOutOfRange = 0x80000000u;   // > the byte size of any matrix (s <= 32768)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t sym_rsrc(const _Float16* m, int64_t ld, int n) {
-    const uint32_t bytes = m ? static_cast<uint32_t>(int64_t(n) * ld * 2) : 0u;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(m), 0, static_cast<int>(bytes), 0x00020000);
-}
-__device__ __forceinline__ uint32_t sym_off(bool ok, int r, int c, int64_t ld) {
-    return ok ? static_cast<uint32_t>((int64_t(r) * ld + c) * 2) : kOutOfRange;
-}
-__device__ __forceinline__ half8v buf_load8(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
-    return __builtin_bit_cast(half8v, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
-}
+// Epilogue stores are buffer instructions issued unconditionally: a chunk outside the matrix gets
+// the offset kOutOfRange, past the resource's size, and the store is dropped. With no conditional
+// memory operation, the compiler's waits count exactly the operations still needed (a conditional
+// one made it wait for every outstanding store before each chunk).
 // aux 2: non-temporal
 template <int AUX = 0>
 __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t rs, uint32_t off, const half8v& v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, static_cast<int>(off), 0, AUX);
-}
-
-constexpr int kRowChunks = EpiH<NsCfg>::ROW_ITERS;   // row chunks of a tile per thread
-
-// Csym row chunks first .. first + N - 1 of this thread (zeros outside the matrix).
-template <int N>
-__device__ __forceinline__ void sym_load(half8v (&cv)[N], __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0,
-                                         int n0, int first) {
-    const int tr = threadIdx.x >> 5, c8 = (threadIdx.x & 31) * 8;
-#pragma unroll
-    for (int it = 0; it < N; ++it) {
-        const int r = m0 + 8 * (first + it) + tr, c = n0 + c8;
-        cv[it] = buf_load8(crs, sym_off(r < n && c < ld, r, c, ld));
-    }
 }
 
 // Row pass: stores the staged f16 tile (rows m0.. below n, columns n0..) into `out` through a
@@ -201,57 +172,38 @@ __device__ __forceinline__ void store_staged(const char* smem, _Float16* out, in
     each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) { buf_store8<2>(trs, vbase + it * rstep, h); });
 }
 
-// Copies the row chunks of an f16 matrix tile (rows m0 + r < n, columns n0 + c < ld of a matrix
-// with leading dimension ld; zeros elsewhere) into the staging, 8 chunks in flight at a time.
-template <class C>
-__device__ __forceinline__ void stage_rows(char* smem, __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0, int n0) {
-    using E = EpiH<C>;
-    _Float16* const base = reinterpret_cast<_Float16*>(smem) + row_chunk_base();
-#pragma unroll
-    for (int h = 0; h < kRowChunks; h += 8) {
-        half8v cv[8];
-        sym_load(cv, crs, ld, n, m0, n0, h);
-#pragma unroll
-        for (int it = 0; it < 8; ++it) *reinterpret_cast<half8v*>(base + (h + it) * E::ROW_STEP) = cv[it];
-    }
-}
-
-// out = f16(alpha * acc + beta * Csym) on an upper-triangle tile of a symmetric s x s matrix
-// (Csym optional: crs of size 0), the reference's single rounding of beta * C + alpha * (A B).
-// Only the upper block triangle is stored: consumers read a block below the diagonal as the
-// transpose of its mirror above it, and a diagonal block either way, so a diagonal tile must be
-// exactly symmetric: its upper triangle is computed and its lower triangle is the mirror.
-// With Csym, its tile is first copied into the staging as is; each value is then replaced in
+// out = f16(fma(beta, Csym, alpha * acc)) on an upper-triangle tile of a symmetric s x s matrix
+// (Csym optional): one rounding to f16 of beta * C + alpha * (A B), where the reference's eager
+// baddbmm rounds it (the fma with an f16 operand is one instruction on gfx950). Only the upper
+// block triangle is stored: consumers read a block below the diagonal as the transpose of its
+// mirror above it, and a diagonal block either way, so a diagonal tile must be exactly symmetric:
+// its upper triangle is computed and its lower triangle is the mirror.
+// With Csym, gemm_tile has loaded its tile into the staging (TileC); each value is replaced in
 // place by the final value computed from it (the same lane reads and writes each position). On a
 // diagonal tile the staging also receives the transposes of the values above the diagonal
 // (stage_f16), so one pass of row chunks stores every tile. HAS_C: the Csym term is present (else
-// crs and beta are unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1
-// would leave as is). DUAL: the tile is also stored to out2 as Q = Z + a I, the diagonal
-// elements rounded from the f16 Z (thorn.py:648, `Z + a * I` in f16): f16(float(Z_ii) + dual_add)
-// with dual_add = f16(a).
+// beta is unused); SCALE: alpha != 1 (else the product is stored unscaled, which x * 1 would
+// leave as is). DUAL: the tile is also stored to out2 as Q = Z + a I, the diagonal elements
+// rounded from the f16 Z (thorn.py:648, `Z + a * I` in f16): f16(float(Z_ii) + dual_add) with
+// dual_add = f16(a).
 template <class C, bool HAS_C, bool SCALE, bool DUAL = false>
-__device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out,
-                                          __amdgpu_buffer_rsrc_t crs, int64_t ld, int n, int m0, int n0,
-                                          float alpha, float beta, _Float16* out2 = nullptr, float dual_add = 0.f) {
+__device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out, int64_t ld,
+                                          int n, int m0, int n0, float alpha, float beta, _Float16* out2 = nullptr,
+                                          float dual_add = 0.f) {
     using E = EpiH<C>;
-    _Float16* const S = reinterpret_cast<_Float16*>(smem);
     const bool diag = m0 == n0;
-    if constexpr (HAS_C) {
-        // requested once the main loop is done: held through it, even a part of them would be
-        // spilled to scratch memory by the register allocator
-        stage_rows<C>(smem, crs, ld, n, m0, n0);
-        lds_barrier();
-    }
     stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a, bool) {
-        floatx4 t;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = SCALE ? alpha * a[e] : a[e];
+        half4 h;
         if constexpr (HAS_C) {
-            const half4 cv = *reinterpret_cast<const half4*>(S + E::rowoff(r) + c);
+            const half4 cv = *reinterpret_cast<const half4*>(smem + E::off(r, c));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t[e] += beta * static_cast<float>(cv[e]);
+            for (int e = 0; e < 4; ++e)
+                h[e] = static_cast<_Float16>(fmaf(beta, static_cast<float>(cv[e]), SCALE ? alpha * a[e] : a[e]));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(SCALE ? alpha * a[e] : a[e]);
         }
-        return t;
+        return h;
     });
     lds_barrier();
     store_staged<C>(smem, out, ld, n, m0, n0);
@@ -260,7 +212,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
             lds_barrier();   // the row pass has read the staging
             const int r = threadIdx.x;
             if (r < C::BM && m0 + r < n) {
-                _Float16& z = S[E::rowoff(r) + r];
+                _Float16& z = *reinterpret_cast<_Float16*>(smem + E::off(r, r));
                 z = static_cast<_Float16>(static_cast<float>(z) + dual_add);
             }
             lds_barrier();
@@ -283,9 +235,9 @@ struct NsOp {
 // Epilogue of an update tile (see ns_phase_kernel). Every field of the matrix table it needs is
 // read once into a register first: stores through the matrix pointers could alias the table in
 // global memory as far as the compiler knows, and it would reload fields after every store.
-// HAS_C: the plain quintic's X <- a X + B X (thorn.py:658): the tile of the input iterate X is
-// staged first and each output is f16(osc * acc + beta * osc * X), the reference's single
-// rounding of a X + B X; otherwise f16(osc * acc).
+// HAS_C: the plain quintic's X <- a X + B X (thorn.py:658): gemm_tile has staged the tile of the
+// input iterate X and each output is f16(fma(beta * osc, X, osc * acc)), one rounding of a X + B X
+// as in the reference; otherwise f16(osc * acc).
 template <bool HAS_C>
 __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
                                               int ti, int tj, const NsOp& op, char* smem, float* scratch) {
@@ -323,23 +275,23 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     }
 
     if constexpr (HAS_C) {
-        stage_rows<NsCfg>(smem, sym_rsrc(xin, ldx, rows), ldx, rows, m0, n0);
-        lds_barrier();
+        // gemm_tile has loaded the tile of the input iterate X into the staging
         const float bx = op.beta * osc;
-        const _Float16* const S = reinterpret_cast<const _Float16*>(smem);
         stage_f16<NsCfg>(acc, smem, false, [&](int r, int c, const floatx4& a, bool) {
-            const half4 xv = *reinterpret_cast<const half4*>(S + EpiH<NsCfg>::rowoff(r) + c);
-            floatx4 t;
+            const half4 xv = *reinterpret_cast<const half4*>(smem + EpiH<NsCfg>::off(r, c));
+            half4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t[e] = osc * a[e] + bx * static_cast<float>(xv[e]);
-            return t;
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(fmaf(bx, static_cast<float>(xv[e]), osc * a[e]));
+            return h;
         });
     } else if (op.first) {
         stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a, bool) {
-            return floatx4{a[0] * osc, a[1] * osc, a[2] * osc, a[3] * osc};
+            return half4{(_Float16)(a[0] * osc), (_Float16)(a[1] * osc), (_Float16)(a[2] * osc), (_Float16)(a[3] * osc)};
         });
     } else {
-        stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) { return a; });
+        stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) {
+            return half4{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3]};
+        });
     }
     lds_barrier();
 
@@ -479,7 +431,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
                                                        TaskList t1, NsOp op1, int t1_first) {
     __shared__ __attribute__((aligned(16))) char smem[EpiH<NsCfg>::SMEM];
-    __shared__ float scratch[4];
+    float* const scratch = reinterpret_cast<float*>(smem + EpiH<NsCfg>::FREE);   // block sums after the row pass
     int b;
     const bool later = t1_first ? xcd_split(blockIdx.x, t1.total, t0.total, b)
                                 : xcd_split(blockIdx.x, t0.total, t1.total, b);
@@ -525,37 +477,40 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
             b_k0 = tj * KB;
         }
     }
+    // the epilogue's C term, loaded by gemm_tile into the staging: the input iterate's tile for the
+    // plain quintic's X <- a X + B X, Csym for a symmetric product
+    TileC ct{nullptr, 0, 0};
+    if (op.csel >= 0) {
+        if (op.kind == kOpUpdate) ct = TileC{op.xsel == kXA ? M.xa : M.xb, M.ldx, M.rows};
+        else if (op.kind == kOpSym) ct = TileC{sym_buf(M, op.csel), M.lds, M.s};
+    }
+    const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_tile<NsCfg>(A, B, ti * NsCfg::BM, tj * NsCfg::BN, KT, a_k0, b_k0, acc, smem, M.zero,
-                     op.kind != kOpUpdate && ti == tj);
+    gemm_tile<NsCfg>(A, B, m0, n0, KT, a_k0, b_k0, ct, acc, smem, op.kind != kOpUpdate && ti == tj);
     if (op.kind == kOpUpdate) {
         if (op.csel >= 0) update_finish<true>(M, acc, local, ti, tj, op, smem, scratch);
         else update_finish<false>(M, acc, local, ti, tj, op, smem, scratch);
     } else if (op.kind == kOpGram) {
-        const __amdgpu_buffer_rsrc_t none = sym_rsrc(nullptr, 0, 0);
-        const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
         if (op.first) {
             const float osc = M.scal[kScalX0Scale];
-            sym_store<NsCfg, false, true>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, osc * osc, 0.f);
+            sym_store<NsCfg, false, true>(acc, smem, M.gram, M.lds, M.s, m0, n0, osc * osc, 0.f);
         } else {
-            sym_store<NsCfg, false, false>(acc, smem, M.gram, none, M.lds, M.s, m0, n0, 1.f, 0.f);
+            sym_store<NsCfg, false, false>(acc, smem, M.gram, M.lds, M.s, m0, n0, 1.f, 0.f);
         }
     } else {
-        const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
         _Float16* const out = sym_buf(M, op.osel);
         if (op.csel >= 0) {
-            const __amdgpu_buffer_rsrc_t crs = sym_rsrc(sym_buf(M, op.csel), M.lds, M.s);
             if (op.osel2 >= 0)
-                sym_store<NsCfg, true, true, true>(acc, smem, out, crs, M.lds, M.s, m0, n0, op.alpha, op.beta,
+                sym_store<NsCfg, true, true, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta,
                                                    sym_buf(M, op.osel2), op.dual_add);
             else if (op.alpha != 1.f)
-                sym_store<NsCfg, true, true>(acc, smem, out, crs, M.lds, M.s, m0, n0, op.alpha, op.beta);
+                sym_store<NsCfg, true, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta);
             else
-                sym_store<NsCfg, true, false>(acc, smem, out, crs, M.lds, M.s, m0, n0, 1.f, op.beta);
+                sym_store<NsCfg, true, false>(acc, smem, out, M.lds, M.s, m0, n0, 1.f, op.beta);
         } else if (op.alpha != 1.f) {
-            sym_store<NsCfg, false, true>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, op.alpha, 0.f);
+            sym_store<NsCfg, false, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, 0.f);
         } else {
-            sym_store<NsCfg, false, false>(acc, smem, out, sym_rsrc(nullptr, 0, 0), M.lds, M.s, m0, n0, 1.f, 0.f);
+            sym_store<NsCfg, false, false>(acc, smem, out, M.lds, M.s, m0, n0, 1.f, 0.f);
         }
     }
 }

@@ -495,10 +495,20 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         L.s = std::min(L.rows, L.cols);
         L.l = std::max(L.rows, L.cols);
         L.tall = L.rows > L.cols;
-        L.ldx = static_cast<int32_t>(align_up(L.cols, 8));
-        L.lds = static_cast<int32_t>(align_up(L.s, 8));
+        // leading dimensions are multiples of 32 (one K tile of the GEMM loop): a K tile of a
+        // K-major row is then inside the row or past its end, never across it
+        L.ldx = static_cast<int32_t>(align_up(L.cols, 32));
+        L.lds = static_cast<int32_t>(align_up(L.s, 32));
         L.flags = d.flags & (THORN_MAT_PER_ROW_NORM | THORN_MAT_MD | THORN_MAT_MD_SCALAR);
         L.adam = (d.flags & THORN_MAT_ADAM) != 0;
+        // the GEMM loop addresses each f16 iterate with 32-bit byte offsets (out-of-range ones
+        // included), which holds below 1 GiB
+        if (!L.adam && int64_t(L.rows) * L.ldx * 2 >= (int64_t(1) << 30)) {
+            delete plan;
+            return fail(THORN_ERR_UNSUPPORTED, "thorn_ortho_plan_create: matrix " + std::to_string(i) +
+                                                   " has more than 2^29 elements (its f16 Newton-Schulz iterate "
+                                                   "would exceed 1 GiB)");
+        }
         L.norm_rows = (d.flags & THORN_MAT_NORM_ROWS) != 0;
         L.mom_tiles_r = static_cast<int32_t>(cdiv(L.rows, thorn::kTileR));
         L.mom_tiles_c = static_cast<int32_t>(cdiv(L.cols, thorn::kTileC));
