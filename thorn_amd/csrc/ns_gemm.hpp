@@ -349,7 +349,9 @@ __device__ __forceinline__ void read_frag(const FragBase<C::TM>& fa_base, const 
 // tile kt+1 is visible and nobody reads stage (kt-1) % 4 any more, which then receives tile kt+3.
 // Sub-step 2 multiplies the ks 1 fragments and, after MFMA q, reads fragment q of the next
 // tile's ks 0 (stage ST+1) and issues the direct loads of tile kt+3: one per two MFMAs when the
-// wave has twice as many MFMAs as loads (full tiles), else one per MFMA.
+// wave has twice as many MFMAs as loads (full tiles), else one per MFMA. (Loading tile kt+4 into
+// stage ST instead, after a wait for this wave's LDS reads, gives the loads one more iteration
+// but measured no faster.)
 // CQ >= 0 (the last three iterations of a tile's K loop): the direct loads fetch quarter CQ of the
 // epilogue's C tile into stage ST+3 instead of a tile past the end of K.
 template <class C, bool AK, bool BK, int ROLE, int ST, int CQ = -1>
@@ -514,6 +516,7 @@ struct EpiH {
     static constexpr int SPARE = C::LDS_BYTES;                     // rows 192..255 live here
     static constexpr int SMEM = C::LDS_BYTES + 64 * PITCH;         // 160 KB
     static constexpr int FREE = 3 * C::STAGE_BYTES;                // stage 3: unused by the staging
+    static_assert(FREE + 256 + 4 * 256 <= SPARE, "scratch slots in the free stage");
     static constexpr int ROW_ITERS = C::BM * (C::BN / 8) / 256;   // row chunks per thread
     static_assert(C::BN / 8 == 32 && C::BM == 256 && C::STAGE_BYTES == 192 * PITCH / 3, "layout");
     static_assert(SMEM <= 160 * 1024, "LDS");
@@ -544,10 +547,16 @@ __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* s
         return floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     };
     auto put = [&](int r, int c, const half4& h) { *reinterpret_cast<half4*>(smem + EpiH<C>::off(r, c)) = h; };
+    // transposes of the 4 values; upper_only (a block on the tile's diagonal): only those above the
+    // diagonal, the others go to a per-lane slot in the free stage (a lane-dependent branch per
+    // element made the compiler reload the block's accumulators inside every branch)
+    const int dump = EpiH<C>::FREE + 256 + 4 * static_cast<int>(threadIdx.x);
     auto put_t = [&](int r, int c, const half4& h, bool upper_only) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (!upper_only || c + e > r) *reinterpret_cast<_Float16*>(smem + EpiH<C>::off(c + e, r)) = h[e];
+        for (int e = 0; e < 4; ++e) {
+            const int a = EpiH<C>::off(c + e, r);
+            *reinterpret_cast<_Float16*>(smem + (!upper_only || c + e > r ? a : dump)) = h[e];
+        }
     };
     auto final4 = [&](int r, int c, const floatx4& a, bool dblk) { return val(r, c, a, dblk); };
     const int lr = lane & 31, lc = 4 * (lane >> 5);
