@@ -510,6 +510,9 @@ def main() -> int:
     ap.add_argument('--polar-decomp-batch-size', type=int, default=None,
                     help="elements per Newton-Schulz batch (the optimizer's polar_decomp_batch_size; "
                          "default: the library's, one batch per group)")
+    ap.add_argument('--single-chain', action='store_true',
+                    help='step the orthogonalized group as one plan on one stream (the library default splits '
+                         'a large group into two chains on two streams)')
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
     ap.add_argument('--vendor-gemm', action='store_true',
@@ -530,6 +533,8 @@ def main() -> int:
     import torch
     import thorn_amd
 
+    if args.single_chain:
+        thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     if args.copy_cal_mib:
@@ -574,23 +579,51 @@ def main() -> int:
     plans = [pl for r in opt._runners.values() for pl in r.plans]
     for pl in plans:
         pl.timing_enable(64 * args.steps)
+    ref = torch.cuda.Event(enable_timing=True)
+    ref.record()
     for _ in range(args.steps):
         one_step()
     torch.cuda.synchronize()
-    kinds: dict = {}
+    # Orthogonalized plans report each launch's start and end (a large group runs as two chains on
+    # two streams whose launches overlap); Adam plans their summed durations. Kernel time is the
+    # union of its launches' intervals, which for launches that do not overlap is their sum.
+    kinds: dict = {}       # kind -> (summed ms, launches)
+    intervals: dict = {}   # kind -> [(start ms, end ms)] (orthogonalized plans)
+    summed: dict = {}      # kind -> summed ms (Adam plans: on the main stream, after the chains)
     for pl in plans:
-        for k, (ms, n) in pl.timing_read().items():
-            tot, cnt = kinds.get(k, (0.0, 0))
-            kinds[k] = (tot + ms, cnt + n)
+        if isinstance(pl, thorn_amd._lib.OrthoPlan):
+            for k, a, b in pl.timing_intervals(ref.cuda_event, 64 * args.steps):
+                tot, cnt = kinds.get(k, (0.0, 0))
+                kinds[k] = (tot + (b - a), cnt + 1)
+                intervals.setdefault(k, []).append((a, b))
+        else:
+            for k, (ms, n) in pl.timing_read().items():
+                tot, cnt = kinds.get(k, (0.0, 0))
+                kinds[k] = (tot + ms, cnt + n)
+                summed[k] = summed.get(k, 0.0) + ms
         pl.timing_enable(0)
+
+    def union_ms(names) -> float:
+        """The union of the launch intervals of the given kernel kinds, plus their summed durations
+        in plans timed without intervals."""
+        iv = sorted(x for k in names for x in intervals.get(k, []))
+        total, end = 0.0, None
+        for a, b in iv:
+            if end is None or a > end:
+                total += b - a
+                end = b
+            elif b > end:
+                total += b - end
+                end = b
+        return total + sum(summed.get(k, 0.0) for k in names)
 
     grp0 = thorn_amd.optim._Group.from_kwargs(**opt.param_groups[0])
     mask = thorn_amd.optim._OrthoRunner.restart_mask(grp0, grp0.iters)
     F = schedule_flops(mats, grp0.iters, mask)
     small = [sh for sh in mats if min(sh) <= SMALL_MAX_S and sh[0] * sh[1] < SMALL_MAX_ELEMS]
     F_small = schedule_flops(small, grp0.iters, mask)
-    ns_ms = sum(kinds.get(k, (0.0, 0))[0] for k in NS_KINDS) / args.steps
-    upd_ms = sum(kinds.get(k, (0.0, 0))[0] for k in ('pre', 'norm', 'rowstats', 'pnn_apply', 'adam')) / args.steps
+    ns_ms = union_ms(NS_KINDS) / args.steps
+    upd_ms = union_ms(('pre', 'norm', 'rowstats', 'pnn_apply', 'adam')) / args.steps
     cbytes = compulsory_bytes(mats, params, n_m)
     # dominant kernel: ns_phase_kernel, which runs the Newton-Schulz products of the large
     # matrices (one launch per schedule step); with no large matrix, ns_small_kernel. Its
@@ -602,8 +635,11 @@ def main() -> int:
         dom_kinds, dom_name, dom_flops = ('small',), 'ns_small_kernel', F_small
     ns_launches = sum(kinds.get(k, (0.0, 0))[1] for k in NS_KINDS) / args.steps
     dom_launches = sum(kinds.get(k, (0.0, 0))[1] for k in dom_kinds) / args.steps
-    dom_ms = sum(kinds.get(k, (0.0, 0))[0] for k in dom_kinds) / args.steps
+    dom_ms = union_ms(dom_kinds) / args.steps
+    dom_sum_ms = sum(kinds.get(k, (0.0, 0))[0] for k in dom_kinds) / args.steps
     ns_flops_per_launch = dom_flops / max(dom_launches, 1)
+    # the dominant kernel's time per launch: the union of its launch intervals per launch (its
+    # launches of two chains overlap one another)
     u_avg = dom_ms / max(dom_launches, 1)
     achieved = ns_flops_per_launch / (u_avg * 1e-3) / 1e12 if u_avg > 0 else 0.0
     phases = {k: {'ms_per_launch': round(ms / n, 4), 'launches_per_step': n / args.steps}
@@ -648,7 +684,10 @@ def main() -> int:
         'roofline': {'kernel': dom_name, 'bound': 'mfma', 'achieved': round(achieved, 1),
                      'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_PEAK_TFLOPS, 4),
                      'traffic': traffic_from_profile(dom_name), 'flops_per_launch': ns_flops_per_launch,
-                     'launches_per_step': dom_launches, 'avg_launch_ms': round(u_avg, 4)},
+                     'launches_per_step': dom_launches, 'avg_launch_ms': round(u_avg, 4),
+                     'active_ms_per_step': round(dom_ms, 3), 'launch_ms_sum_per_step': round(dom_sum_ms, 3),
+                     'chains': max([len(r.plans) if getattr(r, 'chained', False) else 1
+                                    for r in opt._runners.values()] + [1])},
         'launches_per_step': {'ns': ns_launches,
                               'total': sum(n for _, n in kinds.values()) / args.steps},
         'phases': phases,

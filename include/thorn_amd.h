@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 6
+#define THORN_ABI_VERSION 7
 
 enum {
     THORN_OK = 0,
@@ -137,6 +137,14 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
  * which no matrix has THORN_STEP_APPLY (coeffs may then be null). */
 int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
                      uint32_t restart_mask, void* stream);
+/* No counterpart in the reference (its eager step runs on one stream): thorn_ortho_step, and
+ * ns_begin_event (a hipEvent_t, or null) is recorded on the stream once the step's prologue
+ * launches (momentum, norms, first iterate) are enqueued: before its first Newton-Schulz launch,
+ * or at the end of a step without one. For callers that overlap independent work with the
+ * Newton-Schulz launches: THORN runs a large orthogonalized group as two plans on two streams,
+ * the second waiting for this event of the first, so that each fills the other's idle tails. */
+int thorn_ortho_step_event(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+                           uint32_t restart_mask, void* stream, void* ns_begin_event);
 
 /* No counterpart in the reference. For callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): thorn_ortho_fill_table
@@ -235,6 +243,12 @@ enum {
 };
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches);
 int thorn_ortho_timing_read(thorn_ortho_plan_t plan, double* ms, int* launches, int n_kinds);
+/* The same window as start and end times: for each recorded launch (up to max), its kind and its
+ * start and end in milliseconds after ref_event, a hipEvent (timing enabled) that the caller
+ * recorded before the launches on any stream of the device; *n receives the number written. For
+ * launches that overlap other streams' work, whose durations overlap too. Starts a new window. */
+int thorn_ortho_timing_intervals(thorn_ortho_plan_t plan, void* ref_event, double* start_ms, double* end_ms,
+                                 int* kinds, int max, int* n);
 int thorn_adam_timing_enable(thorn_adam_plan_t plan, int max_launches);
 int thorn_adam_timing_read(thorn_adam_plan_t plan, double* ms, int* launches, int n_kinds);
 

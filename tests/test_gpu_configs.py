@@ -206,3 +206,42 @@ def test_config5_every_shape():
         del grads
     _log(f'[gpu]   config 5: {worst}')
     assert math.isfinite(worst['dp'])
+
+
+def test_two_chains_equal_one_plan():
+    """A group of at least CHAIN_MIN_MATRICES large matrices steps as two chains on two streams
+    (thorn_amd.optim._OrthoBatches); every matrix runs the same kernels on the same data as in one
+    plan, so parameters and state must match the one-plan step bit for bit, over steps with the
+    exact and the prescaled first iterate, and per-row normalization on the tall matrices."""
+    import thorn_amd
+    from thorn_amd import optim as OPT
+    gen = torch.Generator().manual_seed(3407)
+    shapes = [(384, 640), (640, 384), (512, 512), (1024, 384)] * 5 + [(3, 384, 512)]
+    init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes]
+    grads = [[torch.randn(sh, generator=gen) * 1e-3 for sh in shapes] for _ in range(3)]
+
+    def run(chains: bool):
+        params = [torch.nn.Parameter(t.to(DEV)) for t in init]
+        keep = OPT.CHAIN_MIN_MATRICES
+        OPT.CHAIN_MIN_MATRICES = 16 if chains else 1 << 30
+        try:
+            opt = thorn_amd.THORN([{'params': params, 'orthogonalize': True, 'lr': 1e-3, 'weight_decay': 0.1}])
+            for gs in grads:
+                for p, g in zip(params, gs):
+                    p.grad = g.to(DEV)
+                opt.step()
+            torch.cuda.synchronize()
+            runner = next(iter(opt._runners.values()))
+            assert runner.chained == chains and len(runner.plans) == (2 if chains else 1)
+            return params, opt
+        finally:
+            OPT.CHAIN_MIN_MATRICES = keep
+
+    pa, oa = run(True)
+    pb, ob = run(False)
+    for i, (p, q) in enumerate(zip(pa, pb)):
+        assert torch.equal(p.detach(), q.detach()), (i, shapes[i])
+        for k, v in oa.state[p].items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, ob.state[q][k]), (i, k)
+    _log(f'two chains: {len(pa)} parameters bitwise equal to one plan over {len(grads)} steps')

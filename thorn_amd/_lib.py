@@ -79,6 +79,7 @@ SIGNATURES = {
     'thorn_ortho_table_bytes': (_sz, [_vp]),
     'thorn_ortho_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
     'thorn_ortho_step': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp]),
+    'thorn_ortho_step_event': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp, _vp]),
     'thorn_ortho_step_noalloc': (_i, [_vp, _vp, _vp, _i, ctypes.c_uint32, _vp]),
     'thorn_adam_plan_create': (_i, [_vp, _i, ctypes.POINTER(_vp)]),
     'thorn_adam_plan_destroy': (None, [_vp]),
@@ -89,6 +90,7 @@ SIGNATURES = {
     'thorn_adam_sparse_step': (_i, [_vp, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
+    'thorn_ortho_timing_intervals': (_i, [_vp, _vp, _vp, _vp, _vp, _i, ctypes.POINTER(_i)]),
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
     'thorn_adam_timing_read': (_i, [_vp, _vp, _vp, _i]),
 }
@@ -96,7 +98,7 @@ KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_f
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
 NOALLOC_SCRATCH_BYTES = 32 << 20
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 
@@ -165,11 +167,18 @@ class OrthoPlan:
         check(self._lib.thorn_ortho_fill_table(self.handle, steps.ctypes.data, workspace, table_dev,
                                                table_host), 'thorn_ortho_fill_table')
 
-    def step(self, table_dev: int, coeffs: np.ndarray, restart_mask: int, stream: int) -> None:
-        """coeffs: (iters, 3) float32; restart_mask: bit i = restart before iteration i."""
+    def step(self, table_dev: int, coeffs: np.ndarray, restart_mask: int, stream: int,
+             ns_begin_event: int = 0) -> None:
+        """coeffs: (iters, 3) float32; restart_mask: bit i = restart before iteration i.
+        ns_begin_event: a hipEvent_t recorded on the stream once the prologue launches are
+        enqueued (thorn_ortho_step_event), or 0."""
         iters = coeffs.shape[0]
-        check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, restart_mask, stream),
-              'thorn_ortho_step')
+        if ns_begin_event:
+            check(self._lib.thorn_ortho_step_event(self.handle, table_dev, coeffs.ctypes.data, iters, restart_mask,
+                                                   stream, ns_begin_event), 'thorn_ortho_step_event')
+        else:
+            check(self._lib.thorn_ortho_step(self.handle, table_dev, coeffs.ctypes.data, iters, restart_mask,
+                                             stream), 'thorn_ortho_step')
 
     def step_noalloc(self, steps: np.ndarray, coeffs: np.ndarray, restart_mask: int, stream: int) -> None:
         """fill_table + step with the library's static device workspace (no allocation)."""
@@ -182,6 +191,19 @@ class OrthoPlan:
 
     def timing_read(self) -> dict:
         return _timing_read(self._lib.thorn_ortho_timing_read, self.handle)
+
+    def timing_intervals(self, ref_event: int, max_launches: int) -> list:
+        """[(kind name, start ms, end ms)] of the recorded launches, relative to ref_event (a
+        timing-enabled hipEvent recorded before them); starts a new window."""
+        s = np.zeros(max(1, max_launches), dtype=np.float64)
+        e = np.zeros_like(s)
+        k = np.zeros(max(1, max_launches), dtype=np.int32)
+        n = ctypes.c_int(0)
+        check(self._lib.thorn_ortho_timing_intervals(self.handle, ref_event, s.ctypes.data, e.ctypes.data,
+                                                     k.ctypes.data, max_launches, ctypes.byref(n)),
+              'thorn_ortho_timing_intervals')
+        return [(KINDS[k[i]] if 0 <= k[i] < len(KINDS) else str(k[i]), float(s[i]), float(e[i]))
+                for i in range(n.value)]
 
     def __del__(self):
         h = getattr(self, 'handle', None)

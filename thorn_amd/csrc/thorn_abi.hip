@@ -117,6 +117,28 @@ int timer_read(LaunchTimer& t, double* ms, int* count, int n_kinds) {
     return of ? THORN_ERR_INVALID : THORN_OK;
 }
 
+// Each recorded launch's kind and its start and end in ms after `ref` (an event recorded by the
+// caller before the launches, timing enabled); starts a new window like timer_read.
+int timer_intervals(LaunchTimer& t, hipEvent_t ref, double* s, double* e, int* kinds, int max, int* n) {
+    *n = 0;
+    const int k = t.used < max ? t.used : max;
+    for (int i = 0; i < t.used; ++i) {
+        if (hipEventSynchronize(t.ev[2 * i + 1]) != hipSuccess) return THORN_ERR_HIP;
+        if (i >= k) continue;
+        float a = 0.f, b = 0.f;
+        if (hipEventElapsedTime(&a, ref, t.ev[2 * i]) != hipSuccess) return THORN_ERR_HIP;
+        if (hipEventElapsedTime(&b, ref, t.ev[2 * i + 1]) != hipSuccess) return THORN_ERR_HIP;
+        s[i] = a;
+        e[i] = b;
+        kinds[i] = t.kind[i];
+    }
+    *n = k;
+    const bool of = t.overflow || t.used > max;
+    t.used = 0;
+    t.overflow = false;
+    return of ? THORN_ERR_INVALID : THORN_OK;
+}
+
 }  // namespace
 
 struct thorn_ortho_plan {
@@ -808,8 +830,12 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     return THORN_OK;
 }
 
-int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
-                     uint32_t restart_mask, void* stream) {
+namespace {
+
+// thorn_ortho_step, recording ns_begin (if not null) on the stream once the prologue launches are
+// enqueued: before the first Newton-Schulz launch, or at the end of a step without one.
+int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+               uint32_t restart_mask, void* stream, hipEvent_t ns_begin) {
     if (!plan || !table_dev) return fail(THORN_ERR_INVALID, "thorn_ortho_step: null argument");
     if (iters < 0 || iters > 32 || (iters > 0 && !coeffs))
         return fail(THORN_ERR_INVALID, "thorn_ortho_step: need 0 <= iters <= 32 and coefficients");
@@ -817,8 +843,13 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         return fail(THORN_ERR_INVALID,
                     "thorn_ortho_step: iters = 0 (momentum only) with matrices flagged THORN_STEP_APPLY");
     const int n = static_cast<int>(plan->mats.size());
-    if (n == 0) return THORN_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    auto signal = [&]() -> int {
+        if (ns_begin && hipEventRecord(ns_begin, st) != hipSuccess)
+            return fail(THORN_ERR_HIP, "thorn_ortho_step_event: hipEventRecord failed");
+        return THORN_OK;
+    };
+    if (n == 0) return signal();
     const char* dev = static_cast<const char*>(table_dev);
     const auto* mats = reinterpret_cast<const thorn::OrthoMat*>(dev + plan->mats_off);
     LaunchTimer& tm = plan->timer;
@@ -850,7 +881,7 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         }
         plan->stepped_ws = plan->filled_ws;
         note_step(plan);
-        return THORN_OK;
+        return signal();
     }
     // The exact first iterate (and the rebuild of prescaled ones out of range): one row of blocks
     // per matrix, a tile per block when some matrix is on the exact path, else 64 blocks per
@@ -860,6 +891,7 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
         THORN_LAUNCH(THORN_KIND_CAST, "ortho_cast_kernel", thorn::ortho_cast_kernel, dim3(std::max(gx, 1), n),
                      dim3(256), 0, st, mats);
     }
+    if ((rc = signal())) return rc;
     // Newton-Schulz: square matrices on the plain quintic, the others on Gram Newton-Schulz with
     // the given restarts (thorn.py:628, 637-658); step k of both schedules shares launch k.
     const NsSchedule sched[2] = {plain_schedule(iters, coeffs), gram_schedule(iters, restart_mask, coeffs)};
@@ -928,6 +960,18 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
     return THORN_OK;
 }
 
+}  // namespace
+
+int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+                     uint32_t restart_mask, void* stream) {
+    return ortho_step(plan, table_dev, coeffs, iters, restart_mask, stream, nullptr);
+}
+
+int thorn_ortho_step_event(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
+                           uint32_t restart_mask, void* stream, void* ns_begin_event) {
+    return ortho_step(plan, table_dev, coeffs, iters, restart_mask, stream, static_cast<hipEvent_t>(ns_begin_event));
+}
+
 int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, const float* coeffs,
                              int iters, uint32_t restart_mask, void* stream) {
     if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_step_noalloc: null plan");
@@ -964,6 +1008,16 @@ int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* s
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches) {
     if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_timing_enable: null plan");
     if (timer_enable(plan->timer, max_launches)) return fail(THORN_ERR_HIP, "thorn_ortho_timing_enable: hipEventCreate failed");
+    return THORN_OK;
+}
+
+int thorn_ortho_timing_intervals(thorn_ortho_plan_t plan, void* ref_event, double* start_ms, double* end_ms,
+                                 int* kinds, int max, int* n) {
+    if (!plan || !ref_event || !n || max < 0 || (max > 0 && (!start_ms || !end_ms || !kinds)))
+        return fail(THORN_ERR_INVALID, "thorn_ortho_timing_intervals: bad argument");
+    const int rc = timer_intervals(plan->timer, static_cast<hipEvent_t>(ref_event), start_ms, end_ms, kinds, max, n);
+    if (rc == THORN_ERR_HIP) return fail(rc, "thorn_ortho_timing_intervals: event query failed");
+    if (rc) return fail(rc, "thorn_ortho_timing_intervals: more launches than the enabled capacity or than max");
     return THORN_OK;
 }
 

@@ -324,6 +324,38 @@ def _plan_shapes(params: list, group: _Group, adam: bool, with_owner: bool = Fal
     return (rows, cols, flags, owner, sub) if with_owner else (rows, cols, flags)
 
 
+class _TableUpload:
+    """Pinned host buffers for a plan's per-step table, used in turn: a buffer is refilled only
+    once the copy that last read it has run (its event). This also bounds how far the host runs
+    ahead of the device: about RING steps. With a group stepping as two chains on two streams, a
+    host four steps ahead (queues full of cross-stream waits) made the device's first ~10 steps
+    1-3 ms slower each, and two steps ahead still varied by 0.2 ms from run to run; one step
+    ahead gave the steady rate from the fourth step on, and cost the one-stream path nothing."""
+    RING = 1
+
+    def __init__(self, nbytes: int):
+        self.nbytes = nbytes
+        self.bufs = [torch.empty(max(1, nbytes), dtype=torch.uint8, pin_memory=True) for _ in range(self.RING)]
+        self.events: list = [None] * self.RING
+        self.i = 0
+
+    def host(self) -> torch.Tensor:
+        """The next buffer, once its last copy has run."""
+        ev = self.events[self.i]
+        if ev is not None:
+            ev.synchronize()
+        return self.bufs[self.i]
+
+    def upload(self, dst: torch.Tensor) -> None:
+        """Copies the buffer of host() into dst on the current stream."""
+        i = self.i
+        dst[:self.nbytes].copy_(self.bufs[i][:self.nbytes], non_blocking=True)
+        if self.events[i] is None:
+            self.events[i] = torch.cuda.Event()
+        self.events[i].record()
+        self.i = (i + 1) % self.RING
+
+
 class _OrthoRunner:
     """One orthogonalized parameter set (or, with adam=True, the decouple_md tensors of a
     non-orthogonalized group, whose update is the Adam step): plan, workspace and the per-step
@@ -343,11 +375,14 @@ class _OrthoRunner:
         self.workspace = (torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
                           if workspace is None else workspace)
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
+        self.upload = _TableUpload(self.plan.table_bytes)
         self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
         self.md = group.decouple_md
 
-    def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None) -> None:
-        """unmasked: id(p) -> False for a parameter whose Magma mask skips this step."""
+    def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None,
+            ns_begin: Optional[torch.cuda.Event] = None) -> None:
+        """unmasked: id(p) -> False for a parameter whose Magma mask skips this step. ns_begin:
+        recorded on the stream once the prologue launches are enqueued (thorn_ortho_step_event)."""
         params, steps = self.params, self.steps
         n = len(self.owner)
         elem = (self.rows * self.cols).astype(np.int64)
@@ -429,14 +464,15 @@ class _OrthoRunner:
                 per = t.numel() // batch[i] if t.numel() > 1 else 0
                 tn[k] = t.data_ptr() + int(b) * per * 4
             steps['target_norm'] = tn
-        host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
+        host = self.upload.host()
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
-        self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
+        self.upload.upload(self.table)
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
         if self.adam or not due.any():   # no polar factor this step: momentum (gains, Magma s) only
             coeffs = coeffs[:0]
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
-                       torch.cuda.current_stream(self.device).cuda_stream)
+                       torch.cuda.current_stream(self.device).cuda_stream,
+                       ns_begin.cuda_event if ns_begin is not None else 0)
 
     @staticmethod
     def restart_mask(group: _Group, iters: int) -> int:
@@ -463,24 +499,70 @@ def _batches(params: list, limit: int) -> list:
     return out
 
 
+def _large_matrices(params: list) -> int:
+    """Matrices of `params` on the library's large-matrix path (s > 256 or r * c >= 2^20; the
+    others run in its one-launch small-matrix kernel)."""
+    n = 0
+    for p in params:
+        r, c, batch = _matrix_view(p)
+        if min(r, c) > SMALL_MAX_S or r * c >= SMALL_MAX_ELEMS:
+            n += batch
+    return n
+
+
+def _two_chains(params: list) -> tuple:
+    """The parameters dealt to two chains of equal Newton-Schulz work: by cost (s^2 * l per
+    matrix), largest first, in the order A B B A A B ..., each chain keeping the group's order."""
+    def cost(p):
+        r, c, batch = _matrix_view(p)
+        return batch * min(r, c) ** 2 * max(r, c)
+    ranked = sorted(range(len(params)), key=lambda i: -cost(params[i]))
+    side = {i: (k % 4 in (1, 2)) for k, i in enumerate(ranked)}
+    return [p for i, p in enumerate(params) if not side[i]], [p for i, p in enumerate(params) if side[i]]
+
+
+# A group with at least this many large-path matrices steps as two chains (_OrthoBatches).
+CHAIN_MIN_MATRICES = 16
+SMALL_MAX_S, SMALL_MAX_ELEMS = 256, 1 << 20   # the library's small-matrix path (thorn_abi.hip)
+
+
 class _OrthoBatches:
     """A group's orthogonalized parameters in batches of at most polar_decomp_batch_size elements
     (thorn.py:1237, 1440): one plan per batch, run in turn on one workspace sized for the largest,
     so the Newton-Schulz buffers of only one batch exist at a time. Plans that share a workspace
     take the exact first iterate (the library keeps the cheaper prescaled one for a plan that
-    stepped last on its workspace)."""
+    stepped last on its workspace).
+
+    A group that is one batch with at least CHAIN_MIN_MATRICES large matrices runs as two chains
+    instead: two plans of equal Newton-Schulz work, each with its own workspace (together the size
+    of one plan's), on two streams of the optimizer, the second starting once the first one's
+    prologue launches are done. Each Newton-Schulz launch ends in a partly idle last round of
+    tiles; the other chain's launches, out of phase, fill it (on bench.py's Qwen3-300M-shaped
+    step, 7.07 -> 6.85 ms on one MI355X).
+    The results are those of one plan bit for bit: every matrix runs the same kernels on the same
+    data."""
 
     def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False):
         batches = _batches(params, limit)
         self.runners = []
+        self.chained = False
         workspace = None
-        if len(batches) > 1:
+        chains = _two_chains(params) if len(params) > 1 else ([], [])
+        if len(batches) == 1 and not adam and _large_matrices(params) >= CHAIN_MIN_MATRICES and all(chains):
+            self.chained = True
+            batches = list(chains)
+            # recorded by the first chain once its prologue is enqueued; the library records it
+            # again each step (a torch event is created when first recorded)
+            self.ns_begin = torch.cuda.Event()
+            self.ns_begin.record(torch.cuda.current_stream(device))
+            self.fork_join = (torch.cuda.Event(), torch.cuda.Event(), torch.cuda.Event())
+        elif len(batches) > 1:
             sizes = [_lib.OrthoPlan(*_plan_shapes(b, group, adam)).workspace_bytes for b in batches]
             workspace = torch.zeros(max(1, max(sizes)), dtype=torch.uint8, device=device)
         for b in batches:
             self.runners.append(_OrthoRunner(b, group, device, adam, workspace))
         self.workspace_bytes = (workspace.numel() if workspace is not None
-                                else self.runners[0].workspace.numel())
+                                else sum(r.workspace.numel() for r in self.runners))
 
     @property
     def plans(self) -> list:
@@ -491,8 +573,26 @@ class _OrthoBatches:
         return [r.workspace for r in self.runners]
 
     def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None) -> None:
-        for r in self.runners:
-            r.run(opt, group, unmasked)
+        if not self.chained:
+            for r in self.runners:
+                r.run(opt, group, unmasked)
+            return
+        dev = self.runners[0].device
+        main = torch.cuda.current_stream(dev)
+        sa, sb = opt._chain_streams(dev)
+        fork, join_a, join_b = self.fork_join
+        fork.record(main)                 # gradients and state as the caller left them
+        sa.wait_event(fork)
+        sb.wait_event(fork)
+        with torch.cuda.stream(sa):
+            self.runners[0].run(opt, group, unmasked, ns_begin=self.ns_begin)
+        sb.wait_event(self.ns_begin)      # the first chain's prologue is done
+        with torch.cuda.stream(sb):
+            self.runners[1].run(opt, group, unmasked)
+        join_a.record(sa)                 # before anything else of the step reads the results
+        join_b.record(sb)
+        main.wait_event(join_a)
+        main.wait_event(join_b)
 
 
 class _AdamRunner:
@@ -503,6 +603,7 @@ class _AdamRunner:
         self.device = device
         self.plan = _lib.AdamPlan([p.numel() for p in params])
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
+        self.upload = _TableUpload(self.plan.table_bytes)
         self.workspace = torch.empty(max(256, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
 
@@ -538,9 +639,9 @@ class _AdamRunner:
             s[k]['apply'] = 1 if (step + 1) % update_rate == 0 and (unmasked is None or unmasked[id(p)]) else 0
             s[k]['degenerate'] = 1 if rect == 0.0 else 0
             s[k]['magma_s'] = state['s'].data_ptr() if group.momentum_align else 0
-        host = torch.empty(self.plan.table_bytes, dtype=torch.uint8, pin_memory=True)
+        host = self.upload.host()
         self.plan.fill_table(s, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
-        self.table[:self.plan.table_bytes].copy_(host, non_blocking=True)
+        self.upload.upload(self.table)
         self.plan.step(self.table.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
 
 
@@ -594,6 +695,7 @@ class THORN(Optimizer):
                 self._param_to_group[id(p)] = group
         self._runners: dict = {}
         self._magma_scratch: dict = {}
+        self._side_streams: dict = {}
         if isinstance(params, nn.Module) and conf.get('gradient_release', False):
             self.setup_gradient_release(params)
 
@@ -713,6 +815,17 @@ class THORN(Optimizer):
     # without a gradient this step) builds a new runner, and the least recently used one beyond
     # this many is dropped with its workspace, so memory stays bounded when the set changes.
     _RUNNERS_PER_GROUP = 2
+
+    def _chain_streams(self, dev: torch.device) -> tuple:
+        """The two streams of a chained group on `dev` (default priority), taken one after the
+        other from torch's stream pool. The runtime maps streams to the device's hardware queues in
+        turn, so the two get different queues; a chain on the caller's stream could share its
+        queue with the other chain's stream and run serialized behind it (measured: 7.3-7.5
+        against 6.8 ms per step on config 2)."""
+        s = self._side_streams.get(dev)
+        if s is None:
+            s = self._side_streams[dev] = (torch.cuda.Stream(dev), torch.cuda.Stream(dev))
+        return s
 
     def _runner(self, key, factory):
         r = self._runners.pop(key, None)
