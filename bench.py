@@ -315,7 +315,7 @@ def _short_kernel_name(name: str) -> str:
     return ''.join(out).strip()
 
 
-def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
+def rocprof_summary(paths: list, cal_mib: int = 0, steps: int = 5) -> str:
     """Markdown summary of rocprofv3 CSV output directories: the kernel statistics table
     (`*kernel_stats.csv`) and, when present, per-kernel counter averages per dispatch
     (`*counter_collection.csv`, one directory per counter pass). With `cal_mib`, FETCH_SIZE /
@@ -329,34 +329,8 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
 
     lines = []
     traces = found('*kernel_trace.csv')
-    if traces:   # the Newton-Schulz launches of the last complete step, config 2's schedules
-        rows = sorted(csv.DictReader(open(traces[0])), key=lambda r: int(r['Start_Timestamp']))
-        starts = [i for i, r in enumerate(rows) if 'ortho_pre_kernel' in r['Kernel_Name']]
-        if len(starts) >= 2:
-            mats, _ = config_shapes(2)
-            gram = gram_ops(5, 4)
-            plain = plain_ops(5)
-            fl = {'gram': lambda s_, l_: s_ * s_ * l_, 'poly': lambda s_, l_: s_ ** 3,
-                  'sym': lambda s_, l_: s_ ** 3, 'update': lambda s_, l_: 2.0 * s_ * s_ * l_}
-            lines += ['Newton-Schulz launches of the last complete step (config 2; Gram-schedule op on the '
-                      '100 non-square matrices / plain-schedule op on the 40 square ones):', '',
-                      '| launch | ops | TFLOP (algorithmic) | us | TFLOP/s |', '|---:|---|---:|---:|---:|']
-            k = 0
-            for r in rows[starts[-2]:starts[-1]]:
-                if 'ns_phase_kernel' not in r['Kernel_Name']:
-                    continue
-                us = (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
-                f = 0.0
-                names = []
-                for sched, pick in ((gram, lambda s_, l_: l_ != s_), (plain, lambda s_, l_: l_ == s_)):
-                    op = sched[k] if k < len(sched) else None
-                    names.append(op or '-')
-                    if op:
-                        f += sum(fl[op](min(sh), max(sh)) for sh in mats if pick(min(sh), max(sh)))
-                k += 1
-                lines.append(f'| {k} | {names[0]} / {names[1]} | {f / 1e12:.3f} | {us:.1f} | '
-                             f'{f / (us * 1e-6) / 1e12:.1f} |')
-            lines.append('')
+    if traces:
+        lines += ns_trace_lines(traces[0], steps)
     for f in found('*kernel_stats.csv'):
         rows = list(csv.DictReader(open(f)))
         lines += ['| kernel | calls | total ms | avg us | min us | max us | % |',
@@ -401,6 +375,67 @@ def rocprof_summary(paths: list, cal_mib: int = 0) -> str:
                 lines.append(f'\nns_phase_kernel HBM bytes per launch: {tot:.6g}')
         lines += mfma_lines(found)
     return '\n'.join(lines)
+
+
+def _union_us(iv: list) -> float:
+    """Length of the union of (start, end) intervals."""
+    total, end = 0.0, None
+    for a, b in sorted(iv):
+        if end is None or a > end:
+            total += b - a
+            end = b
+        elif b > end:
+            total += b - end
+            end = b
+    return total
+
+
+def ns_trace_lines(path: str, steps: int = 5) -> list:
+    """From a rocprofv3 kernel trace of a config-2 bench.py run: ns_phase_kernel's launches in the
+    last `steps` steps (the event-timed pass of `bench.py --steps <steps>`), as summed durations
+    and as the union of their intervals, which is what bench.py reports (a group stepping as two
+    chains on two streams overlaps them); with one stream, also the Newton-Schulz launches of the
+    last complete step, op by op. A stream's steps begin at its ortho_pre_kernel launches."""
+    import csv
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r['Start_Timestamp']))
+    iv = lambda r: (int(r['Start_Timestamp']) / 1e3, int(r['End_Timestamp']) / 1e3)
+    per_stream: dict = {}
+    for r in rows:
+        per_stream.setdefault(r['Stream_Id'], []).append(r)
+    pre = {k: [i for i, r in enumerate(v) if 'ortho_pre_kernel' in r['Kernel_Name']] for k, v in per_stream.items()}
+    chains = {k: v for k, v in pre.items()
+              if any('ns_phase_kernel' in r['Kernel_Name'] for r in per_stream[k])}
+    if not chains or min(len(v) for v in chains.values()) < steps:
+        return []
+    t0 = min(iv(per_stream[k][v[-steps]])[0] for k, v in chains.items())
+    ns = [iv(r) for r in rows if 'ns_phase_kernel' in r['Kernel_Name'] and iv(r)[0] >= t0]
+    out = [f'ns_phase_kernel in the last {steps} steps ({len(chains)} stream(s)): {len(ns) // steps} launches '
+           f'per step; summed durations {sum(b - a for a, b in ns) / len(ns):.1f} us per launch; union of '
+           f'their intervals {_union_us(ns) / steps / 1e3:.3f} ms per step, {_union_us(ns) / len(ns):.1f} us '
+           'per launch', '']
+    if len(chains) != 1:
+        return out
+    (k, starts), = chains.items()
+    seg = [iv(r) for r in per_stream[k][starts[-2]:starts[-1]] if 'ns_phase_kernel' in r['Kernel_Name']]
+    mats, _ = config_shapes(2)
+    gram = gram_ops(5, 4)
+    plain = plain_ops(5)
+    fl = {'gram': lambda s_, l_: s_ * s_ * l_, 'poly': lambda s_, l_: s_ ** 3,
+          'sym': lambda s_, l_: s_ ** 3, 'update': lambda s_, l_: 2.0 * s_ * s_ * l_}
+    out += ['Newton-Schulz launches of the last complete step (config 2; Gram-schedule op on the 100 '
+            'non-square matrices / plain-schedule op on the 40 square ones):', '',
+            '| launch | ops | TFLOP (algorithmic) | us | TFLOP/s |', '|---:|---|---:|---:|---:|']
+    for j, (a, b) in enumerate(seg):
+        f = 0.0
+        names = []
+        for sched, pick in ((gram, lambda s_, l_: l_ != s_), (plain, lambda s_, l_: l_ == s_)):
+            op = sched[j] if j < len(sched) else None
+            names.append(op or '-')
+            if op:
+                f += sum(fl[op](min(sh), max(sh)) for sh in mats if pick(min(sh), max(sh)))
+        out.append(f'| {j + 1} | {names[0]} / {names[1]} | {f / 1e12:.3f} | {b - a:.1f} | '
+                   f'{f / ((b - a) * 1e-6) / 1e12:.1f} |')
+    return out + ['']
 
 
 def mfma_lines(found) -> list:
@@ -521,7 +556,7 @@ def main() -> int:
                     help='print a markdown summary of rocprofv3 CSV output directories and exit')
     args = ap.parse_args()
     if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib))
+        print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib, args.steps))
         return 0
     if args.vendor_gemm:
         return vendor_gemm()
@@ -606,16 +641,8 @@ def main() -> int:
     def union_ms(names) -> float:
         """The union of the launch intervals of the given kernel kinds, plus their summed durations
         in plans timed without intervals."""
-        iv = sorted(x for k in names for x in intervals.get(k, []))
-        total, end = 0.0, None
-        for a, b in iv:
-            if end is None or a > end:
-                total += b - a
-                end = b
-            elif b > end:
-                total += b - end
-                end = b
-        return total + sum(summed.get(k, 0.0) for k in names)
+        return (_union_us([x for k in names for x in intervals.get(k, [])])
+                + sum(summed.get(k, 0.0) for k in names))
 
     grp0 = thorn_amd.optim._Group.from_kwargs(**opt.param_groups[0])
     mask = thorn_amd.optim._OrthoRunner.restart_mask(grp0, grp0.iters)
