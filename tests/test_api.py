@@ -119,3 +119,28 @@ def test_fp16_and_fp64_parameters_are_refused():
         p.grad = torch.zeros(3, 3, dtype=dt)
         with pytest.raises(NotImplementedError, match='fp32 and bf16'):
             opt.step()
+
+
+def test_chain_split_and_count():
+    """The chained group step deals a group's matrices to chains: every parameter exactly once,
+    each chain in the group's order, costs (s^2 * l) balanced by the snake deal, and the chain
+    count one per CHAIN_COST of work between 2 and MAX_CHAINS (Qwen3-300M set: 2, Qwen3-1.7B: 4)."""
+    import bench
+    from thorn_amd import optim as OPT
+    for config, want in ((2, 2), (5, 4)):
+        mats, _ = bench.config_shapes(config)
+        params = [torch.empty(sh, device='meta') for sh in mats]
+        n = OPT._chain_count(params)
+        assert n == want
+        chains = OPT._split_chains(params, n)
+        ids = [id(p) for c in chains for p in c]
+        assert sorted(ids) == sorted(id(p) for p in params)
+        order = {id(p): i for i, p in enumerate(params)}
+        for c in chains:
+            pos = [order[id(p)] for p in c]
+            assert pos == sorted(pos)
+        costs = [sum(OPT._ns_cost(p) for p in c) for c in chains]
+        assert max(costs) - min(costs) <= max(OPT._ns_cost(p) for p in params)
+    params = [torch.empty(1024, 384, device='meta')] * 3
+    assert OPT._chain_count(params) == 2
+    assert [len(c) for c in OPT._split_chains(params, 2)] == [1, 2]   # A B B

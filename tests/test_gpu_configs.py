@@ -208,11 +208,12 @@ def test_config5_every_shape():
     assert math.isfinite(worst['dp'])
 
 
-def test_two_chains_equal_one_plan():
-    """A group of at least CHAIN_MIN_MATRICES large matrices steps as two chains on two streams
-    (thorn_amd.optim._OrthoBatches); every matrix runs the same kernels on the same data as in one
-    plan, so parameters and state must match the one-plan step bit for bit, over steps with the
-    exact and the prescaled first iterate, and per-row normalization on the tall matrices."""
+@pytest.mark.parametrize('n_chains', [2, 3, 4])
+def test_chains_equal_one_plan(n_chains):
+    """A group of at least CHAIN_MIN_MATRICES large matrices steps as 2 to 4 chains on as many
+    streams (thorn_amd.optim._OrthoBatches); every matrix runs the same kernels on the same data as
+    in one plan, so parameters and state must match the one-plan step bit for bit, over steps with
+    the exact and the prescaled first iterate, and per-row normalization on the tall matrices."""
     import thorn_amd
     from thorn_amd import optim as OPT
     gen = torch.Generator().manual_seed(3407)
@@ -222,8 +223,9 @@ def test_two_chains_equal_one_plan():
 
     def run(chains: bool):
         params = [torch.nn.Parameter(t.to(DEV)) for t in init]
-        keep = OPT.CHAIN_MIN_MATRICES
+        keep = OPT.CHAIN_MIN_MATRICES, OPT._chain_count
         OPT.CHAIN_MIN_MATRICES = 16 if chains else 1 << 30
+        OPT._chain_count = lambda ps: n_chains
         try:
             opt = thorn_amd.THORN([{'params': params, 'orthogonalize': True, 'lr': 1e-3, 'weight_decay': 0.1}])
             for gs in grads:
@@ -232,10 +234,10 @@ def test_two_chains_equal_one_plan():
                 opt.step()
             torch.cuda.synchronize()
             runner = next(iter(opt._runners.values()))
-            assert runner.chained == chains and len(runner.plans) == (2 if chains else 1)
+            assert runner.chained == chains and len(runner.plans) == (n_chains if chains else 1)
             return params, opt
         finally:
-            OPT.CHAIN_MIN_MATRICES = keep
+            OPT.CHAIN_MIN_MATRICES, OPT._chain_count = keep
 
     pa, oa = run(True)
     pb, ob = run(False)

@@ -510,19 +510,37 @@ def _large_matrices(params: list) -> int:
     return n
 
 
-def _two_chains(params: list) -> tuple:
-    """The parameters dealt to two chains of equal Newton-Schulz work: by cost (s^2 * l per
-    matrix), largest first, in the order A B B A A B ..., each chain keeping the group's order."""
-    def cost(p):
-        r, c, batch = _matrix_view(p)
-        return batch * min(r, c) ** 2 * max(r, c)
-    ranked = sorted(range(len(params)), key=lambda i: -cost(params[i]))
-    side = {i: (k % 4 in (1, 2)) for k, i in enumerate(ranked)}
-    return [p for i, p in enumerate(params) if not side[i]], [p for i, p in enumerate(params) if side[i]]
+def _ns_cost(p) -> int:
+    """A parameter's Newton-Schulz work in units of s^2 * l per matrix."""
+    r, c, batch = _matrix_view(p)
+    return batch * min(r, c) ** 2 * max(r, c)
 
 
-# A group with at least this many large-path matrices steps as two chains (_OrthoBatches).
+def _chain_count(params: list) -> int:
+    """How many chains a group of large matrices steps as: one per CHAIN_COST of Newton-Schulz
+    work, at least 2 and at most MAX_CHAINS. Measured on one MI355X: the Qwen3-300M set (3.2e11)
+    steps fastest as 2 chains (3: +2.5%, 4: +7.5%), the Qwen3-1.7B set (3.3e12) as 4 (2: +6%)."""
+    return max(2, min(MAX_CHAINS, int(sum(_ns_cost(p) for p in params) // CHAIN_COST)))
+
+
+def _split_chains(params: list, n: int) -> list:
+    """The parameters dealt to n chains of about equal Newton-Schulz work: by cost (s^2 * l per
+    matrix), largest first, in snake order (for two: A B B A A B ...), each chain keeping the
+    group's order."""
+    ranked = sorted(range(len(params)), key=lambda i: -_ns_cost(params[i]))
+    chain = {}
+    for k, i in enumerate(ranked):
+        rnd, pos = divmod(k, n)
+        chain[i] = pos if rnd % 2 == 0 else n - 1 - pos
+    return [[p for i, p in enumerate(params) if chain[i] == c] for c in range(n)]
+
+
+# A group with at least CHAIN_MIN_MATRICES large-path matrices steps as chains (_OrthoBatches),
+# one per CHAIN_COST of work, at most MAX_CHAINS: the device has 4 hardware queues per process,
+# and the caller's stream takes the steps around the chains.
 CHAIN_MIN_MATRICES = 16
+CHAIN_COST = 1.5e11
+MAX_CHAINS = 4
 SMALL_MAX_S, SMALL_MAX_ELEMS = 256, 1 << 20   # the library's small-matrix path (thorn_abi.hip)
 
 
@@ -533,12 +551,13 @@ class _OrthoBatches:
     take the exact first iterate (the library keeps the cheaper prescaled one for a plan that
     stepped last on its workspace).
 
-    A group that is one batch with at least CHAIN_MIN_MATRICES large matrices runs as two chains
-    instead: two plans of equal Newton-Schulz work, each with its own workspace (together the size
-    of one plan's), on two streams of the optimizer, the second starting once the first one's
-    prologue launches are done. Each Newton-Schulz launch ends in a partly idle last round of
-    tiles; the other chain's launches, out of phase, fill it (on bench.py's Qwen3-300M-shaped
-    step, 7.07 -> 6.85 ms on one MI355X).
+    A group that is one batch with at least CHAIN_MIN_MATRICES large matrices runs as 2 to 4
+    chains instead (_chain_count): plans of about equal Newton-Schulz work, each with its own
+    workspace (together the size of one plan's), on streams of the optimizer, each starting once
+    the previous one's prologue launches are enqueued. The chains run out of phase, so one chain's
+    memory-bound launches and the partly idle last round of tiles of each of its Newton-Schulz
+    launches run beside the other chains' launches (bench.py on one MI355X: the Qwen3-300M set
+    7.07 -> 6.85 ms with 2 chains, the Qwen3-1.7B set 70.2 -> 53.8 ms with 4).
     The results are those of one plan bit for bit: every matrix runs the same kernels on the same
     data."""
 
@@ -547,15 +566,17 @@ class _OrthoBatches:
         self.runners = []
         self.chained = False
         workspace = None
-        chains = _two_chains(params) if len(params) > 1 else ([], [])
+        chains = _split_chains(params, _chain_count(params)) if len(params) > 1 else [[]]
         if len(batches) == 1 and not adam and _large_matrices(params) >= CHAIN_MIN_MATRICES and all(chains):
             self.chained = True
-            batches = list(chains)
-            # recorded by the first chain once its prologue is enqueued; the library records it
-            # again each step (a torch event is created when first recorded)
-            self.ns_begin = torch.cuda.Event()
-            self.ns_begin.record(torch.cuda.current_stream(device))
-            self.fork_join = (torch.cuda.Event(), torch.cuda.Event(), torch.cuda.Event())
+            batches = chains
+            # ns_begin[i]: recorded by chain i once its prologue is enqueued (the library records
+            # it again each step; a torch event is created when first recorded)
+            self.ns_begin = [torch.cuda.Event() for _ in chains[:-1]]
+            for ev in self.ns_begin:
+                ev.record(torch.cuda.current_stream(device))
+            self.fork = torch.cuda.Event()
+            self.joins = [torch.cuda.Event() for _ in chains]
         elif len(batches) > 1:
             sizes = [_lib.OrthoPlan(*_plan_shapes(b, group, adam)).workspace_bytes for b in batches]
             workspace = torch.zeros(max(1, max(sizes)), dtype=torch.uint8, device=device)
@@ -579,20 +600,17 @@ class _OrthoBatches:
             return
         dev = self.runners[0].device
         main = torch.cuda.current_stream(dev)
-        sa, sb = opt._chain_streams(dev)
-        fork, join_a, join_b = self.fork_join
-        fork.record(main)                 # gradients and state as the caller left them
-        sa.wait_event(fork)
-        sb.wait_event(fork)
-        with torch.cuda.stream(sa):
-            self.runners[0].run(opt, group, unmasked, ns_begin=self.ns_begin)
-        sb.wait_event(self.ns_begin)      # the first chain's prologue is done
-        with torch.cuda.stream(sb):
-            self.runners[1].run(opt, group, unmasked)
-        join_a.record(sa)                 # before anything else of the step reads the results
-        join_b.record(sb)
-        main.wait_event(join_a)
-        main.wait_event(join_b)
+        streams = opt._chain_streams(dev, len(self.runners))
+        self.fork.record(main)            # gradients and state as the caller left them
+        for i, (r, st) in enumerate(zip(self.runners, streams)):
+            st.wait_event(self.fork)
+            if i > 0:
+                st.wait_event(self.ns_begin[i - 1])   # the previous chain's prologue is done
+            with torch.cuda.stream(st):
+                r.run(opt, group, unmasked, ns_begin=self.ns_begin[i] if i < len(self.ns_begin) else None)
+        for ev, st in zip(self.joins, streams):    # before anything else of the step reads the results
+            ev.record(st)
+            main.wait_event(ev)
 
 
 class _AdamRunner:
@@ -816,16 +834,16 @@ class THORN(Optimizer):
     # this many is dropped with its workspace, so memory stays bounded when the set changes.
     _RUNNERS_PER_GROUP = 2
 
-    def _chain_streams(self, dev: torch.device) -> tuple:
-        """The two streams of a chained group on `dev` (default priority), taken one after the
+    def _chain_streams(self, dev: torch.device, n: int) -> tuple:
+        """The n streams of a chained group on `dev` (default priority), taken one after the
         other from torch's stream pool. The runtime maps streams to the device's hardware queues in
         turn, so the two get different queues; a chain on the caller's stream could share its
         queue with the other chain's stream and run serialized behind it (measured: 7.3-7.5
         against 6.8 ms per step on config 2)."""
-        s = self._side_streams.get(dev)
-        if s is None:
-            s = self._side_streams[dev] = (torch.cuda.Stream(dev), torch.cuda.Stream(dev))
-        return s
+        s = self._side_streams.setdefault(dev, [])
+        while len(s) < n:
+            s.append(torch.cuda.Stream(dev))
+        return tuple(s[:n])
 
     def _runner(self, key, factory):
         r = self._runners.pop(key, None)
