@@ -114,6 +114,13 @@ def test_plan_rejects_bad_shapes():
         _lib.OrthoPlan([4], [4], [_lib.MAT_MD | _lib.MAT_MD_SCALAR])
     with pytest.raises(_lib.ThornError, match='negative'):
         _lib.AdamPlan([3, -1])
+    # limits of the GEMM's and epilogues' 32-bit byte offsets
+    with pytest.raises(_lib.ThornError, match=r'more than 2\^29 elements'):
+        _lib.OrthoPlan([1 << 15], [1 << 14], [0])
+    with pytest.raises(_lib.ThornError, match='unsupported shape'):
+        _lib.OrthoPlan([2], [(1 << 20) + 1], [0])
+    _lib.OrthoPlan([2], [1 << 20], [0])
+    _lib.OrthoPlan([1 << 20], [2], [0])
 
 
 def test_plan_sizes_and_empty_plans():

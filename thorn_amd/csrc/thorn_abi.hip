@@ -491,6 +491,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     };
     for (int i = 0; i < n; ++i) {
         const ThornOrthoMatDesc& d = descs[i];
+        // sides up to 2^20: the epilogues' 32-bit byte offsets from a tile's first row reach
+        // 512 * ld < 2^31
         if (d.rows <= 0 || d.cols <= 0 || d.rows > (1 << 20) || d.cols > (1 << 20) ||
             d.rows * d.cols > (int64_t(1) << 30)) {
             delete plan;
