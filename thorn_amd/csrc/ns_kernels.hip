@@ -439,9 +439,9 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
     const TaskList& tl = second ? t1 : t0;
     const NsOp& op = second ? op1 : op0;
     if (op.kind == kOpNone) return;
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int local = b - tl.starts[k];
+    const int2 task = *reinterpret_cast<const int2*>(tl.map + 2 * b);   // matrix, tile within it
+    const OrthoMat& M = mats[task.x];
+    const int local = task.y;
 
     constexpr int KB = NsCfg::BM / NsCfg::BK;   // K tiles per block
     const int KTs = (M.s + NsCfg::BK - 1) / NsCfg::BK;

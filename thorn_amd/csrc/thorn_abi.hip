@@ -48,6 +48,7 @@ struct MatLayout {
 struct TaskOffsets {
     size_t order, starts;
     int32_t n, total;
+    size_t map = 0;   // the block map (TaskList::map), 0: none
 };
 
 // Optional per-launch timing: a pool of hipEvent pairs recorded around each launch while enabled.
@@ -193,8 +194,9 @@ namespace {
 
 using thorn::NsCfg;
 
-// Appends a task list (order + block starts) to the table layout.
-TaskOffsets add_tasks(size_t& off, const std::vector<int32_t>& order, const std::vector<int64_t>& blocks_of) {
+// Appends a task list (order + block starts, and with `map` the block map) to the table layout.
+TaskOffsets add_tasks(size_t& off, const std::vector<int32_t>& order, const std::vector<int64_t>& blocks_of,
+                      bool map = false) {
     TaskOffsets t;
     t.n = static_cast<int32_t>(order.size());
     int64_t total = 0;
@@ -204,6 +206,10 @@ TaskOffsets add_tasks(size_t& off, const std::vector<int32_t>& order, const std:
     off = align_up(off + sizeof(int32_t) * std::max<size_t>(1, order.size()), 16);
     t.starts = off;
     off = align_up(off + sizeof(int32_t) * (order.size() + 1), 16);
+    if (map) {
+        t.map = off;
+        off = align_up(off + 2 * sizeof(int32_t) * std::max<int64_t>(1, total), 16);
+    }
     return t;
 }
 
@@ -211,11 +217,18 @@ void write_tasks(char* host, const TaskOffsets& t, const std::vector<int32_t>& o
                  const std::vector<int64_t>& blocks_of) {
     int32_t* o = reinterpret_cast<int32_t*>(host + t.order);
     int32_t* s = reinterpret_cast<int32_t*>(host + t.starts);
+    int32_t* m = t.map ? reinterpret_cast<int32_t*>(host + t.map) : nullptr;
     int32_t acc = 0;
     for (size_t k = 0; k < order.size(); ++k) {
         o[k] = order[k];
         s[k] = acc;
-        acc += static_cast<int32_t>(blocks_of[order[k]]);
+        const int32_t nb = static_cast<int32_t>(blocks_of[order[k]]);
+        if (m)
+            for (int32_t j = 0; j < nb; ++j) {
+                m[2 * (acc + j)] = order[k];
+                m[2 * (acc + j) + 1] = j;
+            }
+        acc += nb;
     }
     s[order.size()] = acc;
 }
@@ -226,6 +239,7 @@ thorn::TaskList task_list(const char* dev, const TaskOffsets& t) {
     tl.starts = reinterpret_cast<const int32_t*>(dev + t.starts);
     tl.n = t.n;
     tl.total = t.total;
+    tl.map = t.map ? reinterpret_cast<const int32_t*>(dev + t.map) : nullptr;
     return tl;
 }
 
@@ -657,8 +671,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     off = align_up(sizeof(thorn::OrthoMat) * std::max(1, n), 64);
     plan->pre = add_tasks(off, plan->pre_order, mom_blocks);
     for (int q = 0; q < 2; ++q) {
-        plan->sym[q] = add_tasks(off, plan->sym_order[q], sym_blocks);
-        plan->g3[q] = add_tasks(off, plan->g3_order[q], g3_blocks);
+        plan->sym[q] = add_tasks(off, plan->sym_order[q], sym_blocks, true);
+        plan->g3[q] = add_tasks(off, plan->g3_order[q], g3_blocks, true);
     }
     plan->pnn = add_tasks(off, plan->pnn_order, mom_blocks);
     plan->rs = add_tasks(off, plan->rs_order, one_block);

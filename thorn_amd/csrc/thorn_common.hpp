@@ -269,6 +269,10 @@ struct TaskList {
     const int32_t* starts;
     int32_t n;
     int32_t total;
+    // optional (Newton-Schulz lists): per block b, map[2b] = the matrix (order[k] of its task k)
+    // and map[2b + 1] = b - starts[k], so a block finds its tile with one load instead of a
+    // search of dependent loads
+    const int32_t* map = nullptr;
 };
 
 // One tensor of a non-orthogonalized (Adam) group, flattened.
