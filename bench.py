@@ -548,6 +548,9 @@ def main() -> int:
     ap.add_argument('--single-chain', action='store_true',
                     help='step the orthogonalized group as one plan on one stream (the library default splits '
                          'a large group into two chains on two streams)')
+    ap.add_argument('--per-param', action='store_true',
+                    help='step each parameter on its own, opt.step(param=p), as gradient release does (a '
+                         'variant of the workload, not the headline line: step time only, no roofline)')
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
     ap.add_argument('--vendor-gemm', action='store_true',
@@ -586,6 +589,11 @@ def main() -> int:
         opt.polar_decomp_batch_size = args.polar_decomp_batch_size
 
     def one_step():
+        if args.per_param:   # gradient release: each parameter's step once its gradient is there
+            for p, g in zip(params, grads):
+                p.grad = g
+                opt.step(param=p)
+            return
         for p, g in zip(params, grads):
             p.grad = g
         opt.step()
@@ -609,6 +617,18 @@ def main() -> int:
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
     gpu_ms = ev0.elapsed_time(ev1) / args.steps
+
+    if args.per_param:   # one plan per parameter: step time only
+        print(json.dumps({
+            'metric': 'THORN step ms with gradient release (opt.step(param=p) for each parameter), 1 GPU',
+            'value': round(wall_ms, 3), 'unit': 'ms', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+            'ms_per_step': round(wall_ms, 3), 'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None,
+            'dtype': 'f16', 'data': 'synthetic',
+            'config': {'workload': f'config {args.config}, per-parameter steps', 'matrices': n_m,
+                       'adam_tensors': len(params) - n_m},
+            'gpu_event_ms_per_step': round(gpu_ms, 3), 'first_step_ms': round(first_ms, 1),
+            'runners': len(opt._runners), 'roofline': None, 'cpu_baseline': None}), flush=True)
+        return 0
 
     # per-kernel breakdown: the same K steps again with a HIP event pair around every launch
     plans = [pl for r in opt._runners.values() for pl in r.plans]

@@ -144,3 +144,27 @@ def test_chain_split_and_count():
     params = [torch.empty(1024, 384, device='meta')] * 3
     assert OPT._chain_count(params) == 2
     assert [len(c) for c in OPT._split_chains(params, 2)] == [1, 2]   # A B B
+
+
+def test_runner_cache_keeps_one_runner_per_parameter():
+    """Gradient release steps each parameter on its own: its runners (one per parameter) are kept,
+    up to the group's parameter count, apart from the runners of parameter subsets, of which the
+    two most recently used are kept."""
+    ps = [nn.Parameter(torch.zeros(4, 4)) for _ in range(3)]
+    opt = thorn_amd.THORN([{'params': ps, 'orthogonalize': True}])
+    built = []
+
+    def get(ids):
+        key = ('ortho', 0, 'dev', tuple(ids), ())
+        return opt._runner(key, lambda: built.append(ids) or object())
+
+    for _ in range(3):                       # three steps of gradient release: built once each
+        for i in range(3):
+            get([i])
+    assert built == [[0], [1], [2]]
+    get([0, 1]); get([1, 2]); get([0, 2])   # subsets: the two most recent are kept
+    keys = [k[3] for k in opt._runners]
+    assert (0, 1) not in keys and (1, 2) in keys and (0, 2) in keys
+    assert all((i,) in keys for i in range(3))
+    get([3])                                 # a fourth single-parameter key evicts the oldest one
+    assert sum(1 for k in opt._runners if len(k[3]) == 1) == 3

@@ -340,9 +340,10 @@ class _TableUpload:
         self.i = 0
 
     def host(self) -> torch.Tensor:
-        """The next buffer, once its last copy has run."""
+        """The next buffer, once its last copy has run (a query first: a blocking wait on an event
+        long completed still cost tens of microseconds, per parameter with gradient release)."""
         ev = self.events[self.i]
-        if ev is not None:
+        if ev is not None and not ev.query():
             ev.synchronize()
         return self.bufs[self.i]
 
@@ -356,13 +357,31 @@ class _TableUpload:
         self.i = (i + 1) % self.RING
 
 
+class _SharedWorkspace:
+    """One workspace for the single-parameter runners of a group on a device, which gradient
+    release steps one after another on one stream: as large as the largest of them, zero-filled
+    when allocated or grown. The library lets plans share a workspace whose steps do not overlap
+    (a plan that did not step last on it takes the exact first iterate). Gradient release is there
+    to save memory: the Newton-Schulz buffers then take one workspace for the largest parameter
+    instead of one per parameter (the Qwen3-300M set: 2.3 GB in all)."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.t: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.t is None or self.t.numel() < nbytes:
+            self.t = torch.zeros(max(1, nbytes), dtype=torch.uint8, device=self.device)
+        return self.t
+
+
 class _OrthoRunner:
     """One orthogonalized parameter set (or, with adam=True, the decouple_md tensors of a
     non-orthogonalized group, whose update is the Adam step): plan, workspace and the per-step
     table."""
 
     def __init__(self, params: list, group: _Group, device: torch.device, adam: bool = False,
-                 workspace: Optional[torch.Tensor] = None):
+                 workspace=None):
         self.params = params
         self.device = device
         self.adam = adam
@@ -372,12 +391,22 @@ class _OrthoRunner:
         self.owner = owner
         self.sub = np.asarray(sub, dtype=np.int64)
         self.plan = _lib.OrthoPlan(rows, cols, flags)
-        self.workspace = (torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
-                          if workspace is None else workspace)
+        # a tensor, a _SharedWorkspace, or None: a workspace of its own
+        self.shared = workspace if isinstance(workspace, _SharedWorkspace) else None
+        if self.shared is not None:
+            self._ws = None
+            self.shared.get(self.plan.workspace_bytes)
+        else:
+            self._ws = (torch.zeros(max(1, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
+                        if workspace is None else workspace)
         self.table = torch.empty(max(64, self.plan.table_bytes), dtype=torch.uint8, device=device)
         self.upload = _TableUpload(self.plan.table_bytes)
         self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
         self.md = group.decouple_md
+
+    @property
+    def workspace(self) -> torch.Tensor:
+        return self.shared.get(self.plan.workspace_bytes) if self.shared is not None else self._ws
 
     def run(self, opt: 'THORN', group: _Group, unmasked: Optional[dict] = None,
             ns_begin: Optional[torch.cuda.Event] = None) -> None:
@@ -561,7 +590,10 @@ class _OrthoBatches:
     The results are those of one plan bit for bit: every matrix runs the same kernels on the same
     data."""
 
-    def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False):
+    def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False,
+                 shared: Optional[_SharedWorkspace] = None):
+        """shared: the workspace of a single parameter's runner (gradient release), used when the
+        parameter is one plan."""
         batches = _batches(params, limit)
         self.runners = []
         self.chained = False
@@ -580,10 +612,14 @@ class _OrthoBatches:
         elif len(batches) > 1:
             sizes = [_lib.OrthoPlan(*_plan_shapes(b, group, adam)).workspace_bytes for b in batches]
             workspace = torch.zeros(max(1, max(sizes)), dtype=torch.uint8, device=device)
+        elif shared is not None:
+            workspace = shared
         for b in batches:
             self.runners.append(_OrthoRunner(b, group, device, adam, workspace))
-        self.workspace_bytes = (workspace.numel() if workspace is not None
-                                else sum(r.workspace.numel() for r in self.runners))
+
+    @property
+    def workspace_bytes(self) -> int:
+        return sum({ws.data_ptr(): ws.numel() for ws in self.workspaces}.values())
 
     @property
     def plans(self) -> list:
@@ -714,6 +750,7 @@ class THORN(Optimizer):
         self._runners: dict = {}
         self._magma_scratch: dict = {}
         self._side_streams: dict = {}
+        self._shared_ws: dict = {}   # (group index, device) -> _SharedWorkspace
         if isinstance(params, nn.Module) and conf.get('gradient_release', False):
             self.setup_gradient_release(params)
 
@@ -832,6 +869,10 @@ class THORN(Optimizer):
     # Runners (plan + workspace) kept per group and device: a new set of live parameters (some
     # without a gradient this step) builds a new runner, and the least recently used one beyond
     # this many is dropped with its workspace, so memory stays bounded when the set changes.
+    # Runners of a single parameter (gradient release steps each parameter on its own) are kept
+    # apart, one per parameter of the group at most: their workspaces add up to about one runner
+    # of the whole group, and rebuilding one per call would allocate a workspace and a table each
+    # time and lose the prescaled first iterate.
     _RUNNERS_PER_GROUP = 2
 
     def _chain_streams(self, dev: torch.device, n: int) -> tuple:
@@ -845,12 +886,21 @@ class THORN(Optimizer):
             s.append(torch.cuda.Stream(dev))
         return tuple(s[:n])
 
+    def _shared_workspace(self, gi: int, dev: torch.device) -> _SharedWorkspace:
+        w = self._shared_ws.get((gi, dev))
+        if w is None:
+            w = self._shared_ws[(gi, dev)] = _SharedWorkspace(dev)
+        return w
+
     def _runner(self, key, factory):
+        """The runner of key = (kind, group index, device, parameter ids, ...), built by factory()
+        if it is not kept."""
         r = self._runners.pop(key, None)
         if r is None:
-            slot = key[:3]   # (kind, group index, device)
-            same = [k for k in self._runners if k[:3] == slot]
-            for k in same[:max(0, len(same) - self._RUNNERS_PER_GROUP + 1)]:
+            slot, single = key[:3], len(key[3]) == 1
+            cap = len(self.param_groups[key[1]]['params']) if single else self._RUNNERS_PER_GROUP
+            same = [k for k in self._runners if k[:3] == slot and (len(k[3]) == 1) == single]
+            for k in same[:max(0, len(same) - cap + 1)]:
                 del self._runners[k]
             r = factory()
         self._runners[key] = r   # most recently used last
@@ -914,13 +964,15 @@ class THORN(Optimizer):
                     key = ('ortho', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
                            group.decouple_md, group.split_gain, group.force_per_neuron_norm,
                            group.betas[1] > 0, limit)
-                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit))
+                    shared = self._shared_workspace(gi, dev) if len(ps) == 1 else None
+                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, shared=shared))
                     runner.run(self, group, unmasked)
                 elif group.decouple_md:   # Adam step inside the decouple_md round trip (thorn.py:1704-1721)
                     limit = int(self.polar_decomp_batch_size)
                     key = ('mdadam', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
                            group.split_gain, tuple(_md_norm_rows(p, group) for p in ps), limit)
-                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, adam=True))
+                    shared = self._shared_workspace(gi, dev) if len(ps) == 1 else None
+                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, adam=True, shared=shared))
                     runner.run(self, group, unmasked)
                 else:
                     key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
