@@ -208,18 +208,22 @@ def test_config5_every_shape():
     assert math.isfinite(worst['dp'])
 
 
-@pytest.mark.parametrize('n_chains', [2, 3, 4])
-def test_chains_equal_one_plan(n_chains):
+@pytest.mark.parametrize('n_chains,variant', [(2, 'plain'), (3, 'plain'), (4, 'plain'), (2, 'magma'),
+                                              (2, 'md'), (3, 'update_rate')])
+def test_chains_equal_one_plan(n_chains, variant):
     """A group of at least CHAIN_MIN_MATRICES large matrices steps as 2 to 4 chains on as many
     streams (thorn_amd.optim._OrthoBatches); every matrix runs the same kernels on the same data as
     in one plan, so parameters and state must match the one-plan step bit for bit, over steps with
-    the exact and the prescaled first iterate, and per-row normalization on the tall matrices."""
+    the exact and the prescaled first iterate, and per-row normalization on the tall matrices; also
+    with Magma masks (some matrices skip a step; the masks come from the host PRNG, the same in
+    both runs), decouple_md gains, and update_rate 2 (every other step momentum only)."""
     import thorn_amd
     from thorn_amd import optim as OPT
     gen = torch.Generator().manual_seed(3407)
     shapes = [(384, 640), (640, 384), (512, 512), (1024, 384)] * 5 + [(3, 384, 512)]
     init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes]
-    grads = [[torch.randn(sh, generator=gen) * 1e-3 for sh in shapes] for _ in range(3)]
+    grads = [[torch.randn(sh, generator=gen) * 1e-3 for sh in shapes] for _ in range(4 if variant != 'plain' else 3)]
+    opts = {'magma': {'momentum_align': True}, 'md': {'decouple_md': True}}.get(variant, {})
 
     def run(chains: bool):
         params = [torch.nn.Parameter(t.to(DEV)) for t in init]
@@ -227,7 +231,11 @@ def test_chains_equal_one_plan(n_chains):
         OPT.CHAIN_MIN_MATRICES = 16 if chains else 1 << 30
         OPT._chain_count = lambda ps: n_chains
         try:
-            opt = thorn_amd.THORN([{'params': params, 'orthogonalize': True, 'lr': 1e-3, 'weight_decay': 0.1}])
+            torch.manual_seed(1234)   # Magma's per-parameter PRNG seeds
+            opt = thorn_amd.THORN([{'params': params, 'orthogonalize': True, 'lr': 1e-3, 'weight_decay': 0.1,
+                                    **opts}])
+            if variant == 'update_rate':
+                opt._update_rate = 2
             for gs in grads:
                 for p, g in zip(params, gs):
                     p.grad = g.to(DEV)
@@ -246,4 +254,4 @@ def test_chains_equal_one_plan(n_chains):
         for k, v in oa.state[p].items():
             if torch.is_tensor(v):
                 assert torch.equal(v, ob.state[q][k]), (i, k)
-    _log(f'two chains: {len(pa)} parameters bitwise equal to one plan over {len(grads)} steps')
+    _log(f'{n_chains} chains ({variant}): {len(pa)} parameters bitwise equal to one plan over {len(grads)} steps')
