@@ -531,6 +531,37 @@ def traffic_from_profile(kernel: str) -> float | None:
 # GPU measurement
 # ---------------------------------------------------------------------------------------------
 
+def time_launches(torch, thorn_amd, opt, one_step, steps: int):
+    """Runs `steps` steps with a HIP event pair around every launch of opt's plans. Orthogonalized
+    plans report each launch's start and end (a large group runs as chains on several streams whose
+    launches overlap); Adam plans their summed durations. Returns kind -> (summed ms, launches),
+    kind -> [(start ms, end ms)] and kind -> summed ms of the plans without intervals."""
+    plans = [pl for r in opt._runners.values() for pl in r.plans]
+    for pl in plans:
+        pl.timing_enable(64 * steps)
+    ref = torch.cuda.Event(enable_timing=True)
+    ref.record()
+    for _ in range(steps):
+        one_step()
+    torch.cuda.synchronize()
+    kinds: dict = {}
+    intervals: dict = {}
+    summed: dict = {}
+    for pl in plans:
+        if isinstance(pl, thorn_amd._lib.OrthoPlan):
+            for k, a, b in pl.timing_intervals(ref.cuda_event, 64 * steps):
+                tot, cnt = kinds.get(k, (0.0, 0))
+                kinds[k] = (tot + (b - a), cnt + 1)
+                intervals.setdefault(k, []).append((a, b))
+        else:
+            for k, (ms, n) in pl.timing_read().items():
+                tot, cnt = kinds.get(k, (0.0, 0))
+                kinds[k] = (tot + ms, cnt + n)
+                summed[k] = summed.get(k, 0.0) + ms
+        pl.timing_enable(0)
+    return kinds, intervals, summed
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -631,32 +662,7 @@ def main() -> int:
         return 0
 
     # per-kernel breakdown: the same K steps again with a HIP event pair around every launch
-    plans = [pl for r in opt._runners.values() for pl in r.plans]
-    for pl in plans:
-        pl.timing_enable(64 * args.steps)
-    ref = torch.cuda.Event(enable_timing=True)
-    ref.record()
-    for _ in range(args.steps):
-        one_step()
-    torch.cuda.synchronize()
-    # Orthogonalized plans report each launch's start and end (a large group runs as two chains on
-    # two streams whose launches overlap); Adam plans their summed durations. Kernel time is the
-    # union of its launches' intervals, which for launches that do not overlap is their sum.
-    kinds: dict = {}       # kind -> (summed ms, launches)
-    intervals: dict = {}   # kind -> [(start ms, end ms)] (orthogonalized plans)
-    summed: dict = {}      # kind -> summed ms (Adam plans: on the main stream, after the chains)
-    for pl in plans:
-        if isinstance(pl, thorn_amd._lib.OrthoPlan):
-            for k, a, b in pl.timing_intervals(ref.cuda_event, 64 * args.steps):
-                tot, cnt = kinds.get(k, (0.0, 0))
-                kinds[k] = (tot + (b - a), cnt + 1)
-                intervals.setdefault(k, []).append((a, b))
-        else:
-            for k, (ms, n) in pl.timing_read().items():
-                tot, cnt = kinds.get(k, (0.0, 0))
-                kinds[k] = (tot + ms, cnt + n)
-                summed[k] = summed.get(k, 0.0) + ms
-        pl.timing_enable(0)
+    kinds, intervals, summed = time_launches(torch, thorn_amd, opt, one_step, args.steps)
 
     def union_ms(names) -> float:
         """The union of the launch intervals of the given kernel kinds, plus their summed durations
@@ -689,6 +695,41 @@ def main() -> int:
     # launches of two chains overlap one another)
     u_avg = dom_ms / max(dom_launches, 1)
     achieved = ns_flops_per_launch / (u_avg * 1e-3) / 1e12 if u_avg > 0 else 0.0
+    chains = max([len(r.plans) if getattr(r, 'chained', False) else 1 for r in opt._runners.values()] + [1])
+    # With chains, the dominant kernel's launches share the chip with one another and with the
+    # other chains' memory-bound kernels. The same step as one plan on one stream (a second
+    # optimizer over the same parameters, after every figure above is taken) gives its rate alone.
+    one_chain = None
+    if chains > 1 and not args.momentum_align:
+        keep = thorn_amd.optim.CHAIN_MIN_MATRICES
+        thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
+        try:
+            opt1 = thorn_amd.THORN(groups)
+
+            def step1():
+                for p, g in zip(params, grads):
+                    p.grad = g
+                opt1.step()
+            for _ in range(max(3, args.warmup)):
+                step1()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                step1()
+            e1.record()
+            torch.cuda.synchronize()
+            k1, iv1, su1 = time_launches(torch, thorn_amd, opt1, step1, args.steps)
+            d1 = (_union_us([x for k in dom_kinds for x in iv1.get(k, [])])
+                  + sum(su1.get(k, 0.0) for k in dom_kinds)) / args.steps
+            n1 = sum(k1.get(k, (0.0, 0))[1] for k in dom_kinds) / args.steps
+            a1 = dom_flops / (d1 * 1e-3) / 1e12 if d1 > 0 else 0.0
+            one_chain = {'gpu_ms_per_step': round(e0.elapsed_time(e1) / args.steps, 3), 'achieved': round(a1, 1),
+                         'frac': round(a1 / MFMA_PEAK_TFLOPS, 4), 'launches_per_step': n1,
+                         'avg_launch_ms': round(d1 / max(n1, 1), 4)}
+            del opt1
+        finally:
+            thorn_amd.optim.CHAIN_MIN_MATRICES = keep
     phases = {k: {'ms_per_launch': round(ms / n, 4), 'launches_per_step': n / args.steps}
               for k, (ms, n) in sorted(kinds.items())}
 
@@ -733,8 +774,7 @@ def main() -> int:
                      'traffic': traffic_from_profile(dom_name), 'flops_per_launch': ns_flops_per_launch,
                      'launches_per_step': dom_launches, 'avg_launch_ms': round(u_avg, 4),
                      'active_ms_per_step': round(dom_ms, 3), 'launch_ms_sum_per_step': round(dom_sum_ms, 3),
-                     'chains': max([len(r.plans) if getattr(r, 'chained', False) else 1
-                                    for r in opt._runners.values()] + [1])},
+                     'chains': chains, 'one_chain': one_chain},
         'launches_per_step': {'ns': ns_launches,
                               'total': sum(n for _, n in kinds.values()) / args.steps},
         'phases': phases,
