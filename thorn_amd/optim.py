@@ -1003,6 +1003,9 @@ class THORN(Optimizer):
 
     @torch.no_grad()
     def step(self, closure: Optional[Callable[[], float]] = None, *, param: Optional[torch.nn.Parameter] = None):
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError('THORN.step cannot be captured in a CUDA/HIP graph: every step fills its launch '
+                               'tables on the host and uploads them from pinned memory')
         loss = None
         if closure is not None:
             with torch.enable_grad():
