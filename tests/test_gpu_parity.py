@@ -243,6 +243,40 @@ def test_single_matrix_update(shape, wd):
     _log(f'[gpu]   {w}')
 
 
+# The large-matrix path at its edges: s <= 256 but s * l >= 2^20 (less than one 256-wide tile of
+# the short side), a last tile with one valid row (s = 257), a tall ragged matrix, and a Gram
+# contraction of 262144 over 4 rows (one K tile of the other products, zero-padded to four).
+EDGE_LARGE = [(128, 8192), (8200, 130), (1000, 300), (257, 1030), (4, 262144)]
+
+
+@pytest.mark.parametrize('shape', EDGE_LARGE)
+def test_large_path_edge_shapes(shape):
+    """One step on one matrix of the large-matrix path (ns_phase_kernel) against the oracle and the
+    closed form, at tile edges the configs do not reach."""
+    _log(f'[gpu] large-path edge {shape}')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(shape[0] * 3 + shape[1])
+    p0 = torch.randn(shape, generator=g) * 0.02
+    grad = torch.randn(shape, generator=g) * 1e-3
+    pc = torch.nn.Parameter(p0.clone())
+    pg = torch.nn.Parameter(p0.clone().to(DEV))
+    grp = dict(orthogonalize=True, lr=1e-2, weight_decay=0.1)
+    cpu = O.OracleTHORN([dict(grp, params=[pc])])
+    gpu = thorn_amd.THORN([dict(grp, params=[pg])])
+    pc.grad = grad.clone()
+    pg.grad = grad.clone().to(DEV)
+    cpu.step()
+    gpu.step()
+    torch.cuda.synchronize()
+    assert rel(gpu.state[pg]['moment'], cpu.state[pc]['moment']) <= 1e-6
+    dpg = pg.detach().cpu() - p0
+    dpc = pc.detach() - p0
+    dpe = exact_dp(p0, grad, torch.zeros_like(p0), grp)
+    w = {}
+    check_ortho_dp(dpg, dpc, dpe, w, f'{shape}')
+    _log(f'[gpu]   {w}')
+
+
 @pytest.mark.parametrize('shape', NEAR_SQUARE)
 def test_near_square_matrix_update(shape):
     """Nearly square non-square matrices (see NEAR_SQUARE): the update is within NEAR_SQUARE_TOL of
