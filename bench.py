@@ -580,8 +580,10 @@ def main() -> int:
                     help='step the orthogonalized group as one plan on one stream (the library default splits '
                          'a large group into two chains on two streams)')
     ap.add_argument('--per-param', action='store_true',
-                    help='step each parameter on its own, opt.step(param=p), as gradient release does (a '
+                    help='step each parameter on its own, as gradient release does from its hook (a '
                          'variant of the workload, not the headline line: step time only, no roofline)')
+    ap.add_argument('--in-order', action='store_true',
+                    help='with --per-param: every step on the caller\'s stream, in order')
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
     ap.add_argument('--vendor-gemm', action='store_true',
@@ -604,6 +606,8 @@ def main() -> int:
 
     if args.single_chain:
         thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
+    if args.in_order:
+        thorn_amd.optim.RELEASE_OVERLAP = False
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     if args.copy_cal_mib:
@@ -620,10 +624,11 @@ def main() -> int:
         opt.polar_decomp_batch_size = args.polar_decomp_batch_size
 
     def one_step():
-        if args.per_param:   # gradient release: each parameter's step once its gradient is there
-            for p, g in zip(params, grads):
+        if args.per_param:   # gradient release: each parameter's step once its gradient is there,
+            for p, g in zip(params, grads):   # as the hooks run it, joined as at the end of backward
                 p.grad = g
-                opt.step(param=p)
+                opt._release_step(p, join_later=True)
+            opt._release_join()
             return
         for p, g in zip(params, grads):
             p.grad = g
@@ -655,7 +660,8 @@ def main() -> int:
             'value': round(wall_ms, 3), 'unit': 'ms', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
             'ms_per_step': round(wall_ms, 3), 'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None,
             'dtype': 'f16', 'data': 'synthetic',
-            'config': {'workload': f'config {args.config}, per-parameter steps', 'matrices': n_m,
+            'config': {'workload': f'config {args.config}, per-parameter steps'
+                       + (' in order' if args.in_order else ' (large ones on the release streams)'), 'matrices': n_m,
                        'adam_tensors': len(params) - n_m},
             'gpu_event_ms_per_step': round(gpu_ms, 3), 'first_step_ms': round(first_ms, 1),
             'runners': len(opt._runners), 'roofline': None, 'cpu_baseline': None}), flush=True)

@@ -819,6 +819,49 @@ def test_gradient_release(rate):
     _log('[gpu]   ok')
 
 
+def test_gradient_release_overlapped_equals_in_order():
+    """Gradient release steps large orthogonalized parameters on the optimizer's streams, joined
+    when backward ends (THORN._release_step). Six 512-wide layers (two per stream, so every step
+    takes the exact first iterate, as in one stream) trained three steps through the hooks must
+    match the same training with every step in order on the caller's stream, bit for bit."""
+    thorn_amd = _thorn()
+    from thorn_amd import optim as OPT
+    dims = [512, 640, 512, 768, 512, 1024, 512]
+    gen = torch.Generator().manual_seed(77)
+    init = [torch.randn(dims[i + 1], dims[i], generator=gen) * 0.03 for i in range(6)]
+    xs = [torch.randn(64, 512, generator=gen) for _ in range(3)]
+
+    def run(overlap: bool):
+        model = torch.nn.Sequential(*[torch.nn.Linear(dims[i], dims[i + 1], bias=False) for i in range(6)]).to(DEV)
+        with torch.no_grad():
+            for lin, w in zip(model, init):
+                lin.weight.copy_(w.to(DEV))
+        keep = OPT.RELEASE_OVERLAP
+        OPT.RELEASE_OVERLAP = overlap
+        try:
+            opt = thorn_amd.THORN([{'params': list(model.parameters()), 'orthogonalize': True, 'lr': 1e-2,
+                                    'weight_decay': 0.1}])
+            opt.setup_gradient_release(model)
+            for x in xs:
+                h = x.to(DEV)
+                for lin in model:
+                    h = torch.tanh(lin(h))
+                h.square().mean().backward()
+            torch.cuda.synchronize()
+            assert opt._release_queued is False and not opt._release_pending
+        finally:
+            OPT.RELEASE_OVERLAP = keep
+        return model, opt
+
+    ma, oa = run(True)
+    mb, ob = run(False)
+    for i, (pa, pb) in enumerate(zip(ma.parameters(), mb.parameters())):
+        assert torch.equal(pa.detach(), pb.detach()), i
+        assert torch.equal(oa.state[pa]['moment'], ob.state[pb]['moment']), i
+        assert oa.state[pa]['step'] == ob.state[pb]['step'], i
+    _log('[gpu]   overlapped gradient release equals the in-order steps bit for bit')
+
+
 @pytest.mark.parametrize('rate', [1, 2])
 def test_sparse_gradients(rate):
     """Row-sparse gradients (thorn.py:1667-1700) against the oracle over six steps: an embedding
