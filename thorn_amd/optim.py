@@ -1036,8 +1036,8 @@ class THORN(Optimizer):
         only a few of the device's CUs, and the parameters' steps are independent, so a large
         orthogonalized parameter steps on one of RELEASE_STREAMS streams in turn, after the work
         the caller's stream holds now, and the caller's stream waits for it in _release_join
-        (config 2: 41.2 instead of 79.9 ms per step of hooks). join_later=False joins at once.
-        Other parameters step on the caller's stream."""
+        (config 2: 49.6-65.3 against 94.6-98.7 ms per step of hooks in order). join_later=False
+        joins at once. Other parameters step on the caller's stream."""
         group = self._param_to_group[id(p)]
         if (not RELEASE_OVERLAP or not p.is_cuda or not group['orthogonalize'] or p.grad is None
                 or p.grad.is_sparse or _large_matrices([p]) == 0):
