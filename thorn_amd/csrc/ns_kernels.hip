@@ -247,8 +247,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     // update's tile is staged; every output of the update is the f16 rounding of acc * osc
     // (plus the X term)
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
-    _Float16* const xin = op.xsel == kXA ? M.xa : M.xb;
-    _Float16* const xout = op.xsel == kXA ? M.xb : M.xa;
+    _Float16* const xout = op.xsel == kXA ? M.xb : M.xa;   // the input iterate's tile is in the staging
 
     // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) streams p
     // through a ring of D row chunks: chunk L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32)
