@@ -584,6 +584,9 @@ def main() -> int:
                          'variant of the workload, not the headline line: step time only, no roofline)')
     ap.add_argument('--in-order', action='store_true',
                     help='with --per-param: every step on the caller\'s stream, in order')
+    ap.add_argument('--release-window-mib', type=float, default=None,
+                    help='with --per-param: gradient bytes per gradient-release window (the library\'s '
+                         'RELEASE_WINDOW_BYTES; 0: each parameter alone)')
     ap.add_argument('--copy-cal-mib', type=int, default=0,
                     help='run one torch.neg over this many MiB first (counter calibration)')
     ap.add_argument('--vendor-gemm', action='store_true',
@@ -608,6 +611,8 @@ def main() -> int:
         thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
     if args.in_order:
         thorn_amd.optim.RELEASE_OVERLAP = False
+    if args.release_window_mib is not None:
+        thorn_amd.optim.RELEASE_WINDOW_BYTES = int(args.release_window_mib * (1 << 20))
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     if args.copy_cal_mib:
@@ -661,7 +666,9 @@ def main() -> int:
             'ms_per_step': round(wall_ms, 3), 'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None,
             'dtype': 'f16', 'data': 'synthetic',
             'config': {'workload': f'config {args.config}, per-parameter steps'
-                       + (' in order' if args.in_order else ' (large ones on the release streams)'), 'matrices': n_m,
+                       + (' in order' if args.in_order else
+                          f' (large ones in windows of {thorn_amd.optim.RELEASE_WINDOW_BYTES >> 20} MiB of gradients '
+                          'on the release streams)'), 'matrices': n_m,
                        'adam_tensors': len(params) - n_m},
             'gpu_event_ms_per_step': round(gpu_ms, 3), 'first_step_ms': round(first_ms, 1),
             'runners': len(opt._runners), 'roofline': None, 'cpu_baseline': None}), flush=True)

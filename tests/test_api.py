@@ -168,3 +168,38 @@ def test_runner_cache_keeps_one_runner_per_parameter():
     assert all((i,) in keys for i in range(3))
     get([3])                                 # a fourth single-parameter key evicts the oldest one
     assert sum(1 for k in opt._runners if len(k[3]) == 1) == 3
+
+
+def test_runner_cache_keeps_gradient_release_windows():
+    """Gradient release steps windows of parameters (RELEASE_WINDOW_BYTES of gradients each): their
+    runners are kept apart, up to the group's parameter count, whatever the windows' sizes, and do
+    not displace the runners of the group's own steps."""
+    from thorn_amd import optim as OPT
+    ps = [nn.Parameter(torch.zeros(4, 4)) for _ in range(4)]
+    opt = thorn_amd.THORN([{'params': ps, 'orthogonalize': True}])
+    built = []
+
+    def get(kind, ids):
+        return opt._runner((kind, 0, 'dev', tuple(ids), ()), lambda: built.append((kind, ids)) or object())
+
+    get('ortho', [0, 1, 2, 3])
+    for _ in range(3):                       # three backward passes with the same windows
+        get('release', [3, 2]); get('release', [1]); get('release', [0])
+    assert built == [('ortho', [0, 1, 2, 3]), ('release', [3, 2]), ('release', [1]), ('release', [0])]
+    get('release', [3]); get('release', [2, 1, 0])   # other windows: the oldest ones go beyond 4
+    kinds = [(k[0], k[3]) for k in opt._runners]
+    assert ('ortho', (0, 1, 2, 3)) in kinds and ('release', (3, 2)) not in kinds
+    assert sum(1 for k in kinds if k[0] == 'release') == 4
+    assert OPT._window_full(OPT.RELEASE_WINDOW_BYTES) and not OPT._window_full(OPT.RELEASE_WINDOW_BYTES - 1)
+
+
+def test_gradient_release_on_cpu_steps_at_once():
+    """Parameters off the GPU (and small or non-orthogonalized ones) never wait in a window: the
+    hook's step runs at once and the hook drops the gradient."""
+    p = nn.Parameter(torch.zeros(4, 4))
+    opt = thorn_amd.THORN([{'params': [p], 'orthogonalize': True}])
+    p.grad = torch.ones(4, 4)
+    called = []
+    opt.step = lambda closure=None, *, param=None: called.append(param)
+    assert opt._release_step(p, join_later=True) is True
+    assert called == [p] and not opt._release_windows

@@ -819,11 +819,17 @@ def test_gradient_release(rate):
     _log('[gpu]   ok')
 
 
-def test_gradient_release_overlapped_equals_in_order():
-    """Gradient release steps large orthogonalized parameters on the optimizer's streams, joined
-    when backward ends (THORN._release_step). Six 512-wide layers (two per stream, so every step
-    takes the exact first iterate, as in one stream) trained three steps through the hooks must
-    match the same training with every step in order on the caller's stream, bit for bit."""
+@pytest.mark.parametrize('window,rate', [(0, 1), (3 << 20, 1), (None, 1), (None, 2)])
+def test_gradient_release_overlapped_equals_in_order(window, rate):
+    """Gradient release steps large orthogonalized parameters in windows of RELEASE_WINDOW_BYTES
+    of gradients, one plan each, on the optimizer's streams, joined when backward ends
+    (THORN._release_step). Six 512-wide layers (below 2^20 elements, so every step takes the exact
+    first iterate) trained three steps through the hooks must match the same training with every
+    step in order on the caller's stream, bit for bit: windows of one parameter (0), of two in
+    backward order (3 MiB: two windows stepped from hooks, the last one when backward ends), and
+    the default (all six, stepped when backward ends); with update_rate 2 a window's matrices step
+    every other backward."""
+    _log(f'[gpu] gradient release, window {window}, update_rate {rate}')
     thorn_amd = _thorn()
     from thorn_amd import optim as OPT
     dims = [512, 640, 512, 768, 512, 1024, 512]
@@ -836,24 +842,29 @@ def test_gradient_release_overlapped_equals_in_order():
         with torch.no_grad():
             for lin, w in zip(model, init):
                 lin.weight.copy_(w.to(DEV))
-        keep = OPT.RELEASE_OVERLAP
+        keep = OPT.RELEASE_OVERLAP, OPT.RELEASE_WINDOW_BYTES
         OPT.RELEASE_OVERLAP = overlap
+        if window is not None:
+            OPT.RELEASE_WINDOW_BYTES = window
         try:
             opt = thorn_amd.THORN([{'params': list(model.parameters()), 'orthogonalize': True, 'lr': 1e-2,
                                     'weight_decay': 0.1}])
-            opt.setup_gradient_release(model)
+            opt.setup_gradient_release(model, update_rate=rate)
             for x in xs:
                 h = x.to(DEV)
                 for lin in model:
                     h = torch.tanh(lin(h))
                 h.square().mean().backward()
             torch.cuda.synchronize()
-            assert opt._release_queued is False and not opt._release_pending
+            assert opt._release_queued is False and not opt._release_pending and not opt._release_windows
+            assert all(p.grad is None for p in model.parameters())
         finally:
-            OPT.RELEASE_OVERLAP = keep
+            OPT.RELEASE_OVERLAP, OPT.RELEASE_WINDOW_BYTES = keep
         return model, opt
 
     ma, oa = run(True)
+    sizes = sorted(len(k[3]) for k in oa._runners if k[0] == 'release')
+    assert sizes == {0: [1] * 6, 3 << 20: [2, 2, 2], None: [6]}[window], sizes
     mb, ob = run(False)
     for i, (pa, pb) in enumerate(zip(ma.parameters(), mb.parameters())):
         assert torch.equal(pa.detach(), pb.detach()), i

@@ -358,14 +358,13 @@ class _TableUpload:
 
 
 class _SharedWorkspace:
-    """The workspace of the single-parameter runners of a group on a device (gradient release),
-    one buffer per stream they run on: as large as the largest of them, zero-filled when allocated
-    or grown. The library lets plans share a workspace whose steps do not overlap (a plan that did
-    not step last on it takes the exact first iterate); steps on one stream never overlap, steps on
-    different streams may (THORN._release_step), so each stream has its own buffer. Gradient
-    release is there to save memory: the Newton-Schulz buffers then take a workspace for the
-    largest parameter per stream instead of one per parameter (the Qwen3-300M set: 2.3 GB in
-    all)."""
+    """The workspace of the single-parameter and gradient-release window runners of a group on a
+    device, one buffer per stream they run on: as large as the largest of them, zero-filled when
+    allocated or grown. The library lets plans share a workspace whose steps do not overlap (a plan
+    that did not step last on it takes the exact first iterate); steps on one stream never overlap,
+    steps on different streams may (THORN._release_flush), so each stream has its own buffer.
+    Gradient release is there to save memory: the Newton-Schulz buffers then take a workspace for
+    the largest window per stream instead of one per parameter or window."""
 
     def __init__(self, device: torch.device):
         self.device = device
@@ -578,6 +577,16 @@ MAX_CHAINS = 4
 # device's 4 hardware queues of a process (4 of them measured 54.8 ms on config 2's hooks, 3 41.2).
 RELEASE_STREAMS = 3
 RELEASE_OVERLAP = True   # False: every released step on the caller's stream, in order
+# Gradient release keeps the gradients of large orthogonalized parameters until this many bytes of
+# them are there (or backward ends) and steps them as one plan: one parameter's Newton-Schulz
+# launches fill only 10-48 of the device's 256 CUs. This bounds the gradient memory held back
+# beyond the reference's (which drops each gradient in its hook); 0 steps each parameter alone.
+RELEASE_WINDOW_BYTES = 256 << 20
+
+
+def _window_full(grad_bytes: int) -> bool:
+    """A gradient-release window holding grad_bytes of gradients steps now."""
+    return grad_bytes >= RELEASE_WINDOW_BYTES
 SMALL_MAX_S, SMALL_MAX_ELEMS = 256, 1 << 20   # the library's small-matrix path (thorn_abi.hip)
 
 
@@ -599,14 +608,14 @@ class _OrthoBatches:
     data."""
 
     def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False,
-                 shared: Optional[_SharedWorkspace] = None):
-        """shared: the workspace of a single parameter's runner (gradient release), used when the
-        parameter is one plan."""
+                 shared: Optional[_SharedWorkspace] = None, chain: bool = True):
+        """shared: the per-stream workspace of gradient release's runners, used when the parameters
+        are one plan. chain=False: never chains (gradient release runs on the chains' streams)."""
         batches = _batches(params, limit)
         self.runners = []
         self.chained = False
         workspace = None
-        chains = _split_chains(params, _chain_count(params)) if len(params) > 1 else [[]]
+        chains = _split_chains(params, _chain_count(params)) if len(params) > 1 and chain else [[]]
         if len(batches) == 1 and not adam and _large_matrices(params) >= CHAIN_MIN_MATRICES and all(chains):
             self.chained = True
             batches = chains
@@ -763,6 +772,8 @@ class THORN(Optimizer):
         self._release_events: dict = {}    # device -> the fork event and one join event per stream
         self._release_next = 0
         self._release_queued = False   # a join is queued for the end of the current backward pass
+        # (group index, device) -> [stream, parameters, gradient bytes]: a window not stepped yet
+        self._release_windows: dict = {}
         if isinstance(params, nn.Module) and conf.get('gradient_release', False):
             self.setup_gradient_release(params)
 
@@ -881,10 +892,9 @@ class THORN(Optimizer):
     # Runners (plan + workspace) kept per group and device: a new set of live parameters (some
     # without a gradient this step) builds a new runner, and the least recently used one beyond
     # this many is dropped with its workspace, so memory stays bounded when the set changes.
-    # Runners of a single parameter (gradient release steps each parameter on its own) are kept
-    # apart, one per parameter of the group at most: their workspaces add up to about one runner
-    # of the whole group, and rebuilding one per call would allocate a workspace and a table each
-    # time and lose the prescaled first iterate.
+    # Runners of a single parameter and those of gradient release's windows are kept apart, one per
+    # parameter of the group at most: they share one workspace per stream, and rebuilding one per
+    # call would allocate a table and a pinned buffer each time.
     _RUNNERS_PER_GROUP = 2
 
     def _chain_streams(self, dev: torch.device, n: int) -> tuple:
@@ -909,9 +919,10 @@ class THORN(Optimizer):
         if it is not kept."""
         r = self._runners.pop(key, None)
         if r is None:
-            slot, single = key[:3], len(key[3]) == 1
+            per_param = lambda k: len(k[3]) == 1 or k[0] == 'release'
+            slot, single = key[:3], per_param(key)
             cap = len(self.param_groups[key[1]]['params']) if single else self._RUNNERS_PER_GROUP
-            same = [k for k in self._runners if k[:3] == slot and (len(k[3]) == 1) == single]
+            same = [k for k in self._runners if k[:3] == slot and per_param(k) == single]
             for k in same[:max(0, len(same) - cap + 1)]:
                 del self._runners[k]
             r = factory()
@@ -919,7 +930,9 @@ class THORN(Optimizer):
         return r
 
     # -- step (thorn.py:1583-1753) ---------------------------------------------------------------
-    def _step_params(self, params: list, group: _Group, gi: int) -> None:
+    def _step_params(self, params: list, group: _Group, gi: int, release: bool = False) -> None:
+        """release: a gradient-release window of large orthogonalized parameters (_release_flush),
+        one plan on the current stream's shared workspace, never chained."""
         live = []
         sparse = []
         for p in params:
@@ -973,11 +986,12 @@ class THORN(Optimizer):
             with torch.cuda.device(dev):
                 if group.orthogonalize:
                     limit = int(self.polar_decomp_batch_size)
-                    key = ('ortho', gi, dev, tuple(id(p) for p in ps), tuple(tuple(p.shape) for p in ps),
-                           group.decouple_md, group.split_gain, group.force_per_neuron_norm,
-                           group.betas[1] > 0, limit)
-                    shared = self._shared_workspace(gi, dev) if len(ps) == 1 else None
-                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, shared=shared))
+                    key = ('release' if release else 'ortho', gi, dev, tuple(id(p) for p in ps),
+                           tuple(tuple(p.shape) for p in ps), group.decouple_md, group.split_gain,
+                           group.force_per_neuron_norm, group.betas[1] > 0, limit)
+                    shared = self._shared_workspace(gi, dev) if len(ps) == 1 or release else None
+                    runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, shared=shared,
+                                                                     chain=not release))
                     runner.run(self, group, unmasked)
                 elif group.decouple_md:   # Adam step inside the decouple_md round trip (thorn.py:1704-1721)
                     limit = int(self.polar_decomp_batch_size)
@@ -1031,39 +1045,69 @@ class THORN(Optimizer):
             self._step_params([param], _Group.from_kwargs(**group), gi)
         return loss
 
-    def _release_step(self, p: torch.Tensor, join_later: bool) -> None:
-        """step(param=p) as gradient release runs it. The Newton-Schulz launches of one matrix fill
-        only a few of the device's CUs, and the parameters' steps are independent, so a large
-        orthogonalized parameter steps on one of RELEASE_STREAMS streams in turn, after the work
-        the caller's stream holds now, and the caller's stream waits for it in _release_join
-        (config 2: 49.6-65.3 against 94.6-98.7 ms per step of hooks in order). join_later=False
+    def _release_step(self, p: torch.Tensor, join_later: bool) -> bool:
+        """step(param=p) as gradient release runs it. Returns whether p's gradient may be dropped
+        now; False: its step is queued in a window, whose step drops the gradient itself.
+
+        The Newton-Schulz launches of one matrix fill only a few of the device's CUs, and the
+        parameters' steps are independent, so a large orthogonalized parameter joins its group's
+        window: once the window holds RELEASE_WINDOW_BYTES of gradients it steps as one plan on the
+        next of RELEASE_STREAMS streams (_release_flush), and the caller's stream waits for it in
+        _release_join, which also steps what the windows still hold. join_later=False steps and
         joins at once. Other parameters step on the caller's stream."""
         group = self._param_to_group[id(p)]
         if (not RELEASE_OVERLAP or not p.is_cuda or not group['orthogonalize'] or p.grad is None
                 or p.grad.is_sparse or _large_matrices([p]) == 0):
             self.step(param=p)
+            return True
+        gi = next(i for i, g in enumerate(self.param_groups) if g is group)
+        key = (gi, p.device)
+        cur = torch.cuda.current_stream(p.device)
+        w = self._release_windows.get(key)
+        if w is not None and (w[0] != cur or any(q is p for q in w[1])):
+            self._release_flush(key)   # a window holds gradients of one stream, each parameter once
+            w = None
+        if w is None:
+            w = self._release_windows[key] = [cur, [], 0]
+        w[1].append(p)
+        w[2] += p.grad.numel() * p.grad.element_size()
+        if not join_later or _window_full(w[2]):
+            self._release_flush(key)
+        if not join_later:
+            self._release_join()
+        return False
+
+    def _release_flush(self, key) -> None:
+        """Step the parameters of window `key` as one plan on the next release stream, after the
+        work their gradients' stream holds now, and drop their gradients as the hooks do. Config
+        2's hooks on one MI355X: 7.67 ms per step with 256 MiB windows, 40.4 with one parameter
+        per window, 82.9 in order on the caller's stream, 6.8 for the grouped step."""
+        w = self._release_windows.pop(key, None)
+        if w is None:
             return
-        dev = p.device
-        main = torch.cuda.current_stream(dev)
+        src, ps, _ = w
+        gi, dev = key
         k = self._release_next % RELEASE_STREAMS
         self._release_next += 1
         st = self._chain_streams(dev, RELEASE_STREAMS)[k]
         evs = self._release_events.get(dev)
         if evs is None:
             evs = self._release_events[dev] = [torch.cuda.Event() for _ in range(RELEASE_STREAMS + 1)]
-        evs[0].record(main)   # a wait takes the event as it is when enqueued, so one event serves
+        evs[0].record(src)   # a wait takes the event as it is when enqueued, so one event serves
         st.wait_event(evs[0])
-        g = p.grad
-        with torch.cuda.stream(st):
-            self.step(param=p)
-        g.record_stream(st)   # the caller drops the gradient once the hook returns
+        grads = [p.grad for p in ps]
+        with torch.no_grad(), torch.cuda.stream(st):
+            self._step_params(ps, _Group.from_kwargs(**self.param_groups[gi]), gi, release=True)
+        for p, g in zip(ps, grads):
+            g.record_stream(st)   # dropped here, still read by the stream's step
+            p.grad = None
         self._release_pending.setdefault(dev, set()).add(k)
-        if not join_later:
-            self._release_join()
 
     def _release_join(self) -> None:
-        """The caller's streams wait for every released step: for the last work of each stream
-        that ran one (a stream runs its steps in order)."""
+        """Step what the windows still hold; then the caller's streams wait for every released
+        step: for the last work of each stream that ran one (a stream runs its steps in order)."""
+        for key in list(self._release_windows):
+            self._release_flush(key)
         for dev, ks in self._release_pending.items():
             main = torch.cuda.current_stream(dev)
             streams = self._chain_streams(dev, RELEASE_STREAMS)
@@ -1073,25 +1117,28 @@ class THORN(Optimizer):
                 main.wait_event(evs[k + 1])
         self._release_pending = {}
         self._release_queued = False
+        self._release_next = 0
 
-    def _release_hook_step(self, p: torch.Tensor) -> None:
+    def _release_hook_step(self, p: torch.Tensor) -> bool:
         """From a post-accumulate-grad hook: the released steps of one backward pass are joined
-        when it ends (a callback of the autograd engine), before anything after backward runs."""
+        when it ends (a callback of the autograd engine, run on the caller's streams once they
+        have waited for the gradients), before anything after backward runs. Returns whether the
+        hook drops p's gradient (see _release_step)."""
         if not self._release_queued:
             try:
                 torch.autograd.Variable._execution_engine.queue_callback(self._release_join)
                 self._release_queued = True
             except RuntimeError:   # not inside a backward pass: join at once
                 pass
-        self._release_step(p, join_later=self._release_queued)
+        return self._release_step(p, join_later=self._release_queued)
 
     def setup_gradient_release(self, model: nn.Module, update_rate: int = 1, ignore_existing_hooks: bool = False):
         """thorn.py:1755-1776: step each parameter from its post-accumulate-grad hook (large
         orthogonalized parameters on the optimizer's streams, joined when the backward pass ends:
         _release_step)."""
         def _hook(param: torch.Tensor, optimizer: 'THORN'):
-            optimizer._release_hook_step(cast(Parameter, param))
-            param.grad = None
+            if optimizer._release_hook_step(cast(Parameter, param)):
+                param.grad = None
 
         hooks = []
         for p in model.parameters():
