@@ -819,8 +819,9 @@ def test_gradient_release(rate):
     _log('[gpu]   ok')
 
 
-@pytest.mark.parametrize('window,rate', [(0, 1), (3 << 20, 1), (None, 1), (None, 2)])
-def test_gradient_release_overlapped_equals_in_order(window, rate):
+@pytest.mark.parametrize('window,rate,limit', [(0, 1, None), (3 << 20, 1, None), (None, 1, None), (None, 2, None),
+                                               (None, 1, 400_000)])
+def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
     """Gradient release steps large orthogonalized parameters in windows of RELEASE_WINDOW_BYTES
     of gradients, one plan each, on the optimizer's streams, joined when backward ends
     (THORN._release_step). Six 512-wide layers (below 2^20 elements, so every step takes the exact
@@ -828,8 +829,9 @@ def test_gradient_release_overlapped_equals_in_order(window, rate):
     step in order on the caller's stream, bit for bit: windows of one parameter (0), of two in
     backward order (3 MiB: two windows stepped from hooks, the last one when backward ends), and
     the default (all six, stepped when backward ends); with update_rate 2 a window's matrices step
-    every other backward."""
-    _log(f'[gpu] gradient release, window {window}, update_rate {rate}')
+    every other backward; with polar_decomp_batch_size 400000 the window of six is six batches,
+    which run in turn on the stream's shared workspace (no workspace per window)."""
+    _log(f'[gpu] gradient release, window {window}, update_rate {rate}, batch limit {limit}')
     thorn_amd = _thorn()
     from thorn_amd import optim as OPT
     dims = [512, 640, 512, 768, 512, 1024, 512]
@@ -849,6 +851,8 @@ def test_gradient_release_overlapped_equals_in_order(window, rate):
         try:
             opt = thorn_amd.THORN([{'params': list(model.parameters()), 'orthogonalize': True, 'lr': 1e-2,
                                     'weight_decay': 0.1}])
+            if limit is not None:
+                opt.polar_decomp_batch_size = limit
             opt.setup_gradient_release(model, update_rate=rate)
             for x in xs:
                 h = x.to(DEV)
@@ -865,6 +869,9 @@ def test_gradient_release_overlapped_equals_in_order(window, rate):
     ma, oa = run(True)
     sizes = sorted(len(k[3]) for k in oa._runners if k[0] == 'release')
     assert sizes == {0: [1] * 6, 3 << 20: [2, 2, 2], None: [6]}[window], sizes
+    for k, r in oa._runners.items():
+        if k[0] == 'release':
+            assert len(r.runners) == (6 if limit else 1) and all(x.shared is not None for x in r.runners)
     mb, ob = run(False)
     for i, (pa, pb) in enumerate(zip(ma.parameters(), mb.parameters())):
         assert torch.equal(pa.detach(), pb.detach()), i

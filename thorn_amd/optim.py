@@ -609,8 +609,8 @@ class _OrthoBatches:
 
     def __init__(self, params: list, group: _Group, device: torch.device, limit: int, adam: bool = False,
                  shared: Optional[_SharedWorkspace] = None, chain: bool = True):
-        """shared: the per-stream workspace of gradient release's runners, used when the parameters
-        are one plan. chain=False: never chains (gradient release runs on the chains' streams)."""
+        """shared: the per-stream workspace of single-parameter and gradient-release runners, used
+        by every batch. chain=False: never chains (gradient release runs on the chains' streams)."""
         batches = _batches(params, limit)
         self.runners = []
         self.chained = False
@@ -626,11 +626,11 @@ class _OrthoBatches:
                 ev.record(torch.cuda.current_stream(device))
             self.fork = torch.cuda.Event()
             self.joins = [torch.cuda.Event() for _ in chains]
+        elif shared is not None:   # batches, if several, run in turn on the stream's shared buffer
+            workspace = shared
         elif len(batches) > 1:
             sizes = [_lib.OrthoPlan(*_plan_shapes(b, group, adam)).workspace_bytes for b in batches]
             workspace = torch.zeros(max(1, max(sizes)), dtype=torch.uint8, device=device)
-        elif shared is not None:
-            workspace = shared
         for b in batches:
             self.runners.append(_OrthoRunner(b, group, device, adam, workspace))
 
