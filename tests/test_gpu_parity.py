@@ -819,9 +819,11 @@ def test_gradient_release(rate):
     _log('[gpu]   ok')
 
 
-@pytest.mark.parametrize('window,rate,limit', [(0, 1, None), (3 << 20, 1, None), (None, 1, None), (None, 2, None),
-                                               (None, 1, 400_000)])
-def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
+@pytest.mark.parametrize('window,rate,limit,extra', [
+    (0, 1, None, {}), (3 << 20, 1, None, {}), (None, 1, None, {}), (None, 2, None, {}), (None, 1, 400_000, {}),
+    (3 << 20, 1, None, {'momentum_align': True}), (3 << 20, 1, None, {'decouple_md': True})],
+    ids=['alone', 'pairs', 'all', 'all-rate2', 'all-batched', 'pairs-magma', 'pairs-md'])
+def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra):
     """Gradient release steps large orthogonalized parameters in windows of RELEASE_WINDOW_BYTES
     of gradients, one plan each, on the optimizer's streams, joined when backward ends
     (THORN._release_step). Six 512-wide layers (below 2^20 elements, so every step takes the exact
@@ -830,8 +832,10 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
     backward order (3 MiB: two windows stepped from hooks, the last one when backward ends), and
     the default (all six, stepped when backward ends); with update_rate 2 a window's matrices step
     every other backward; with polar_decomp_batch_size 400000 the window of six is six batches,
-    which run in turn on the stream's shared workspace (no workspace per window)."""
-    _log(f'[gpu] gradient release, window {window}, update_rate {rate}, batch limit {limit}')
+    which run in turn on the stream's shared workspace (no workspace per window); Magma masks (one
+    draw per parameter from its own PRNG state) and decouple_md gains do not depend on the windows
+    either."""
+    _log(f'[gpu] gradient release, window {window}, update_rate {rate}, batch limit {limit}, {extra}')
     thorn_amd = _thorn()
     from thorn_amd import optim as OPT
     dims = [512, 640, 512, 768, 512, 1024, 512]
@@ -840,6 +844,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
     xs = [torch.randn(64, 512, generator=gen) for _ in range(3)]
 
     def run(overlap: bool):
+        torch.manual_seed(123)   # Magma's PRNG states are seeded from the device generator
         model = torch.nn.Sequential(*[torch.nn.Linear(dims[i], dims[i + 1], bias=False) for i in range(6)]).to(DEV)
         with torch.no_grad():
             for lin, w in zip(model, init):
@@ -850,7 +855,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
             OPT.RELEASE_WINDOW_BYTES = window
         try:
             opt = thorn_amd.THORN([{'params': list(model.parameters()), 'orthogonalize': True, 'lr': 1e-2,
-                                    'weight_decay': 0.1}])
+                                    'weight_decay': 0.1, **extra}])
             if limit is not None:
                 opt.polar_decomp_batch_size = limit
             opt.setup_gradient_release(model, update_rate=rate)
@@ -877,6 +882,8 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit):
         assert torch.equal(pa.detach(), pb.detach()), i
         assert torch.equal(oa.state[pa]['moment'], ob.state[pb]['moment']), i
         assert oa.state[pa]['step'] == ob.state[pb]['step'], i
+        for k, v in oa.state[pa].items():
+            assert (torch.equal(v, ob.state[pb][k]) if torch.is_tensor(v) else v == ob.state[pb][k]), (i, k)
     _log('[gpu]   overlapped gradient release equals the in-order steps bit for bit')
 
 
