@@ -821,8 +821,9 @@ def test_gradient_release(rate):
 
 @pytest.mark.parametrize('window,rate,limit,extra', [
     (0, 1, None, {}), (3 << 20, 1, None, {}), (None, 1, None, {}), (None, 2, None, {}), (None, 1, 400_000, {}),
-    (3 << 20, 1, None, {'momentum_align': True}), (3 << 20, 1, None, {'decouple_md': True})],
-    ids=['alone', 'pairs', 'all', 'all-rate2', 'all-batched', 'pairs-magma', 'pairs-md'])
+    (3 << 20, 1, None, {'momentum_align': True}), (3 << 20, 1, None, {'decouple_md': True}),
+    (None, 1, None, {'raise': True})],
+    ids=['alone', 'pairs', 'all', 'all-rate2', 'all-batched', 'pairs-magma', 'pairs-md', 'all-raising'])
 def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra):
     """Gradient release steps large orthogonalized parameters in windows of RELEASE_WINDOW_BYTES
     of gradients, one plan each, on the optimizer's streams, joined when backward ends
@@ -834,7 +835,9 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
     every other backward; with polar_decomp_batch_size 400000 the window of six is six batches,
     which run in turn on the stream's shared workspace (no workspace per window); Magma masks (one
     draw per parameter from its own PRNG state) and decouple_md gains do not depend on the windows
-    either."""
+    either. 'raise': the second backward pass raises after the last three layers' hooks ran; the
+    next pass's first hook steps what the failed one left, then its own, as the in-order steps
+    did during the failed pass."""
     _log(f'[gpu] gradient release, window {window}, update_rate {rate}, batch limit {limit}, {extra}')
     thorn_amd = _thorn()
     from thorn_amd import optim as OPT
@@ -842,12 +845,36 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
     gen = torch.Generator().manual_seed(77)
     init = [torch.randn(dims[i + 1], dims[i], generator=gen) * 0.03 for i in range(6)]
     xs = [torch.randn(64, 512, generator=gen) for _ in range(3)]
+    extra = dict(extra)
+    raising = extra.pop('raise', False)
+
+    class Boom(torch.autograd.Function):   # identity whose backward raises on the second pass
+        armed = False
+
+        @staticmethod
+        def forward(ctx, x):
+            return x.view_as(x)
+
+        @staticmethod
+        def backward(ctx, g):
+            if Boom.armed:
+                raise RuntimeError('planted failure in backward')
+            return g
+
+    class BoomModule(torch.nn.Module):
+        def forward(self, x):
+            return Boom.apply(x)
 
     def run(overlap: bool):
         torch.manual_seed(123)   # Magma's PRNG states are seeded from the device generator
-        model = torch.nn.Sequential(*[torch.nn.Linear(dims[i], dims[i + 1], bias=False) for i in range(6)]).to(DEV)
+        mods = []
+        for i in range(6):
+            mods += [torch.nn.Linear(dims[i], dims[i + 1], bias=False), torch.nn.Tanh()]
+            if raising and i == 2:
+                mods.append(BoomModule())
+        model = torch.nn.Sequential(*mods).to(DEV)
         with torch.no_grad():
-            for lin, w in zip(model, init):
+            for lin, w in zip([m for m in model if isinstance(m, torch.nn.Linear)], init):
                 lin.weight.copy_(w.to(DEV))
         keep = OPT.RELEASE_OVERLAP, OPT.RELEASE_WINDOW_BYTES
         OPT.RELEASE_OVERLAP = overlap
@@ -859,11 +886,15 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
             if limit is not None:
                 opt.polar_decomp_batch_size = limit
             opt.setup_gradient_release(model, update_rate=rate)
-            for x in xs:
-                h = x.to(DEV)
-                for lin in model:
-                    h = torch.tanh(lin(h))
-                h.square().mean().backward()
+            for it, x in enumerate(xs):
+                h = model(x.to(DEV))   # a backward pass that raised is recovered from here
+                Boom.armed = raising and it == 1
+                try:
+                    h.square().mean().backward()
+                except RuntimeError as e:
+                    assert Boom.armed and 'planted failure' in str(e)
+                finally:
+                    Boom.armed = False
             torch.cuda.synchronize()
             assert opt._release_queued is False and not opt._release_pending and not opt._release_windows
             assert all(p.grad is None for p in model.parameters())
@@ -873,7 +904,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
 
     ma, oa = run(True)
     sizes = sorted(len(k[3]) for k in oa._runners if k[0] == 'release')
-    assert sizes == {0: [1] * 6, 3 << 20: [2, 2, 2], None: [6]}[window], sizes
+    assert sizes == ([3, 6] if raising else {0: [1] * 6, 3 << 20: [2, 2, 2], None: [6]}[window]), sizes
     for k, r in oa._runners.items():
         if k[0] == 'release':
             assert len(r.runners) == (6 if limit else 1) and all(x.shared is not None for x in r.runners)

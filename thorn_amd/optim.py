@@ -772,8 +772,10 @@ class THORN(Optimizer):
         self._release_events: dict = {}    # device -> the fork event and one join event per stream
         self._release_next = 0
         self._release_queued = False   # a join is queued for the end of the current backward pass
-        # (group index, device) -> [stream, parameters, gradient bytes]: a window not stepped yet
+        # (group index, device) -> [stream, [(parameter, gradient)], gradient bytes]: a window not
+        # stepped yet
         self._release_windows: dict = {}
+        self._release_task = -1   # the autograd graph task that queued the pending join
         if isinstance(params, nn.Module) and conf.get('gradient_release', False):
             self.setup_gradient_release(params)
 
@@ -1032,6 +1034,7 @@ class THORN(Optimizer):
         if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
             raise RuntimeError('THORN.step cannot be captured in a CUDA/HIP graph: every step fills its launch '
                                'tables on the host and uploads them from pinned memory')
+        self._release_recover()
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -1045,47 +1048,48 @@ class THORN(Optimizer):
             self._step_params([param], _Group.from_kwargs(**group), gi)
         return loss
 
-    def _release_step(self, p: torch.Tensor, join_later: bool) -> bool:
-        """step(param=p) as gradient release runs it. Returns whether p's gradient may be dropped
-        now; False: its step is queued in a window, whose step drops the gradient itself.
+    def _release_step(self, p: torch.Tensor, join_later: bool) -> None:
+        """step(param=p) as gradient release runs it, with p.grad as it is now; the caller may drop
+        p.grad afterwards (a window keeps the tensor).
 
         The Newton-Schulz launches of one matrix fill only a few of the device's CUs, and the
         parameters' steps are independent, so a large orthogonalized parameter joins its group's
-        window: once the window holds RELEASE_WINDOW_BYTES of gradients it steps as one plan on the
-        next of RELEASE_STREAMS streams (_release_flush), and the caller's stream waits for it in
-        _release_join, which also steps what the windows still hold. join_later=False steps and
-        joins at once. Other parameters step on the caller's stream."""
+        window with its gradient: once the window holds RELEASE_WINDOW_BYTES of gradients it steps
+        as one plan on the next of RELEASE_STREAMS streams (_release_flush), and the caller's
+        stream waits for it in _release_join, which also steps what the windows still hold.
+        join_later=False steps and joins at once. Other parameters step on the caller's stream."""
         group = self._param_to_group[id(p)]
         if (not RELEASE_OVERLAP or not p.is_cuda or not group['orthogonalize'] or p.grad is None
                 or p.grad.is_sparse or _large_matrices([p]) == 0):
             self.step(param=p)
-            return True
+            return
         gi = next(i for i, g in enumerate(self.param_groups) if g is group)
         key = (gi, p.device)
         cur = torch.cuda.current_stream(p.device)
         w = self._release_windows.get(key)
-        if w is not None and (w[0] != cur or any(q is p for q in w[1])):
+        if w is not None and (w[0] != cur or any(q is p for q, _ in w[1])):
             self._release_flush(key)   # a window holds gradients of one stream, each parameter once
             w = None
         if w is None:
             w = self._release_windows[key] = [cur, [], 0]
-        w[1].append(p)
-        w[2] += p.grad.numel() * p.grad.element_size()
+        g = p.grad
+        w[1].append((p, g))
+        w[2] += g.numel() * g.element_size()
         if not join_later or _window_full(w[2]):
             self._release_flush(key)
         if not join_later:
             self._release_join()
-        return False
 
     def _release_flush(self, key) -> None:
-        """Step the parameters of window `key` as one plan on the next release stream, after the
-        work their gradients' stream holds now, and drop their gradients as the hooks do. Config
-        2's hooks on one MI355X: 7.67 ms per step with 256 MiB windows, 40.4 with one parameter
-        per window, 82.9 in order on the caller's stream, 6.8 for the grouped step."""
+        """Step the parameters of window `key` with the gradients it holds, as one plan on the next
+        release stream, after the work their gradients' stream holds now; each parameter's .grad is
+        left as it was before (None after its hook). Config 2's hooks on one MI355X: 7.67 ms per
+        step with 256 MiB windows, 40.4 with one parameter per window, 82.9 in order on the
+        caller's stream, 6.8 for the grouped step."""
         w = self._release_windows.pop(key, None)
         if w is None:
             return
-        src, ps, _ = w
+        src, entries, _ = w
         gi, dev = key
         k = self._release_next % RELEASE_STREAMS
         self._release_next += 1
@@ -1095,12 +1099,17 @@ class THORN(Optimizer):
             evs = self._release_events[dev] = [torch.cuda.Event() for _ in range(RELEASE_STREAMS + 1)]
         evs[0].record(src)   # a wait takes the event as it is when enqueued, so one event serves
         st.wait_event(evs[0])
-        grads = [p.grad for p in ps]
-        with torch.no_grad(), torch.cuda.stream(st):
-            self._step_params(ps, _Group.from_kwargs(**self.param_groups[gi]), gi, release=True)
-        for p, g in zip(ps, grads):
-            g.record_stream(st)   # dropped here, still read by the stream's step
-            p.grad = None
+        ps = [p for p, _ in entries]
+        now = [p.grad for p in ps]
+        try:
+            for p, g in entries:
+                p.grad = g
+            with torch.no_grad(), torch.cuda.stream(st):
+                self._step_params(ps, _Group.from_kwargs(**self.param_groups[gi]), gi, release=True)
+        finally:
+            for (p, g), held in zip(entries, now):
+                g.record_stream(st)   # released here, still read by the stream's step
+                p.grad = held
         self._release_pending.setdefault(dev, set()).add(k)
 
     def _release_join(self) -> None:
@@ -1119,26 +1128,41 @@ class THORN(Optimizer):
         self._release_queued = False
         self._release_next = 0
 
-    def _release_hook_step(self, p: torch.Tensor) -> bool:
+    def _release_recover(self) -> None:
+        """Steps and joins what a backward pass that raised left behind: its end-of-backward
+        callback never ran, so its windows were not stepped and the caller's stream does not wait
+        for its release streams. Called before the model's next forward, the next hook and step(),
+        so the parameters are those the reference's hooks left before anything reads them.
+        Nothing to do (one comparison) otherwise."""
+        if self._release_queued and torch._C._current_graph_task_id() != self._release_task:
+            self._release_join()
+
+    def _release_hook_step(self, p: torch.Tensor) -> None:
         """From a post-accumulate-grad hook: the released steps of one backward pass are joined
         when it ends (a callback of the autograd engine, run on the caller's streams once they
-        have waited for the gradients), before anything after backward runs. Returns whether the
-        hook drops p's gradient (see _release_step)."""
+        have waited for the gradients), before anything after backward runs."""
+        self._release_recover()
+        task = torch._C._current_graph_task_id()
         if not self._release_queued:
             try:
                 torch.autograd.Variable._execution_engine.queue_callback(self._release_join)
                 self._release_queued = True
+                self._release_task = task
             except RuntimeError:   # not inside a backward pass: join at once
                 pass
-        return self._release_step(p, join_later=self._release_queued)
+        self._release_step(p, join_later=self._release_queued)
 
     def setup_gradient_release(self, model: nn.Module, update_rate: int = 1, ignore_existing_hooks: bool = False):
         """thorn.py:1755-1776: step each parameter from its post-accumulate-grad hook (large
-        orthogonalized parameters on the optimizer's streams, joined when the backward pass ends:
-        _release_step)."""
+        orthogonalized parameters in windows on the optimizer's streams, joined when the backward
+        pass ends: _release_step); the model's forward first recovers from a backward pass that
+        raised (_release_recover)."""
         def _hook(param: torch.Tensor, optimizer: 'THORN'):
-            if optimizer._release_hook_step(cast(Parameter, param)):
-                param.grad = None
+            optimizer._release_hook_step(cast(Parameter, param))
+            param.grad = None
+
+        def _before_forward(module: nn.Module, args, optimizer: 'THORN'):
+            optimizer._release_recover()
 
         hooks = []
         for p in model.parameters():
@@ -1151,5 +1175,6 @@ class THORN(Optimizer):
                     raise ValueError('Model already has post_accumulate_grad_hooks. If this is expected, '
                                      'pass `ignore_existing_hooks=True`.')
                 hooks.append(p.register_post_accumulate_grad_hook(partial(_hook, optimizer=self)))
+        hooks.append(model.register_forward_pre_hook(partial(_before_forward, optimizer=self)))
         model._gradient_release_hooks = hooks
         self._update_rate = update_rate
