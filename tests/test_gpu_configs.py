@@ -255,3 +255,52 @@ def test_chains_equal_one_plan(n_chains, variant):
             if torch.is_tensor(v):
                 assert torch.equal(v, ob.state[q][k]), (i, k)
     _log(f'{n_chains} chains ({variant}): {len(pa)} parameters bitwise equal to one plan over {len(grads)} steps')
+
+
+@pytest.mark.parametrize('adam_first', [False, True], ids=['ortho-first', 'adam-first'])
+def test_adam_beside_chains_equals_in_order(adam_first):
+    """step() runs the non-orthogonalized groups on a stream of their own beside an orthogonalized
+    group that steps as two chains (THORN._adam_side_stream). Their tensors (an embedding-sized
+    one with Adam-atan2, a vector, a bf16 tensor stepped through its fp32 working copy, a RAdam
+    group with eps > 0) are disjoint from the matrices, so parameters and state must match the
+    same steps with every group in order on the caller's stream, bit for bit, whichever group
+    comes first."""
+    import thorn_amd
+    from thorn_amd import optim as OPT
+    gen = torch.Generator().manual_seed(2024)
+    shapes = [(384, 640), (640, 384), (512, 512), (1024, 384)] * 5 + [(3, 384, 512)]
+    others = [(2000, 64), (640,), (128, 96)]
+    radam = [(300,)]
+    init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes + others + radam]
+    grads = [[torch.randn(t.shape, generator=gen) * 1e-3 for t in init] for _ in range(3)]
+
+    def run(overlap: bool):
+        params = [torch.nn.Parameter(t.to(DEV)) for t in init]
+        params[len(shapes) + 2] = torch.nn.Parameter(init[len(shapes) + 2].to(DEV, torch.bfloat16))
+        ortho = {'params': params[:len(shapes)], 'orthogonalize': True, 'lr': 1e-3, 'weight_decay': 0.1}
+        adam = {'params': params[len(shapes):len(shapes) + len(others)], 'orthogonalize': False, 'lr': 1e-3,
+                'weight_decay': 0.1}
+        rad = {'params': params[len(shapes) + len(others):], 'orthogonalize': False, 'lr': 1e-3, 'eps': 1e-8,
+               'rectify': True, 'weight_decay': 0.0}
+        keep = OPT.ADAM_OVERLAP
+        OPT.ADAM_OVERLAP = overlap
+        try:
+            opt = thorn_amd.THORN([adam, rad, ortho] if adam_first else [ortho, adam, rad])
+            for gs in grads:
+                for p, g in zip(params, gs):
+                    p.grad = g.to(DEV, p.dtype)
+                opt.step()
+            torch.cuda.synchronize()
+            assert bool(opt._adam_streams) == overlap
+            assert all(p.grad is None for p in params)
+            return params, opt
+        finally:
+            OPT.ADAM_OVERLAP = keep
+
+    pa, oa = run(True)
+    pb, ob = run(False)
+    for i, (p, q) in enumerate(zip(pa, pb)):
+        assert torch.equal(p.detach(), q.detach()), i
+        for k, v in oa.state[p].items():
+            assert (torch.equal(v, ob.state[q][k]) if torch.is_tensor(v) else v == ob.state[q][k]), (i, k)
+    _log(f'[gpu]   Adam groups beside two chains ({"adam" if adam_first else "ortho"} first): bitwise equal')

@@ -582,6 +582,10 @@ RELEASE_OVERLAP = True   # False: every released step on the caller's stream, in
 # launches fill only 10-48 of the device's 256 CUs. This bounds the gradient memory held back
 # beyond the reference's (which drops each gradient in its hook); 0 steps each parameter alone.
 RELEASE_WINDOW_BYTES = 256 << 20
+# step() runs the non-orthogonalized groups on a stream of their own beside an orthogonalized group
+# that steps as chains (THORN._adam_side_stream): their memory-bound launches then overlap the
+# chains' GEMMs (config 2 on one MI355X: 6.68-6.69 against 6.75-6.77 ms per step).
+ADAM_OVERLAP = True
 
 
 def _window_full(grad_bytes: int) -> bool:
@@ -767,6 +771,9 @@ class THORN(Optimizer):
         self._runners: dict = {}
         self._magma_scratch: dict = {}
         self._side_streams: dict = {}
+        self._adam_streams: dict = {}   # device -> the non-orthogonalized groups' stream in step()
+        self._adam_events: dict = {}    # device -> (fork, join) events of that stream
+        self._chains_two: dict = {}     # (live parameter ids, batch limit) -> steps as 2 chains
         self._shared_ws: dict = {}   # (group index, device) -> _SharedWorkspace
         self._release_pending: dict = {}   # device -> streams with released steps not joined yet
         self._release_events: dict = {}    # device -> the fork event and one join event per stream
@@ -910,6 +917,45 @@ class THORN(Optimizer):
             s.append(torch.cuda.Stream(dev))
         return tuple(s[:n])
 
+    def _adam_side_stream(self) -> Optional[torch.cuda.Stream]:
+        """The stream step() runs the non-orthogonalized groups on, beside the caller's stream with
+        the orthogonalized ones, or None: every group in order on the caller's stream. A side stream
+        only pays beside an orthogonalized group that steps as chains (a Newton-Schulz block fills a
+        CU, so memory-bound blocks only displace the GEMMs of one plan, and on small groups the
+        events cost more than the overlap gives), and only with at most two chains, so that the
+        caller's stream, the chains and this one use the 4 hardware queues of a process. All
+        gradients on one device, those of the non-orthogonalized groups dense."""
+        if not ADAM_OVERLAP:
+            return None
+        devs, chained, other = set(), False, False
+        limit = int(self.polar_decomp_batch_size)
+        for g in self.param_groups:
+            live = [p for p in g['params'] if p.grad is not None]
+            devs.update(p.device for p in live)
+            if g['orthogonalize']:
+                key = (tuple(id(p) for p in live), limit)
+                c = self._chains_two.get(key)
+                if c is None:   # the chain test walks every matrix: once per set of live parameters
+                    if len(self._chains_two) > 64:
+                        self._chains_two.clear()
+                    c = self._chains_two[key] = (_large_matrices(live) >= CHAIN_MIN_MATRICES
+                                                 and _chain_count(live) <= 2 and len(_batches(live, limit)) == 1)
+                chained = chained or c
+            elif live:
+                if any(p.grad.is_sparse for p in live):
+                    return None
+                other = True
+        if not (chained and other and len(devs) == 1):
+            return None
+        dev = devs.pop()
+        if dev.type != 'cuda':
+            return None
+        st = self._adam_streams.get(dev)
+        if st is None:
+            st = self._adam_streams[dev] = torch.cuda.Stream(dev)
+            self._adam_events[dev] = (torch.cuda.Event(), torch.cuda.Event())
+        return st
+
     def _shared_workspace(self, gi: int, dev: torch.device) -> _SharedWorkspace:
         w = self._shared_ws.get((gi, dev))
         if w is None:
@@ -1040,8 +1086,28 @@ class THORN(Optimizer):
             with torch.enable_grad():
                 loss = closure()
         if param is None:
-            for gi, group in enumerate(self.param_groups):
-                self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+            side = self._adam_side_stream()
+            if side is None:
+                for gi, group in enumerate(self.param_groups):
+                    self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+            else:
+                main = torch.cuda.current_stream(side.device)
+                fork, join = self._adam_events[side.device]
+                fork.record(main)   # gradients and state as the caller left them
+                side.wait_event(fork)
+                try:
+                    for gi, group in enumerate(self.param_groups):   # in order: a group that raises
+                        if group['orthogonalize']:                    # stops the later ones
+                            self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+                            continue
+                        grads = [p.grad for p in group['params'] if p.grad is not None]
+                        with torch.cuda.stream(side):
+                            self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+                        for g in grads:
+                            g.record_stream(side)   # the step may drop them; the stream still reads them
+                finally:
+                    join.record(side)
+                    main.wait_event(join)
         else:
             group = self._param_to_group[id(param)]
             gi = next(i for i, g in enumerate(self.param_groups) if g is group)
