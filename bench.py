@@ -579,6 +579,9 @@ def main() -> int:
     ap.add_argument('--single-chain', action='store_true',
                     help='step the orthogonalized group as one plan on one stream (the library default splits '
                          'a large group into two chains on two streams)')
+    ap.add_argument('--no-one-chain', action='store_true',
+                    help='skip the one-plan pass behind roofline.one_chain (kernel traces: that pass runs on '
+                         'the caller\'s stream after the chained steps)')
     ap.add_argument('--per-param', action='store_true',
                     help='step each parameter on its own, as gradient release does from its hook (a '
                          'variant of the workload, not the headline line: step time only, no roofline)')
@@ -713,7 +716,7 @@ def main() -> int:
     # other chains' memory-bound kernels. The same step as one plan on one stream (a second
     # optimizer over the same parameters, after every figure above is taken) gives its rate alone.
     one_chain = None
-    if chains > 1 and not args.momentum_align:
+    if chains > 1 and not args.momentum_align and not args.no_one_chain:
         keep = thorn_amd.optim.CHAIN_MIN_MATRICES
         thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
         try:
