@@ -822,8 +822,9 @@ def test_gradient_release(rate):
 @pytest.mark.parametrize('window,rate,limit,extra', [
     (0, 1, None, {}), (3 << 20, 1, None, {}), (None, 1, None, {}), (None, 2, None, {}), (None, 1, 400_000, {}),
     (3 << 20, 1, None, {'momentum_align': True}), (3 << 20, 1, None, {'decouple_md': True}),
-    (None, 1, None, {'raise': True})],
-    ids=['alone', 'pairs', 'all', 'all-rate2', 'all-batched', 'pairs-magma', 'pairs-md', 'all-raising'])
+    (None, 1, None, {'raise': True}), (3 << 20, 1, None, {'bf16': True})],
+    ids=['alone', 'pairs', 'all', 'all-rate2', 'all-batched', 'pairs-magma', 'pairs-md', 'all-raising',
+         'pairs-bf16'])
 def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra):
     """Gradient release steps large orthogonalized parameters in windows of RELEASE_WINDOW_BYTES
     of gradients, one plan each, on the optimizer's streams, joined when backward ends
@@ -847,6 +848,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
     xs = [torch.randn(64, 512, generator=gen) for _ in range(3)]
     extra = dict(extra)
     raising = extra.pop('raise', False)
+    dtype = torch.bfloat16 if extra.pop('bf16', False) else torch.float32   # the reference's README example
 
     class Boom(torch.autograd.Function):   # identity whose backward raises on the second pass
         armed = False
@@ -872,7 +874,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
             mods += [torch.nn.Linear(dims[i], dims[i + 1], bias=False), torch.nn.Tanh()]
             if raising and i == 2:
                 mods.append(BoomModule())
-        model = torch.nn.Sequential(*mods).to(DEV)
+        model = torch.nn.Sequential(*mods).to(DEV, dtype)
         with torch.no_grad():
             for lin, w in zip([m for m in model if isinstance(m, torch.nn.Linear)], init):
                 lin.weight.copy_(w.to(DEV))
@@ -887,7 +889,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
                 opt.polar_decomp_batch_size = limit
             opt.setup_gradient_release(model, update_rate=rate)
             for it, x in enumerate(xs):
-                h = model(x.to(DEV))   # a backward pass that raised is recovered from here
+                h = model(x.to(DEV, dtype))   # a backward pass that raised is recovered from here
                 Boom.armed = raising and it == 1
                 try:
                     h.square().mean().backward()
@@ -904,7 +906,8 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
 
     ma, oa = run(True)
     sizes = sorted(len(k[3]) for k in oa._runners if k[0] == 'release')
-    assert sizes == ([3, 6] if raising else {0: [1] * 6, 3 << 20: [2, 2, 2], None: [6]}[window]), sizes
+    want = {0: [1] * 6, 3 << 20: [2, 2, 2] if dtype == torch.float32 else [2, 4], None: [6]}[window]
+    assert sizes == ([3, 6] if raising else want), sizes
     for k, r in oa._runners.items():
         if k[0] == 'release':
             assert len(r.runners) == (6 if limit else 1) and all(x.shared is not None for x in r.runners)
