@@ -584,7 +584,8 @@ RELEASE_OVERLAP = True   # False: every released step on the caller's stream, in
 RELEASE_WINDOW_BYTES = 256 << 20
 # step() runs the non-orthogonalized groups on a stream of their own beside an orthogonalized group
 # that steps as chains (THORN._adam_side_stream): their memory-bound launches then overlap the
-# chains' GEMMs (config 2 on one MI355X: 6.68-6.69 against 6.75-6.77 ms per step).
+# chains' GEMMs (config 2 on two MI355X boxes: 6.68-6.69 against 6.75-6.77 and 6.70-6.74 against
+# 6.74-6.76 ms per step).
 ADAM_OVERLAP = True
 
 
