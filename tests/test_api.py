@@ -203,3 +203,36 @@ def test_gradient_release_on_cpu_steps_at_once():
     opt.step = lambda closure=None, *, param=None: called.append(param)
     opt._release_step(p, join_later=True)
     assert called == [p] and not opt._release_windows
+
+
+def test_adam_beside_chains_decision():
+    """step() runs the non-orthogonalized groups on a side stream only beside an orthogonalized group
+    that steps as at most two chains (config 2: yes; config 5's four chains: no), with dense
+    gradients, and when the batch limit keeps the matrices one plan."""
+    import bench
+    from thorn_amd import optim as OPT
+
+    def params(shapes):
+        ps = [nn.Parameter(torch.empty(sh, device='meta')) for sh in shapes]
+        for p in ps:
+            p.grad = torch.empty(p.shape, device='meta')
+        return ps
+
+    emb = nn.Parameter(torch.zeros(10, 4))   # a row-sparse embedding gradient
+    emb.grad = torch.sparse_coo_tensor(torch.tensor([[1, 3]]), torch.ones(2, 4), (10, 4))
+
+    m2, o2 = bench.config_shapes(2)
+    m5, _ = bench.config_shapes(5)
+    adam = [sh for shapes, _ in o2 for sh in shapes]
+    big = 2 * 1024 ** 3
+    assert OPT._adam_beside_chains([(True, params(m2)), (False, params(adam))], big, {})
+    assert OPT._adam_beside_chains([(False, params(adam)), (True, params(m2))], big, {})
+    assert not OPT._adam_beside_chains([(True, params(m5)), (False, params(adam))], big, {})      # 4 chains
+    assert not OPT._adam_beside_chains([(True, params(m2[:15])), (False, params(adam))], big, {})  # no chains
+    assert not OPT._adam_beside_chains([(True, params(m2)), (False, params(adam) + [emb])], big, {})
+    assert not OPT._adam_beside_chains([(True, params(m2)), (False, [])], big, {})
+    assert not OPT._adam_beside_chains([(True, params(m2)), (False, params(adam))], 1 << 24, {})  # batches
+    cache = {}
+    ps = params(m2)
+    OPT._adam_beside_chains([(True, ps), (False, params(adam))], big, cache)
+    assert list(cache.values()) == [True] and list(cache)[0][0] == tuple(id(p) for p in ps)

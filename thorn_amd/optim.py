@@ -595,6 +595,31 @@ def _window_full(grad_bytes: int) -> bool:
 SMALL_MAX_S, SMALL_MAX_ELEMS = 256, 1 << 20   # the library's small-matrix path (thorn_abi.hip)
 
 
+def _adam_beside_chains(live: list, limit: int, cache: dict) -> bool:
+    """Whether step() runs the non-orthogonalized groups beside the orthogonalized ones: live is
+    [(orthogonalize, parameters with a gradient)] per group. Some orthogonalized group must step as
+    two chains (one batch of at least CHAIN_MIN_MATRICES large matrices, at most two chains, so
+    that the caller's stream, the chains and the side stream fit the 4 hardware queues of a
+    process), some non-orthogonalized group must have gradients, all of them dense. cache: (live
+    parameter ids, limit) -> the chain test, which walks every matrix."""
+    chained = other = False
+    for ortho, ps in live:
+        if ortho:
+            key = (tuple(id(p) for p in ps), limit)
+            c = cache.get(key)
+            if c is None:
+                if len(cache) > 64:
+                    cache.clear()
+                c = cache[key] = (_large_matrices(ps) >= CHAIN_MIN_MATRICES and _chain_count(ps) <= 2
+                                  and len(_batches(ps, limit)) == 1)
+            chained = chained or c
+        elif ps:
+            if any(p.grad.is_sparse for p in ps):
+                return False
+            other = True
+    return chained and other
+
+
 class _OrthoBatches:
     """A group's orthogonalized parameters in batches of at most polar_decomp_batch_size elements
     (thorn.py:1237, 1440): one plan per batch, run in turn on one workspace sized for the largest,
@@ -928,25 +953,11 @@ class THORN(Optimizer):
         gradients on one device, those of the non-orthogonalized groups dense."""
         if not ADAM_OVERLAP:
             return None
-        devs, chained, other = set(), False, False
-        limit = int(self.polar_decomp_batch_size)
-        for g in self.param_groups:
-            live = [p for p in g['params'] if p.grad is not None]
-            devs.update(p.device for p in live)
-            if g['orthogonalize']:
-                key = (tuple(id(p) for p in live), limit)
-                c = self._chains_two.get(key)
-                if c is None:   # the chain test walks every matrix: once per set of live parameters
-                    if len(self._chains_two) > 64:
-                        self._chains_two.clear()
-                    c = self._chains_two[key] = (_large_matrices(live) >= CHAIN_MIN_MATRICES
-                                                 and _chain_count(live) <= 2 and len(_batches(live, limit)) == 1)
-                chained = chained or c
-            elif live:
-                if any(p.grad.is_sparse for p in live):
-                    return None
-                other = True
-        if not (chained and other and len(devs) == 1):
+        live = [(g['orthogonalize'], [p for p in g['params'] if p.grad is not None]) for g in self.param_groups]
+        if not _adam_beside_chains(live, int(self.polar_decomp_batch_size), self._chains_two):
+            return None
+        devs = {p.device for _, ps in live for p in ps}
+        if len(devs) != 1:
             return None
         dev = devs.pop()
         if dev.type != 'cuda':
