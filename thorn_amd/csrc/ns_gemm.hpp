@@ -7,13 +7,14 @@
 // read either K-major (ds_read_b128 fragments) or MN-major (two ds_read_tr16_b64 transposing
 // reads), so no matrix is ever transposed in memory.
 //
-// The loop is shaped by how one wave per SIMD spends its cycles (measured on an MI355X with
-// timing-only copies): the MFMAs alone take ~1070 cycles per K tile of 32 (1024 ideal), the LDS
-// fragment reads add no cycles, and each direct load costs issue and wait time. So every direct
-// load is one buffer instruction whose out-of-range lanes (rows or K past the operand) the
-// hardware turns into zeros, with one vector add to advance it; the K loop is unrolled over the
-// four stages so every LDS address is a per-lane base plus an immediate; and on full tiles the
-// direct loads are spaced one per two MFMAs.
+// A block is 512 threads, two waves per SIMD, and the two waves of a SIMD take turns: while the
+// waves of one group issue nothing but MFMAs on fragments already in their registers, the waves
+// of the other group read their next fragments from LDS, issue the direct loads of a later K
+// tile and wait for them; a block barrier hands the MFMA pipes over. A wave's memory waits
+// therefore never hold up the MFMA pipe of its SIMD. (With one wave per SIMD interleaving its
+// loads between its MFMAs, measured on an MI355X: ~1400-1460 cycles per K tile of 32 at
+// K = 1024 against 1200-1330 this way, and 1210 against 1050-1070 at K = 8192, 1024 being the
+// MFMA time; the chip runs this load power-limited at 1.4-1.6 GHz either way.)
 #pragma once
 
 #include <type_traits>
@@ -24,20 +25,20 @@ namespace thorn {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-// Block tile BM x BN (256 x 256), K step 32, 256 threads as 2 x 2 waves, each wave owning
-// (BM/2) x (BN/2) of the tile. S = 4 pipeline stages of LDS.
-template <int BM_, int BN_, int S_ = 4>
-struct GemmCfg {
-    static constexpr int BM = BM_, BN = BN_, BK = 32, S = S_;
-    static constexpr int WM = BM / 2, WN = BN / 2;
-    static constexpr int TM = WM / 32, TN = WN / 32;
+// Block tile 256 x 256, K step 32, 4 pipeline stages of LDS, 512 threads. SIMD s owns the
+// 128 x 128 quadrant (s >> 1, s & 1) of a tile; its wave of group 0 (wave s) the left 64 columns
+// of it, its wave of group 1 (wave s + 4) the right 64.
+struct NsCfg {
+    static constexpr int BM = 256, BN = 256, BK = 32, S = 4;
+    static constexpr int NT = 512, NW = NT / 64;
     static constexpr int A_BYTES = BM * BK * 2;          // one stage of A, no padding
     static constexpr int B_BYTES = BN * BK * 2;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-    static constexpr int LDS_BYTES = S * STAGE_BYTES;
-    static constexpr int A_LOADS = BM / 64;               // 1 KB direct loads per wave per stage
-    static constexpr int B_LOADS = BN / 64;
-    static constexpr int LOADS_PER_STAGE = A_LOADS + B_LOADS;
+    static constexpr int LDS_BYTES = S * STAGE_BYTES;    // 128 KB
+    static constexpr int A_LOADS = A_BYTES / 1024 / NW;  // 1 KB direct loads per wave per stage
+    static constexpr int B_LOADS = B_BYTES / 1024 / NW;
+    static constexpr int LOADS = A_LOADS + B_LOADS;      // 4
+    static_assert(A_LOADS == B_LOADS && LOADS == 4, "per-wave load slots");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
@@ -74,6 +75,15 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
 }
 
+// Makes v opaque to the compiler: it is kept in registers as computed, and every later use reads
+// those bits (the compiler may not recompute it another way).
+__device__ __forceinline__ void opaque(half4& v) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 b = __builtin_bit_cast(u32x2, v);
+    asm volatile("" : "+v"(b));
+    v = __builtin_bit_cast(half4, b);
+}
+
 // LDS layouts of one stage, 16-byte chunks, XOR-swizzled so that the fragment reads of a wave
 // hit distinct banks:
 //   K-major:  MN rows x 4 chunks (64 B); chunk c of row r sits at r*64 + (c ^ ((r >> 2) & 3))*16.
@@ -82,18 +92,19 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 //             The 32 lanes of a ds_read_tr16_b64 pair read 4 k-rows x 4 chunks: 16 distinct
 //             chunks mod 16, all 64 banks.
 // A direct load writes 64 consecutive chunk slots (1 KB) at the address in M0, so each lane loads
-// the global chunk whose swizzled position is its slot.
+// the global chunk whose swizzled position is its slot. Wave w owns slots [1024 (w P + q),
+// 1024 (w P + q + 1)) of an operand's stage, q < P = PER_WAVE.
 //
 // OperandDma holds the buffer resource of one operand and, per lane, the byte offset of each of
-// its MN/64 chunk loads per stage for the next K tile to load (`cur`, advanced by `step` after
-// each load). Loads of consecutive tiles are issued in order; begin_tile switches the offsets to
-// the K-major layout at tile k0 (a symmetric matrix stored as its upper block triangle is read
+// its chunk loads per stage for the next K tile to load (`cur`, advanced by `step` after each
+// load). Loads of consecutive tiles are issued in order; begin_tile switches the offsets to the
+// K-major layout at tile k0 (a symmetric matrix stored as its upper block triangle is read
 // MN-major, from the transposed mirror block, before its diagonal block) and to out of range at
 // tile kend, so the tiles that round K up to whole loop iterations, and the prefetches past the
 // end, load zeros.
 template <int MN>
 struct OperandDma {
-    static constexpr int PER_WAVE = MN / 64;
+    static constexpr int PER_WAVE = MN * NsCfg::BK * 2 / 1024 / NsCfg::NW;
     u32x4 rsrc;
     uint32_t cur[PER_WAVE];
     uint32_t kmaj[PER_WAVE];   // K-major offsets of tile 0
@@ -150,12 +161,14 @@ struct OperandDma {
     }
 
     // Direct load q of this wave for the current tile into LDS at m0 (wave-uniform byte address).
+    // The compiler writes M0 right before the asm, whose s_nop gives the one wait state that an
+    // M0 write needs before an LDS DMA reads it (a hazard the compiler does not see inside asm).
     // It is inline assembly so that the compiler does not track it as an LDS write: its
     // conservative aliasing would otherwise wait for every outstanding load before the next LDS
     // fragment read and serialize the pipeline. The main loop orders the loads explicitly
-    // (lds_wait_barrier); the "memory" clobber keeps LDS accesses from moving across them.
+    // (waits and barriers); the "memory" clobber keeps LDS accesses from moving across them.
     __device__ __forceinline__ void issue(int q, uint32_t m0) {
-        asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(cur[q]), "s"(rsrc), "{m0}"(m0) : "memory");
+        asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(cur[q]), "s"(rsrc), "{m0}"(m0) : "memory");
         cur[q] += step;
     }
 };
@@ -164,10 +177,10 @@ struct OperandDma {
 // m0.., columns n0.. of a matrix with leading dimension ld and `rows` valid rows (ptr null: no C
 // term, every load reads zeros). gemm_tile loads it into the epilogue's staging (EpiH) by direct
 // loads: rows 192-255 in the prologue, into the 32 KB past the pipeline stages, and rows 0-63,
-// 64-127 and 128-191 in the last three K iterations, into stages 0, 1 and 2 as the loop releases
-// them (in place of the loads of tiles past the end, so every iteration still issues one stage
-// of loads per wave). Quarter q of the tile is 32 loads of two 512-byte staging rows each; wave w
-// issues loads 8w .. 8w+7.
+// 64-127 and 128-191 in the last three memory phases, into stages 0, 1 and 2 as the loop
+// releases them (in place of the loads of tiles past the end, so every memory phase still issues
+// one stage's share of loads per wave). Quarter q of the tile is 32 loads of two 512-byte
+// staging rows each; wave w issues loads 4w .. 4w+3.
 struct TileC {
     const _Float16* ptr;
     int64_t ld;
@@ -175,24 +188,25 @@ struct TileC {
 };
 
 struct TileCDma {
+    static constexpr int PER_WAVE = 32 / NsCfg::NW;
     u32x4 rsrc;
-    uint32_t off[8];     // quarter 0 offsets of this lane's 8 loads; quarter q adds q * qstep
-    uint32_t qstep;      // bytes of 64 rows
+    uint32_t off[PER_WAVE];   // quarter 0 offsets of this lane's loads; quarter q adds q * qstep
+    uint32_t qstep;           // bytes of 64 rows
     __device__ __forceinline__ void init(const TileC& c, int m0, int n0, int wave, int lane) {
         rsrc = sgpr_rsrc(c.ptr, c.ptr ? static_cast<uint32_t>(int64_t(c.rows) * c.ld * 2) : 0u);
         qstep = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(128 * c.ld));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int row = 2 * (wave * 8 + j) + (lane >> 5);   // within quarter 0
-            const int ch = (lane & 31) ^ (row & 31);             // staging position lane & 31
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int row = 2 * (wave * PER_WAVE + j) + (lane >> 5);   // within quarter 0
+            const int ch = (lane & 31) ^ (row & 31);                    // staging position lane & 31
             const int col = n0 + 8 * ch;
             off[j] = col < c.ld ? static_cast<uint32_t>((int64_t(m0 + row) * c.ld + col) * 2) : kOutOfRange;
         }
     }
-    // load j (0..7) of quarter q into LDS at m0 (wave-uniform)
+    // load j of quarter q into LDS at m0 (wave-uniform)
     __device__ __forceinline__ void issue(int j, int q, uint32_t m0) {
         const uint32_t o = off[j] + q * qstep;
-        asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(o), "s"(rsrc), "{m0}"(m0) : "memory");
+        asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(o), "s"(rsrc), "{m0}"(m0) : "memory");
     }
 };
 
@@ -219,12 +233,13 @@ __device__ __forceinline__ half8 frag(const char* lds, int t0, int ks, int lane)
     return half8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 }
 
-// Per-lane LDS fragment bases of one operand of the main loop (operand tiles of MN = 256). The
-// four stages are two pairs 65536 bytes apart, so that every other part of an address fits the
-// 16-bit immediate offset of the read:
-//   K-major: b[pair][ks]; the wave's row offset is in the base, fragment i adds i * 2048 (32 rows
+// Per-lane LDS fragment bases of one operand of the main loop (operand tiles of MN = 256): the
+// 32-wide fragments I = 0 .. NI-1 at columns (or rows) w0 + 32 I. The four stages are two pairs
+// 65536 bytes apart, so that every other part of an address fits the 16-bit immediate offset of
+// the read:
+//   K-major: b[pair][ks]; the wave's row offset is in the base, fragment I adds I * 2048 (32 rows
 //            of 64 B) and the odd stage of a pair 32768.
-//   MN-major: b[pair][i] per fragment (the XOR swizzle of chunk c = 4j + cl by 4x is 4(j ^ x) + cl
+//   MN-major: b[pair][I] per fragment (the XOR swizzle of chunk c = 4j + cl by 4x is 4(j ^ x) + cl
 //            with j the fragment's 32-column block and x = k & 3 the lane's, so the fragment's part
 //            is lane-dependent); ks adds 16 k-rows (8192 B) and the second read 4 k-rows (2048 B).
 template <int NI>
@@ -263,6 +278,7 @@ __device__ __forceinline__ half8 frag_at(const FragBase<NI>& fb) {
         static_assert(imm < 65536, "immediate offset");
         return *reinterpret_cast<lds_h8*>(fb.b[ST >> 1][KS] + imm);
     } else {
+        static_assert(I < NI, "fragment base");
         constexpr int imm = SB + OPOFF + KS * 8192;
         static_assert(imm + 2048 < 65536, "immediate offset");
         const uint32_t a = fb.b[ST >> 1][I] + imm;
@@ -273,15 +289,6 @@ __device__ __forceinline__ half8 frag_at(const FragBase<NI>& fb) {
     }
 }
 
-// This wave's direct loads except the newest N are complete, then the block barrier: after it,
-// every wave's loads up to that point are visible in LDS. The "memory" clobber keeps the
-// compiler from moving LDS reads above it.
-template <int N>
-__device__ __forceinline__ void lds_wait_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
 // Block barrier for LDS traffic only: this wave's LDS accesses are complete, then s_barrier.
 // Unlike __syncthreads() it does not wait for outstanding global stores, so an epilogue's
 // stores keep draining while the next staging pass runs.
@@ -289,38 +296,67 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Work split of a tile between its four waves. A diagonal tile of a symmetric result is only
-// stored as its upper block triangle (the epilogue mirrors it), so of its 8 x 8 grid of 32 x 32
-// blocks only the 36 with j >= i are computed: waves 0 and 3 take the blocks of their diagonal
-// quadrants with j >= i (10 each), waves 1 and 2 split the upper-right quadrant (rows 0-63 and
-// 64-127, 8 blocks each), and nobody computes the lower-left quadrant. The slowest wave then
-// issues 10 MFMAs per k16 step instead of 16.
-enum TileRole : int { kRoleFull = 0, kRoleTri = 1, kRoleHalf = 2 };
+// A bare block barrier between the phases of the main loop. The scheduling barriers keep the
+// compiler from moving MFMAs (which are not memory operations) across it.
+__device__ __forceinline__ void phase_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
-template <int ROLE, int TM, int TN>
+// Work split of a tile between the 8 waves, as the 32 x 32 blocks each one computes. A wave's
+// blocks are (A fragment a_idx(x), B fragment b_idx(y)) for its block list (x, y), where A
+// fragment I covers tile rows abase + 32 I and B fragment J tile columns bbase + 32 J (abase and
+// bbase per wave, TileWork). A diagonal tile of a symmetric result is only stored as its upper
+// block triangle (the epilogue mirrors it), so of its 8 x 8 grid of blocks only the 36 with
+// J >= I are computed:
+//   full tile (kRoleFull): each wave its 128 x 64 (A 0-3, B 0-1);
+//   diagonal quadrants (SIMDs 0 and 3, base 0 or 128): kRoleDiagA takes block rows {0, 3} of the
+//     quadrant's upper triangle (5 blocks: (0,0) .. (0,3), (3,3)), kRoleDiagB rows {1, 2} (5:
+//     (1,1) .. (1,3), (2,2), (2,3));
+//   upper-right quadrant (SIMDs 1 and 2): kRoleHalf, 64 x 64 each (rows 0-63 or 64-127 of it,
+//     columns 0-63 or 64-127 by group);
+// nobody computes the lower-left quadrant. The waves of one group then issue at most 5 MFMAs
+// per k16 step against 8 on a full tile.
+enum TileRole : int { kRoleFull = 0, kRoleDiagA = 1, kRoleDiagB = 2, kRoleHalf = 3 };
+
+template <int ROLE>
 struct RoleMap {
-    static constexpr int N = ROLE == kRoleFull ? TM * TN : ROLE == kRoleTri ? TM * (TM + 1) / 2 : 2 * TN;
-    // (i, j) of this wave's q-th MFMA block, rows before columns
-    static constexpr int i(int q) {
-        if (ROLE == kRoleFull || ROLE == kRoleHalf) return q / TN;
-        int r = 0;
-        while (q >= TN - r) {
-            q -= TN - r;
-            ++r;
-        }
-        return r;
+    static constexpr int NA = ROLE == kRoleFull ? 4 : 2;                      // A fragments per k16 step
+    static constexpr int NB = ROLE == kRoleFull ? 2 : ROLE == kRoleDiagA ? 4 : ROLE == kRoleDiagB ? 3 : 2;
+    static constexpr int N = ROLE == kRoleFull ? 8 : ROLE == kRoleHalf ? 4 : 5;   // blocks
+    static constexpr int AF = ROLE == kRoleHalf ? 2 : 4;                      // FragBase sizes
+    static constexpr int BF = ROLE == kRoleFull || ROLE == kRoleHalf ? 2 : 4;
+    // fragment index of A slot x / B slot y
+    static constexpr int a_idx(int x) {
+        return ROLE == kRoleDiagA ? (x == 0 ? 0 : 3) : ROLE == kRoleDiagB ? 1 + x : x;
     }
-    static constexpr int j(int q) {
-        if (ROLE != kRoleTri) return q % TN;
-        int r = 0;
-        while (q >= TN - r) {
-            q -= TN - r;
-            ++r;
-        }
-        return r + q;
+    static constexpr int b_idx(int y) { return ROLE == kRoleDiagB ? 1 + y : y; }
+    // A slot and B slot of block q
+    static constexpr int bx(int q) {
+        return ROLE == kRoleFull ? q / 2 : ROLE == kRoleHalf ? q / 2 : ROLE == kRoleDiagA ? (q < 4 ? 0 : 1)
+                                                                                          : (q < 3 ? 0 : 1);
     }
-    static constexpr int NA = ROLE == kRoleHalf ? 2 : TM;   // A fragments per k16 step
-    static constexpr int NF = NA + TN;                       // fragments per k16 step
+    static constexpr int by(int q) {
+        return ROLE == kRoleFull ? q % 2 : ROLE == kRoleHalf ? q % 2 : ROLE == kRoleDiagA ? (q < 4 ? q : 3)
+                                                                                          : (q < 3 ? q : q - 2);
+    }
+    // block q lies on the tile's diagonal (diagonal roles only; their A and B bases are equal)
+    static constexpr bool on_diag(int q) {
+        return (ROLE == kRoleDiagA || ROLE == kRoleDiagB) && a_idx(bx(q)) == b_idx(by(q));
+    }
+};
+
+// The wave's role and fragment bases in a tile: waves s and s + 4 share SIMD s.
+struct TileWork {
+    int role, abase, bbase;
+    __device__ __forceinline__ TileWork(bool diag, int wave) {
+        const int simd = wave & 3, grp = wave >> 2;
+        const bool dq = simd == 0 || simd == 3;   // a diagonal quadrant of a diagonal tile
+        role = !diag ? kRoleFull : dq ? (grp == 0 ? kRoleDiagA : kRoleDiagB) : kRoleHalf;
+        abase = !diag ? (simd >> 1) * 128 : dq ? (simd == 0 ? 0 : 128) : (simd == 1 ? 0 : 64);
+        bbase = !diag ? (simd & 1) * 128 + grp * 64 : dq ? abase : 128 + grp * 64;
+    }
 };
 
 // f(std::integral_constant<int, Q>) for Q = B .. E-1, as straight-line code with Q a constant.
@@ -332,172 +368,189 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// Fragment Q of a k16 step of stage ST in the order the MFMAs use them: A0, B0 .. B(TN-1),
-// A1 .. A(NA-1), in the layouts AK / BK (true = K-major).
-template <class C, bool AK, bool BK, int ST, int KS, int Q>
-__device__ __forceinline__ void read_frag(const FragBase<C::TM>& fa_base, const FragBase<C::TN>& fb_base,
-                                          half8 (&ra)[C::TM], half8 (&rb)[C::TN]) {
-    if constexpr (Q == 0) ra[0] = frag_at<AK, ST, KS, 0, 0>(fa_base);
-    else if constexpr (Q <= C::TN) rb[Q - 1] = frag_at<BK, ST, KS, C::A_BYTES, Q - 1>(fb_base);
-    else ra[Q - C::TN] = frag_at<AK, ST, KS, 0, Q - C::TN>(fa_base);
+// The fragments of one K tile (both k16 steps) of a role.
+template <int ROLE>
+struct Frags {
+    using R = RoleMap<ROLE>;
+    half8 a[2][R::NA];
+    half8 b[2][R::NB];
+};
+
+// MFMA phase of a K tile: every block's two k16 steps, from registers only. The MFMA is issued as
+// B^T A^T, so each 32 x 32 accumulator comes out transposed: lane l holds row (l & 31) and the
+// four consecutive columns 8*(r/4) + 4*(l/32) + 0..3 in registers r..r+3.
+template <int ROLE>
+__device__ __forceinline__ void mfma_phase(const Frags<ROLE>& f, floatx16 (&acc)[RoleMap<ROLE>::N]) {
+    using R = RoleMap<ROLE>;
+    static_for<0, 2>([&](auto kc) {
+        constexpr int ks = decltype(kc)::value;
+        static_for<0, R::N>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[ks][R::by(q)], f.a[ks][R::bx(q)], acc[q], 0, 0, 0);
+        });
+    });
 }
 
-// K tile kt, held in stage ST = kt % 4, as one basic block of two k16 sub-steps of RoleMap::N
-// MFMAs, the order of every instruction fixed explicitly. Sub-step 1 multiplies the ks 0
-// fragments (fa[0], fb[0]) and reads the ks 1 fragments of stage ST after MFMA q. Then every
-// wave waits for its own loads of tile kt+1 and meets the others at the block barrier: after it,
-// tile kt+1 is visible and nobody reads stage (kt-1) % 4 any more, which then receives tile kt+3.
-// Sub-step 2 multiplies the ks 1 fragments and, after MFMA q, reads fragment q of the next
-// tile's ks 0 (stage ST+1) and issues the direct loads of tile kt+3: one per two MFMAs when the
-// wave has twice as many MFMAs as loads (full tiles), else one per MFMA. (Loading tile kt+4 into
-// stage ST instead, after a wait for this wave's LDS reads, gives the loads one more iteration
-// but measured no faster.)
-// CQ >= 0 (the last three iterations of a tile's K loop): the direct loads fetch quarter CQ of the
-// epilogue's C tile into stage ST+3 instead of a tile past the end of K.
+// Memory phase of K tile kt, held in stage ST = kt % 4: this wave's fragments of tile kt, then its
+// share of the direct loads of tile kt+3 into stage (ST+3) % 4 (which both groups finished reading
+// before the barrier that started this phase), then the wait for its own loads of tile kt+1 (all
+// but the newest two tiles' loads) and for the fragments. CQ >= 0 (the last three memory phases of
+// a tile): the loads fetch quarter CQ of the epilogue's C tile into stage CQ instead of a tile
+// past the end of K.
 template <class C, bool AK, bool BK, int ROLE, int ST, int CQ = -1>
-__device__ __forceinline__ void k_iter(int kt, OperandDma<C::BM>& da, OperandDma<C::BN>& db, TileCDma& dc,
-                                       floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
-                                       half8 (&fb)[2][C::TN], const FragBase<C::TM>& ba, const FragBase<C::TN>& bb,
-                                       uint32_t m0base, uint32_t lds0) {
-    using R = RoleMap<ROLE, C::TM, C::TN>;
-    constexpr int NM = R::N, NF = R::NF;
-    constexpr int NA = OperandDma<C::BM>::PER_WAVE, NB = OperandDma<C::BN>::PER_WAVE;
-    constexpr bool SPREAD = NM >= 2 * (NA + NB);
-    constexpr int SN = (ST + 1) & 3, SL = (ST + 3) & 3;
-    static_assert(NF <= NM && NA + NB <= NM, "one fragment and one direct load per MFMA at most");
-    static_assert(NA + NB == 8, "a quarter of C is 8 loads per wave, one stage of operand loads");
-    static_for<0, NM>([&](auto qc) {
-        constexpr int q = decltype(qc)::value, i = R::i(q), j = R::j(q);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (q < NF) read_frag<C, AK, BK, ST, 1, q>(ba, bb, fa[1], fb[1]);
-        __builtin_amdgcn_sched_barrier(0);
+__device__ __forceinline__ void mem_phase(int kt, Frags<ROLE>& f, const FragBase<RoleMap<ROLE>::AF>& ba,
+                                          const FragBase<RoleMap<ROLE>::BF>& bb, OperandDma<C::BM>& da,
+                                          OperandDma<C::BN>& db, TileCDma& dc, uint32_t m0w, uint32_t lds0) {
+    using R = RoleMap<ROLE>;
+    static_for<0, 2>([&](auto kc) {
+        constexpr int ks = decltype(kc)::value;
+        static_for<0, R::NA>([&](auto xc) {
+            constexpr int x = decltype(xc)::value;
+            f.a[ks][x] = frag_at<AK, ST, ks, 0, R::a_idx(x)>(ba);
+        });
+        static_for<0, R::NB>([&](auto yc) {
+            constexpr int y = decltype(yc)::value;
+            f.b[ks][y] = frag_at<BK, ST, ks, C::A_BYTES, R::b_idx(y)>(bb);
+        });
     });
-    lds_wait_barrier<(C::S - 3) * C::LOADS_PER_STAGE>();
+    constexpr int SL = (ST + 3) & 3;
+    da.begin_tile(kt + 3);
+    db.begin_tile(kt + 3);
+    if constexpr (CQ >= 0) {
+        static_assert(SL == CQ, "quarter q of C goes to stage q");
+        const uint32_t wq = lds0 + CQ * C::STAGE_BYTES +
+                            __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * TileCDma::PER_WAVE * 1024;
+        static_for<0, TileCDma::PER_WAVE>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            dc.issue(j, CQ, wq + j * 1024);
+        });
+    } else {
+        static_for<0, C::A_LOADS>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            da.issue(q, m0w + SL * C::STAGE_BYTES + q * 1024);
+        });
+        static_for<0, C::B_LOADS>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            db.issue(q, m0w + SL * C::STAGE_BYTES + C::A_BYTES + q * 1024);
+        });
+    }
     __builtin_amdgcn_sched_barrier(0);
-    da.begin_tile(kt + C::S - 1);
-    db.begin_tile(kt + C::S - 1);
-    static_for<0, NM>([&](auto qc) {
-        constexpr int q = decltype(qc)::value, i = R::i(q), j = R::j(q);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (q < NF) read_frag<C, AK, BK, SN, 0, q>(ba, bb, fa[0], fb[0]);
-        constexpr int d = SPREAD ? (q % 2 == 0 ? q / 2 : NA + NB) : q;
-        if constexpr (CQ >= 0) {
-            static_assert(SL == CQ, "quarter q of C goes to stage q");
-            const uint32_t wq = lds0 + CQ * C::STAGE_BYTES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 8192;
-            if constexpr (d < NA + NB) dc.issue(d, CQ, wq + d * 1024);
-        } else if constexpr (d < NA) {
-            da.issue(d, m0base + SL * C::STAGE_BYTES + d * 1024);
-        } else if constexpr (d < NA + NB) {
-            db.issue(d - NA, m0base + SL * C::STAGE_BYTES + C::A_BYTES + (d - NA) * 1024);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    });
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * C::LOADS) : "memory");
+    phase_barrier();
 }
 
 // The K tiles [lo, hi) of gemm_tile in one operand layout (AK / BK); lo and hi are multiples of 4,
-// so tile lo is in stage 0 and the loop body is the four stages' iterations with no exit in
-// between (an exit per iteration made the compiler copy the accumulators at every one). On entry
-// the stages hold tiles lo .. lo+2 (tile lo visible to every wave); the ks 0 fragments of tile lo
-// are read first, in this segment's layouts.
-// `last`: this is the tile's last segment; its last block of four iterations loads C quarters
-// 0-2 in its last three.
+// so tile lo is in stage 0 and each loop iteration is the four stages' memory and MFMA phases
+// with no exit in between. `last`: this is the tile's last segment; the memory phases of its last
+// three tiles load C quarters 0-2.
 template <class C, bool AK, bool BK, int ROLE>
-__device__ __forceinline__ void gemm_segment(int lo, int hi, bool last, OperandDma<C::BM>& da, OperandDma<C::BN>& db,
-                                             TileCDma& dc, floatx16 (&acc)[C::TM][C::TN], half8 (&fa)[2][C::TM],
-                                             half8 (&fb)[2][C::TN], uint32_t lds0, uint32_t m0base) {
+__device__ __forceinline__ void gemm_segment(int lo, int hi, bool last, const TileWork& tw, OperandDma<C::BM>& da,
+                                             OperandDma<C::BN>& db, TileCDma& dc,
+                                             floatx16 (&acc)[RoleMap<ROLE>::N], uint32_t lds0, uint32_t m0w) {
     if (lo >= hi) return;
-    using R = RoleMap<ROLE, C::TM, C::TN>;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // kRoleHalf: wave 1 takes rows 0-63, wave 2 rows 64-127 of the upper-right quadrant
-    const int wm = ROLE == kRoleHalf ? (wave >> 1) * (C::WM / 2) : (wave >> 1) * C::WM;
-    const int wn = ROLE == kRoleHalf ? C::WN : (wave & 1) * C::WN;
-    FragBase<C::TM> ba;
-    FragBase<C::TN> bb;
-    if (AK) ba.init_kmajor(lds0, wm, lane);
-    else ba.init_mnmajor(lds0, wm, lane);
-    if (BK) bb.init_kmajor(lds0, wn, lane);
-    else bb.init_mnmajor(lds0, wn, lane);
-    static_for<0, R::NF>([&](auto qc) { read_frag<C, AK, BK, 0, 0, decltype(qc)::value>(ba, bb, fa[0], fb[0]); });
+    using R = RoleMap<ROLE>;
+    const int lane = threadIdx.x & 63;
+    FragBase<R::AF> ba;
+    FragBase<R::BF> bb;
+    if (AK) ba.init_kmajor(lds0, tw.abase, lane);
+    else ba.init_mnmajor(lds0, tw.abase, lane);
+    if (BK) bb.init_kmajor(lds0, tw.bbase, lane);
+    else bb.init_mnmajor(lds0, tw.bbase, lane);
+    Frags<ROLE> f;
     const int body_end = last ? hi - 4 : hi;
     for (int kt = lo; kt < body_end; kt += 4) {
-        k_iter<C, AK, BK, ROLE, 0>(kt, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 1>(kt + 1, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 2>(kt + 2, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 3>(kt + 3, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
+        mem_phase<C, AK, BK, ROLE, 0>(kt, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 1>(kt + 1, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 2>(kt + 2, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 3>(kt + 3, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
     }
     if (last) {
         const int kt = hi - 4;
-        k_iter<C, AK, BK, ROLE, 0>(kt, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 1, 0>(kt + 1, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 2, 1>(kt + 2, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
-        k_iter<C, AK, BK, ROLE, 3, 2>(kt + 3, da, db, dc, acc, fa, fb, ba, bb, m0base, lds0);
+        mem_phase<C, AK, BK, ROLE, 0>(kt, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 1, 0>(kt + 1, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 2, 1>(kt + 2, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
+        mem_phase<C, AK, BK, ROLE, 3, 2>(kt + 3, f, ba, bb, da, db, dc, m0w, lds0);
+        mfma_phase<ROLE>(f, acc);
+        phase_barrier();
     }
 }
 
-// acc = A[m0 + wm + 32i .., 0:K] * B[0:K, n0 + wn + 32j ..] over KT K tiles of 32, A read
-// MN-major for tiles t < a_k0 and K-major from there on, B likewise with b_k0 (a_k0 <= b_k0; each
-// a multiple of 4 or >= KT): at most three segments, MN/MN, K/MN and K/K, in that order, through
-// one 4-stage pipeline of direct loads. K runs to KT rounded up to a multiple of 4; the tiles
-// past KT load zeros. The MFMA is issued as B^T A^T, so each 32 x 32 accumulator comes out
-// transposed: lane l holds row (l & 31) and the four consecutive columns 8*(r/4) + 4*(l/32) + 0..3
-// in registers r..r+3, which the epilogue writes to LDS as one 8-byte store. `diag`: the tile is a
-// diagonal tile of a symmetric result (m0 == n0), split by TileRole; every role passes the same
-// barriers (one per K tile, and the final one). `ct`: the epilogue's C tile, loaded into the
-// staging (TileC). Ends with every load and LDS read complete and a block barrier: the staging
-// holds C and the rest of the stages is free.
-template <class C>
+// acc = A[rows of the wave's blocks, 0:K] * B[0:K, columns of its blocks] over KT K tiles of 32,
+// A read MN-major for tiles t < a_k0 and K-major from there on, B likewise with b_k0 (a_k0 <=
+// b_k0; each a multiple of 4 or >= KT): at most three segments, MN/MN, K/MN and K/K, in that
+// order, through one 4-stage pipeline of direct loads. K runs to KT rounded up to a multiple of
+// 4; the tiles past KT load zeros.
+//
+// Phases: every wave runs memory phase kt, barrier, MFMA phase kt, barrier for kt = 0, 1, ...;
+// group 1 starts one phase late (an extra barrier before its first phase) and group 0 ends with
+// an extra barrier, so in every phase one group multiplies and the other loads. Tile kt+3's loads
+// are issued in memory phase kt (by each group, its share); a stage is refilled only after both
+// groups have read it (phase 2 kt + 1 is the last to read tile kt, whose stage tile kt+4 receives
+// in phase 2 kt + 2 at the earliest); each wave waits for its loads of tile kt+1 at the end of
+// memory phase kt, before the barrier after which group 0 reads tile kt+1.
+//
+// `tw`: the wave's role and bases (a diagonal tile of a symmetric result computes only its upper
+// blocks, TileWork). `ct`: the epilogue's C tile, loaded into the staging (TileC). Ends with
+// every load and LDS read complete and a block barrier: the staging holds C and the rest of the
+// stages is free.
+template <class C, int ROLE>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0, int KT, int a_k0,
-                                          int b_k0, const TileC& ct, floatx16 (&acc)[C::TM][C::TN], char* smem,
-                                          bool diag = false) {
+                                          int b_k0, const TileC& ct, const TileWork& tw,
+                                          floatx16 (&acc)[RoleMap<ROLE>::N], char* smem) {
     static_assert(C::S == 4 && C::BM == 256 && C::BN == 256, "the unrolled loop and the LDS bases assume these");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = floatx16{};
+    for (int q = 0; q < RoleMap<ROLE>::N; ++q) acc[q] = floatx16{};
     const int KT4 = (KT + 3) & ~3;
     OperandDma<C::BM> da;
     OperandDma<C::BN> db;
     da.init(A, m0, wave, lane, a_k0, KT);
     db.init(B, n0, wave, lane, b_k0, KT);
-    constexpr int NA = OperandDma<C::BM>::PER_WAVE, NB = OperandDma<C::BN>::PER_WAVE;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
-    const uint32_t m0base = lds0 + wave * NA * 1024;
+    const uint32_t m0w = lds0 + wave * C::A_LOADS * 1024;
     TileCDma dc;
     dc.init(ct, m0, n0, wave, lane);
-    static_for<0, 8>([&](auto jc) {   // C rows 192-255 into the 32 KB past the stages
+    static_for<0, TileCDma::PER_WAVE>([&](auto jc) {   // C rows 192-255 into the 32 KB past the stages
         constexpr int j = decltype(jc)::value;
-        dc.issue(j, 3, lds0 + C::LDS_BYTES + wave * 8192 + j * 1024);
+        dc.issue(j, 3, lds0 + C::LDS_BYTES + wave * TileCDma::PER_WAVE * 1024 + j * 1024);
     });
     static_for<0, C::S - 1>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
         da.begin_tile(t);
         db.begin_tile(t);
-        static_for<0, NA>([&](auto qc) {
+        static_for<0, C::A_LOADS>([&](auto qc) {
             constexpr int q = decltype(qc)::value;
-            da.issue(q, m0base + t * C::STAGE_BYTES + q * 1024);
+            da.issue(q, m0w + t * C::STAGE_BYTES + q * 1024);
         });
-        static_for<0, NB>([&](auto qc) {
+        static_for<0, C::B_LOADS>([&](auto qc) {
             constexpr int q = decltype(qc)::value;
-            db.issue(q, m0base + t * C::STAGE_BYTES + C::A_BYTES + q * 1024);
+            db.issue(q, m0w + t * C::STAGE_BYTES + C::A_BYTES + q * 1024);
         });
     });
-    lds_wait_barrier<(C::S - 2) * C::LOADS_PER_STAGE>();   // tile 0 visible
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * C::LOADS) : "memory");   // tile 0 (and C rows 192-255)
+    phase_barrier();
+    if (wave >= 4) phase_barrier();   // group 1 starts one phase late
     const int k1 = a_k0 < KT ? a_k0 : KT4;
     const int k2 = b_k0 < k1 ? k1 : (b_k0 < KT ? b_k0 : KT4);
     const int lastseg = KT4 > k2 ? 2 : (k2 > k1 ? 1 : 0);   // segments are never all empty (KT >= 1)
-    auto segments = [&](auto role) {
-        constexpr int ROLE = decltype(role)::value;
-        half8 fa[2][C::TM], fb[2][C::TN];
-        gemm_segment<C, false, false, ROLE>(0, k1, lastseg == 0, da, db, dc, acc, fa, fb, lds0, m0base);
-        gemm_segment<C, true, false, ROLE>(k1, k2, lastseg == 1, da, db, dc, acc, fa, fb, lds0, m0base);
-        gemm_segment<C, true, true, ROLE>(k2, KT4, lastseg == 2, da, db, dc, acc, fa, fb, lds0, m0base);
-    };
-    if (!diag) segments(std::integral_constant<int, kRoleFull>{});
-    else if (wave == 0 || wave == 3) segments(std::integral_constant<int, kRoleTri>{});
-    else segments(std::integral_constant<int, kRoleHalf>{});
+    gemm_segment<C, false, false, ROLE>(0, k1, lastseg == 0, tw, da, db, dc, acc, lds0, m0w);
+    gemm_segment<C, true, false, ROLE>(k1, k2, lastseg == 1, tw, da, db, dc, acc, lds0, m0w);
+    gemm_segment<C, true, true, ROLE>(k2, KT4, lastseg == 2, tw, da, db, dc, acc, lds0, m0w);
+    if (wave < 4) phase_barrier();    // group 0 waits out group 1's last MFMA phase
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -508,7 +561,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // 16-byte chunk c of row r at position c ^ (r & 31). The swizzle lets a direct load write two
 // whole rows (TileC), spreads the 32 consecutive rows that the lanes of one accumulator block write
 // (stage_f16) over the banks, and leaves each row's chunks a permutation for the row pass (32 lanes
-// per row). All four waves stage at once; diagonal tiles of symmetric results also stage the
+// per row). All eight waves stage at once; diagonal tiles of symmetric results also stage the
 // transposes of their upper values, which keeps them exactly symmetric.
 template <class C>
 struct EpiH {
@@ -516,9 +569,11 @@ struct EpiH {
     static constexpr int SPARE = C::LDS_BYTES;                     // rows 192..255 live here
     static constexpr int SMEM = C::LDS_BYTES + 64 * PITCH;         // 160 KB
     static constexpr int FREE = 3 * C::STAGE_BYTES;                // stage 3: unused by the staging
-    static_assert(FREE + 256 + 4 * 256 <= SPARE, "scratch slots in the free stage");
-    static constexpr int ROW_ITERS = C::BM * (C::BN / 8) / 256;   // row chunks per thread
+    static constexpr int ROWS = C::NT / 32;                        // rows per pass of the block
+    static constexpr int ROW_ITERS = C::BM / ROWS;                 // row chunks per thread
+    static_assert(FREE + 256 + 4 * C::NT <= SPARE, "scratch slots in the free stage");
     static_assert(C::BN / 8 == 32 && C::BM == 256 && C::STAGE_BYTES == 192 * PITCH / 3, "layout");
+    static_assert(ROWS == 16 && 192 % ROWS == 0, "a pass of rows lies on one side of row 192");
     static_assert(SMEM <= 160 * 1024, "LDS");
     // byte offset of row r's start (r wave-uniform or compile-time above 192 or not)
     __device__ static __forceinline__ int rowbase(int r) { return r * PITCH + (r >= 192 ? SPARE - 192 * PITCH : 0); }
@@ -528,23 +583,22 @@ struct EpiH {
     }
 };
 
-// Stages val(r, c, a, dblk) for the accumulators this wave owns: val gives the final f16 values
-// of tile-local row r, columns c .. c+3 from their 4 accumulators a (computing the rounding to f16
-// itself lets an fma with an f16 operand fuse into one instruction); dblk (wave-uniform) says that
-// the 32 x 32 block holds elements of the tile's diagonal, r == c + e for some e, which only the
-// diagonal blocks of waves 0 and 3 on a diagonal tile do. The caller separates this from the
-// previous use of smem and from the reads that follow with barriers.
-// On a diagonal tile (gemm_tile's `diag`, symmetric results only) the blocks sit where TileRole
-// put them (waves 1 and 2: rows 0-63 and 64-127 of the upper-right quadrant; waves 0 and 3: the
-// blocks on and above the diagonal of their quadrants) and every value above the tile's diagonal
-// is also written at its transposed position, so the staged tile is exactly symmetric: the
-// diagonal blocks of waves 0 and 3 are written whole first, then the transposes of their upper
-// elements replace the lower ones (a wave's LDS writes complete in program order).
-template <class C, class Val>
-__device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* smem, bool diag, Val val) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    auto quad = [&](int i, int j, int q) {
-        return floatx4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+// Stages val(r, c, a) for the accumulators this wave owns: val gives the final f16 values of
+// tile-local row r, columns c .. c+3 from their 4 accumulators a (computing the rounding to f16
+// itself lets an fma with an f16 operand fuse into one instruction). The caller separates this
+// from the previous use of smem and from the reads that follow with barriers.
+// On a diagonal tile (symmetric results only) the blocks sit where TileWork put them and every
+// value above the tile's diagonal is also written at its transposed position, so the staged tile
+// is exactly symmetric: a block on the diagonal is written whole first, then the transposes of its
+// upper elements replace the lower ones (a wave's LDS writes complete in program order, and each
+// block on the diagonal belongs to one wave).
+template <class C, int ROLE, class Val>
+__device__ __forceinline__ void stage_f16(floatx16 (&acc)[RoleMap<ROLE>::N], char* smem, bool diag,
+                                          const TileWork& tw, Val val) {
+    using R = RoleMap<ROLE>;
+    const int lane = threadIdx.x & 63;
+    auto quad = [&](int q, int e) {
+        return floatx4{acc[q][4 * e], acc[q][4 * e + 1], acc[q][4 * e + 2], acc[q][4 * e + 3]};
     };
     auto put = [&](int r, int c, const half4& h) { *reinterpret_cast<half4*>(smem + EpiH<C>::off(r, c)) = h; };
     // transposes of the 4 values; upper_only (a block on the tile's diagonal): only those above the
@@ -558,77 +612,52 @@ __device__ __forceinline__ void stage_f16(floatx16 (&acc)[C::TM][C::TN], char* s
             *reinterpret_cast<_Float16*>(smem + (!upper_only || c + e > r ? a : dump)) = h[e];
         }
     };
-    auto final4 = [&](int r, int c, const floatx4& a, bool dblk) { return val(r, c, a, dblk); };
     const int lr = lane & 31, lc = 4 * (lane >> 5);
-    if (diag && (wave == 1 || wave == 2)) {
-        const int r0 = (wave >> 1) * (C::WM / 2);
+    static_for<0, R::N>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        const int r = tw.abase + 32 * R::a_idx(R::bx(q)) + lr;
+        const int cb = tw.bbase + 32 * R::b_idx(R::by(q)) + lc;
+        half4 h[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int e = 0; e < 4; ++e) {
+            h[e] = val(r, cb + 8 * e, quad(q, e));
+            // one rounding for both copies: left visible, the compiler recomputed the value for the
+            // transposed copy as a single-rounding fma_mix and the direct one as mul + convert,
+            // which differ in rare elements and break the exact symmetry
+            opaque(h[e]);
+            put(r, cb + 8 * e, h[e]);
+            if (!R::on_diag(q) && diag) put_t(r, cb + 8 * e, h[e], false);
+        }
+        if constexpr (R::on_diag(q)) {
+            __builtin_amdgcn_sched_barrier(0);   // the whole block first
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = r0 + 32 * i + lr, c = C::WN + 32 * j + 8 * q + lc;
-                    const half4 h = final4(r, c, quad(i, j, q), false);
-                    put(r, c, h);
-                    put_t(r, c, h, false);
-                }
-    } else if (diag) {
-        const int wm = (wave >> 1) * C::WM;
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = i; j < C::TN; ++j) {
-                half4 h[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = wm + 32 * i + lr, c = wm + 32 * j + 8 * q + lc;
-                    h[q] = final4(r, c, quad(i, j, q), i == j);
-                    put(r, c, h[q]);
-                    if (j > i) put_t(r, c, h[q], false);
-                }
-                if (j == i) {
-                    __builtin_amdgcn_sched_barrier(0);   // the whole block first
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) put_t(wm + 32 * i + lr, wm + 32 * j + 8 * q + lc, h[q], true);
-                }
-            }
-    } else {
-        const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = wm + 32 * i + lr, c = wn + 32 * j + 8 * q + lc;
-                    put(r, c, final4(r, c, quad(i, j, q), false));
-                }
-    }
+            for (int e = 0; e < 4; ++e) put_t(r, cb + 8 * e, h[e], true);
+        }
+    });
 }
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
 // fn(it, r, c8, h) over this thread's row chunks it = 0 .. ROW_ITERS-1 in row order: h = staged
-// row r = 8 * it + tid / 32, columns c8 = 8 * (tid % 32) .. c8 + 7. The chunk's swizzled
-// position is (tid % 32) ^ (r & 31) = ((tid % 32) ^ (tid / 32)) ^ (8 * (it % 4)), so four per-lane
+// row r = 16 * it + tid / 32, columns c8 = 8 * (tid % 32) .. c8 + 7. The chunk's swizzled
+// position is (tid % 32) ^ (r & 31) = ((tid % 32) ^ (tid / 32)) ^ (16 * (it % 2)), so two per-lane
 // bases cover every chunk, the rest of each address being a constant. The bases are opaque to
-// the compiler, which then adds the constants rather than keep 32 addresses live.
+// the compiler, which then adds the constants rather than keep 16 addresses live.
 template <class C, class Fn>
 __device__ __forceinline__ void each_row_chunk_h(const char* smem, Fn fn) {
     using E = EpiH<C>;
     const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31, c8 = ck * 8;
-    int base[4];
+    int base[2];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        base[a] = tr * E::PITCH + (((ck ^ tr) ^ (8 * a)) << 4);
+    for (int a = 0; a < 2; ++a) {
+        base[a] = tr * E::PITCH + (((ck ^ tr) ^ (16 * a)) << 4);
         asm volatile("" : "+v"(base[a]));
     }
 #pragma unroll
     for (int it = 0; it < E::ROW_ITERS; ++it) {
-        const int r = 8 * it + tr;
-        const int rb = 8 * it * E::PITCH + (8 * it >= 192 ? E::SPARE - 192 * E::PITCH : 0);
-        fn(it, r, c8, *reinterpret_cast<const half8v*>(smem + base[it & 3] + rb));
+        const int r = E::ROWS * it + tr;
+        const int rb = E::ROWS * it * E::PITCH + (E::ROWS * it >= 192 ? E::SPARE - 192 * E::PITCH : 0);
+        fn(it, r, c8, *reinterpret_cast<const half8v*>(smem + base[it & 1] + rb));
     }
 }
 

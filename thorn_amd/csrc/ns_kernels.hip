@@ -15,9 +15,6 @@
 
 namespace thorn {
 
-// One tile configuration for every Newton-Schulz GEMM: 256 x 256 tiles, one block per CU.
-using NsCfg = GemmCfg<256, 256, 4>;
-
 __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) {
     Operand op;
     op.ptr = xsel == kXA ? M.xa : M.xb;
@@ -168,7 +165,7 @@ __device__ __forceinline__ void store_staged(const char* smem, _Float16* out, in
         __builtin_amdgcn_make_buffer_rsrc(out + int64_t(m0) * ld, 0, static_cast<int>(rows * ld * 2), 0x00020000);
     const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
     const uint32_t vbase = n0 + 8 * ck < ld ? static_cast<uint32_t>((tr * ld + n0 + 8 * ck) * 2) : kOutOfRange;
-    const uint32_t rstep = static_cast<uint32_t>(16 * ld);   // bytes of 8 rows
+    const uint32_t rstep = static_cast<uint32_t>(EpiH<C>::ROWS * ld * 2);   // bytes of a pass of rows
     each_row_chunk_h<C>(smem, [&](int it, int, int, const half8v& h) { buf_store8<2>(trs, vbase + it * rstep, h); });
 }
 
@@ -186,13 +183,13 @@ __device__ __forceinline__ void store_staged(const char* smem, _Float16* out, in
 // leave as is). DUAL: the tile is also stored to out2 as Q = Z + a I, the diagonal elements
 // rounded from the f16 Z (thorn.py:648, `Z + a * I` in f16): f16(float(Z_ii) + dual_add) with
 // dual_add = f16(a).
-template <class C, bool HAS_C, bool SCALE, bool DUAL = false>
-__device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* smem, _Float16* out, int64_t ld,
-                                          int n, int m0, int n0, float alpha, float beta, _Float16* out2 = nullptr,
-                                          float dual_add = 0.f) {
+template <class C, int ROLE, bool HAS_C, bool SCALE, bool DUAL = false>
+__device__ __forceinline__ void sym_store(floatx16 (&acc)[RoleMap<ROLE>::N], const TileWork& tw, char* smem,
+                                          _Float16* out, int64_t ld, int n, int m0, int n0, float alpha, float beta,
+                                          _Float16* out2 = nullptr, float dual_add = 0.f) {
     using E = EpiH<C>;
     const bool diag = m0 == n0;
-    stage_f16<C>(acc, smem, diag, [&](int r, int c, const floatx4& a, bool) {
+    stage_f16<C, ROLE>(acc, smem, diag, tw, [&](int r, int c, const floatx4& a) {
         half4 h;
         if constexpr (HAS_C) {
             const half4 cv = *reinterpret_cast<const half4*>(smem + E::off(r, c));
@@ -210,7 +207,7 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[C::TM][C::TN], char* s
     if constexpr (DUAL) {
         if (diag) {
             lds_barrier();   // the row pass has read the staging
-            const int r = threadIdx.x;
+            const int r = threadIdx.x;   // the diagonal element of row r (threads past 256 have none)
             if (r < C::BM && m0 + r < n) {
                 _Float16& z = *reinterpret_cast<_Float16*>(smem + E::off(r, r));
                 z = static_cast<_Float16>(static_cast<float>(z) + dual_add);
@@ -239,8 +236,9 @@ struct NsOp {
 // input iterate X and each output is f16(fma(beta * osc, X, osc * acc)), one rounding of a X + B X
 // as in the reference; otherwise f16(osc * acc).
 template <bool HAS_C>
-__device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[NsCfg::TM][NsCfg::TN], int local,
-                                              int ti, int tj, const NsOp& op, char* smem, float* scratch) {
+__device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)[RoleMap<kRoleFull>::N],
+                                              const TileWork& tw, int local, int ti, int tj, const NsOp& op,
+                                              char* smem, float* scratch) {
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int rows = M.rows, cols = M.cols, ldx = M.ldx, flags = M.flags;
     // the stored first iterate is sigma * u up to the factor x0scale, applied as the first
@@ -249,20 +247,25 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
     _Float16* const xout = op.xsel == kXA ? M.xb : M.xa;   // the input iterate's tile is in the staging
 
-    // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) streams p
-    // through a ring of D row chunks: chunk L is row m0 + 8*L + tid/32, columns n0 + 8*(tid%32)
-    // .. +7, requested into slot L % D as soon as chunk L - D has been used, the first D before
-    // the tile is staged. Buffer instructions address it as one resource over the tile's rows
-    // (scalar registers), a per-lane offset shared by every chunk and a wave-uniform row offset,
-    // so no per-chunk address occupies vector registers.
+    // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) holds this
+    // thread's part of the p tile in registers, half of it at a time: chunk L is row
+    // m0 + 16*L + tid/32, columns n0 + 8*(tid%32) .. +7. The first half is requested before the
+    // tile is staged, the second once the first is applied, and each half is waited for in full
+    // (vmcnt 0) before its first store. The compiler's own wait for a load counts the memory
+    // operations issued after it, which is exact only if no store is among them: a store may
+    // complete before an older load, and the count would then be reached with the load still in
+    // flight (measured: nondeterministic p with an 8-chunk ring refilled between the stores).
+    // Buffer instructions address p as one resource over the tile's rows (scalar registers), a
+    // per-lane offset shared by every chunk and a wave-uniform row offset, so no per-chunk address
+    // occupies vector registers.
     const bool apply_full = op.final_iter && !(flags & kFlagPNN) && (flags & kFlagVec4) &&
                             m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols;
-    constexpr int D = 8;
     constexpr int NC = EpiH<NsCfg>::ROW_ITERS;
+    constexpr int D = NC / 2;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         M.p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
     const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
-    auto soff = [&](int L) { return 8 * L * cols * 4; };
+    auto soff = [&](int L) { return EpiH<NsCfg>::ROWS * L * cols * 4; };
     float4 ring[D][2];
     auto fetch = [&](int L) {
         ring[L % D][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, soff(L), 0));
@@ -276,7 +279,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     if constexpr (HAS_C) {
         // gemm_tile has loaded the tile of the input iterate X into the staging
         const float bx = op.beta * osc;
-        stage_f16<NsCfg>(acc, smem, false, [&](int r, int c, const floatx4& a, bool) {
+        stage_f16<NsCfg, kRoleFull>(acc, smem, false, tw, [&](int r, int c, const floatx4& a) {
             const half4 xv = *reinterpret_cast<const half4*>(smem + EpiH<NsCfg>::off(r, c));
             half4 h;
 #pragma unroll
@@ -284,11 +287,11 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
             return h;
         });
     } else if (op.first) {
-        stage_f16<NsCfg>(acc, smem, false, [&](int, int, const floatx4& a, bool) {
+        stage_f16<NsCfg, kRoleFull>(acc, smem, false, tw, [&](int, int, const floatx4& a) {
             return half4{(_Float16)(a[0] * osc), (_Float16)(a[1] * osc), (_Float16)(a[2] * osc), (_Float16)(a[3] * osc)};
         });
     } else {
-        stage_f16<NsCfg>(acc, smem, false, [](int, int, const floatx4& a, bool) {
+        stage_f16<NsCfg, kRoleFull>(acc, smem, false, tw, [](int, int, const floatx4& a) {
             return half4{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3]};
         });
     }
@@ -300,7 +303,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const int tr = threadIdx.x >> 5, ck = threadIdx.x & 31;
     const bool col_ok = n0 + 8 * ck < ldx;
     const uint32_t vbase = col_ok ? static_cast<uint32_t>((tr * ldx + n0 + 8 * ck) * 2) : kOutOfRange;
-    const uint32_t rstep = static_cast<uint32_t>(16 * ldx);   // bytes of 8 rows
+    const uint32_t rstep = static_cast<uint32_t>(EpiH<NsCfg>::ROWS * ldx * 2);   // bytes of a pass of rows
     auto tile_rsrc = [&](_Float16* base) {
         const int trows = rows - m0 < NsCfg::BM ? rows - m0 : NsCfg::BM;
         return __builtin_amdgcn_make_buffer_rsrc(base + int64_t(m0) * ldx, 0, trows * ldx * 2, 0x00020000);
@@ -336,7 +339,8 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
             }
             static_assert(NsCfg::BN / 8 == 32, "one row per 32 lanes (one 8-column chunk per lane)");
             t = sum32_upper(m0 + lr < rows && col_ok ? t : 0.f);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, t), qrs, qoff + it * 32, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, t), qrs, qoff + it * EpiH<NsCfg>::ROWS * 4,
+                                                  0, 0);
         });
         return;
     }
@@ -359,9 +363,12 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         }
     };
     if (apply_full) {
-        // No memory operation in the pass is conditional, so each wait covers exactly the load
-        // it needs.
         each_row_chunk_h<NsCfg>(smem, [&](int L, int, int, const half8v& h) {
+            if (L == D) {   // the second half, once the first is applied (L is a constant)
+#pragma unroll
+                for (int k = D; k < NC; ++k) fetch(k);
+            }
+            if (L % D == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the half is in
             const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
             float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
             step8(pv, h);
@@ -372,7 +379,11 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
                                                    prs, voff, soff(L), 0);
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(pv[4], pv[5], pv[6], pv[7])),
                                                    prs, voff + 16, soff(L), 0);
-            if (L + D < NC) fetch(L + D);
+            // Two wait states before any VALU writes the data registers of these 16-byte stores
+            // (gfx950 needs them after a store of more than 8 bytes). The compiler inserts them
+            // itself, but it counts the scheduling barrier below as one: measured, a VALU write
+            // right after the second store corrupted its first element.
+            asm volatile("s_nop 1");
             __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: no hoisted LDS reads
         });
     } else {   // edge tiles: each chunk loaded where it is used
@@ -406,6 +417,39 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     }
 }
 
+// A Gram or symmetric-product tile (see ns_phase_kernel) in this wave's role: the main loop, then
+// the store of the upper-triangle tile (with its mirror on a diagonal tile).
+template <int ROLE>
+__device__ __forceinline__ void sym_tile(const OrthoMat& M, const NsOp& op, const Operand& A, const Operand& B, int m0,
+                                         int n0, int KT, int a_k0, int b_k0, const TileC& ct, const TileWork& tw,
+                                         char* smem) {
+    floatx16 acc[RoleMap<ROLE>::N];
+    gemm_tile<NsCfg, ROLE>(A, B, m0, n0, KT, a_k0, b_k0, ct, tw, acc, smem);
+    if (op.kind == kOpGram) {
+        if (op.first) {
+            const float osc = M.scal[kScalX0Scale];
+            sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, M.gram, M.lds, M.s, m0, n0, osc * osc, 0.f);
+        } else {
+            sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, M.gram, M.lds, M.s, m0, n0, 1.f, 0.f);
+        }
+        return;
+    }
+    _Float16* const out = sym_buf(M, op.osel);
+    if (op.csel >= 0) {
+        if (op.osel2 >= 0)
+            sym_store<NsCfg, ROLE, true, true, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta,
+                                                     sym_buf(M, op.osel2), op.dual_add);
+        else if (op.alpha != 1.f)
+            sym_store<NsCfg, ROLE, true, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta);
+        else
+            sym_store<NsCfg, ROLE, true, false>(acc, tw, smem, out, M.lds, M.s, m0, n0, 1.f, op.beta);
+    } else if (op.alpha != 1.f) {
+        sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, 0.f);
+    } else {
+        sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, out, M.lds, M.s, m0, n0, 1.f, 0.f);
+    }
+}
+
 // A Newton-Schulz phase launch: t0.total blocks run op0 over the tiles of task list t0, the other
 // t1.total blocks run op1 over t1, each XCD taking its eighth of the list with the longer tiles
 // first (t1_first: t1's; see xcd_split). The two operations belong to disjoint sets of matrices
@@ -427,7 +471,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 //     from their mirror above it. The output goes to the other iterate buffer. See update_finish
 //     for the epilogue.
 // All three run the same main loop (gemm_tile) with per-operation operands and layouts.
-__global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
+__global__ __launch_bounds__(NsCfg::NT) void ns_phase_kernel(const OrthoMat* __restrict__ mats, TaskList t0, NsOp op0,
                                                        TaskList t1, NsOp op1, int t1_first) {
     __shared__ __attribute__((aligned(16))) char smem[EpiH<NsCfg>::SMEM];
     float* const scratch = reinterpret_cast<float*>(smem + EpiH<NsCfg>::FREE);   // block sums after the row pass
@@ -484,33 +528,21 @@ __global__ __launch_bounds__(256) void ns_phase_kernel(const OrthoMat* __restric
         else if (op.kind == kOpSym) ct = TileC{sym_buf(M, op.csel), M.lds, M.s};
     }
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
-    floatx16 acc[NsCfg::TM][NsCfg::TN];
-    gemm_tile<NsCfg>(A, B, m0, n0, KT, a_k0, b_k0, ct, acc, smem, op.kind != kOpUpdate && ti == tj);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     if (op.kind == kOpUpdate) {
-        if (op.csel >= 0) update_finish<true>(M, acc, local, ti, tj, op, smem, scratch);
-        else update_finish<false>(M, acc, local, ti, tj, op, smem, scratch);
-    } else if (op.kind == kOpGram) {
-        if (op.first) {
-            const float osc = M.scal[kScalX0Scale];
-            sym_store<NsCfg, false, true>(acc, smem, M.gram, M.lds, M.s, m0, n0, osc * osc, 0.f);
-        } else {
-            sym_store<NsCfg, false, false>(acc, smem, M.gram, M.lds, M.s, m0, n0, 1.f, 0.f);
-        }
-    } else {
-        _Float16* const out = sym_buf(M, op.osel);
-        if (op.csel >= 0) {
-            if (op.osel2 >= 0)
-                sym_store<NsCfg, true, true, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta,
-                                                   sym_buf(M, op.osel2), op.dual_add);
-            else if (op.alpha != 1.f)
-                sym_store<NsCfg, true, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta);
-            else
-                sym_store<NsCfg, true, false>(acc, smem, out, M.lds, M.s, m0, n0, 1.f, op.beta);
-        } else if (op.alpha != 1.f) {
-            sym_store<NsCfg, false, true>(acc, smem, out, M.lds, M.s, m0, n0, op.alpha, 0.f);
-        } else {
-            sym_store<NsCfg, false, false>(acc, smem, out, M.lds, M.s, m0, n0, 1.f, 0.f);
-        }
+        const TileWork tw(false, wave);
+        floatx16 acc[RoleMap<kRoleFull>::N];
+        gemm_tile<NsCfg, kRoleFull>(A, B, m0, n0, KT, a_k0, b_k0, ct, tw, acc, smem);
+        if (op.csel >= 0) update_finish<true>(M, acc, tw, local, ti, tj, op, smem, scratch);
+        else update_finish<false>(M, acc, tw, local, ti, tj, op, smem, scratch);
+        return;
+    }
+    const TileWork tw(ti == tj, wave);
+    switch (tw.role) {
+        case kRoleFull: sym_tile<kRoleFull>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
+        case kRoleDiagA: sym_tile<kRoleDiagA>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
+        case kRoleDiagB: sym_tile<kRoleDiagB>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
+        default: sym_tile<kRoleHalf>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
     }
 }
 

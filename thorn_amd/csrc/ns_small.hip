@@ -108,7 +108,7 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(stages)) + wave * 1024;
     auto issue = [&](int t) {
         const void* p = ok ? static_cast<const void*>(src + int64_t(t) * 64) : zero;
-        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p),
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p),
                      "{m0}"(lds0 + (t % kSmallStages) * kSmallStageBytes)
                      : "memory");
     };

@@ -934,8 +934,8 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
         // longer tiles first; on equal contraction lengths the square set's list first (measured
         // slightly faster: NS 5.87 against 5.89 ms per step on config 2)
         const int square_first = klen(0) >= klen(1) ? 1 : 0;
-        THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(256), 0, st, mats, tl[1],
-                     op[1], tl[0], op[0], square_first);
+        THORN_LAUNCH(kind, "ns_phase_kernel", thorn::ns_phase_kernel, dim3(total), dim3(thorn::NsCfg::NT), 0, st,
+                     mats, tl[1], op[1], tl[0], op[0], square_first);
     }
     if (plan->small_live.n > 0) {   // every small matrix's whole schedule in one launch
         thorn::SmallSchedule ss{};
