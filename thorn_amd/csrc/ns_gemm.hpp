@@ -414,12 +414,22 @@ __device__ __forceinline__ void mem_phase(int kt, Frags<ROLE>& f, const FragBase
         });
     });
     constexpr int SL = (ST + 3) & 3;
-    da.begin_tile(kt + 3);
-    db.begin_tile(kt + 3);
+    // The layouts switch at a few tiles only: a scalar branch around the switch (left to itself,
+    // the compiler made both switches selects in every memory phase).
+    const int t = kt + 3;
+    if (t == da.k0 || t == db.k0 || t == da.kend) {
+        asm volatile("");
+        da.begin_tile(t);
+        db.begin_tile(t);
+    }
+    // M0 addresses recomputed from the wave's base in every phase (one scalar add each): hoisted
+    // out of the loop, the 16 stage addresses took scalar registers that then spilled.
+    uint32_t mw = m0w;
+    asm volatile("" : "+s"(mw));
     if constexpr (CQ >= 0) {
         static_assert(SL == CQ, "quarter q of C goes to stage q");
-        const uint32_t wq = lds0 + CQ * C::STAGE_BYTES +
-                            __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * TileCDma::PER_WAVE * 1024;
+        const uint32_t wq = mw - __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * C::A_LOADS * 1024 +
+                            CQ * C::STAGE_BYTES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * TileCDma::PER_WAVE * 1024;
         static_for<0, TileCDma::PER_WAVE>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             dc.issue(j, CQ, wq + j * 1024);
@@ -427,11 +437,11 @@ __device__ __forceinline__ void mem_phase(int kt, Frags<ROLE>& f, const FragBase
     } else {
         static_for<0, C::A_LOADS>([&](auto qc) {
             constexpr int q = decltype(qc)::value;
-            da.issue(q, m0w + SL * C::STAGE_BYTES + q * 1024);
+            da.issue(q, mw + SL * C::STAGE_BYTES + q * 1024);
         });
         static_for<0, C::B_LOADS>([&](auto qc) {
             constexpr int q = decltype(qc)::value;
-            db.issue(q, m0w + SL * C::STAGE_BYTES + C::A_BYTES + q * 1024);
+            db.issue(q, mw + SL * C::STAGE_BYTES + C::A_BYTES + q * 1024);
         });
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -247,21 +247,16 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
     const float osc = op.first ? M.scal[kScalX0Scale] : 1.f;
     _Float16* const xout = op.xsel == kXA ? M.xb : M.xa;   // the input iterate's tile is in the staging
 
-    // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) holds this
-    // thread's part of the p tile in registers, half of it at a time: chunk L is row
-    // m0 + 16*L + tid/32, columns n0 + 8*(tid%32) .. +7. The first half is requested before the
-    // tile is staged, the second once the first is applied, and each half is waited for in full
-    // (vmcnt 0) before its first store. The compiler's own wait for a load counts the memory
-    // operations issued after it, which is exact only if no store is among them: a store may
-    // complete before an older load, and the count would then be reached with the load still in
-    // flight (measured: nondeterministic p with an 8-chunk ring refilled between the stores).
-    // Buffer instructions address p as one resource over the tile's rows (scalar registers), a
-    // per-lane offset shared by every chunk and a wave-uniform row offset, so no per-chunk address
-    // occupies vector registers.
+    // The direct apply of a whole tile (every tile of a matrix with 256-multiple sides) streams p
+    // through a ring of D row chunks: chunk L is row m0 + 16*L + tid/32, columns n0 + 8*(tid%32)
+    // .. +7, requested into slot L % D as soon as chunk L - D has been used, the first D before
+    // the tile is staged. Buffer instructions address it as one resource over the tile's rows
+    // (scalar registers), a per-lane offset shared by every chunk and a wave-uniform row offset,
+    // so no per-chunk address occupies vector registers.
     const bool apply_full = op.final_iter && !(flags & kFlagPNN) && (flags & kFlagVec4) &&
                             m0 + NsCfg::BM <= rows && n0 + NsCfg::BN <= cols;
     constexpr int NC = EpiH<NsCfg>::ROW_ITERS;
-    constexpr int D = NC / 2;
+    constexpr int D = 8;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         M.p + ((int64_t)m0 * cols + n0), 0, NsCfg::BM * cols * 4, 0x00020000);
     const int voff = ((threadIdx.x >> 5) * cols + (threadIdx.x & 31) * 8) * 4;
@@ -363,12 +358,9 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
         }
     };
     if (apply_full) {
+        // No memory operation in the pass is conditional, so each wait covers exactly the load
+        // it needs.
         each_row_chunk_h<NsCfg>(smem, [&](int L, int, int, const half8v& h) {
-            if (L == D) {   // the second half, once the first is applied (L is a constant)
-#pragma unroll
-                for (int k = D; k < NC; ++k) fetch(k);
-            }
-            if (L % D == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the half is in
             const float4 p0 = ring[L % D][0], p1 = ring[L % D][1];
             float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
             step8(pv, h);
@@ -384,6 +376,7 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
             // itself, but it counts the scheduling barrier below as one: measured, a VALU write
             // right after the second store corrupted its first element.
             asm volatile("s_nop 1");
+            if (L + D < NC) fetch(L + D);
             __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: no hoisted LDS reads
         });
     } else {   // edge tiles: each chunk loaded where it is used
