@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 7
+#define THORN_ABI_VERSION 8
 
 enum {
     THORN_OK = 0,
@@ -120,8 +120,16 @@ void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan);
 size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
 /* The int32 at this byte offset of the workspace is nonzero after a step in which a cluster of
  * workgroups of the small-matrix Newton-Schulz launch did not all become resident (its bounded
- * barrier wait expired; that step's small-matrix updates are then not valid). */
+ * barrier wait expired; that step's small-matrix updates are then not valid). Each step clears it
+ * before its Newton-Schulz launches, so it reports the last step only; a caller reads it once the
+ * step is done (the thorn_amd package copies it to pinned memory behind every step and raises
+ * RuntimeError at the next step when it was set). */
 #define THORN_WS_STATUS_OFFSET 256
+/* Polls (a 64-cycle sleep each) of the small-matrix launch's bounded cluster barrier before it
+ * gives up and sets the status word; default 2^24. No counterpart in the reference: a test hook
+ * that makes the wait expire from the host (0: at the first wait that would block) while every
+ * kernel still exits normally. */
+int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);
@@ -146,8 +154,9 @@ int thorn_ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float
 int thorn_ortho_step_event(thorn_ortho_plan_t plan, const void* table_dev, const float* coeffs, int iters,
                            uint32_t restart_mask, void* stream, void* ns_begin_event);
 
-/* No counterpart in the reference. For callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): thorn_ortho_fill_table
+/* No counterpart in the reference. For callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc; it copies its table from host memory, and is not made or
+ * tested for HIP graph capture): thorn_ortho_fill_table
  * and thorn_ortho_step in one call, with the workspace and the device table in a file-scope
  * device array of THORN_NOALLOC_SCRATCH_BYTES per GPU instead of caller memory. It calls no
  * hipMalloc or hipFree; the plan (thorn_ortho_plan_create, made beforehand) holds the host side

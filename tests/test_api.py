@@ -236,3 +236,45 @@ def test_adam_beside_chains_decision():
     ps = params(m2)
     OPT._adam_beside_chains([(True, ps), (False, params(adam))], big, cache)
     assert list(cache.values()) == [True] and list(cache)[0][0] == tuple(id(p) for p in ps)
+
+
+def test_status_watch_raises_for_a_set_status_word():
+    """The small-matrix launch's status word, copied behind each step into a ring of pinned slots:
+    a completed slot holding a nonzero word raises RuntimeError at the next check (not before its
+    event completes, unless the check waits), and the ring checks its oldest slot before reusing it."""
+    from thorn_amd import optim as OPT
+
+    class Ev:
+        def __init__(self):
+            self.done = False
+            self.waited = 0
+
+        def query(self):
+            return self.done
+
+        def synchronize(self):
+            self.waited += 1
+            self.done = True
+
+    w = OPT._StatusWatch.__new__(OPT._StatusWatch)
+    w.host = torch.zeros(w.SLOTS, dtype=torch.int32)
+    w.events = [Ev() for _ in range(w.SLOTS)]
+    w.pending = [False] * w.SLOTS
+    w.next = 0
+    # slots 0 and 1 recorded; slot 1's step timed out and has not completed yet
+    w.pending[0] = w.pending[1] = True
+    w.next = 2
+    w.host[1] = 1
+    w.events[0].done = True
+    w.check()                        # slot 0 completed clean; slot 1 still in flight
+    assert w.pending == [False, True, False, False] and w.events[1].waited == 0
+    with pytest.raises(RuntimeError, match='timed out'):
+        w.check(wait=True)
+    assert w.pending == [False] * w.SLOTS and int(w.host[1]) == 0
+    w.check(wait=True)               # reported once
+    # a clean word never raises, completed or waited for
+    w.pending[3] = True
+    w.events[3].done = True
+    w.check()
+    assert not any(w.pending)
+

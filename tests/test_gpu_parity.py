@@ -1061,3 +1061,49 @@ def test_changing_live_set_keeps_memory_bounded():
         assert n_ortho <= 2, n_ortho
     _log(f'[gpu]   memory allocated per step: {mem}')
     assert max(mem[4:]) <= max(mem[:4]), mem
+
+
+def test_small_launch_timeout_is_reported():
+    """The small-matrix launch's cluster barrier waits a bounded number of polls. A spin limit of 0
+    set from the host makes every wait that would block give up at once (the kernels still run to
+    their end, reading and writing the same buffers): the step's status word is set, and
+    check_status() raises RuntimeError. The next step clears the word; with the default limit back
+    the steps report nothing, and a fresh optimizer's update matches the oracle."""
+    _log('[gpu] small-matrix launch: barrier timeout forced from the host')
+    thorn_amd = _thorn()
+    g = torch.Generator().manual_seed(7)
+    p0 = torch.randn(256, 640, generator=g) * 0.02
+    grads = [torch.randn(256, 640, generator=g) * 1e-3 for _ in range(3)]
+    p = torch.nn.Parameter(p0.clone().to(DEV))
+    opt = thorn_amd.THORN([dict(orthogonalize=True, params=[p], lr=2e-3)])
+    p.grad = grads[0].to(DEV)
+    opt.step()
+    opt.check_status()
+    plans = [x.plan for r in opt._runners.values() for x in getattr(r, 'runners', ())]
+    assert plans
+    for pl in plans:
+        pl.set_spin_limit(0)
+    p.grad = grads[1].to(DEV)
+    opt.step()
+    with pytest.raises(RuntimeError, match='timed out'):
+        opt.check_status()
+    for pl in plans:
+        pl.set_spin_limit(1 << 24)
+    p.grad = grads[2].to(DEV)
+    opt.step()
+    opt.check_status()
+    opt.step()   # the check at the start of a step sees the clean word too
+    opt.check_status()
+    # a clean optimizer on the same input, against the oracle
+    q = torch.nn.Parameter(p0.clone().to(DEV))
+    c = torch.nn.Parameter(p0.clone())
+    gpu = thorn_amd.THORN([dict(orthogonalize=True, params=[q], lr=2e-3)])
+    cpu = O.OracleTHORN([dict(orthogonalize=True, params=[c], lr=2e-3)])
+    q.grad = grads[0].to(DEV)
+    c.grad = grads[0].clone()
+    gpu.step()
+    cpu.step()
+    gpu.check_status()
+    r = rel((q.detach().cpu() - p0), (c.detach() - p0))
+    assert r <= 2e-2, r
+    _log('[gpu]   ok')

@@ -89,6 +89,7 @@ SIGNATURES = {
     'thorn_adam_step': (_i, [_vp, _vp, _vp]),
     'thorn_adam_sparse_step': (_i, [_vp, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
+    'thorn_ortho_set_spin_limit': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
     'thorn_ortho_timing_intervals': (_i, [_vp, _vp, _vp, _vp, _vp, _i, ctypes.POINTER(_i)]),
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
@@ -98,7 +99,7 @@ KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_f
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
 NOALLOC_SCRATCH_BYTES = 32 << 20
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 
@@ -188,6 +189,9 @@ class OrthoPlan:
 
     def timing_enable(self, max_launches: int) -> None:
         check(self._lib.thorn_ortho_timing_enable(self.handle, max_launches), 'thorn_ortho_timing_enable')
+
+    def set_spin_limit(self, polls: int) -> None:
+        check(self._lib.thorn_ortho_set_spin_limit(self.handle, polls), 'thorn_ortho_set_spin_limit')
 
     def timing_read(self) -> dict:
         return _timing_read(self._lib.thorn_ortho_timing_read, self.handle)

@@ -43,8 +43,9 @@ struct SmallSchedule {
 
 // Barrier of the C workgroups of one matrix: sense-reversing (count, generation) in the
 // workspace, agent-scope release on arrival and acquire on departure. The wait is bounded: a
-// cluster whose members are not all resident cannot hang the GPU; it sets *err and goes on.
-__device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err) {
+// cluster whose members are not all resident cannot hang the GPU; after `spin` polls (each a
+// 64-cycle sleep) it sets *err and goes on.
+__device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int spin) {
     __syncthreads();
     if (C > 1 && threadIdx.x == 0) {
         int* cnt = bar;
@@ -57,11 +58,11 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err) {
         } else {
             int it = 0;
             while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++it > (1 << 24)) {
+                if (it++ >= spin) {
                     __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
+                __builtin_amdgcn_s_sleep(1);
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
@@ -225,7 +226,7 @@ __device__ __forceinline__ void small_store_final(const _Float16* stage, const O
 // Each operation's output is cut into super-tiles of up to 128 x 128 dealt to the cluster's
 // workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
 __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
-                                                                 SmallSchedule sc, int* err) {
+                                                                 SmallSchedule sc, int* err, int spin) {
     __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
     static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
     const int k = find_task(tl.starts, tl.n, blockIdx.x);
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
                 small_store(stage, V.xw(xo), V.lp, V.xwt(xo), V.sp, m0, n0, lane);
             }
         }
-        cluster_barrier(bar, C, err);
+        cluster_barrier(bar, C, err, spin);
     }
 }
 

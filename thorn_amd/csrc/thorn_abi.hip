@@ -167,6 +167,7 @@ struct thorn_ortho_plan {
     std::vector<int32_t> kept;
     std::vector<char> host_table;   // host side of the table for thorn_ortho_step_noalloc
     LaunchTimer timer;
+    int spin_limit = 1 << 24;   // polls of the small-matrix cluster barrier before it gives up
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
     const void* filled_ws = nullptr;   // workspace of the last fill_table
@@ -870,6 +871,8 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
     const auto* mats = reinterpret_cast<const thorn::OrthoMat*>(dev + plan->mats_off);
     LaunchTimer& tm = plan->timer;
     int rc, slot;
+    int* const status = reinterpret_cast<int*>(static_cast<char*>(const_cast<void*>(plan->filled_ws)) +
+                                               THORN_WS_STATUS_OFFSET);
 #define THORN_LAUNCH(kind, name, ...)                      \
     slot = tm.begin(kind, st);                             \
     hipLaunchKernelGGL(__VA_ARGS__);                       \
@@ -879,7 +882,7 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel,
-                 dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n);
+                 dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n, status);
     if (plan->adam_live.n > 0) {   // the Adam step of the decouple_md tensors of an Adam group
         const thorn::TaskList ad = task_list(dev, plan->adam_live);
         THORN_LAUNCH(THORN_KIND_ADAM, "ortho_adam_apply_kernel", thorn::ortho_adam_apply_kernel, dim3(ad.total),
@@ -945,10 +948,9 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
                                                        std::to_string(thorn::kSmallMaxOps) +
                                                        " Newton-Schulz operations for the small-matrix path");
         }
-        int* status = reinterpret_cast<int*>(static_cast<char*>(const_cast<void*>(plan->filled_ws)) +
-                                             THORN_WS_STATUS_OFFSET);
         THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel, dim3(plan->small_live.total),
-                     dim3(thorn::kSmallThreads), 0, st, mats, task_list(dev, plan->small_live), ss, status);
+                     dim3(thorn::kSmallThreads), 0, st, mats, task_list(dev, plan->small_live), ss, status,
+                     plan->spin_limit);
     }
     if (plan->rs_live.n > 0) {
         const thorn::TaskList rs = task_list(dev, plan->rs_live);
@@ -1019,6 +1021,12 @@ int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* s
     const int rc = thorn_ortho_step(plan, table_dev, coeffs, iters, restart_mask, stream);
     plan->stepped_ws = nullptr;   // the next call may find another plan's data in the array
     return rc;
+}
+
+int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls) {
+    if (!plan || polls < 0) return fail(THORN_ERR_INVALID, "thorn_ortho_set_spin_limit: null plan or negative limit");
+    plan->spin_limit = polls;
+    return THORN_OK;
 }
 
 int thorn_ortho_timing_enable(thorn_ortho_plan_t plan, int max_launches) {

@@ -378,6 +378,48 @@ class _SharedWorkspace:
         return t
 
 
+class _StatusWatch:
+    """The workspace status word (set when a cluster of the small-matrix launch timed out waiting
+    for its workgroups to become resident) read behind every step that ran that launch: copied into
+    a ring of pinned slots with an event each. Completed slots are checked at the start of the next
+    step, so the host never waits for the GPU unless all slots are still in flight."""
+    SLOTS = 4
+
+    def __init__(self):
+        self.host = torch.zeros(self.SLOTS, dtype=torch.int32, pin_memory=True)
+        self.events = [torch.cuda.Event() for _ in range(self.SLOTS)]
+        self.pending = [False] * self.SLOTS
+        self.next = 0
+
+    def record(self, workspace: torch.Tensor, stream: torch.cuda.Stream) -> None:
+        i = self.next
+        if self.pending[i]:
+            self._check(i)
+        word = workspace[_lib.WS_STATUS_OFFSET:_lib.WS_STATUS_OFFSET + 4].view(torch.int32)
+        with torch.cuda.stream(stream):
+            self.host[i:i + 1].copy_(word, non_blocking=True)
+        self.events[i].record(stream)
+        self.pending[i] = True
+        self.next = (i + 1) % self.SLOTS
+
+    def check(self, wait: bool = False) -> None:
+        """Raises RuntimeError if a completed step (every recorded step with wait=True) set the word."""
+        for k in range(self.SLOTS):
+            i = (self.next + k) % self.SLOTS   # oldest first
+            if self.pending[i] and (wait or self.events[i].query()):
+                self._check(i)
+
+    def _check(self, i: int) -> None:
+        self.events[i].synchronize()
+        self.pending[i] = False
+        if int(self.host[i]) != 0:
+            self.host[i] = 0
+            raise RuntimeError('THORN: the small-matrix Newton-Schulz launch timed out waiting for a '
+                               'cluster of its workgroups to become resident; that step left the '
+                               'parameters of its matrices with min(rows, cols) <= 256 and rows * cols '
+                               '< 2^20 partly updated')
+
+
 class _OrthoRunner:
     """One orthogonalized parameter set (or, with adam=True, the decouple_md tensors of a
     non-orthogonalized group, whose update is the Adam step): plan, workspace and the per-step
@@ -406,6 +448,10 @@ class _OrthoRunner:
         self.upload = _TableUpload(self.plan.table_bytes)
         self.steps = np.zeros(len(rows), dtype=_lib.ORTHO_MAT_STEP)
         self.md = group.decouple_md
+        # matrices of the small-matrix launch, whose status word is read behind each step
+        self.small = ((np.minimum(self.rows, self.cols) <= SMALL_MAX_S)
+                      & (self.rows * self.cols < SMALL_MAX_ELEMS))
+        self.status = _StatusWatch() if self.small.any() and not adam else None
 
     @property
     def workspace(self) -> torch.Tensor:
@@ -416,6 +462,8 @@ class _OrthoRunner:
         """unmasked: id(p) -> False for a parameter whose Magma mask skips this step. ns_begin:
         recorded on the stream once the prologue launches are enqueued (thorn_ortho_step_event)."""
         params, steps = self.params, self.steps
+        if self.status is not None:
+            self.status.check()
         n = len(self.owner)
         elem = (self.rows * self.cols).astype(np.int64)
         bytes_off = self.sub * elem * 4
@@ -502,9 +550,11 @@ class _OrthoRunner:
         coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
         if self.adam or not due.any():   # no polar factor this step: momentum (gains, Magma s) only
             coeffs = coeffs[:0]
+        stream = torch.cuda.current_stream(self.device)
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
-                       torch.cuda.current_stream(self.device).cuda_stream,
-                       ns_begin.cuda_event if ns_begin is not None else 0)
+                       stream.cuda_stream, ns_begin.cuda_event if ns_begin is not None else 0)
+        if self.status is not None and coeffs.shape[0] and (due & self.small).any():
+            self.status.record(self.workspace, stream)
 
     @staticmethod
     def restart_mask(group: _Group, iters: int) -> int:
@@ -984,7 +1034,7 @@ class THORN(Optimizer):
             cap = len(self.param_groups[key[1]]['params']) if single else self._RUNNERS_PER_GROUP
             same = [k for k in self._runners if k[:3] == slot and per_param(k) == single]
             for k in same[:max(0, len(same) - cap + 1)]:
-                del self._runners[k]
+                self._check_status(self._runners.pop(k))
             r = factory()
         self._runners[key] = r   # most recently used last
         return r
@@ -1125,6 +1175,19 @@ class THORN(Optimizer):
             gi = next(i for i, g in enumerate(self.param_groups) if g is group)
             self._step_params([param], _Group.from_kwargs(**group), gi)
         return loss
+
+    def check_status(self) -> None:
+        """Waits for the steps enqueued so far and raises RuntimeError if one of them had its
+        small-matrix Newton-Schulz launch time out (step() makes the same check without waiting,
+        for the steps already completed, when it starts)."""
+        for r in list(self._runners.values()):
+            self._check_status(r)
+
+    @staticmethod
+    def _check_status(r) -> None:
+        for x in getattr(r, 'runners', ()):
+            if x.status is not None:
+                x.status.check(wait=True)
 
     def _release_step(self, p: torch.Tensor, join_later: bool) -> None:
         """step(param=p) as gradient release runs it, with p.grad as it is now; the caller may drop
