@@ -236,6 +236,15 @@ def test_adam_beside_chains_decision():
     ps = params(m2)
     OPT._adam_beside_chains([(True, ps), (False, params(adam))], big, cache)
     assert list(cache.values()) == [True] and list(cache)[0][0] == tuple(id(p) for p in ps)
+    # one 3-D parameter of 28 large matrices is one plan, never chains: no side stream either
+    stacked = params([(28, 1024, 1024)])
+    assert OPT._large_matrices(stacked) == 28
+    assert OPT._chain_plan(stacked, big) is None
+    assert not OPT._adam_beside_chains([(True, stacked), (False, params(adam))], big, {})
+    # the decision is the chained step's own: _chain_plan on the same parameters
+    for shapes, want in ((m2, 2), (m5, 4), (m2[:15], None)):
+        ch = OPT._chain_plan(params(shapes), big)
+        assert (None if ch is None else len(ch)) == want
 
 
 def test_status_watch_raises_for_a_set_status_word():

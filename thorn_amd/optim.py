@@ -21,6 +21,7 @@ gradient on a parameter that is not contiguous fp32.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 import weakref
 from dataclasses import dataclass, field, fields, MISSING
@@ -258,14 +259,23 @@ class _Shadow:
         self.grad = torch.empty(p.shape, dtype=torch.float32, device=p.device)
         self.state: dict = {}
 
+    def reserve(self, state: dict) -> bool:
+        """Allocates the fp32 copies of state tensors that have none (or another shape); True if
+        it allocated any."""
+        fresh = False
+        for k, v in state.items():
+            if torch.is_tensor(v) and (k not in self.state or self.state[k].shape != v.shape):
+                self.state[k] = torch.empty(v.shape, dtype=torch.float32, device=v.device)
+                fresh = True
+        return fresh
+
     def load(self, p: torch.Tensor, state: dict) -> None:
+        """Copies the parameter, its gradient and its state in (reserve() first)."""
         self.param.data.copy_(p.detach())
         self.grad.copy_(p.grad)
         self.param.grad = self.grad
         for k, v in state.items():
             if torch.is_tensor(v):
-                if k not in self.state or self.state[k].shape != v.shape:
-                    self.state[k] = torch.empty(v.shape, dtype=torch.float32, device=v.device)
                 self.state[k].copy_(v)
             else:
                 self.state[k] = v
@@ -617,6 +627,17 @@ def _split_chains(params: list, n: int) -> list:
     return [[p for i, p in enumerate(params) if chain[i] == c] for c in range(n)]
 
 
+def _chain_plan(params: list, limit: int) -> Optional[list]:
+    """The chains a group's orthogonalized parameters step as (_OrthoBatches), or None for one
+    stream: chains need one batch under `limit` with at least CHAIN_MIN_MATRICES large-path
+    matrices and at least one parameter per chain (a single 3-D parameter of many matrices is one
+    plan)."""
+    if len(params) < 2 or _large_matrices(params) < CHAIN_MIN_MATRICES or len(_batches(params, limit)) != 1:
+        return None
+    chains = _split_chains(params, _chain_count(params))
+    return chains if all(chains) else None
+
+
 # A group with at least CHAIN_MIN_MATRICES large-path matrices steps as chains (_OrthoBatches),
 # one per CHAIN_COST of work, at most MAX_CHAINS: the device has 4 hardware queues per process,
 # and the caller's stream takes the steps around the chains.
@@ -637,6 +658,13 @@ RELEASE_WINDOW_BYTES = 256 << 20
 # chains' GEMMs (config 2 on two MI355X boxes: 6.68-6.69 against 6.75-6.77 and 6.70-6.74 against
 # 6.74-6.76 ms per step).
 ADAM_OVERLAP = True
+
+
+def _wait_for(home: torch.cuda.Stream) -> None:
+    """The current stream of home's device waits for the work enqueued on home so far."""
+    ev = torch.cuda.Event()
+    ev.record(home)
+    torch.cuda.current_stream(home.device).wait_event(ev)
 
 
 def _window_full(grad_bytes: int) -> bool:
@@ -660,8 +688,8 @@ def _adam_beside_chains(live: list, limit: int, cache: dict) -> bool:
             if c is None:
                 if len(cache) > 64:
                     cache.clear()
-                c = cache[key] = (_large_matrices(ps) >= CHAIN_MIN_MATRICES and _chain_count(ps) <= 2
-                                  and len(_batches(ps, limit)) == 1)
+                chains = _chain_plan(ps, limit)
+                c = cache[key] = chains is not None and len(chains) <= 2
             chained = chained or c
         elif ps:
             if any(p.grad.is_sparse for p in ps):
@@ -695,8 +723,8 @@ class _OrthoBatches:
         self.runners = []
         self.chained = False
         workspace = None
-        chains = _split_chains(params, _chain_count(params)) if len(params) > 1 and chain else [[]]
-        if len(batches) == 1 and not adam and _large_matrices(params) >= CHAIN_MIN_MATRICES and all(chains):
+        chains = _chain_plan(params, limit) if chain and not adam else None
+        if chains is not None:
             self.chained = True
             batches = chains
             # ns_begin[i]: recorded by chain i once its prologue is enqueued (the library records
@@ -746,6 +774,15 @@ class _OrthoBatches:
             main.wait_event(ev)
 
 
+class _AdamBatch:
+    """The plain Adam tensors of every non-orthogonalized group of one step, per device, and the
+    rest of those groups' step (working-copy write-back, step counts), run after the launch."""
+
+    def __init__(self):
+        self.entries: dict = {}
+        self.finish: list = []
+
+
 class _AdamRunner:
     """All tensors of the non-orthogonalized groups of one step: one multi-tensor launch."""
 
@@ -766,12 +803,12 @@ class _AdamRunner:
     def workspaces(self) -> list:
         return [self.workspace]
 
-    def run(self, entries: list, update_rate: int = 1, unmasked: Optional[dict] = None) -> None:
-        """entries: (p, state, group) per tensor, in plan order. A tensor's parameter is written
-        only when its step is due under update_rate (thorn.py:1706-1707) and not masked by Magma;
-        m and v always are."""
+    def run(self, entries: list, update_rate: int = 1) -> None:
+        """entries: (p, state, group, unmasked) per tensor, in plan order, from any number of
+        groups. A tensor's parameter is written only when its step is due under update_rate
+        (thorn.py:1706-1707) and not masked by Magma (unmasked False); m and v always are."""
         s = self.steps
-        for k, (p, state, group) in enumerate(entries):
+        for k, (p, state, group, unmasked) in enumerate(entries):
             step = state['step']
             beta1, beta2 = group.betas
             rect = _compute_rect(group, step)
@@ -787,7 +824,7 @@ class _AdamRunner:
             s[k]['bc1'] = 1 / (1 - beta1 ** step)
             s[k]['bc2'] = 1 / (1 - beta2 ** step)
             s[k]['eps'] = group.eps
-            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 and (unmasked is None or unmasked[id(p)]) else 0
+            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 and unmasked else 0
             s[k]['degenerate'] = 1 if rect == 0.0 else 0
             s[k]['magma_s'] = state['s'].data_ptr() if group.momentum_align else 0
         host = self.upload.host()
@@ -1031,7 +1068,9 @@ class THORN(Optimizer):
         if r is None:
             per_param = lambda k: len(k[3]) == 1 or k[0] == 'release'
             slot, single = key[:3], per_param(key)
-            cap = len(self.param_groups[key[1]]['params']) if single else self._RUNNERS_PER_GROUP
+            # key[1] < 0: the one Adam launch of a whole step, over every non-orthogonalized group
+            cap = (len(self.param_groups[key[1]]['params']) if single and key[1] >= 0
+                   else self._RUNNERS_PER_GROUP)
             same = [k for k in self._runners if k[:3] == slot and per_param(k) == single]
             for k in same[:max(0, len(same) - cap + 1)]:
                 self._check_status(self._runners.pop(k))
@@ -1040,16 +1079,29 @@ class THORN(Optimizer):
         return r
 
     # -- step (thorn.py:1583-1753) ---------------------------------------------------------------
-    def _step_params(self, params: list, group: _Group, gi: int, release: bool = False) -> None:
+    def _step_params(self, params: list, group: _Group, gi: int, release: bool = False,
+                     adam: Optional['_AdamBatch'] = None, home: Optional[torch.cuda.Stream] = None) -> None:
         """release: a gradient-release window of large orthogonalized parameters (_release_flush),
-        one plan on the current stream's shared workspace, never chained."""
+        one plan on the current stream's shared workspace, never chained. adam: the step's batch
+        of plain Adam tensors; a non-orthogonalized group without decouple_md adds its dense
+        tensors to it (and the rest of their step, after the launch) instead of launching.
+        home: the caller's stream when this runs on another one (the Adam side stream, a release
+        stream). New optimizer state and working copies are allocated and initialized there, so
+        the caching allocator ties them to the stream every other one joins back into, and the
+        current stream waits for that initialization."""
         live = []
         sparse = []
+        fresh = False   # state or working copies were made on `home` in this call
         for p in params:
             if p is None or p.grad is None:
                 continue
             self._validate(p, group)
-            self._init_state(p, group)
+            if home is not None and 'step' not in self.state[p]:
+                with torch.cuda.stream(home):
+                    self._init_state(p, group)
+                fresh = True
+            else:
+                self._init_state(p, group)
             g = p.grad
             if g.is_sparse and not group.orthogonalize:
                 if group.decouple_md or g.sparse_dim() != 1:   # thorn.py:1671-1672
@@ -1061,6 +1113,9 @@ class THORN(Optimizer):
                     sparse.append((p, g))
                     continue
             live.append(p)
+        if fresh and home is not None:
+            _wait_for(home)
+            fresh = False
         # Magma masks, one PRNG draw per parameter that steps (thorn.py:1392, 1679, 1702)
         unmasked = None
         if group.momentum_align:
@@ -1078,17 +1133,23 @@ class THORN(Optimizer):
         for p in live:
             if _needs_shadow(p):
                 sh = self._shadows.get(id(p))
-                if sh is None or sh.param.shape != p.shape:
-                    if sh is None:
-                        weakref.finalize(p, self._drop_shadow, id(p))
-                    else:
-                        self._shadow_state.pop(id(sh.param), None)
-                    sh = self._shadows[id(p)] = _Shadow(p)
-                    self._shadow_state[id(sh.param)] = sh.state
-                sh.load(p, self.state[p])
+                with torch.cuda.stream(home) if home is not None else contextlib.nullcontext():
+                    if sh is None or sh.param.shape != p.shape:
+                        if sh is None:
+                            weakref.finalize(p, self._drop_shadow, id(p))
+                        else:
+                            self._shadow_state.pop(id(sh.param), None)
+                        sh = self._shadows[id(p)] = _Shadow(p)
+                        self._shadow_state[id(sh.param)] = sh.state
+                        fresh = True
+                    fresh = sh.reserve(self.state[p]) or fresh
                 shadows[p] = sh
-                if unmasked is not None:
-                    unmasked[id(sh.param)] = unmasked[id(p)]
+        if fresh and home is not None:
+            _wait_for(home)
+        for p, sh in shadows.items():
+            sh.load(p, self.state[p])
+            if unmasked is not None:
+                unmasked[id(sh.param)] = unmasked[id(p)]
         by_dev: dict = {}
         for p in live:
             by_dev.setdefault(p.device, []).append(shadows[p].param if p in shadows else p)
@@ -1111,15 +1172,45 @@ class THORN(Optimizer):
                     runner = self._runner(key, lambda: _OrthoBatches(ps, group, dev, limit, adam=True, shared=shared))
                     runner.run(self, group, unmasked)
                 else:
-                    key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
-                    runner = self._runner(key, lambda: _AdamRunner(ps, dev))
-                    runner.run([(p, self._state_of(p), group) for p in ps], self._update_rate, unmasked)
-        for p, sh in shadows.items():
-            sh.store(p, self.state[p])
-        for p in live:
-            if group.none_grad:
-                p.grad = None
-            self.state[p]['step'] += 1
+                    entries = [(p, self._state_of(p), group,
+                                True if unmasked is None else unmasked[id(p)]) for p in ps]
+                    if adam is not None:
+                        adam.entries.setdefault(dev, []).extend(entries)
+                    else:
+                        self._adam_launch(gi, dev, entries)
+
+        def finish():
+            for p, sh in shadows.items():
+                sh.store(p, self.state[p])
+            for p in live:
+                if group.none_grad:
+                    p.grad = None
+                self.state[p]['step'] += 1
+
+        if adam is not None and not group.orthogonalize and not group.decouple_md:
+            adam.finish.append(finish)
+        else:
+            finish()
+
+    def _adam_launch(self, gi: int, dev: torch.device, entries: list) -> None:
+        """One multi-tensor Adam launch over entries (p, state, group, unmasked); gi < 0: the
+        batch of a whole step."""
+        ps = [e[0] for e in entries]
+        key = ('adam', gi, dev, tuple(id(p) for p in ps), tuple(p.numel() for p in ps))
+        runner = self._runner(key, lambda: _AdamRunner(ps, dev))
+        runner.run(entries, self._update_rate)
+
+    def _adam_flush(self, adam: '_AdamBatch') -> None:
+        """The step's one Adam launch per device, then the rest of those groups' step."""
+        try:
+            for dev, entries in adam.entries.items():
+                with torch.cuda.device(dev):
+                    self._adam_launch(-1, dev, entries)
+        finally:
+            for f in adam.finish:
+                f()
+            adam.entries.clear()
+            adam.finish.clear()
 
     def _drop_shadow(self, key: int) -> None:
         sh = self._shadows.pop(key, None)
@@ -1148,28 +1239,39 @@ class THORN(Optimizer):
             with torch.enable_grad():
                 loss = closure()
         if param is None:
+            # the plain Adam tensors of every non-orthogonalized group: one launch per device,
+            # after the groups before a group that raises (in order: it stops the later ones)
+            adam = _AdamBatch()
             side = self._adam_side_stream()
             if side is None:
-                for gi, group in enumerate(self.param_groups):
-                    self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+                try:
+                    for gi, group in enumerate(self.param_groups):
+                        self._step_params(group['params'], _Group.from_kwargs(**group), gi, adam=adam)
+                finally:
+                    self._adam_flush(adam)
             else:
                 main = torch.cuda.current_stream(side.device)
                 fork, join = self._adam_events[side.device]
                 fork.record(main)   # gradients and state as the caller left them
                 side.wait_event(fork)
                 try:
-                    for gi, group in enumerate(self.param_groups):   # in order: a group that raises
-                        if group['orthogonalize']:                    # stops the later ones
+                    for gi, group in enumerate(self.param_groups):
+                        if group['orthogonalize']:
                             self._step_params(group['params'], _Group.from_kwargs(**group), gi)
                             continue
                         grads = [p.grad for p in group['params'] if p.grad is not None]
                         with torch.cuda.stream(side):
-                            self._step_params(group['params'], _Group.from_kwargs(**group), gi)
+                            self._step_params(group['params'], _Group.from_kwargs(**group), gi, adam=adam,
+                                              home=main)
                         for g in grads:
                             g.record_stream(side)   # the step may drop them; the stream still reads them
                 finally:
-                    join.record(side)
-                    main.wait_event(join)
+                    try:
+                        with torch.cuda.stream(side):
+                            self._adam_flush(adam)
+                    finally:
+                        join.record(side)
+                        main.wait_event(join)
         else:
             group = self._param_to_group[id(param)]
             gi = next(i for i, g in enumerate(self.param_groups) if g is group)
@@ -1246,7 +1348,7 @@ class THORN(Optimizer):
             for p, g in entries:
                 p.grad = g
             with torch.no_grad(), torch.cuda.stream(st):
-                self._step_params(ps, _Group.from_kwargs(**self.param_groups[gi]), gi, release=True)
+                self._step_params(ps, _Group.from_kwargs(**self.param_groups[gi]), gi, release=True, home=src)
         finally:
             for (p, g), held in zip(entries, now):
                 g.record_stream(st)   # released here, still read by the stream's step
