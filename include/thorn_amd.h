@@ -228,6 +228,23 @@ typedef struct ThornAdamSparseStep {
 int thorn_adam_sparse_step(const ThornAdamSparseStep* step, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * thorn::sym_addmm (thorn.py:298-368, the custom op behind every Newton-Schulz product of the
+ * reference): out = beta * C + alpha * (A @ B) for products A @ B and C that are symmetric, f16,
+ * batched: A (nn, m, k), B (nn, k, m), C absent (c_mats = 0), one (m, m) matrix for every product
+ * (c_mats = 1) or (nn, m, m) (c_mats = nn); element strides of each as {batch, row, column} (any
+ * strides; a 2-D C's batch stride is unused). out is contiguous (nn, m, m). As the reference's
+ * Triton kernel (thorn.py:209-280), only the upper block triangle of A @ B (and of C) is read
+ * and computed, with fp32 accumulation and one rounding to f16; the rest is its mirror.
+ * workspace: thorn_sym_addmm_workspace_bytes() bytes of device memory, 256-byte aligned; calls
+ * that share it must not overlap. Limits: nn <= 65535 (thorn.py:332), m * round_up(k, 32) and
+ * m * round_up(m, 8) below 2^30 elements.
+ * ------------------------------------------------------------------------------------------ */
+size_t thorn_sym_addmm_workspace_bytes(int64_t nn, int64_t m, int64_t k, int64_t c_mats);
+int thorn_sym_addmm(const void* a, const int64_t* a_strides, const void* b, const int64_t* b_strides, const void* c,
+                    const int64_t* c_strides, int64_t c_mats, void* out, int64_t nn, int64_t m, int64_t k,
+                    float alpha, float beta, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Optional launch timing (measurement only; no counterpart in the reference). While enabled, the
  * *_step functions record a hipEvent pair around every launch, up to `max_launches` launches;
  * *_timing_read waits for them, writes the summed milliseconds and launch counts per kernel

@@ -287,3 +287,25 @@ def test_status_watch_raises_for_a_set_status_word():
     w.check()
     assert not any(w.pending)
 
+
+
+def test_sym_addmm_op_registration_and_checks():
+    """thorn::sym_addmm is registered as in the reference (thorn.py:298): the fake impl gives the
+    (..., M, M) result shape on meta tensors, the reference's argument checks raise AssertionError,
+    and tensors the library does not take (CPU, float32) are refused rather than computed."""
+    import thorn_amd  # noqa: F401  (registers the op)
+    op = torch.ops.thorn.sym_addmm
+    A = torch.empty(2, 3, 40, 70, device='meta', dtype=torch.float16)
+    B = torch.empty(2, 3, 70, 40, device='meta', dtype=torch.float16)
+    assert op(A, B, None, 1.0, 1.0).shape == (2, 3, 40, 40)
+    assert op(A, B, torch.empty(40, 40, device='meta', dtype=torch.float16), 2.0, 0.5).shape == (2, 3, 40, 40)
+    # the checks run before anything is computed (the fake impl, like the reference's, has none)
+    a, b = torch.zeros(2, 3, 40, 70, dtype=torch.float16), torch.zeros(2, 3, 70, 40, dtype=torch.float16)
+    with pytest.raises(AssertionError, match='B must be'):
+        op(a, a, None, 1.0, 1.0)
+    with pytest.raises(AssertionError, match='C must be'):
+        op(a, b, torch.zeros(2, 40, 41, dtype=torch.float16), 1.0, 1.0)
+    with pytest.raises(AssertionError, match='C must be'):
+        op(a, b, torch.zeros(3, 40, 40, dtype=torch.float16), 1.0, 1.0)
+    with pytest.raises(NotImplementedError, match='float16 CUDA'):
+        op(torch.zeros(4, 6, dtype=torch.float16), torch.zeros(6, 4, dtype=torch.float16), None, 1.0, 1.0)

@@ -1145,3 +1145,50 @@ def test_small_launch_timeout_is_reported():
     r = rel((q.detach().cpu() - p0), (c.detach() - p0))
     assert r <= 2e-2, r
     _log('[gpu]   ok')
+
+
+SYM_CASES = [
+    # (batch dims, M, K, C kind, alpha, beta, B as a transposed view of A)
+    ((), 300, 700, None, 1.0, 1.0, True),        # Gram R = X X^T, two tile rows
+    ((2, 3), 200, 200, 'batched', 0.7, -1.3, False),
+    ((4,), 513, 513, '2d', 1.0, 2.5, False),     # three tile rows, ragged edges
+    ((5,), 64, 33, 'batched', 1.0, 1.0, True),   # K not a multiple of 32
+    ((), 256, 1024, '2d', -0.25, 0.5, True),
+]
+
+
+@pytest.mark.parametrize('case', SYM_CASES, ids=lambda c: f'{c[0]}x{c[1]}x{c[2]}-{c[3]}')
+def test_sym_addmm_against_oracle(case):
+    """torch.ops.thorn.sym_addmm (the library's thorn_sym_addmm) against the oracle's sym_addmm
+    (thorn.py:321-343, eager baddbmm on the device) and against the f64 product, on symmetric
+    products (A = X, B = X^T, or A = B symmetric) with batched, 2-D and absent C:
+    within 1e-3 relative Frobenius (the f16 rounding of the result; both accumulate in fp32), and
+    each result exactly symmetric (its lower block triangle is the mirror)."""
+    import thorn_amd  # noqa: F401
+    batch, M, K, ckind, alpha, beta, gram = case
+    _log(f'[gpu] sym_addmm {case}')
+    g = torch.Generator().manual_seed(M * 7 + K)
+    if gram:
+        X = (torch.randn(*batch, M, K, generator=g) / math.sqrt(K)).half()
+        A, B = X.to(DEV), X.to(DEV).mT          # a strided view, as the Newton-Schulz Gram matrix
+    else:   # A = B = S symmetric (Z = b R + c R R of the Newton-Schulz iteration)
+        assert M == K
+        S = torch.randn(*batch, M, M, generator=g) / math.sqrt(M)
+        S = ((S + S.mT) / 2).half().to(DEV)
+        A, B = S, S
+    C = None
+    if ckind is not None:
+        shape = (M, M) if ckind == '2d' else (*batch, M, M)
+        Cr = torch.randn(*shape, generator=g)
+        C = ((Cr + Cr.mT) / 2).half().to(DEV)
+    out = torch.ops.thorn.sym_addmm(A, B, C, alpha, beta)
+    torch.cuda.synchronize()
+    assert out.shape == (*batch, M, M) and out.dtype == torch.float16 and out.is_contiguous()
+    assert torch.equal(out, out.mT), 'result not exactly symmetric'
+    ref = O.sym_addmm(A, B.contiguous(), C, alpha=alpha, beta=beta)
+    exact = alpha * (A.double() @ B.double())
+    if C is not None:
+        exact = exact + beta * C.double()
+    r_or, r_ex = rel(out, ref), rel(out, exact)
+    _log(f'[gpu]   vs oracle {r_or:.2e}, vs f64 {r_ex:.2e}, oracle vs f64 {rel(ref, exact):.2e}')
+    assert r_or <= 1e-3 and r_ex <= 1e-3, (r_or, r_ex)

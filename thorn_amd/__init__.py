@@ -5,6 +5,7 @@ constructor, parameter groups, state layout and ``step``. The step runs as hand-
 kernels in ``libthorn_amd.so`` (C ABI: include/thorn_amd.h); there is no CPU or PyTorch-op
 fallback.
 """
+from . import ops  # registers the thorn::sym_addmm custom op (thorn.py:298)
 from .optim import THORN, THORNGroup, THORNNonOrthoGroup, THORNOrthoGroup
 
 __version__ = '3.1.1'

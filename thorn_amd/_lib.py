@@ -88,6 +88,9 @@ SIGNATURES = {
     'thorn_adam_fill_table': (_i, [_vp, _vp, _vp, _vp, _vp]),
     'thorn_adam_step': (_i, [_vp, _vp, _vp]),
     'thorn_adam_sparse_step': (_i, [_vp, _vp]),
+    'thorn_sym_addmm_workspace_bytes': (_sz, [ctypes.c_int64] * 4),
+    'thorn_sym_addmm': (_i, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
+                             ctypes.c_int64, _f, _f, _vp, _sz, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
     'thorn_ortho_set_spin_limit': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),

@@ -10,6 +10,7 @@
 //     at the end X <- Q X.
 //   Plain quintic (square matrices, thorn.py:654-658): A = X X^T, B = b A + c A A, X <- a X + B X.
 // The first iterate is u / (||u||_F + 1e-8) rounded to f16 (thorn.py:632-635).
+#pragma once
 #include "ns_gemm.hpp"
 #include "thorn_kernels.hpp"
 

@@ -2,6 +2,7 @@
 // the launch sequence. One translation unit: the kernel sources are included below.
 #include "../../include/thorn_amd.h"
 #include "ns_small.hip"
+#include "sym_addmm.hip"
 #include "update_kernels.hip"
 
 #include <algorithm>
@@ -474,6 +475,34 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(uint4* __restrict__ p, i
         p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 }  // namespace thorn
+
+namespace {
+
+// Workspace layout of thorn_sym_addmm: packed A, packed B^T, packed C, the upper block triangles.
+struct SymAddmmLayout {
+    int64_t kp, mp;
+    size_t a, bt, c, out, bytes;
+};
+
+SymAddmmLayout sym_addmm_layout(int64_t nn, int64_t m, int64_t k, int64_t c_mats) {
+    SymAddmmLayout L;
+    L.kp = std::max<int64_t>(32, cdiv(k, 32) * 32);
+    L.mp = cdiv(m, 8) * 8;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off = align_up(off + bytes, kAlign); return o; };
+    L.a = take(size_t(nn) * m * L.kp * 2);
+    L.bt = take(size_t(nn) * m * L.kp * 2);
+    L.c = take(size_t(c_mats) * m * L.mp * 2);
+    L.out = take(size_t(nn) * m * L.mp * 2);
+    L.bytes = std::max<size_t>(off, kAlign);
+    return L;
+}
+
+unsigned grid_for(int64_t items, int per_block) {
+    return static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(cdiv(items, per_block), 1), 1 << 20));
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -1225,6 +1254,75 @@ int thorn_adam_sparse_step(const ThornAdamSparseStep* S, void* stream) {
     }
     hipLaunchKernelGGL(thorn::adam_sparse_kernel, dim3(static_cast<unsigned>(S->nnz)), dim3(256), 0, st, a);
     return check_launch("adam_sparse_kernel");
+}
+
+size_t thorn_sym_addmm_workspace_bytes(int64_t nn, int64_t m, int64_t k, int64_t c_mats) {
+    if (nn < 0 || m < 0 || k < 0 || c_mats < 0) return 0;
+    return sym_addmm_layout(nn, m, k, c_mats).bytes;
+}
+
+int thorn_sym_addmm(const void* a, const int64_t* as, const void* b, const int64_t* bs, const void* c,
+                    const int64_t* cs, int64_t c_mats, void* out, int64_t nn, int64_t m, int64_t k, float alpha,
+                    float beta, void* workspace, size_t workspace_bytes, void* stream) {
+    if (nn < 0 || m < 0 || k < 0) return fail(THORN_ERR_INVALID, "thorn_sym_addmm: negative size");
+    if (nn > 65535) return fail(THORN_ERR_INVALID, "thorn_sym_addmm: more than 65535 products");
+    if (c_mats != 0 && c_mats != 1 && c_mats != nn)
+        return fail(THORN_ERR_INVALID, "thorn_sym_addmm: c_mats must be 0, 1 or nn");
+    if (nn == 0 || m == 0) return THORN_OK;
+    if (!a || !b || !as || !bs || !out || !workspace || (c_mats > 0 && (!c || !cs)))
+        return fail(THORN_ERR_INVALID, "thorn_sym_addmm: null argument");
+    const SymAddmmLayout L = sym_addmm_layout(nn, m, k, c_mats);
+    if (m * L.kp >= (int64_t(1) << 30) || m * L.mp >= (int64_t(1) << 30))
+        return fail(THORN_ERR_INVALID, "thorn_sym_addmm: a matrix of 2^30 elements or more");
+    if (workspace_bytes < L.bytes || (reinterpret_cast<uintptr_t>(workspace) & (kAlign - 1)) != 0)
+        return fail(THORN_ERR_INVALID, "thorn_sym_addmm: workspace too small or not 256-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    auto* pa = reinterpret_cast<_Float16*>(ws + L.a);
+    auto* pb = reinterpret_cast<_Float16*>(ws + L.bt);
+    auto* pc = reinterpret_cast<_Float16*>(ws + L.c);
+    auto* po = reinterpret_cast<_Float16*>(ws + L.out);
+    const auto* A = static_cast<const _Float16*>(a);
+    const auto* B = static_cast<const _Float16*>(b);
+    const int mi = static_cast<int>(m), kpi = static_cast<int>(L.kp), mpi = static_cast<int>(L.mp);
+    const int ki = static_cast<int>(std::min<int64_t>(k, L.kp));
+    // rows of A (K contiguous); rows of B^T: column n of B, element k at b[k * bs[1] + n * bs[2]]
+    const int64_t ach = nn * m * (L.kp / 8);
+    hipLaunchKernelGGL(thorn::sym_pack_kernel, dim3(grid_for(ach, thorn::kSymPackThreads)),
+                       dim3(thorn::kSymPackThreads), 0, st, A, as[0], as[1], as[2], pa, mi, ki, kpi, ach);
+    if (int rc = check_launch("sym_pack_kernel")) return rc;
+    hipLaunchKernelGGL(thorn::sym_pack_kernel, dim3(grid_for(ach, thorn::kSymPackThreads)),
+                       dim3(thorn::kSymPackThreads), 0, st, B, bs[0], bs[2], bs[1], pb, mi, ki, kpi, ach);
+    if (int rc = check_launch("sym_pack_kernel")) return rc;
+    if (c_mats > 0) {
+        const int64_t cch = c_mats * m * (L.mp / 8);
+        hipLaunchKernelGGL(thorn::sym_pack_kernel, dim3(grid_for(cch, thorn::kSymPackThreads)),
+                           dim3(thorn::kSymPackThreads), 0, st, static_cast<const _Float16*>(c), cs[0], cs[1], cs[2],
+                           pc, mi, mi, mpi, cch);
+        if (int rc = check_launch("sym_pack_kernel")) return rc;
+    }
+    thorn::SymAddmmArgs p;
+    p.a = pa;
+    p.bt = pb;
+    p.c = c_mats > 0 ? pc : nullptr;
+    p.out = po;
+    p.ab_mat = m * L.kp;
+    p.c_mat = c_mats > 1 ? m * L.mp : 0;
+    p.o_mat = m * L.mp;
+    p.m = mi;
+    p.kp = kpi;
+    p.mp = mpi;
+    const int64_t T = cdiv(m, thorn::NsCfg::BM);
+    p.tiles = static_cast<int>(T * (T + 1) / 2);
+    p.alpha = alpha;
+    p.beta = beta;
+    hipLaunchKernelGGL(thorn::sym_addmm_kernel, dim3(static_cast<unsigned>(nn * p.tiles)), dim3(thorn::NsCfg::NT), 0,
+                       st, p);
+    if (int rc = check_launch("sym_addmm_kernel")) return rc;
+    const int64_t total = nn * m * m;
+    hipLaunchKernelGGL(thorn::sym_unpack_kernel, dim3(grid_for(total, thorn::kSymPackThreads)),
+                       dim3(thorn::kSymPackThreads), 0, st, po, mpi, static_cast<_Float16*>(out), mi, total);
+    return check_launch("sym_unpack_kernel");
 }
 
 int thorn_adam_timing_enable(thorn_adam_plan_t plan, int max_launches) {
