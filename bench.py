@@ -204,11 +204,13 @@ def gemm_probe(m: int = 256, k: int = 768, n: int = 256) -> dict:
     return out
 
 
-def cpu_baseline(config: int, budget_s: float = 20.0) -> dict:
+def cpu_baseline(config: int, budget_s: float = 300.0) -> dict:
     """The oracle (the reference's eager algorithm, oracle/thorn_oracle.py) timed on this host.
 
     Per distinct matrix shape of the workload, cheapest first: one oracle step on one matrix of
-    that shape, timed when the f16 GEMM probe predicts it fits the remaining budget ('measured');
+    that shape, timed when the f16 GEMM probe (scaled by the measured-to-predicted ratio of the
+    shapes already timed) predicts it fits the remaining budget ('measured'; config 2's five shapes
+    take about 4 minutes on a 16-thread EPYC share, each reported on stderr as it ends);
     otherwise its time is the shape's schedule flops at the probe's f16 rate, times the ratio of
     measured to probe-predicted time of the measured shapes, or of a 256 x 768 proxy matrix when
     none was measured ('probe-scaled'). Each shape's time is multiplied by its count. The Adam
@@ -243,10 +245,12 @@ def cpu_baseline(config: int, budget_s: float = 20.0) -> dict:
     per_shape, ratios = {}, []
     for sh in sorted(counts, key=ref_flops):
         predicted = ref_flops(sh) / rate
+        scale = sorted(ratios)[len(ratios) // 2] if ratios else 1.0
         left = budget_s - (time.perf_counter() - t_start)
-        if predicted < left:
+        if predicted * scale < left:
             t = one_step(sh)
             ratios.append(t / predicted)
+            print(f'cpu_baseline: {sh[0]}x{sh[1]} one oracle step {t:.1f} s', file=sys.stderr, flush=True)
             per_shape[sh] = {'count': counts[sh], 'gflop': round(ref_flops(sh) / 1e9, 2), 's': round(t, 3),
                              'how': 'measured'}
     if not ratios:   # calibrate on a proxy with the workload's most common aspect ratio
@@ -572,7 +576,8 @@ def main() -> int:
                     help='Magma on every group (a variant of the workload, not the headline line: masked '
                          'matrices skip Newton-Schulz, so the per-launch flops vary and no roofline is given)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--cpu-budget', type=float, default=20.0)
+    ap.add_argument('--cpu-budget', type=float, default=300.0,
+                    help='seconds of oracle time on the host for cpu_baseline (config 2: every shape fits)')
     ap.add_argument('--polar-decomp-batch-size', type=int, default=None,
                     help="elements per Newton-Schulz batch (the optimizer's polar_decomp_batch_size; "
                          "default: the library's, one batch per group)")
@@ -715,7 +720,7 @@ def main() -> int:
     # With chains, the dominant kernel's launches share the chip with one another and with the
     # other chains' memory-bound kernels. The same step as one plan on one stream (a second
     # optimizer over the same parameters, after every figure above is taken) gives its rate alone.
-    one_chain = None
+    one_chain = upd_one = None
     if chains > 1 and not args.momentum_align and not args.no_one_chain:
         keep = thorn_amd.optim.CHAIN_MIN_MATRICES
         thorn_amd.optim.CHAIN_MIN_MATRICES = 1 << 30
@@ -740,6 +745,13 @@ def main() -> int:
                   + sum(su1.get(k, 0.0) for k in dom_kinds)) / args.steps
             n1 = sum(k1.get(k, (0.0, 0))[1] for k in dom_kinds) / args.steps
             a1 = dom_flops / (d1 * 1e-3) / 1e12 if d1 > 0 else 0.0
+            # the update kernels alone: on one stream (no chains, no Adam side stream) nothing
+            # overlaps them, so the union of their intervals is their own time
+            uk = ('pre', 'norm', 'rowstats', 'pnn_apply', 'adam')
+            upd1 = (_union_us([x for k in uk for x in iv1.get(k, [])]) + sum(su1.get(k, 0.0) for k in uk)) / args.steps
+            if upd1 > 0:
+                upd_one = {'ms_per_step': round(upd1, 3), 'gbps': round(cbytes / (upd1 * 1e-3) / 1e9, 1),
+                           'hbm_frac': round(cbytes / (upd1 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
             one_chain = {'gpu_ms_per_step': round(e0.elapsed_time(e1) / args.steps, 3), 'achieved': round(a1, 1),
                          'frac': round(a1 / MFMA_PEAK_TFLOPS, 4), 'launches_per_step': n1,
                          'avg_launch_ms': round(d1 / max(n1, 1), 4)}
@@ -784,7 +796,8 @@ def main() -> int:
                'mfma_frac': round(F / (ns_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4) if ns_ms > 0 else None},
         'update': {'compulsory_bytes': cbytes, 'ms_per_step': round(upd_ms, 3),
                    'gbps': round(cbytes / (upd_ms * 1e-3) / 1e9, 1) if upd_ms > 0 else None,
-                   'hbm_frac': round(cbytes / (upd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if upd_ms > 0 else None},
+                   'hbm_frac': round(cbytes / (upd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if upd_ms > 0 else None,
+                   'one_chain': upd_one},
         'roofline': {'kernel': dom_name, 'bound': 'mfma', 'achieved': round(achieved, 1),
                      'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_PEAK_TFLOPS, 4),
                      'traffic': traffic_from_profile(dom_name), 'flops_per_launch': ns_flops_per_launch,
