@@ -127,8 +127,9 @@ def test_plan_sizes_and_empty_plans():
     p = _lib.OrthoPlan([1024, 3072], [1024, 1024], [0, _lib.MAT_PER_ROW_NORM])
     # two f16 iterates per matrix (the per-row-normalized u' reuses the one the last update does
     # not read); s x s f16 buffers: R and Z for the square matrix, R, Z and two Q for the tall one
-    # (Gram Newton-Schulz); the per-tile partial sums add well under 1%
-    want = 2 * 2 * (1024 * 1024 + 3072 * 1024) + (2 + 4) * 2 * 1024 * 1024
+    # (Gram Newton-Schulz), each its upper block triangle of 256 x 256 blocks (10 of 16 for
+    # s = 1024); the per-tile partial sums add well under 1%
+    want = 2 * 2 * (1024 * 1024 + 3072 * 1024) + (2 + 4) * 2 * (10 * 256 * 256)
     assert want <= p.workspace_bytes <= want * 1.01
     assert p.table_bytes > 0
     e = _lib.OrthoPlan([], [], [])

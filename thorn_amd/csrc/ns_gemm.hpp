@@ -50,11 +50,39 @@ struct NsCfg {
 // a K-major row is either entirely inside the row or entirely past its end; rows * ld * 2 bytes
 // is below 2^30 (checked when a plan is created), so every byte offset of the loop, out-of-range
 // ones included, fits 32 bits.
+// packed: a symmetric s x s matrix (rows = s, ld = its padded width) stored as the panels of its
+// upper block triangle (SqPanel): element (i, j), j >= 256 * (i / 256), of block row b = i / 256
+// at ptr[panel_off(b) + (i - 256 b) * panel_ld(b) + j - 256 b]. Its operand rows start at a
+// multiple of 256 (one block row), read K-major in its own panel from its diagonal block on, and
+// MN-major before it, block by block from the mirror blocks in the panels above.
 struct Operand {
     const _Float16* ptr;
     int64_t ld;
     int32_t rows;
+    int32_t packed;
 };
+
+// The panels of a packed s x s matrix with padded width ld (a multiple of 32): panel b holds block
+// row b, rows [256 b, min(256 b + 256, s)) and columns [256 b, ld), with row length ld - 256 b.
+struct SqPanel {
+    int64_t off;   // elements from the matrix's base
+    int64_t ld;
+    int32_t rows;
+};
+__host__ __device__ __forceinline__ int64_t panel_off(int64_t ld, int64_t b) { return 256 * (b * ld - 128 * b * (b - 1)); }
+__host__ __device__ __forceinline__ SqPanel sq_panel(int s, int64_t ld, int b) {
+    SqPanel p;
+    p.off = panel_off(ld, b);
+    p.ld = ld - 256 * b;
+    p.rows = s - 256 * b < 256 ? s - 256 * b : 256;
+    return p;
+}
+// Elements of a packed s x s matrix (all of its panels).
+__host__ __device__ __forceinline__ int64_t packed_elems(int s, int64_t ld) {
+    const int last = (s + 255) / 256 - 1;
+    const SqPanel p = sq_panel(s, ld, last);
+    return p.off + p.rows * p.ld;
+}
 
 // Byte offset past the end of every operand: the hardware range check of a buffer access turns it
 // into a zero load or a dropped store.
@@ -105,43 +133,65 @@ __device__ __forceinline__ void opaque(half4& v) {
 template <int MN>
 struct OperandDma {
     static constexpr int PER_WAVE = MN * NsCfg::BK * 2 / 1024 / NsCfg::NW;
+    static constexpr int KB = 256 / NsCfg::BK;   // K tiles per 256-block of a packed operand
     u32x4 rsrc;
     uint32_t cur[PER_WAVE];
-    uint32_t kmaj[PER_WAVE];   // K-major offsets of tile 0
+    uint32_t kmaj[PER_WAVE];   // K-major offsets of tile 0 (a packed operand: as if its panel began at tile 0)
     uint32_t step;             // bytes per K tile in the current layout
     int k0, kend;
+    // a packed operand: the matrix's padded width (its rows start at 32 k0); else 0. Held in a
+    // vector register (the same in every lane): it is read once per 256 of K in the MN-major
+    // part only, and the main loop has no scalar register to spare for it.
+    int pwv;
 
-    __device__ __forceinline__ static void offsets(const Operand& op, int mn0, int wave, int lane, bool km,
-                                                   uint32_t (&o)[PER_WAVE]) {
+    // K-major offsets of rows [mn0, mn0 + MN) in a layout with row stride ld from element base
+    // (rows below `rows` valid), minus `back` bytes
+    __device__ __forceinline__ static void km_offsets(int mn0, int rows, int64_t base, int64_t ld, int wave, int lane,
+                                                      uint32_t back, uint32_t (&o)[PER_WAVE]) {
 #pragma unroll
         for (int q = 0; q < PER_WAVE; ++q) {
             const int slot = (wave * PER_WAVE + q) * 64 + lane;
-            if (km) {
-                const int r = slot >> 2, pc = slot & 3;
-                const int c = pc ^ ((r >> 2) & 3);
-                const int row = mn0 + r;
-                o[q] = row < op.rows ? static_cast<uint32_t>((int64_t(row) * op.ld + c * 8) * 2) : kOutOfRange;
-            } else {
-                constexpr int CH = MN / 8;
-                const int k = slot / CH, pc = slot % CH;
-                const int c = pc ^ ((k & 3) << 2);
-                const int col = mn0 + c * 8;
-                o[q] = col < op.ld ? static_cast<uint32_t>((int64_t(k) * op.ld + col) * 2) : kOutOfRange;
-            }
+            const int r = slot >> 2, pc = slot & 3;
+            const int c = pc ^ ((r >> 2) & 3);
+            o[q] = mn0 + r < rows ? static_cast<uint32_t>((base + int64_t(r) * ld + c * 8) * 2) - back : kOutOfRange;
+        }
+    }
+
+    // MN-major offsets of columns [mn0, mn0 + MN) (those below cmax valid) of one K tile's 32 rows,
+    // row stride ld, column c at element base + c - cshift
+    __device__ __forceinline__ static void mn_offsets(int mn0, int cmax, int64_t base, int64_t ld, int cshift, int wave,
+                                                      int lane, uint32_t (&o)[PER_WAVE]) {
+        constexpr int CH = MN / 8;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const int slot = (wave * PER_WAVE + q) * 64 + lane;
+            const int k = slot / CH, pc = slot % CH;
+            const int c = pc ^ ((k & 3) << 2);
+            const int col = mn0 + c * 8;
+            o[q] = col < cmax ? static_cast<uint32_t>((base + int64_t(k) * ld + col - cshift) * 2) : kOutOfRange;
         }
     }
 
     __device__ __forceinline__ void init(const Operand& op, int mn0, int wave, int lane, int k0_, int kend_) {
-        rsrc = sgpr_rsrc(op.ptr, static_cast<uint32_t>(int64_t(op.rows) * op.ld * 2));
-        offsets(op, mn0, wave, lane, true, kmaj);
         k0 = k0_;
         kend = kend_;
+        pwv = op.packed ? static_cast<int>(op.ld) : 0;
+        asm volatile("" : "+v"(pwv));
+        if (op.packed) {   // block row b = mn0 / 256 (k0 = KB b): K-major in panel b from tile k0 on
+            const SqPanel last = sq_panel(op.rows, op.ld, (op.rows + 255) / 256 - 1);
+            rsrc = sgpr_rsrc(op.ptr, static_cast<uint32_t>((last.off + last.rows * last.ld) * 2));
+            const SqPanel pb = sq_panel(op.rows, op.ld, mn0 / 256);
+            km_offsets(0, pb.rows, pb.off, pb.ld, wave, lane, static_cast<uint32_t>(64 * k0), kmaj);
+        } else {
+            rsrc = sgpr_rsrc(op.ptr, static_cast<uint32_t>(int64_t(op.rows) * op.ld * 2));
+            km_offsets(mn0, op.rows, int64_t(mn0) * op.ld, op.ld, wave, lane, 0u, kmaj);
+        }
         if (k0 <= 0) {
 #pragma unroll
             for (int q = 0; q < PER_WAVE; ++q) cur[q] = kmaj[q];
             step = 64;
-        } else {
-            offsets(op, mn0, wave, lane, false, cur);
+        } else {   // MN-major from tile 0: a packed operand's block 0 is in panel 0, row stride ld
+            mn_offsets(mn0, static_cast<int>(op.ld), 0, op.ld, 0, wave, lane, cur);
             step = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(64 * op.ld));
         }
     }
@@ -158,6 +208,26 @@ struct OperandDma {
 #pragma unroll
             for (int q = 0; q < PER_WAVE; ++q) cur[q] = kOutOfRange;
         }
+    }
+
+    // Tile t (a multiple of KB, read MN-major: t < k0) starts block b = t / KB; a packed operand
+    // holds it in panel b. The offsets move there by a constant: having walked the 256 rows of
+    // block b - 1, a lane at k-row k of the tile and column j is at
+    //   P(b-1) + (256 + k) ld(b-1) + j - 256 (b-1),
+    // and P(b) = P(b-1) + 256 ld(b-1), ld(b) = ld(b-1) - 256 put element (256 b + k, j) at
+    //   P(b) + k ld(b) + j - 256 b = that - 256 (k + 1);
+    // the step (32 rows) shrinks by 32 * 256 elements. Lanes out of range stay out of range (they
+    // have moved by at least 8 steps).
+    __device__ __forceinline__ void next_panel() {
+        if (__builtin_amdgcn_readfirstlane(pwv) == 0) return;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+        constexpr int CH = MN / 8;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const int k = ((wave * PER_WAVE + q) * 64 + lane) / CH;
+            cur[q] -= static_cast<uint32_t>(512 * (k + 1));
+        }
+        step -= 2 * 32 * 256;
     }
 
     // Direct load q of this wave for the current tile into LDS at m0 (wave-uniform byte address).
@@ -181,10 +251,13 @@ struct OperandDma {
 // releases them (in place of the loads of tiles past the end, so every memory phase still issues
 // one stage's share of loads per wave). Quarter q of the tile is 32 loads of two 512-byte
 // staging rows each; wave w issues loads 4w .. 4w+3.
+// r0, c0: the matrix row and column at ptr (a panel of a packed matrix; 0 otherwise), rows the
+// valid rows from there.
 struct TileC {
     const _Float16* ptr;
     int64_t ld;
     int32_t rows;
+    int32_t r0, c0;
 };
 
 struct TileCDma {
@@ -414,13 +487,33 @@ __device__ __forceinline__ void mem_phase(int kt, Frags<ROLE>& f, const FragBase
         });
     });
     constexpr int SL = (ST + 3) & 3;
-    // The layouts switch at a few tiles only: a scalar branch around the switch (left to itself,
-    // the compiler made both switches selects in every memory phase).
+    // The layouts switch at a few tiles only (and a packed operand read MN-major changes panel
+    // every 256 of K): a scalar branch around the switch (left to itself, the compiler made both
+    // switches selects in every memory phase).
     const int t = kt + 3;
     if (t == da.k0 || t == db.k0 || t == da.kend) {
         asm volatile("");
         da.begin_tile(t);
         db.begin_tile(t);
+    }
+    // Tiles that start a 256-block (t % 8 == 0) are loaded in the phases with ST == 1 only, and
+    // an operand changes panel only where it is read MN-major.
+    if constexpr (ST == 1 && CQ < 0 && (!AK || !BK)) {
+        static_assert(OperandDma<C::BM>::KB == 8, "blocks of 8 K tiles");
+        if (t % 8 == 0) {
+            if constexpr (!AK) {
+                if (t > 0 && t < da.k0) {
+                    asm volatile("");
+                    da.next_panel();
+                }
+            }
+            if constexpr (!BK) {
+                if (t > 0 && t < db.k0) {
+                    asm volatile("");
+                    db.next_panel();
+                }
+            }
+        }
     }
     // M0 addresses recomputed from the wave's base in every phase (one scalar add each): hoisted
     // out of the loop, the 16 stage addresses took scalar registers that then spilled.
@@ -533,7 +626,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
     const uint32_t m0w = lds0 + wave * C::A_LOADS * 1024;
     TileCDma dc;
-    dc.init(ct, m0, n0, wave, lane);
+    dc.init(ct, m0 - ct.r0, n0 - ct.c0, wave, lane);
     static_for<0, TileCDma::PER_WAVE>([&](auto jc) {   // C rows 192-255 into the 32 KB past the stages
         constexpr int j = decltype(jc)::value;
         dc.issue(j, 3, lds0 + C::LDS_BYTES + wave * TileCDma::PER_WAVE * 1024 + j * 1024);

@@ -21,6 +21,7 @@ __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) 
     op.ptr = xsel == kXA ? M.xa : M.xb;
     op.ld = M.ldx;
     op.rows = M.rows;
+    op.packed = 0;
     return op;
 }
 
@@ -33,11 +34,13 @@ __device__ __forceinline__ _Float16* sym_buf(const OrthoMat& M, int sel) {
     }
 }
 
+// An s x s workspace matrix (R, Z, QA, QB): its upper block triangle in panels (Operand::packed).
 __device__ __forceinline__ Operand square_operand(const _Float16* p, const OrthoMat& M) {
     Operand op;
     op.ptr = p;
     op.ld = M.lds;
     op.rows = M.s;
+    op.packed = 1;
     return op;
 }
 
@@ -184,9 +187,24 @@ __device__ __forceinline__ void store_staged(const char* smem, _Float16* out, in
 // leave as is). DUAL: the tile is also stored to out2 as Q = Z + a I, the diagonal elements
 // rounded from the f16 Z (thorn.py:648, `Z + a * I` in f16): f16(float(Z_ii) + dual_add) with
 // dual_add = f16(a).
+// Where the tile at (m0, n0) of a result goes: its rows [m0, m0 + rows) are rows [0, rows) at ptr,
+// column c at ptr column c - c0, row stride ld (a panel of a packed matrix, or the matrix itself
+// from row m0 with c0 = 0).
+struct TileOut {
+    _Float16* ptr;
+    int64_t ld;
+    int32_t rows, c0;
+};
+
+// The tile (ti, tj), tj >= ti, of a packed s x s workspace matrix at base.
+__device__ __forceinline__ TileOut packed_out(_Float16* base, const OrthoMat& M, int ti) {
+    const SqPanel p = sq_panel(M.s, M.lds, ti);
+    return TileOut{base + p.off, p.ld, p.rows, 256 * ti};
+}
+
 template <class C, int ROLE, bool HAS_C, bool SCALE, bool DUAL = false>
 __device__ __forceinline__ void sym_store(floatx16 (&acc)[RoleMap<ROLE>::N], const TileWork& tw, char* smem,
-                                          _Float16* out, int64_t ld, int n, int m0, int n0, float alpha, float beta,
+                                          const TileOut& o, int m0, int n0, float alpha, float beta,
                                           _Float16* out2 = nullptr, float dual_add = 0.f) {
     using E = EpiH<C>;
     const bool diag = m0 == n0;
@@ -204,18 +222,18 @@ __device__ __forceinline__ void sym_store(floatx16 (&acc)[RoleMap<ROLE>::N], con
         return h;
     });
     lds_barrier();
-    store_staged<C>(smem, out, ld, n, m0, n0);
+    store_staged<C>(smem, o.ptr, o.ld, o.rows, 0, n0 - o.c0);
     if constexpr (DUAL) {
         if (diag) {
             lds_barrier();   // the row pass has read the staging
             const int r = threadIdx.x;   // the diagonal element of row r (threads past 256 have none)
-            if (r < C::BM && m0 + r < n) {
+            if (r < C::BM && r < o.rows) {
                 _Float16& z = *reinterpret_cast<_Float16*>(smem + E::off(r, r));
                 z = static_cast<_Float16>(static_cast<float>(z) + dual_add);
             }
             lds_barrier();
         }
-        store_staged<C>(smem, out2, ld, n, m0, n0);
+        store_staged<C>(smem, out2, o.ld, o.rows, 0, n0 - o.c0);
     }
 }
 
@@ -419,28 +437,30 @@ __device__ __forceinline__ void sym_tile(const OrthoMat& M, const NsOp& op, cons
                                          char* smem) {
     floatx16 acc[RoleMap<ROLE>::N];
     gemm_tile<NsCfg, ROLE>(A, B, m0, n0, KT, a_k0, b_k0, ct, tw, acc, smem);
+    const int ti = m0 / NsCfg::BM;
     if (op.kind == kOpGram) {
+        const TileOut o = packed_out(M.gram, M, ti);
         if (op.first) {
             const float osc = M.scal[kScalX0Scale];
-            sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, M.gram, M.lds, M.s, m0, n0, osc * osc, 0.f);
+            sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, o, m0, n0, osc * osc, 0.f);
         } else {
-            sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, M.gram, M.lds, M.s, m0, n0, 1.f, 0.f);
+            sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, o, m0, n0, 1.f, 0.f);
         }
         return;
     }
-    _Float16* const out = sym_buf(M, op.osel);
+    const TileOut o = packed_out(sym_buf(M, op.osel), M, ti);
     if (op.csel >= 0) {
         if (op.osel2 >= 0)
-            sym_store<NsCfg, ROLE, true, true, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta,
-                                                     sym_buf(M, op.osel2), op.dual_add);
+            sym_store<NsCfg, ROLE, true, true, true>(acc, tw, smem, o, m0, n0, op.alpha, op.beta,
+                                                     packed_out(sym_buf(M, op.osel2), M, ti).ptr, op.dual_add);
         else if (op.alpha != 1.f)
-            sym_store<NsCfg, ROLE, true, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, op.beta);
+            sym_store<NsCfg, ROLE, true, true>(acc, tw, smem, o, m0, n0, op.alpha, op.beta);
         else
-            sym_store<NsCfg, ROLE, true, false>(acc, tw, smem, out, M.lds, M.s, m0, n0, 1.f, op.beta);
+            sym_store<NsCfg, ROLE, true, false>(acc, tw, smem, o, m0, n0, 1.f, op.beta);
     } else if (op.alpha != 1.f) {
-        sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, out, M.lds, M.s, m0, n0, op.alpha, 0.f);
+        sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, o, m0, n0, op.alpha, 0.f);
     } else {
-        sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, out, M.lds, M.s, m0, n0, 1.f, 0.f);
+        sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, o, m0, n0, 1.f, 0.f);
     }
 }
 
@@ -516,10 +536,14 @@ __global__ __launch_bounds__(NsCfg::NT) void ns_phase_kernel(const OrthoMat* __r
     }
     // the epilogue's C term, loaded by gemm_tile into the staging: the input iterate's tile for the
     // plain quintic's X <- a X + B X, Csym for a symmetric product
-    TileC ct{nullptr, 0, 0};
+    TileC ct{nullptr, 0, 0, 0, 0};
     if (op.csel >= 0) {
-        if (op.kind == kOpUpdate) ct = TileC{op.xsel == kXA ? M.xa : M.xb, M.ldx, M.rows};
-        else if (op.kind == kOpSym) ct = TileC{sym_buf(M, op.csel), M.lds, M.s};
+        if (op.kind == kOpUpdate) {
+            ct = TileC{op.xsel == kXA ? M.xa : M.xb, M.ldx, M.rows, 0, 0};
+        } else if (op.kind == kOpSym) {   // tile (ti, tj) of a packed matrix: in panel ti
+            const SqPanel p = sq_panel(M.s, M.lds, ti);
+            ct = TileC{sym_buf(M, op.csel) + p.off, p.ld, p.rows, ti * NsCfg::BM, ti * NsCfg::BM};
+        }
     }
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));

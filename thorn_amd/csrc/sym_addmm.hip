@@ -52,12 +52,13 @@ __device__ __forceinline__ void sym_addmm_tile(const SymAddmmArgs& p, const Oper
                                                char* smem) {
     floatx16 acc[RoleMap<ROLE>::N];
     gemm_tile<NsCfg, ROLE>(A, B, m0, n0, p.kp / NsCfg::BK, 0, 0, ct, tw, acc, smem);
+    const TileOut o{out + int64_t(m0) * p.mp, p.mp, p.m - m0, 0};
     if (ct.ptr) {
-        if (p.alpha != 1.f) sym_store<NsCfg, ROLE, true, true>(acc, tw, smem, out, p.mp, p.m, m0, n0, p.alpha, p.beta);
-        else sym_store<NsCfg, ROLE, true, false>(acc, tw, smem, out, p.mp, p.m, m0, n0, 1.f, p.beta);
+        if (p.alpha != 1.f) sym_store<NsCfg, ROLE, true, true>(acc, tw, smem, o, m0, n0, p.alpha, p.beta);
+        else sym_store<NsCfg, ROLE, true, false>(acc, tw, smem, o, m0, n0, 1.f, p.beta);
     } else {
-        if (p.alpha != 1.f) sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, out, p.mp, p.m, m0, n0, p.alpha, 0.f);
-        else sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, out, p.mp, p.m, m0, n0, 1.f, 0.f);
+        if (p.alpha != 1.f) sym_store<NsCfg, ROLE, false, true>(acc, tw, smem, o, m0, n0, p.alpha, 0.f);
+        else sym_store<NsCfg, ROLE, false, false>(acc, tw, smem, o, m0, n0, 1.f, 0.f);
     }
 }
 
@@ -72,7 +73,8 @@ __global__ __launch_bounds__(NsCfg::NT) void sym_addmm_kernel(SymAddmmArgs p) {
     B.ptr = p.bt + b * p.ab_mat;
     A.ld = B.ld = p.kp;
     A.rows = B.rows = p.m;
-    const TileC ct{p.c ? p.c + b * p.c_mat : nullptr, p.mp, p.m};
+    A.packed = B.packed = 0;
+    const TileC ct{p.c ? p.c + b * p.c_mat : nullptr, p.mp, p.m, 0, 0};
     _Float16* const out = p.out + b * p.o_mat;
     const int m0 = ti * NsCfg::BM, n0 = tj * NsCfg::BN;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));

@@ -597,7 +597,8 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
                      : 0;
         // an Adam-group tensor runs no Newton-Schulz: no iterate or s x s buffers
         const size_t xbytes = L.adam ? 0 : size_t(L.rows) * L.ldx * 2;
-        const size_t sbytes = L.adam || L.is_small ? 0 : size_t(L.s) * L.lds * 2;
+        // R, Z, QA, QB: the upper block triangle in panels (SqPanel)
+        const size_t sbytes = L.adam || L.is_small ? 0 : size_t(thorn::packed_elems(L.s, L.lds)) * 2;
         const bool square = L.rows == L.cols;   // the plain quintic needs no Q (thorn.py:654-658)
         if (L.is_small) {
             const size_t sp = align_up(L.s, 32), lp = align_up(L.l, 32);
