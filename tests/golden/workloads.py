@@ -169,6 +169,30 @@ def md_adam_small(steps: int = 20):
     return params, groups, lambda s, i, prm: grads[(s, i)]
 
 
+def md_adam_axes(steps: int = 12):
+    """decouple_md on Adam groups whose norm runs over dim -2, the columns of each trailing
+    matrix (norm_axis = -2, and 0 on a 2-D tensor; thorn.py:594-595, 1717), with row/column gains
+    and with a scalar gain, beside a per-row (-1) group. No golden vectors: checked against the
+    oracle, whose norm is torch's over the same dims."""
+    gen = torch.Generator().manual_seed(37)
+    cols_split = [(48, 20), (2, 10, 14)]
+    cols_scalar = [(24, 36)]
+    rows = [(18, 30)]
+    sets = [cols_split, cols_scalar, rows]
+    shapes = [sh for st in sets for sh in st]
+    params = [_leaf(torch.randn(sh, generator=gen) * 0.02) for sh in shapes]
+    grads = _grads(gen, shapes, steps, 1e-3, outlier_rows=0.05)
+    groups = [
+        {'orthogonalize': False, 'params': params[0:2], 'lr': 2e-3, 'weight_decay': 0.1, 'decouple_md': True,
+         'norm_axis': -2},
+        {'orthogonalize': False, 'params': params[2:3], 'lr': 2e-3, 'weight_decay': 0.0, 'decouple_md': True,
+         'split_gain': False, 'norm_axis': 0, 'eps': 1e-8},
+        {'orthogonalize': False, 'params': params[3:4], 'lr': 1e-3, 'weight_decay': 0.1, 'decouple_md': True,
+         'norm_axis': -1},
+    ]
+    return params, groups, lambda s, i, prm: grads[(s, i)]
+
+
 class _MdNet(torch.nn.Module):
     def __init__(self, gen):
         super().__init__()

@@ -56,8 +56,8 @@ def test_invalid_hyperparameters_raise_value_error_at_step(bad, msg):
 
 
 def test_unsupported_features_raise_not_implemented():
-    """decouple_md runs on Adam groups too; a norm axis other than the trailing matrix or the last
-    dim is refused before anything is computed."""
+    """decouple_md runs on Adam groups too; a norm axis across the leading dims (not the trailing
+    matrix, its rows or its columns) is refused before anything is computed."""
     p = nn.Parameter(torch.zeros(2, 3, 3))
     opt = thorn_amd.THORN([{'orthogonalize': False, 'params': [p], 'lr': 1e-3, 'decouple_md': True,
                             'norm_axis': 0}])
@@ -111,13 +111,16 @@ def test_polar_decomp_batches():
     assert thorn_amd.THORN.polar_decomp_batch_size == 2 * 1024 ** 3
 
 
-def test_fp16_and_fp64_parameters_are_refused():
-    """bf16 and fp32 parameters step; fp16 and fp64 raise before anything is computed."""
-    for dt in (torch.float16, torch.float64):
-        p = nn.Parameter(torch.zeros(3, 3, dtype=dt))
+def test_unsupported_dtypes_are_refused():
+    """fp32, bf16, fp16 and fp64 parameters step (the last three through fp32 working copies);
+    other dtypes (complex, fp8) raise before anything is computed."""
+    from thorn_amd import optim as OPT
+    assert set(OPT._DTYPES) == {torch.float32, torch.bfloat16, torch.float16, torch.float64}
+    for dt in (torch.complex64, torch.float8_e4m3fn):
+        p = nn.Parameter(torch.zeros(3, 3, dtype=dt), requires_grad=False)
         opt = thorn_amd.THORN([{'orthogonalize': True, 'params': [p], 'lr': 1e-3}])
         p.grad = torch.zeros(3, 3, dtype=dt)
-        with pytest.raises(NotImplementedError, match='fp32 and bf16'):
+        with pytest.raises(NotImplementedError, match='fp32, bf16, fp16 and fp64'):
             opt.step()
 
 

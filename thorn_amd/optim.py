@@ -224,16 +224,18 @@ def _magma_unmasked(state: dict) -> bool:
     return draw % 2 == 0
 
 
-# Storage types of parameters, gradients and state. Others than contiguous fp32 step through fp32
-# working copies (_Shadow). fp16 is not among them: the reference's fp16 Adam underflows g^2
-# (1e-6 at a 1e-3 gradient) where fp32 arithmetic does not, so its trajectory is not one an fp32
-# computation can follow.
-_DTYPES = (torch.float32, torch.bfloat16)
+# Storage types of parameters, gradients and state (the reference is generic over them: its state
+# takes p.dtype, thorn.py:1591-1634). Others than contiguous fp32 step through fp32 working copies
+# (_Shadow) in fp32 arithmetic: bf16 and fp16 round the results to their dtype once per step (the
+# reference rounds after each of its ops, and its fp16 Adam underflows g^2, 1e-6 at a 1e-3
+# gradient, which fp32 does not); fp64 adds each step's fp32 change to its fp64 values, which
+# keep their low-order bits.
+_DTYPES = (torch.float32, torch.bfloat16, torch.float16, torch.float64)
 
 
 def _check_tensor(t: torch.Tensor, what: str) -> None:
     if t.dtype not in _DTYPES:
-        raise NotImplementedError(f'THORN on MI355X supports fp32 and bf16 tensors; {what} is {t.dtype}')
+        raise NotImplementedError(f'THORN on MI355X supports fp32, bf16, fp16 and fp64 tensors; {what} is {t.dtype}')
     if not t.is_cuda:
         raise RuntimeError(f'THORN on MI355X needs device tensors; {what} is on {t.device}')
 
@@ -252,40 +254,81 @@ class _Shadow:
     and its state are rounded to their own dtype once per step (the reference rounds after every
     torch op, thorn.py:1381, 1404, 702), and per-row normalization uses the dtype's eps (:720)."""
 
-    def __init__(self, p: torch.Tensor):
-        self.param = torch.nn.Parameter(torch.empty(p.shape, dtype=torch.float32, device=p.device),
+    # transposed: the working copy is p's trailing matrices transposed (a decouple_md norm over
+    # dim -2 becomes one over rows); state tensors are transposed with it and the row and column
+    # gains (with their moments) swap roles
+    _SWAP = {'row_gain': 'col_gain', 'col_gain': 'row_gain', 'row_gain_moment': 'col_gain_moment',
+             'col_gain_moment': 'row_gain_moment', 'row_gain_variance': 'col_gain_variance',
+             'col_gain_variance': 'row_gain_variance'}
+
+    def __init__(self, p: torch.Tensor, transposed: bool = False):
+        self.transposed = transposed
+        shape = p.mT.shape if transposed else p.shape
+        self.param = torch.nn.Parameter(torch.empty(shape, dtype=torch.float32, device=p.device),
                                         requires_grad=False)
         self.param._thorn_dtype = p.dtype
-        self.grad = torch.empty(p.shape, dtype=torch.float32, device=p.device)
+        if transposed:
+            self.param._thorn_md_mode = 'rows'
+        self.grad = torch.empty(shape, dtype=torch.float32, device=p.device)
         self.state: dict = {}
+        # fp64: the fp32 values as loaded, so that store() adds the step's change to the fp64 ones
+        self.delta = p.dtype == torch.float64
+        self.p0 = torch.empty_like(self.param.data) if self.delta else None
+        self.state0: dict = {}
+
+    def _key(self, k: str) -> str:
+        return self._SWAP.get(k, k) if self.transposed else k
+
+    def _view(self, t: torch.Tensor) -> torch.Tensor:
+        """t in the working copy's orientation (a view)."""
+        return t.mT if self.transposed and t.ndim >= 2 else t
 
     def reserve(self, state: dict) -> bool:
         """Allocates the fp32 copies of state tensors that have none (or another shape); True if
         it allocated any."""
         fresh = False
         for k, v in state.items():
-            if torch.is_tensor(v) and (k not in self.state or self.state[k].shape != v.shape):
-                self.state[k] = torch.empty(v.shape, dtype=torch.float32, device=v.device)
+            if not torch.is_tensor(v):
+                continue
+            wk, shape = self._key(k), self._view(v).shape
+            if wk not in self.state or self.state[wk].shape != shape:
+                self.state[wk] = torch.empty(shape, dtype=torch.float32, device=v.device)
+                if self.delta:
+                    self.state0[wk] = torch.empty_like(self.state[wk])
                 fresh = True
         return fresh
 
     def load(self, p: torch.Tensor, state: dict) -> None:
         """Copies the parameter, its gradient and its state in (reserve() first)."""
-        self.param.data.copy_(p.detach())
-        self.grad.copy_(p.grad)
+        self.param.data.copy_(self._view(p.detach()))
+        self.grad.copy_(self._view(p.grad))
         self.param.grad = self.grad
+        if self.delta:
+            self.p0.copy_(self.param.data)
         for k, v in state.items():
+            wk = self._key(k)
             if torch.is_tensor(v):
-                self.state[k].copy_(v)
+                self.state[wk].copy_(self._view(v))
+                if self.delta:
+                    self.state0[wk].copy_(self.state[wk])
             else:
-                self.state[k] = v
+                self.state[wk] = v
 
     def store(self, p: torch.Tensor, state: dict) -> None:
+        """Writes the step back: rounded to the dtype, or (fp64) as v + (new - loaded)."""
         with torch.no_grad():
-            p.copy_(self.param.data)
+            pv = self._view(p)
+            if self.delta:
+                pv.add_(self.param.data).sub_(self.p0)
+            else:
+                pv.copy_(self.param.data)
         for k, v in state.items():
             if torch.is_tensor(v):
-                v.copy_(self.state[k])
+                wk, vv = self._key(k), self._view(v)
+                if self.delta:
+                    vv.add_(self.state[wk]).sub_(self.state0[wk])
+                else:
+                    vv.copy_(self.state[wk])
 
 
 def _matrix_view(p: torch.Tensor) -> tuple:
@@ -296,19 +339,33 @@ def _matrix_view(p: torch.Tensor) -> tuple:
     return 1, max(1, p.numel()), 1
 
 
-def _md_norm_rows(p: torch.Tensor, group: _Group) -> bool:
+def _md_norm_mode(p: torch.Tensor, group: _Group) -> str:
     """decouple_md renormalization axis of a non-orthogonalized tensor (thorn.py:594-595, 1717):
-    False for a norm over each trailing matrix (the default; a vector's whole length), True for a
-    norm over each row (norm_axis = -1 on ndim >= 2). Other axes are not implemented."""
+    'matrix' for a norm over each trailing matrix (the default; a vector's whole length), 'rows'
+    for one over each row (norm_axis = -1 on ndim >= 2), 'cols' for one over each column of the
+    trailing matrices (norm_axis = -2), which steps through a transposed working copy (_Shadow)
+    with the roles of its row and column gains swapped. Norms across the leading dims (matrices)
+    are not implemented. A working copy reports its own mode (_thorn_md_mode)."""
+    mode = getattr(p, '_thorn_md_mode', None)
+    if mode is not None:
+        return mode
     ax = group.norm_axis_(p)
     nd = max(p.ndim, 1)
     dims = sorted({(a % nd) for a in (ax if isinstance(ax, (tuple, list)) else (ax,))})
     if p.ndim <= 1 or dims == [nd - 2, nd - 1]:
-        return False
+        return 'matrix'
     if dims == [nd - 1]:
-        return True
+        return 'rows'
+    if dims == [nd - 2]:
+        return 'cols'
     raise NotImplementedError(f'decouple_md with norm_axis={ax!r} on a {p.ndim}-d tensor is not implemented '
-                              'on the MI355X path (supported: the last two dims, or the last dim)')
+                              'on the MI355X path (supported: the last two dims, the last dim, or dim -2)')
+
+
+def _md_norm_rows(p: torch.Tensor, group: _Group) -> bool:
+    """The library's per-row renormalization (THORN_MAT_NORM_ROWS) for a tensor of a
+    non-orthogonalized decouple_md group (its working copy's rows for a norm over columns)."""
+    return _md_norm_mode(p, group) != 'matrix'
 
 
 def _plan_shapes(params: list, group: _Group, adam: bool, with_owner: bool = False):
@@ -956,12 +1013,7 @@ class THORN(Optimizer):
         if g.shape != p.shape:
             raise AssertionError(f'gradient shape {tuple(g.shape)} != parameter shape {tuple(p.shape)}')
         _check_tensor(p, 'parameter')
-        if g.is_sparse:
-            if g.dtype != torch.float32 or not g.is_cuda or p.dtype != torch.float32 or not p.is_contiguous():
-                raise NotImplementedError('THORN on MI355X needs a contiguous fp32 parameter and gradient '
-                                          'for a sparse gradient')
-        else:
-            _check_tensor(g, 'gradient')
+        _check_tensor(g, 'gradient')
         if g.device != p.device:
             raise RuntimeError('gradient and parameter are on different devices')
 
@@ -978,13 +1030,27 @@ class THORN(Optimizer):
         row_len = p.numel() // rows if rows else 0
         idx = g.indices()[0].contiguous()
         vals = g.values().reshape(idx.numel(), row_len).contiguous()
+        # a parameter (or state) that is not contiguous fp32 steps through fp32 copies of the
+        # gradient's rows (the rows 0 .. nnz-1 of a compact parameter), written back rounded to its
+        # dtype (fp64: as its value plus the fp32 change); the other rows are not touched
+        direct = all(t.dtype == torch.float32 and t.is_contiguous()
+                     for t in (p, state['moment'], state['variance'], vals))
+        if direct:
+            tp, tm, tv, trows, tvals = p, state['moment'], state['variance'], idx, vals
+        else:
+            def rows_of(t):
+                return t.detach().index_select(0, idx).reshape(idx.numel(), row_len).float()
+            tp, tm, tv = rows_of(p), rows_of(state['moment']), rows_of(state['variance'])
+            before = [t.clone() for t in (tp, tm, tv)] if p.dtype == torch.float64 else None
+            trows = torch.arange(idx.numel(), device=idx.device, dtype=idx.dtype)
+            tvals = vals.float()
         rec = np.zeros(1, dtype=_lib.ADAM_SPARSE_STEP)
-        rec['p'] = p.data_ptr()
-        rec['m'] = state['moment'].data_ptr()
-        rec['v'] = state['variance'].data_ptr()
-        rec['g_values'] = vals.data_ptr()
-        rec['g_rows'] = idx.data_ptr()
-        rec['rows'] = rows
+        rec['p'] = tp.data_ptr()
+        rec['m'] = tm.data_ptr()
+        rec['v'] = tv.data_ptr()
+        rec['g_values'] = tvals.data_ptr()
+        rec['g_rows'] = trows.data_ptr()
+        rec['rows'] = tp.shape[0]
         rec['row_len'] = row_len
         rec['nnz'] = idx.numel()
         rec['lr'] = group.lr * rect * 1.0
@@ -997,11 +1063,22 @@ class THORN(Optimizer):
         rec['eps'] = group.eps
         rec['apply'] = 1 if (step + 1) % self._update_rate == 0 and unmasked else 0
         rec['degenerate'] = 1 if rect == 0.0 else 0
+        s32 = None
         if group.momentum_align:
-            rec['magma_s'] = state['s'].data_ptr()
+            s32 = state['s'] if state['s'].dtype == torch.float32 else state['s'].float()
+            rec['magma_s'] = s32.data_ptr()
             rec['magma_work'] = self._magma_work(p.device).data_ptr()
         with torch.cuda.device(p.device):
             _lib.adam_sparse_step(rec, torch.cuda.current_stream(p.device).cuda_stream)
+        if s32 is not None and s32 is not state['s']:
+            state['s'].copy_(s32)
+        if not direct:
+            with torch.no_grad():
+                for i, (dst, new) in enumerate(((p, tp), (state['moment'], tm), (state['variance'], tv))):
+                    shape = (idx.numel(), *dst.shape[1:])
+                    if before is not None:   # fp64: the row values plus the fp32 change
+                        new = dst.index_select(0, idx) + (new - before[i]).double().reshape(shape)
+                    dst.index_copy_(0, idx, new.reshape(shape).to(dst.dtype))
 
     def _magma_work(self, dev: torch.device) -> torch.Tensor:
         """Device scratch of the sparse Magma statistics (one per device; steps on one stream)."""
@@ -1131,15 +1208,17 @@ class THORN(Optimizer):
         # parameters that are not contiguous fp32 step through their fp32 working copies
         shadows = {}
         for p in live:
-            if _needs_shadow(p):
+            # a decouple_md norm over dim -2 of an Adam group's tensor: a transposed working copy
+            tr = group.decouple_md and not group.orthogonalize and _md_norm_mode(p, group) == 'cols'
+            if tr or _needs_shadow(p):
                 sh = self._shadows.get(id(p))
                 with torch.cuda.stream(home) if home is not None else contextlib.nullcontext():
-                    if sh is None or sh.param.shape != p.shape:
+                    if sh is None or sh.transposed != tr or sh.param.shape != (p.mT.shape if tr else p.shape):
                         if sh is None:
                             weakref.finalize(p, self._drop_shadow, id(p))
                         else:
                             self._shadow_state.pop(id(sh.param), None)
-                        sh = self._shadows[id(p)] = _Shadow(p)
+                        sh = self._shadows[id(p)] = _Shadow(p, transposed=tr)
                         self._shadow_state[id(sh.param)] = sh.state
                         fresh = True
                     fresh = sh.reserve(self.state[p]) or fresh
