@@ -118,12 +118,13 @@ void thorn_ortho_plan_destroy(thorn_ortho_plan_t plan);
  * in f16, prescaled by a power of two the previous step stored there (rebuilt exactly when the
  * gradient scale moved by more than 16x); the first step on a workspace takes the exact path. */
 size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
-/* The int32 at this byte offset of the workspace is nonzero after a step in which a cluster of
+/* The int32 at this byte offset of the workspace becomes nonzero in a step in which a cluster of
  * workgroups of the small-matrix Newton-Schulz launch did not all become resident (its bounded
- * barrier wait expired; that step's small-matrix updates are then not valid). Each step clears it
- * before its Newton-Schulz launches, so it reports the last step only; a caller reads it once the
- * step is done (the thorn_amd package copies it to pinned memory behind every step and raises
- * RuntimeError at the next step when it was set). */
+ * barrier wait expired; that step's small-matrix updates are then not valid), and stays so until
+ * the caller clears it (a zero-filled workspace starts clear; the library never clears it, so a
+ * caller may read it every few steps). The thorn_amd package reads it every 16 steps that ran
+ * the launch, and at THORN.check_status(), into pinned memory, raises RuntimeError when it is set
+ * and clears it. */
 #define THORN_WS_STATUS_OFFSET 256
 /* Polls (a 64-cycle sleep each) of the small-matrix launch's bounded cluster barrier before it
  * gives up and sets the status word; default 2^24. No counterpart in the reference: a test hook

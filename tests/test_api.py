@@ -251,9 +251,10 @@ def test_adam_beside_chains_decision():
 
 
 def test_status_watch_raises_for_a_set_status_word():
-    """The small-matrix launch's status word, copied behind each step into a ring of pinned slots:
-    a completed slot holding a nonzero word raises RuntimeError at the next check (not before its
-    event completes, unless the check waits), and the ring checks its oldest slot before reusing it."""
+    """The small-matrix launch's status word, read into a ring of pinned slots: a completed slot
+    holding a nonzero word raises RuntimeError at the next check (not before its event completes,
+    unless the check waits), once, and clears the word on the device; reads happen every PERIOD
+    steps that ran the launch."""
     from thorn_amd import optim as OPT
 
     class Ev:
@@ -268,11 +269,18 @@ def test_status_watch_raises_for_a_set_status_word():
             self.waited += 1
             self.done = True
 
+    class Runner:
+        workspace = torch.zeros(1024, dtype=torch.uint8)
+
     w = OPT._StatusWatch.__new__(OPT._StatusWatch)
+    w.runner = Runner()
     w.host = torch.zeros(w.SLOTS, dtype=torch.int32)
     w.events = [Ev() for _ in range(w.SLOTS)]
     w.pending = [False] * w.SLOTS
     w.next = 0
+    w.unread = 0
+    w.stream = None
+    Runner.workspace[256:260].view(torch.int32).fill_(1)   # the device word, set by a timeout
     # slots 0 and 1 recorded; slot 1's step timed out and has not completed yet
     w.pending[0] = w.pending[1] = True
     w.next = 2
@@ -283,7 +291,14 @@ def test_status_watch_raises_for_a_set_status_word():
     with pytest.raises(RuntimeError, match='timed out'):
         w.check(wait=True)
     assert w.pending == [False] * w.SLOTS and int(w.host[1]) == 0
+    assert int(Runner.workspace[256:260].view(torch.int32)) == 0   # cleared
     w.check(wait=True)               # reported once
+    # reads every PERIOD steps
+    reads = []
+    w.record = lambda: reads.append(w.unread) or setattr(w, 'unread', 0)
+    for _ in range(2 * w.PERIOD + 3):
+        w.stepped(None)
+    assert reads == [w.PERIOD, w.PERIOD] and w.unread == 3
     # a clean word never raises, completed or waited for
     w.pending[3] = True
     w.events[3].done = True

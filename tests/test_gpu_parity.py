@@ -1112,8 +1112,8 @@ def test_small_launch_timeout_is_reported():
     """The small-matrix launch's cluster barrier waits a bounded number of polls. A spin limit of 0
     set from the host makes every wait that would block give up at once (the kernels still run to
     their end, reading and writing the same buffers): the step's status word is set, and
-    check_status() raises RuntimeError. The next step clears the word; with the default limit back
-    the steps report nothing, and a fresh optimizer's update matches the oracle."""
+    check_status() raises RuntimeError and clears it; with the default limit back the steps report
+    nothing, and a fresh optimizer's update matches the oracle."""
     _log('[gpu] small-matrix launch: barrier timeout forced from the host')
     thorn_amd = _thorn()
     g = torch.Generator().manual_seed(7)

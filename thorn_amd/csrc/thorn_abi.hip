@@ -590,7 +590,11 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         // small matrices run their whole Newton-Schulz in ns_small_kernel and are applied by
         // ortho_pnn_apply_kernel (u' in xa); they always take the exact first iterate
         L.is_small = !L.adam && L.s <= thorn::kSmallMaxS && int64_t(L.rows) * L.cols < kPrescaleMinElems;
-        L.cluster = L.s <= 128 ? 1 : 4;
+        // workgroups of its small-matrix cluster: one for s <= 128 (its s x s products are one
+        // 128 x 128 super-tile, so more would only add barriers); above, one per super-tile of the
+        // largest output (s x s, or the s x l update), at least 4 and at most 16, so that the
+        // update takes one round
+        L.cluster = L.s <= 128 ? 1 : static_cast<int32_t>(std::min<int64_t>(16, std::max<int64_t>(4, cdiv(L.s, 128) * cdiv(L.l, 128))));
         L.rowsq_tiles = static_cast<int32_t>(L.is_small ? cdiv(L.cols, 32) : L.g3_tiles_n);
         L.n_psq = md ? static_cast<int32_t>(pnn || L.adam || L.is_small ? mom_tiles
                                                                          : int64_t(L.g3_tiles_m) * L.g3_tiles_n)
@@ -912,7 +916,7 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
     THORN_LAUNCH(THORN_KIND_NORM, "ortho_norm_kernel", thorn::ortho_norm_kernel,
-                 dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n, status);
+                 dim3(n, plan->md.n > 0 ? thorn::kNormSlices : 1), dim3(256), 0, st, mats, n);
     if (plan->adam_live.n > 0) {   // the Adam step of the decouple_md tensors of an Adam group
         const thorn::TaskList ad = task_list(dev, plan->adam_live);
         THORN_LAUNCH(THORN_KIND_ADAM, "ortho_adam_apply_kernel", thorn::ortho_adam_apply_kernel, dim3(ad.total),

@@ -243,14 +243,10 @@ __device__ __forceinline__ void norm_sigma_magma(const OrthoMat* __restrict__ ma
     }
 }
 
-// status: the workspace's status word (THORN_WS_STATUS_OFFSET), cleared here so that it reports
-// this step's small-matrix launch only.
-__global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats,
-                                                         int* __restrict__ status) {
+__global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restrict__ mats, int n_mats) {
     __shared__ float scratch[12];
     const OrthoMat& M = mats[blockIdx.x];
     const int slice = blockIdx.y;
-    if (blockIdx.x == 0 && slice == 0 && threadIdx.x == 0) *status = 0;
     if (slice == 0) norm_sigma_magma(mats, n_mats, M, scratch);
     // the small-matrix launch's cluster barrier starts from count 0 (its generation may be any
     // value): the workspace may hold another plan's data

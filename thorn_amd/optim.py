@@ -405,6 +405,11 @@ class _TableUpload:
         self.bufs = [torch.empty(max(1, nbytes), dtype=torch.uint8, pin_memory=True) for _ in range(self.RING)]
         self.events: list = [None] * self.RING
         self.i = 0
+        # what the device table holds (its last upload): a table equal to it is not copied again
+        # (the kernels only read the table; with fixed gradient buffers and hyperparameters a
+        # plan's table repeats from step to step)
+        self.last = torch.empty(max(1, nbytes), dtype=torch.uint8)
+        self.last_dst = None
 
     def host(self) -> torch.Tensor:
         """The next buffer, once its last copy has run (a query first: a blocking wait on an event
@@ -415,9 +420,14 @@ class _TableUpload:
         return self.bufs[self.i]
 
     def upload(self, dst: torch.Tensor) -> None:
-        """Copies the buffer of host() into dst on the current stream."""
+        """Copies the buffer of host() into dst on the current stream (unless dst holds it)."""
         i = self.i
-        dst[:self.nbytes].copy_(self.bufs[i][:self.nbytes], non_blocking=True)
+        src = self.bufs[i][:self.nbytes]
+        key = (dst.data_ptr(), dst.device)
+        if self.last_dst != key or not torch.equal(src, self.last[:self.nbytes]):
+            dst[:self.nbytes].copy_(src, non_blocking=True)
+            self.last[:self.nbytes].copy_(src)
+            self.last_dst = key
         if self.events[i] is None:
             self.events[i] = torch.cuda.Event()
         self.events[i].record()
@@ -446,31 +456,52 @@ class _SharedWorkspace:
 
 
 class _StatusWatch:
-    """The workspace status word (set when a cluster of the small-matrix launch timed out waiting
-    for its workgroups to become resident) read behind every step that ran that launch: copied into
-    a ring of pinned slots with an event each. Completed slots are checked at the start of the next
-    step, so the host never waits for the GPU unless all slots are still in flight."""
+    """The workspace status word of a runner: set by a cluster of the small-matrix launch that
+    timed out waiting for its workgroups to become resident, and kept set until read here (the
+    library never clears it). Every PERIOD steps that ran the launch it is copied into a ring of
+    pinned slots with an event each; completed slots are checked at the start of each step, so
+    the host never waits for the device unless all slots are still in flight, and a timeout is
+    reported within PERIOD steps. check(wait=True) (THORN.check_status) reads it at once. A set
+    word raises RuntimeError and is cleared on the device."""
     SLOTS = 4
+    PERIOD = 16
 
-    def __init__(self):
+    def __init__(self, runner: '_OrthoRunner'):
+        self.runner = runner
         self.host = torch.zeros(self.SLOTS, dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(self.SLOTS)]
         self.pending = [False] * self.SLOTS
         self.next = 0
+        self.unread = 0          # steps since the last read
+        self.stream = None       # the stream of the last step
 
-    def record(self, workspace: torch.Tensor, stream: torch.cuda.Stream) -> None:
+    def _word(self) -> torch.Tensor:
+        ws = self.runner.workspace
+        return ws[_lib.WS_STATUS_OFFSET:_lib.WS_STATUS_OFFSET + 4].view(torch.int32)
+
+    def stepped(self, stream: torch.cuda.Stream) -> None:
+        """After a step that ran the small-matrix launch on stream."""
+        self.stream = stream
+        self.unread += 1
+        if self.unread >= self.PERIOD:
+            self.record()
+
+    def record(self) -> None:
         i = self.next
         if self.pending[i]:
             self._check(i)
-        word = workspace[_lib.WS_STATUS_OFFSET:_lib.WS_STATUS_OFFSET + 4].view(torch.int32)
-        with torch.cuda.stream(stream):
-            self.host[i:i + 1].copy_(word, non_blocking=True)
-        self.events[i].record(stream)
+        with torch.cuda.stream(self.stream):
+            self.host[i:i + 1].copy_(self._word(), non_blocking=True)
+        self.events[i].record(self.stream)
         self.pending[i] = True
         self.next = (i + 1) % self.SLOTS
+        self.unread = 0
 
     def check(self, wait: bool = False) -> None:
-        """Raises RuntimeError if a completed step (every recorded step with wait=True) set the word."""
+        """Raises RuntimeError if a completed read (with wait=True: a read of every step so far)
+        found the word set."""
+        if wait and self.unread:
+            self.record()
         for k in range(self.SLOTS):
             i = (self.next + k) % self.SLOTS   # oldest first
             if self.pending[i] and (wait or self.events[i].query()):
@@ -480,7 +511,10 @@ class _StatusWatch:
         self.events[i].synchronize()
         self.pending[i] = False
         if int(self.host[i]) != 0:
-            self.host[i] = 0
+            self.host.zero_()
+            self.pending = [False] * self.SLOTS
+            with torch.cuda.stream(self.stream):
+                self._word().zero_()
             raise RuntimeError('THORN: the small-matrix Newton-Schulz launch timed out waiting for a '
                                'cluster of its workgroups to become resident; that step left the '
                                'parameters of its matrices with min(rows, cols) <= 256 and rows * cols '
@@ -518,7 +552,7 @@ class _OrthoRunner:
         # matrices of the small-matrix launch, whose status word is read behind each step
         self.small = ((np.minimum(self.rows, self.cols) <= SMALL_MAX_S)
                       & (self.rows * self.cols < SMALL_MAX_ELEMS))
-        self.status = _StatusWatch() if self.small.any() and not adam else None
+        self.status = _StatusWatch(self) if self.small.any() and not adam else None
 
     @property
     def workspace(self) -> torch.Tensor:
@@ -621,7 +655,7 @@ class _OrthoRunner:
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
                        stream.cuda_stream, ns_begin.cuda_event if ns_begin is not None else 0)
         if self.status is not None and coeffs.shape[0] and (due & self.small).any():
-            self.status.record(self.workspace, stream)
+            self.status.stepped(stream)
 
     @staticmethod
     def restart_mask(group: _Group, iters: int) -> int:
@@ -865,25 +899,24 @@ class _AdamRunner:
         groups. A tensor's parameter is written only when its step is due under update_rate
         (thorn.py:1706-1707) and not masked by Magma (unmasked False); m and v always are."""
         s = self.steps
-        for k, (p, state, group, unmasked) in enumerate(entries):
-            step = state['step']
-            beta1, beta2 = group.betas
-            rect = _compute_rect(group, step)
-            s[k]['p'] = p.data_ptr()
-            s[k]['g'] = p.grad.data_ptr()
-            s[k]['m'] = state['moment'].data_ptr()
-            s[k]['v'] = state['variance'].data_ptr()
-            s[k]['lr'] = group.lr * rect * 1.0
-            s[k]['weight_decay'] = group.weight_decay
-            s[k]['beta2'] = beta2
-            s[k]['w1'] = 1 - beta1
-            s[k]['w2'] = 1 - beta2
-            s[k]['bc1'] = 1 / (1 - beta1 ** step)
-            s[k]['bc2'] = 1 / (1 - beta2 ** step)
-            s[k]['eps'] = group.eps
-            s[k]['apply'] = 1 if (step + 1) % update_rate == 0 and unmasked else 0
-            s[k]['degenerate'] = 1 if rect == 0.0 else 0
-            s[k]['magma_s'] = state['s'].data_ptr() if group.momentum_align else 0
+        # one column at a time (a structured-array field per element costs a microsecond each)
+        steps = [e[1]['step'] for e in entries]
+        rect = [_compute_rect(e[2], st) for e, st in zip(entries, steps)]
+        s['p'] = [e[0].data_ptr() for e in entries]
+        s['g'] = [e[0].grad.data_ptr() for e in entries]
+        s['m'] = [e[1]['moment'].data_ptr() for e in entries]
+        s['v'] = [e[1]['variance'].data_ptr() for e in entries]
+        s['lr'] = [e[2].lr * r * 1.0 for e, r in zip(entries, rect)]
+        s['weight_decay'] = [e[2].weight_decay for e in entries]
+        s['beta2'] = [e[2].betas[1] for e in entries]
+        s['w1'] = [1 - e[2].betas[0] for e in entries]
+        s['w2'] = [1 - e[2].betas[1] for e in entries]
+        s['bc1'] = [1 / (1 - e[2].betas[0] ** st) for e, st in zip(entries, steps)]
+        s['bc2'] = [1 / (1 - e[2].betas[1] ** st) for e, st in zip(entries, steps)]
+        s['eps'] = [e[2].eps for e in entries]
+        s['apply'] = [1 if (st + 1) % update_rate == 0 and e[3] else 0 for e, st in zip(entries, steps)]
+        s['degenerate'] = [1 if r == 0.0 else 0 for r in rect]
+        s['magma_s'] = [e[1]['s'].data_ptr() if e[2].momentum_align else 0 for e in entries]
         host = self.upload.host()
         self.plan.fill_table(s, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.upload.upload(self.table)
