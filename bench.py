@@ -280,8 +280,10 @@ def cpu_baseline(config: int, budget_s: float = 300.0) -> dict:
     n_meas = sum(v['how'] == 'measured' for v in per_shape.values())
     return {
         'value': round(est * 1000.0, 1), 'unit': 'ms per full step', 'cores': threads, 'kind': 'port',
-        'sample': f'{n_meas}/{len(per_shape)} shapes measured, rest probe-scaled; Adam sliced; '
-                  f'{time.perf_counter() - t_start:.0f} s',
+        'sample': (f'{n_meas}/{len(per_shape)} shapes measured'
+                   + ('' if n_meas == len(per_shape) else ', rest probe-scaled')
+                   + f' (one oracle step on one matrix of each, times its count); Adam sliced; '
+                   f'{time.perf_counter() - t_start:.0f} s'),
         'host': host, 'gemm_probe': probe, 'probe_to_oracle_ratio': round(ratio, 3),
         'per_shape': {f'{r}x{c}': v for (r, c), v in per_shape.items()}, 'adam': adam,
     }

@@ -39,18 +39,26 @@ def hipcc() -> str:
     return exe
 
 
-def build(verbose: bool = False) -> Path:
-    """Compiles the library in place and returns its path (always rebuilds)."""
-    tmp = LIB.with_suffix('.so.tmp')
-    cmd = [hipcc(), *HIPCC_FLAGS, f'-I{ROOT / "include"}', str(SRC), '-o', str(tmp)]
+# The measurement build: the same library with per-block timestamps in ns_phase_kernel
+# (`python -m thorn_amd.blocksplit`); never loaded by THORN itself.
+LIB_TS = PKG / 'libthorn_amd_ts.so'
+
+
+def build(verbose: bool = False, timestamps: bool = False) -> Path:
+    """Compiles the library (timestamps: the measurement build) in place and returns its path
+    (always rebuilds)."""
+    out = LIB_TS if timestamps else LIB
+    tmp = out.with_suffix('.so.tmp')
+    cmd = [hipcc(), *HIPCC_FLAGS, *(['-DTHORN_BLOCK_TIMESTAMPS'] if timestamps else []), f'-I{ROOT / "include"}',
+           str(SRC), '-o', str(tmp)]
     if verbose:
         print(' '.join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}')
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == '__main__':
-    print(build(verbose='-v' in sys.argv))
+    print(build(verbose='-v' in sys.argv, timestamps='--timestamps' in sys.argv))

@@ -23,6 +23,10 @@
 
 namespace thorn {
 
+// The start of a tile's main loop, for the per-block timestamps of a measurement build
+// (-DTHORN_BLOCK_TIMESTAMPS; ns_kernels.hip); nothing otherwise.
+__device__ __forceinline__ void ts_loop_start();
+
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // Block tile 256 x 256, K step 32, 4 pipeline stages of LDS, 512 threads. SIMD s owns the
@@ -646,6 +650,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
     });
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * C::LOADS) : "memory");   // tile 0 (and C rows 192-255)
     phase_barrier();
+    ts_loop_start();
     if (wave >= 4) phase_barrier();   // group 1 starts one phase late
     const int k1 = a_k0 < KT ? a_k0 : KT4;
     const int k2 = b_k0 < k1 ? k1 : (b_k0 < KT ? b_k0 : KT4);

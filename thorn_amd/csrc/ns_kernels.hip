@@ -16,6 +16,65 @@
 
 namespace thorn {
 
+// Per-block timestamps of ns_phase_kernel, in a measurement build only (-DTHORN_BLOCK_TIMESTAMPS,
+// `python -m thorn_amd.blocksplit`): thread 0 of each block takes a slot and records, with
+// s_memrealtime (100 MHz) and s_memtime (shader clock), the block's start [0], its main loop's
+// start [1] (gemm_tile, after the prologue's loads are issued and tile 0 has landed), the loop's
+// end [2] and the block's end [3] (clock values at 4 + k), its hardware and XCC ids [8] and the
+// tile's kind, diagonal or final flag and K tiles [9]. thorn_block_timestamps copies them out.
+#ifdef THORN_BLOCK_TIMESTAMPS
+constexpr unsigned kTsSlots = 262144;
+__device__ unsigned long long g_ts[12 * kTsSlots];
+__device__ unsigned int g_ts_n;
+__device__ unsigned long long g_ls[2 * 4096];   // per CU: the loop start of its running block
+__device__ __forceinline__ unsigned ts_cu() {
+    unsigned hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    return ((xcc & 15) << 8) | ((hw >> 8) & 255);
+}
+__device__ __forceinline__ void ts_loop_start() {
+    if (threadIdx.x == 0) {
+        const unsigned c = ts_cu();
+        g_ls[2 * c] = __builtin_amdgcn_s_memrealtime();
+        g_ls[2 * c + 1] = __builtin_amdgcn_s_memtime();
+    }
+}
+__device__ __forceinline__ void ts_mark(unsigned slot, int k) {
+    if (threadIdx.x == 0) {
+        g_ts[12 * slot + k] = __builtin_amdgcn_s_memrealtime();
+        g_ts[12 * slot + 4 + k] = __builtin_amdgcn_s_memtime();
+        if (k == 2) {
+            const unsigned cu = ts_cu();
+            g_ts[12 * slot + 1] = g_ls[2 * cu];
+            g_ts[12 * slot + 5] = g_ls[2 * cu + 1];
+        }
+    }
+}
+__device__ __forceinline__ unsigned ts_begin() {
+    unsigned slot = 0;
+    if (threadIdx.x == 0) {
+        slot = atomicAdd(&g_ts_n, 1u) % kTsSlots;
+        unsigned hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        g_ts[12 * slot + 8] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
+    }
+    ts_mark(slot, 0);
+    return slot;
+}
+__device__ __forceinline__ void ts_end(unsigned slot, unsigned long long meta) {
+    __syncthreads();
+    ts_mark(slot, 3);
+    if (threadIdx.x == 0) g_ts[12 * slot + 9] = meta;
+}
+#else
+__device__ __forceinline__ void ts_loop_start() {}
+__device__ __forceinline__ void ts_mark(unsigned, int) {}
+__device__ __forceinline__ unsigned ts_begin() { return 0; }
+__device__ __forceinline__ void ts_end(unsigned, unsigned long long) {}
+#endif
+
 __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) {
     Operand op;
     op.ptr = xsel == kXA ? M.xa : M.xb;
@@ -434,9 +493,10 @@ __device__ __forceinline__ void update_finish(const OrthoMat& M, floatx16 (&acc)
 template <int ROLE>
 __device__ __forceinline__ void sym_tile(const OrthoMat& M, const NsOp& op, const Operand& A, const Operand& B, int m0,
                                          int n0, int KT, int a_k0, int b_k0, const TileC& ct, const TileWork& tw,
-                                         char* smem) {
+                                         char* smem, unsigned tslot) {
     floatx16 acc[RoleMap<ROLE>::N];
     gemm_tile<NsCfg, ROLE>(A, B, m0, n0, KT, a_k0, b_k0, ct, tw, acc, smem);
+    ts_mark(tslot, 2);
     const int ti = m0 / NsCfg::BM;
     if (op.kind == kOpGram) {
         const TileOut o = packed_out(M.gram, M, ti);
@@ -496,6 +556,7 @@ __global__ __launch_bounds__(NsCfg::NT) void ns_phase_kernel(const OrthoMat* __r
     const TaskList& tl = second ? t1 : t0;
     const NsOp& op = second ? op1 : op0;
     if (op.kind == kOpNone) return;
+    const unsigned slot = ts_begin();
     const int2 task = *reinterpret_cast<const int2*>(tl.map + 2 * b);   // matrix, tile within it
     const OrthoMat& M = mats[task.x];
     const int local = task.y;
@@ -551,17 +612,21 @@ __global__ __launch_bounds__(NsCfg::NT) void ns_phase_kernel(const OrthoMat* __r
         const TileWork tw(false, wave);
         floatx16 acc[RoleMap<kRoleFull>::N];
         gemm_tile<NsCfg, kRoleFull>(A, B, m0, n0, KT, a_k0, b_k0, ct, tw, acc, smem);
+        ts_mark(slot, 2);
         if (op.csel >= 0) update_finish<true>(M, acc, tw, local, ti, tj, op, smem, scratch);
         else update_finish<false>(M, acc, tw, local, ti, tj, op, smem, scratch);
+        ts_end(slot, (unsigned long long)(op.kind | (op.final_iter << 4) | (KT << 8)) |
+                         ((unsigned long long)blockIdx.x << 32));
         return;
     }
     const TileWork tw(ti == tj, wave);
     switch (tw.role) {
-        case kRoleFull: sym_tile<kRoleFull>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
-        case kRoleDiagA: sym_tile<kRoleDiagA>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
-        case kRoleDiagB: sym_tile<kRoleDiagB>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
-        default: sym_tile<kRoleHalf>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem); break;
+        case kRoleFull: sym_tile<kRoleFull>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem, slot); break;
+        case kRoleDiagA: sym_tile<kRoleDiagA>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem, slot); break;
+        case kRoleDiagB: sym_tile<kRoleDiagB>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem, slot); break;
+        default: sym_tile<kRoleHalf>(M, op, A, B, m0, n0, KT, a_k0, b_k0, ct, tw, smem, slot); break;
     }
+    ts_end(slot, (unsigned long long)(op.kind | ((ti == tj) << 4) | (KT << 8)) | ((unsigned long long)blockIdx.x << 32));
 }
 
 }  // namespace thorn

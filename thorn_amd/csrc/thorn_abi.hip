@@ -506,6 +506,18 @@ unsigned grid_for(int64_t items, int per_block) {
 
 extern "C" {
 
+#ifdef THORN_BLOCK_TIMESTAMPS
+// Measurement build only (not in thorn_amd.h): copies the per-block timestamps (12 words per
+// block, see ns_kernels.hip) and their count, and starts a new window.
+int thorn_block_timestamps(unsigned long long* host, unsigned* n) {
+    if (hipMemcpyFromSymbol(n, HIP_SYMBOL(thorn::g_ts_n), sizeof(unsigned)) != hipSuccess) return THORN_ERR_HIP;
+    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(thorn::g_ts), sizeof(thorn::g_ts)) != hipSuccess) return THORN_ERR_HIP;
+    const unsigned z = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(thorn::g_ts_n), &z, sizeof(unsigned)) != hipSuccess) return THORN_ERR_HIP;
+    return THORN_OK;
+}
+#endif
+
 int thorn_abi_version(void) { return THORN_ABI_VERSION; }
 
 const char* thorn_last_error(void) { return g_last_error.c_str(); }
