@@ -229,8 +229,8 @@ def test_config5_every_shape():
 @pytest.mark.parametrize('n_chains,variant', [(2, 'plain'), (3, 'plain'), (4, 'plain'), (2, 'magma'),
                                               (2, 'md'), (3, 'update_rate')])
 def test_chains_equal_one_plan(n_chains, variant):
-    """A group of at least CHAIN_MIN_MATRICES large matrices steps as 2 to 4 chains on as many
-    streams (thorn_amd.optim._OrthoBatches); every matrix runs the same kernels on the same data as
+    """A group of at least CHAIN_MIN_MATRICES large matrices steps as chains on as many streams
+    (thorn_amd.optim._OrthoBatches; two by default, forced to 2, 3 and 4 here); every matrix runs the same kernels on the same data as
     in one plan, so parameters and state must match the one-plan step bit for bit, over steps with
     the exact and the prescaled first iterate, and per-row normalization on the tall matrices; also
     with Magma masks (some matrices skip a step; the masks come from the host PRNG, the same in

@@ -3,6 +3,7 @@
 #include "../../include/thorn_amd.h"
 #include "ns_small.hip"
 #include "sym_addmm.hip"
+#include "task_layout.hpp"
 #include "update_kernels.hip"
 
 #include <algorithm>
@@ -215,24 +216,22 @@ TaskOffsets add_tasks(size_t& off, const std::vector<int32_t>& order, const std:
     return t;
 }
 
-void write_tasks(char* host, const TaskOffsets& t, const std::vector<int32_t>& order,
+// Writes a task list's order and block starts, and its block map if it has one (see
+// task_layout.hpp: big matrices striped over the XCDs' chunks).
+bool write_tasks(char* host, const TaskOffsets& t, const std::vector<int32_t>& order,
                  const std::vector<int64_t>& blocks_of) {
     int32_t* o = reinterpret_cast<int32_t*>(host + t.order);
     int32_t* s = reinterpret_cast<int32_t*>(host + t.starts);
-    int32_t* m = t.map ? reinterpret_cast<int32_t*>(host + t.map) : nullptr;
     int32_t acc = 0;
     for (size_t k = 0; k < order.size(); ++k) {
         o[k] = order[k];
         s[k] = acc;
-        const int32_t nb = static_cast<int32_t>(blocks_of[order[k]]);
-        if (m)
-            for (int32_t j = 0; j < nb; ++j) {
-                m[2 * (acc + j)] = order[k];
-                m[2 * (acc + j) + 1] = j;
-            }
-        acc += nb;
+        acc += static_cast<int32_t>(blocks_of[order[k]]);
     }
     s[order.size()] = acc;
+    if (!t.map) return true;
+    return thorn_layout::write_block_map(reinterpret_cast<int32_t*>(host + t.map), order.data(),
+                                         static_cast<int>(order.size()), blocks_of.data());
 }
 
 thorn::TaskList task_list(const char* dev, const TaskOffsets& t) {

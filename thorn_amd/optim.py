@@ -700,10 +700,14 @@ def _ns_cost(p) -> int:
 
 
 def _chain_count(params: list) -> int:
-    """How many chains a group of large matrices steps as: one per CHAIN_COST of Newton-Schulz
-    work, at least 2 and at most MAX_CHAINS. Measured on one MI355X: the Qwen3-300M set (3.2e11)
-    steps fastest as 2 chains (3: +2.5%, 4: +7.5%), the Qwen3-1.7B set (3.3e12) as 4 (2: +6%)."""
-    return max(2, min(MAX_CHAINS, int(sum(_ns_cost(p) for p in params) // CHAIN_COST)))
+    """How many chains a group of large matrices steps as: 2 while its Newton-Schulz work
+    (sum of s^2 * l) is at most CHAIN_MAX_COST, else 1 (one plan). Measured on MI355X boxes, one
+    process per config: the Qwen3-300M set (3.2e11) 6.82-6.85 ms with 2 chains against 7.06-7.11
+    with one (3: 6.87); its decouple_md variant 8.86-8.89 against 9.00-9.04; the Qwen3-1.7B set
+    (3.3e12) 49.9-50.1 ms with one against 50.2-52.4 with 2, 51.0-52.0 with 3 and 52.4-52.6 with 4.
+    (Before the block map striped a large matrix's tiles over the XCDs, four chains filled the long
+    tails its 8192 x 8192 matrix left in every launch: 53.8 against 70.2 ms.)"""
+    return 2 if sum(_ns_cost(p) for p in params) <= CHAIN_MAX_COST else 1
 
 
 def _split_chains(params: list, n: int) -> list:
@@ -725,16 +729,17 @@ def _chain_plan(params: list, limit: int) -> Optional[list]:
     plan)."""
     if len(params) < 2 or _large_matrices(params) < CHAIN_MIN_MATRICES or len(_batches(params, limit)) != 1:
         return None
-    chains = _split_chains(params, _chain_count(params))
+    n = _chain_count(params)
+    if n < 2:
+        return None
+    chains = _split_chains(params, n)
     return chains if all(chains) else None
 
 
-# A group with at least CHAIN_MIN_MATRICES large-path matrices steps as chains (_OrthoBatches),
-# one per CHAIN_COST of work, at most MAX_CHAINS: the device has 4 hardware queues per process,
-# and the caller's stream takes the steps around the chains.
+# A group with at least CHAIN_MIN_MATRICES large-path matrices and at most CHAIN_MAX_COST of
+# Newton-Schulz work (sum of s^2 * l) steps as two chains (_OrthoBatches, _chain_count).
 CHAIN_MIN_MATRICES = 16
-CHAIN_COST = 1.5e11
-MAX_CHAINS = 4
+CHAIN_MAX_COST = 1e12
 # Streams of the gradient-release steps (_release_step): with the caller's own, as many as the
 # device's 4 hardware queues of a process (4 of them measured 54.8 ms on config 2's hooks, 3 41.2).
 RELEASE_STREAMS = 3
@@ -796,13 +801,13 @@ class _OrthoBatches:
     take the exact first iterate (the library keeps the cheaper prescaled one for a plan that
     stepped last on its workspace).
 
-    A group that is one batch with at least CHAIN_MIN_MATRICES large matrices runs as 2 to 4
-    chains instead (_chain_count): plans of about equal Newton-Schulz work, each with its own
-    workspace (together the size of one plan's), on streams of the optimizer, each starting once
-    the previous one's prologue launches are enqueued. The chains run out of phase, so one chain's
-    memory-bound launches and the partly idle last round of tiles of each of its Newton-Schulz
-    launches run beside the other chains' launches (bench.py on one MI355X: the Qwen3-300M set
-    7.07 -> 6.85 ms with 2 chains, the Qwen3-1.7B set 70.2 -> 53.8 ms with 4).
+    A group that is one batch with at least CHAIN_MIN_MATRICES large matrices and at most
+    CHAIN_MAX_COST of work runs as two chains instead (_chain_plan, _chain_count): plans of about
+    equal Newton-Schulz work, each with its own workspace (together the size of one plan's), on
+    streams of the optimizer, the second starting once the first one's prologue launches are
+    enqueued. The chains run out of phase, so one chain's memory-bound launches and the partly
+    idle last round of tiles of each of its Newton-Schulz launches run beside the other chain's
+    launches (the Qwen3-300M set: 7.07-7.11 -> 6.82-6.85 ms per step).
     The results are those of one plan bit for bit: every matrix runs the same kernels on the same
     data."""
 
