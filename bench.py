@@ -321,7 +321,7 @@ def _short_kernel_name(name: str) -> str:
     return ''.join(out).strip()
 
 
-def rocprof_summary(paths: list, cal_mib: int = 0, steps: int = 5) -> str:
+def rocprof_summary(paths: list, cal_mib: int = 0, steps: int = 5, config: int = 2) -> str:
     """Markdown summary of rocprofv3 CSV output directories: the kernel statistics table
     (`*kernel_stats.csv`) and, when present, per-kernel counter averages per dispatch
     (`*counter_collection.csv`, one directory per counter pass). With `cal_mib`, FETCH_SIZE /
@@ -336,7 +336,7 @@ def rocprof_summary(paths: list, cal_mib: int = 0, steps: int = 5) -> str:
     lines = []
     traces = found('*kernel_trace.csv')
     if traces:
-        lines += ns_trace_lines(traces[0], steps)
+        lines += ns_trace_lines(traces[0], steps, config)
     for f in found('*kernel_stats.csv'):
         rows = list(csv.DictReader(open(f)))
         lines += ['| kernel | calls | total ms | avg us | min us | max us | % |',
@@ -396,7 +396,7 @@ def _union_us(iv: list) -> float:
     return total
 
 
-def ns_trace_lines(path: str, steps: int = 5) -> list:
+def ns_trace_lines(path: str, steps: int = 5, config: int = 2) -> list:
     """From a rocprofv3 kernel trace of a config-2 bench.py run: ns_phase_kernel's launches in the
     last `steps` steps (the event-timed pass of `bench.py --steps <steps>`), as summed durations
     and as the union of their intervals, which is what bench.py reports (a group stepping as two
@@ -423,13 +423,15 @@ def ns_trace_lines(path: str, steps: int = 5) -> list:
         return out
     (k, starts), = chains.items()
     seg = [iv(r) for r in per_stream[k][starts[-2]:starts[-1]] if 'ns_phase_kernel' in r['Kernel_Name']]
-    mats, _ = config_shapes(2)
+    mats, _ = config_shapes(config)
+    mats = [sh for sh in mats if not (min(sh) <= SMALL_MAX_S and sh[0] * sh[1] < SMALL_MAX_ELEMS)]
     gram = gram_ops(5, 4)
     plain = plain_ops(5)
+    n_sq = sum(1 for sh in mats if sh[0] == sh[1])
     fl = {'gram': lambda s_, l_: s_ * s_ * l_, 'poly': lambda s_, l_: s_ ** 3,
           'sym': lambda s_, l_: s_ ** 3, 'update': lambda s_, l_: 2.0 * s_ * s_ * l_}
-    out += ['Newton-Schulz launches of the last complete step (config 2; Gram-schedule op on the 100 '
-            'non-square matrices / plain-schedule op on the 40 square ones):', '',
+    out += [f'Newton-Schulz launches of the last complete step (config {config}; Gram-schedule op on the '
+            f'{len(mats) - n_sq} non-square matrices / plain-schedule op on the {n_sq} square ones):', '',
             '| launch | ops | TFLOP (algorithmic) | us | TFLOP/s |', '|---:|---|---:|---:|---:|']
     for j, (a, b) in enumerate(seg):
         f = 0.0
@@ -605,7 +607,7 @@ def main() -> int:
                     help='print a markdown summary of rocprofv3 CSV output directories and exit')
     args = ap.parse_args()
     if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib, args.steps))
+        print(rocprof_summary(args.rocprof_summary, args.copy_cal_mib, args.steps, args.config))
         return 0
     if args.vendor_gemm:
         return vendor_gemm()
