@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 8
+#define THORN_ABI_VERSION 9
 
 enum {
     THORN_OK = 0,
@@ -131,6 +131,13 @@ size_t thorn_ortho_workspace_bytes(thorn_ortho_plan_t plan);
  * that makes the wait expire from the host (0: at the first wait that would block) while every
  * kernel still exits normally. */
 int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls);
+/* No counterpart in the reference (its eager step is one launch per operation): a step whose
+ * matrices all take the small-matrix path (short side <= 256, fewer than 2^20 elements), none with
+ * decouple_md or Magma, all with THORN_STEP_APPLY, on the workspace the plan last stepped on, runs
+ * as one launch (momentum, norm, first iterate, Newton-Schulz, row statistics and the update of p,
+ * each matrix by its cluster of workgroups) instead of six; its results are bit for bit those of
+ * the separate launches. On by default; enable = 0 keeps the separate launches (for comparison). */
+int thorn_ortho_set_small_fusion(thorn_ortho_plan_t plan, int enable);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);

@@ -1154,6 +1154,69 @@ def test_small_launch_timeout_is_reported():
     _log('[gpu]   ok')
 
 
+def test_small_plan_fused_launch_equals_separate_launches():
+    """A group whose matrices all take the small-matrix path runs, from its second step on one
+    workspace, as one fused launch (momentum, norm, first iterate, Newton-Schulz, row statistics and
+    the update of p in ns_small_kernel<true>). Against the same steps with the fusion turned off
+    (six launches per step), every parameter and state tensor is equal bit for bit after each of
+    five steps: config 4's matrices (per-row normalized and not, float4 and scalar layouts, one
+    workgroup per matrix) and a second group of (640, 256), (200, 300) and (130, 129) matrices
+    (clusters of 10, 6 and 4 workgroups, padded sides)."""
+    import bench
+    thorn_amd = _thorn()
+    lib = _lib()
+    _log('[gpu] small-matrix plans: one fused launch against the separate launches, bit for bit')
+    params_cpu, _, groups_cpu, _ = bench.build_workload(4, 'cpu')
+    g = torch.Generator().manual_seed(21)
+    extra = [torch.randn(r, c, generator=g) * 0.02 for r, c in ((640, 256), (200, 300), (130, 129))]
+
+    def make():
+        ps = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params_cpu]
+        xs = [torch.nn.Parameter(x.clone().to(DEV)) for x in extra]
+        groups = _clone_groups(groups_cpu, ps) + [dict(orthogonalize=True, params=xs, lr=2e-3, weight_decay=0.1)]
+        return ps + xs, thorn_amd.THORN(groups)
+
+    def ortho_plans(opt):
+        return [pl for r in opt._runners.values() for pl in r.plans if isinstance(pl, lib.OrthoPlan)]
+
+    pa, fused = make()
+    pb, sep = make()
+    flags = [f for grp in fused.param_groups if grp['orthogonalize']
+             for f in thorn_amd.optim._plan_shapes(grp['params'], thorn_amd.optim._Group.from_kwargs(**grp), False)[2]]
+    assert any(f & lib.MAT_PER_ROW_NORM for f in flags) and any(not f & lib.MAT_PER_ROW_NORM for f in flags), flags
+    counts = {}
+    for step in range(1, 6):
+        grads = [torch.randn(p.shape, generator=g) * 1e-2 for p in pa]
+        for p, q, gr in zip(pa, pb, grads):
+            p.grad = gr.to(DEV)
+            q.grad = gr.to(DEV)
+        if step == 2:   # the plans exist after the first step (which is never fused)
+            for pl in ortho_plans(sep):
+                pl.set_small_fusion(False)
+            for pl in ortho_plans(fused) + ortho_plans(sep):
+                pl.timing_enable(64)
+        fused.step()
+        sep.step()
+        torch.cuda.synchronize()
+        for i, (p, q) in enumerate(zip(pa, pb)):
+            assert torch.equal(p, q), (step, i, tuple(p.shape), (p - q).abs().max().item())
+            for k, v in fused.state[p].items():
+                if torch.is_tensor(v):
+                    assert torch.equal(v, sep.state[q][k]), (step, i, k)
+        if step == 2:
+            counts = {name: [pl.timing_read() for pl in ortho_plans(o)] for name, o in (('fused', fused), ('sep', sep))}
+            for pl in ortho_plans(fused) + ortho_plans(sep):
+                pl.timing_enable(0)
+    fused.check_status()
+    sep.check_status()
+    # the fused optimizer's step was one small-matrix launch per plan, the other's six
+    for t in counts['fused']:
+        assert set(t) == {'small'} and t['small'][1] == 1, t
+    for t in counts['sep']:
+        assert {'pre', 'norm', 'cast', 'small', 'pnn_apply'} <= set(t), t
+    _log(f'[gpu]   launches of step 2: fused {counts["fused"]}, separate {counts["sep"]}')
+
+
 SYM_CASES = [
     # (batch dims, M, K, C kind, alpha, beta, B as a transposed view of A)
     ((), 300, 700, None, 1.0, 1.0, True),        # Gram R = X X^T, two tile rows

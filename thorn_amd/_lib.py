@@ -93,6 +93,7 @@ SIGNATURES = {
                              ctypes.c_int64, _f, _f, _vp, _sz, _vp]),
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
     'thorn_ortho_set_spin_limit': (_i, [_vp, _i]),
+    'thorn_ortho_set_small_fusion': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
     'thorn_ortho_timing_intervals': (_i, [_vp, _vp, _vp, _vp, _vp, _i, ctypes.POINTER(_i)]),
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
@@ -102,7 +103,7 @@ KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_f
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
 NOALLOC_SCRATCH_BYTES = 32 << 20
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 
@@ -195,6 +196,9 @@ class OrthoPlan:
 
     def set_spin_limit(self, polls: int) -> None:
         check(self._lib.thorn_ortho_set_spin_limit(self.handle, polls), 'thorn_ortho_set_spin_limit')
+
+    def set_small_fusion(self, enable: bool) -> None:
+        check(self._lib.thorn_ortho_set_small_fusion(self.handle, int(bool(enable))), 'thorn_ortho_set_small_fusion')
 
     def timing_read(self) -> dict:
         return _timing_read(self._lib.thorn_ortho_timing_read, self.handle)

@@ -2,7 +2,7 @@
 
 Usage (on an MI355X, after ``python -m thorn_amd.build --timestamps``)::
 
-    python -m thorn_amd.blocksplit [--config N] [--single-chain]
+    python -m thorn_amd.blocksplit [--config N] [--single-chain] [--separate]
 
 It loads the measurement build (``libthorn_amd_ts.so``: the library with per-block timestamps in
 ``ns_phase_kernel``, see ``csrc/ns_kernels.hip``) in place of the library, runs warm-up steps of a
@@ -11,7 +11,10 @@ BASELINE workload (``bench.build_workload``), then one step whose blocks it repo
 * per kind of tile (Gram, symmetric product, update; diagonal, final): the mean prologue (block
   start to main-loop start: task lookup, operand descriptors, the first three K tiles' loads and
   the wait for tile 0), main loop (with the shader clocks per K tile), and epilogue;
-* per CU: busy time out of the step's Newton-Schulz span, and the gaps between its blocks.
+* per CU: busy time out of the step's Newton-Schulz span, and the gaps between its blocks;
+* for ``ns_small_kernel`` (matrices with a short side of at most 256), per matrix: its cluster of
+  workgroups and their prologue (the fused step's momentum, norm and first iterate), schedule and
+  epilogue (the fused step's update of p), from the launch's first workgroup start.
 
 Timestamps are ``s_memrealtime`` (100 MHz) for times and ``s_memtime`` (shader clock) for cycles.
 """
@@ -33,6 +36,8 @@ def main(argv=None) -> int:
     ap.add_argument('--config', type=int, default=2)
     ap.add_argument('--single-chain', action='store_true', help='one plan on one stream (no chains)')
     ap.add_argument('--warmup', type=int, default=4)
+    ap.add_argument('--separate', action='store_true',
+                    help='small-matrix plans without the fused step (thorn_ortho_set_small_fusion(plan, 0))')
     args = ap.parse_args(argv)
 
     sys.path.insert(0, str(ROOT))
@@ -60,8 +65,13 @@ def main(argv=None) -> int:
         for p, g in zip(params, grads):
             p.grad = g
         opt.step()
-    for _ in range(args.warmup):
+    for w in range(max(1, args.warmup)):
         step()
+        if w == 0 and args.separate:   # the plans exist after the first step
+            for r in opt._runners.values():
+                for pl in r.plans:
+                    if isinstance(pl, _lib.OrthoPlan):
+                        pl.set_small_fusion(False)
     torch.cuda.synchronize()
     if fetch(buf.ctypes.data, n.ctypes.data) != 0:
         raise SystemExit('thorn_block_timestamps failed')
@@ -83,6 +93,32 @@ def main(argv=None) -> int:
     hwid = hw & 0xFFFFFFFF
     cuid = (((xcc * 8 + ((hwid >> 13) & 0x7)) * 2 + ((hwid >> 12) & 0x1)) * 16 + ((hwid >> 8) & 0xF))
     kind, flag, kt = meta & 0xF, (meta >> 4) & 0xF, (meta >> 8) & 0xFFFFFF
+    small = kind == 4
+    if small.any():
+        shapes = [(r, c) for grp in opt.param_groups if grp['orthogonalize']
+                  for r, c in zip(*thorn_amd.optim._plan_shapes(grp['params'],
+                                                                thorn_amd.optim._Group.from_kwargs(**grp), False)[:2])]
+        s0 = rs[small].min()
+        print(f'ns_small_kernel ({"fused step" if flag[small].max() else "schedule only"}): '
+              f'{small.sum()} workgroups, {(re[small].max() - s0) / 100:.1f} us from the first start to the last end')
+        print('| matrix | workgroups | start us | prologue us | schedule us | epilogue us | end us |')
+        print('|---|---:|---:|---:|---:|---:|---:|')
+        mat = (meta >> 20) & 0xFFF
+        for i in sorted(set(mat[small].tolist())):
+            m = small & (mat == i)
+            shape = shapes[i] if i < len(shapes) else '?'
+            print(f'| {shape} | {m.sum()} | {(rs[m].min() - s0) / 100:.1f} | {((rp[m] - rs[m]) / 100).max():.1f} | '
+                  f'{((rl[m] - rp[m]) / 100).max():.1f} | {((re[m] - rl[m]) / 100).max():.1f} | '
+                  f'{(re[m].max() - s0) / 100:.1f} |')
+        keep = ~small
+        if not keep.any():
+            return 0
+        R, rs, rp, rl, re, cp, cl, hw, meta = (R[keep], rs[keep], rp[keep], rl[keep], re[keep], cp[keep], cl[keep],
+                                               hw[keep], meta[keep])
+        kind, flag, kt, N = kind[keep], flag[keep], kt[keep], int(keep.sum())
+        xcc = (hw >> 32) & 0xF
+        hwid = hw & 0xFFFFFFFF
+        cuid = (((xcc * 8 + ((hwid >> 13) & 0x7)) * 2 + ((hwid >> 12) & 0x1)) * 16 + ((hwid >> 8) & 0xF))
     t0 = rs.min()
     span = (re.max() - t0) / 100.0
     print(f'config {args.config}{" (one chain)" if args.single_chain else ""}: step {e0.elapsed_time(e1):.3f} ms '

@@ -68,11 +68,19 @@ __device__ __forceinline__ void ts_end(unsigned slot, unsigned long long meta) {
     ts_mark(slot, 3);
     if (threadIdx.x == 0) g_ts[12 * slot + 9] = meta;
 }
+// ns_small_kernel's workgroups: [1] and [2] are the ends of its prologue and of its schedule
+__device__ __forceinline__ void ts_point(unsigned slot, int k) {
+    if (threadIdx.x == 0) {
+        g_ts[12 * slot + k] = __builtin_amdgcn_s_memrealtime();
+        g_ts[12 * slot + 4 + k] = __builtin_amdgcn_s_memtime();
+    }
+}
 #else
 __device__ __forceinline__ void ts_loop_start() {}
 __device__ __forceinline__ void ts_mark(unsigned, int) {}
 __device__ __forceinline__ unsigned ts_begin() { return 0; }
 __device__ __forceinline__ void ts_end(unsigned, unsigned long long) {}
+__device__ __forceinline__ void ts_point(unsigned, int) {}
 #endif
 
 __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) {
@@ -127,6 +135,37 @@ __device__ __forceinline__ SmallView small_view(const OrthoMat& M) {
     return v;
 }
 
+// The padding of a small matrix's first iterate (rows s .. s_p and columns l .. l_p of both
+// orientations of slot 0) cleared by threads tid = 0 .. nt-1.
+__device__ __forceinline__ void small_x0_padding(const OrthoMat& M, const SmallView& V, int tid, int nt) {
+    for (int e = tid; e < (V.sp - M.s) * V.lp; e += nt) {   // rows s .. s_p
+        const int i = M.s + e / V.lp, j = e % V.lp;
+        V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
+        V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
+    }
+    for (int e = tid; e < M.s * (V.lp - M.l); e += nt) {     // columns l .. l_p
+        const int i = e / (V.lp - M.l), j = M.l + e % (V.lp - M.l);
+        V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
+        V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
+    }
+}
+
+// Row r, columns c0 + lane + 64 e (e < 4), of a small matrix's first iterate f16(u / denom), u from
+// the updated moment and the gradient, straight into both wide orientations of iterate slot 0.
+__device__ __forceinline__ void small_x0_row(const OrthoMat& M, const SmallView& V, int r, int c0, int lane,
+                                             float denom, float beta1) {
+    const int64_t rb = (int64_t)r * M.cols;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int c = c0 + lane + 64 * e;
+        if (c >= M.cols) continue;
+        const _Float16 x = (_Float16)(fmaf(ldg<float>(M.m + rb + c), beta1, ldg<float>(M.g + rb + c)) / denom);
+        const int i = M.tall ? c : r, j = M.tall ? r : c;   // wide (s x l) position
+        V.xw(0)[int64_t(i) * V.lp + j] = x;
+        V.xwt(0)[int64_t(j) * V.sp + i] = x;
+    }
+}
+
 // First iterate, exact form (thorn.py:632-635): xb = f16(u / (||u||_F + 1e-8)) with
 // u = g + beta1 * m recomputed from the gradient (times the decouple_md gains: ortho_pre_kernel
 // writes g back for those matrices, as the reference's g.mul_ does) and the updated moment, the
@@ -149,17 +188,7 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
     // that run in turn on one workspace).
     if (blockIdx.x == 0) {
         if (M.flags & kFlagSmall) {
-            const SmallView V = small_view(M);
-            for (int e = threadIdx.x; e < (V.sp - M.s) * V.lp; e += 256) {   // rows s .. s_p
-                const int i = M.s + e / V.lp, j = e % V.lp;
-                V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
-                V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
-            }
-            for (int e = threadIdx.x; e < M.s * (V.lp - M.l); e += 256) {     // columns l .. l_p
-                const int i = e / (V.lp - M.l), j = M.l + e % (V.lp - M.l);
-                V.xw(0)[int64_t(i) * V.lp + j] = _Float16(0.f);
-                V.xwt(0)[int64_t(j) * V.sp + i] = _Float16(0.f);
-            }
+            small_x0_padding(M, small_view(M), threadIdx.x, 256);
         } else if (M.ldx > M.cols) {
             for (int e = threadIdx.x; e < M.rows * (M.ldx - M.cols); e += 256) {
                 const int r = e / (M.ldx - M.cols), c = M.cols + e % (M.ldx - M.cols);
@@ -176,18 +205,8 @@ __global__ __launch_bounds__(256) void ortho_cast_kernel(const OrthoMat* __restr
             if (r >= M.rows) break;
             const int64_t rb = (int64_t)r * M.cols;
             _Float16* xrow = M.xb + (int64_t)r * M.ldx;
-            if (M.flags & kFlagSmall) {   // straight into both wide orientations of iterate slot 0
-                const SmallView V = small_view(M);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int c = c0 + lane + 64 * e;
-                    if (c >= M.cols) continue;
-                    const _Float16 x =
-                        (_Float16)(fmaf(ldg<float>(M.m + rb + c), beta1, ldg<float>(M.g + rb + c)) / denom);
-                    const int i = M.tall ? c : r, j = M.tall ? r : c;   // wide (s x l) position
-                    V.xw(0)[int64_t(i) * V.lp + j] = x;
-                    V.xwt(0)[int64_t(j) * V.sp + i] = x;
-                }
+            if (M.flags & kFlagSmall) {
+                small_x0_row(M, small_view(M), r, c0, lane, denom, beta1);
             } else if (vec) {
                 const int c = c0 + 4 * lane;
                 if (c >= M.cols) continue;

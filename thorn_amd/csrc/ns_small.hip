@@ -18,7 +18,18 @@
 // The first iterate is written into xw[0] and xwt[0] by ortho_cast_kernel;
 // u' goes to xa in the parameter's orientation, with the per-row partial sums of u'^2 that the
 // per-row normalization needs.
+//
+// A plan whose matrices all take this path (none with decouple_md, Magma or an Adam step, every
+// one applied this step) runs its whole step as ns_small_kernel<true>: each cluster also does, for
+// its own matrix, the work of ortho_pre_kernel (momentum, tile partials of ||u||^2),
+// ortho_norm_kernel (the norm) and ortho_cast_kernel (the first iterate) before the schedule, and
+// of ortho_rowstats_kernel and ortho_pnn_apply_kernel (the update of p) after it: one launch in
+// place of six, two more cluster barriers. The elementwise parts keep those kernels' 16 x 256
+// tiles, thread layouts and summation orders (each 256-thread quarter of a workgroup takes one
+// tile at a time; the norm, the row statistics and the apply are the same device functions), so
+// every value is bit for bit the one the separate launches give.
 #include "ns_kernels.hip"
+#include "update_kernels.hip"
 
 namespace thorn {
 
@@ -53,7 +64,10 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int s
         const int g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int a = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         if (a == C - 1) {
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // a subtraction, not a store of 0: should a member that gave up waiting arrive at the
+            // next barrier first, its arrival is kept, and every launch, whose members each arrive
+            // once at every barrier, leaves the count at 0
+            __hip_atomic_fetch_add(cnt, -C, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_fetch_add(gen, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             int it = 0;
@@ -221,13 +235,178 @@ __device__ __forceinline__ void small_store_final(const _Float16* stage, const O
     }
 }
 
+// The fused step's prologue and epilogue: a workgroup's four 256-thread quarters take elementwise
+// tiles 4 member + q, then 4 (member + C) + q, ... of the matrix.
+constexpr int kQuarter = 256;
+static_assert(kSmallThreads == 4 * kQuarter, "four quarters of a workgroup");
+
+// ortho_pre_kernel's momentum for a matrix without decouple_md, Magma or an Adam step, on
+// elementwise tile t by one quarter (t256 = 0..255 in that kernel's thread layout): m <- beta1 m +
+// g, stored; returns this thread's sum of u^2, u = g + beta1 m, in that kernel's order.
+__device__ __forceinline__ float small_momentum_tile(const OrthoMat& M, int t, int t256) {
+    const int lane = t256 & 63, wave = t256 >> 6;
+    const int tr = t / M.mom_tiles_c, tc = t % M.mom_tiles_c;
+    const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
+    const int nrows = M.rows - r0;
+    const float beta1 = M.beta1;
+    float nrm = 0.f;
+    if (M.flags & kFlagVec4) {
+        const int c = c0 + 4 * lane;
+        if (c >= M.cols) return 0.f;
+        float4 gv[4], mv[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            gv[rr] = mv[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rr >= nrows) continue;
+            const int64_t o = (int64_t)(r0 + rr) * M.cols + c;
+            gv[rr] = ldg_nt<float4>(M.g + o);
+            mv[rr] = ldg_nt<float4>(M.m + o);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            if (rr >= nrows) break;
+            const float g[4] = {gv[rr].x, gv[rr].y, gv[rr].z, gv[rr].w};
+            float m[4] = {mv[rr].x, mv[rr].y, mv[rr].z, mv[rr].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                m[e] = m[e] * beta1 + g[e];
+                const float u = fmaf(m[e], beta1, g[e]);
+                nrm += u * u;
+            }
+            stg_nt<float4>(M.m + (int64_t)(r0 + rr) * M.cols + c, make_float4(m[0], m[1], m[2], m[3]));
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            if (rr >= nrows) break;
+            const int64_t rb = (int64_t)(r0 + rr) * M.cols;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = c0 + lane + 64 * e;
+                if (c >= M.cols) continue;
+                const float g = ldg<float>(M.g + rb + c);
+                const float m = ldg<float>(M.m + rb + c) * beta1 + g;
+                stg_nt<float>(M.m + rb + c, m);
+                const float u = fmaf(m, beta1, g);
+                nrm += u * u;
+            }
+        }
+    }
+    return nrm;
+}
+
+// First iterate of elementwise tile t by one quarter: the values of small_x0_row; the orientation
+// in which the tile's columns are contiguous stored directly, the other through the quarter's LDS
+// transpose `tt` (256 rows of kX0Pitch halves, row c - c0 holding rows r0 .. r0 + 15) as 16-byte
+// chunks of 8 rows (rows past the matrix, inside the padded side, receive zeros). All quarters
+// call it the same number of times (block barriers); `active`: t is a tile of the matrix.
+constexpr int kX0Pitch = 24;   // halves: 16-byte aligned rows, spread over the banks
+static_assert(4 * kQuarter * kX0Pitch * 2 <= kSmallStages * kSmallStageBytes, "four transposes in the ring");
+__device__ __forceinline__ void small_x0_tile(const OrthoMat& M, const SmallView& V, int t, int t256, bool active,
+                                              float denom, _Float16* tt) {
+    const int lane = t256 & 63, wave = t256 >> 6;
+    const int r0 = (t / M.mom_tiles_c) * kTileR, c0 = (t % M.mom_tiles_c) * kTileC;
+    _Float16* const direct = M.tall ? V.xwt(0) : V.xw(0);   // row r of the parameter, contiguous
+    const int ldd = M.tall ? V.sp : V.lp;
+    _Float16* const tpose = M.tall ? V.xw(0) : V.xwt(0);    // column c of the parameter, contiguous
+    const int ldt = M.tall ? V.lp : V.sp;
+    if (active) {
+        const float beta1 = M.beta1;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int rl = wave * 4 + rr, r = r0 + rl;
+            const int64_t rb = (int64_t)r * M.cols;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int cl = lane + 64 * e, c = c0 + cl;
+                _Float16 x = _Float16(0.f);
+                if (r < M.rows && c < M.cols) {
+                    x = (_Float16)(fmaf(ldg<float>(M.m + rb + c), beta1, ldg<float>(M.g + rb + c)) / denom);
+                    direct[int64_t(r) * ldd + c] = x;
+                }
+                tt[cl * kX0Pitch + rl] = x;
+            }
+        }
+    }
+    __syncthreads();
+    if (active) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int chunk = t256 + kQuarter * h2, cl = chunk >> 1, h = chunk & 1;
+            if (c0 + cl < M.cols)
+                stg<half8>(tpose + int64_t(c0 + cl) * ldt + r0 + 8 * h,
+                           *reinterpret_cast<const half8*>(tt + cl * kX0Pitch + 8 * h));
+        }
+    }
+    __syncthreads();   // the transpose is read before the next round writes it
+}
+
+// Before the schedule: the momentum and the tile partials of ||u||^2 (each tile's sum over its 256
+// threads as block_sum adds them), a cluster barrier, the norm and, in member 0, the matrix's
+// scalars, the first iterate f16(u / (||u|| + 1e-8)) and its padding, a cluster barrier.
+__device__ __forceinline__ void small_fused_prologue(const OrthoMat& M, const SmallView& V, int member, int C,
+                                                     float* red, char* stages, int* bar, int* err, int spin) {
+    const int q = threadIdx.x / kQuarter, t256 = threadIdx.x % kQuarter;
+    const int ntiles = M.mom_tiles_r * M.mom_tiles_c, per = 4 * C;
+    for (int t0 = 0; t0 < ntiles; t0 += per) {   // the same trip count in every quarter (barriers)
+        const int t = t0 + 4 * member + q;
+        float nrm = t < ntiles ? small_momentum_tile(M, t, t256) : 0.f;
+        nrm = wave_sum(nrm);
+        __syncthreads();   // the previous round's reads of red are done
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = nrm;
+        __syncthreads();
+        if (t < ntiles && t256 == 0) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += red[4 * q + i];
+            M.normpart[t] = sum;
+        }
+    }
+    cluster_barrier(bar, C, err, spin);
+    const float s = norm_partials(M, red);
+    if (member == 0 && threadIdx.x == 0) norm_write_scales(M, s);
+    const float denom = norm_denom(s);
+    if (member == 0) small_x0_padding(M, V, threadIdx.x, kSmallThreads);
+    _Float16* const tt = reinterpret_cast<_Float16*>(stages) + q * kQuarter * kX0Pitch;
+    for (int t0 = 0; t0 < ntiles; t0 += per) {
+        const int t = t0 + 4 * member + q;
+        small_x0_tile(M, V, t < ntiles ? t : 0, t256, t < ntiles, denom, tt);
+    }
+    cluster_barrier(bar, C, err, spin);
+}
+
+// After the schedule (its last barrier has made every member's u' and row sums visible): gamma and
+// the row scales s_i of per-row-normalized matrices (every member computes them, into LDS while
+// the rows fit; member 0 also stores gamma, as ortho_rowstats_kernel does), then p's update on
+// this member's tiles.
+constexpr int kFusedMaxScaleRows = kSmallStages * kSmallStageBytes / 4;
+__device__ __forceinline__ void small_fused_apply(const OrthoMat& M, int member, int C, float* red, char* stages) {
+    const int q = threadIdx.x / kQuarter, t256 = threadIdx.x % kQuarter;
+    const bool pnn = M.flags & kFlagPNN;
+    float* const sc = reinterpret_cast<float*>(stages);
+    const bool staged = M.rows <= kFusedMaxScaleRows;
+    const float gamma = pnn ? pnn_gamma(M, red, staged ? sc : nullptr) : 1.f;   // its block_sum syncs sc
+    if (pnn && member == 0 && threadIdx.x == 0) M.scal[kScalGamma] = gamma;
+    const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
+    for (int t = 4 * member + q; t < ntiles; t += 4 * C) {
+        if (staged)
+            (void)pnn_apply_tile(M, t, t256, M.xa, gamma, [&](int row) { return sc[row]; });
+        else
+            (void)pnn_apply_tile(M, t, t256, M.xa, gamma,
+                                 [&](int row) { return pnn_row_scale(M, pnn_row_sum(M, row)); });
+    }
+}
+
 // One launch: the schedule of every small matrix in the task list (blocks starts[k] ..
 // starts[k+1]-1 are the cluster of matrix order[k]). err: set when a cluster barrier times out.
 // Each operation's output is cut into super-tiles of up to 128 x 128 dealt to the cluster's
 // workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
+// FUSED: the plan's whole step (small_fused_prologue, the schedule, small_fused_apply).
+template <bool FUSED>
 __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
                                                                  SmallSchedule sc, int* err, int spin) {
     __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
+    __shared__ float red[kSmallWaves];
     static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
     const int k = find_task(tl.starts, tl.n, blockIdx.x);
     const OrthoMat& M = mats[tl.order[k]];
@@ -238,6 +417,9 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
     const SmallView V = small_view(M);
     int* const bar = M.small_bar;
     const int set = M.rows == M.cols ? 0 : 1;
+    const unsigned tslot = ts_begin();
+    if constexpr (FUSED) small_fused_prologue(M, V, member, C, red, stages, bar, err, spin);
+    ts_point(tslot, 1);
 
     const int nops = sc.n[set];
     for (int q = 0; q < nops; ++q) {
@@ -304,6 +486,11 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
         }
         cluster_barrier(bar, C, err, spin);
     }
+    ts_point(tslot, 2);
+    if constexpr (FUSED) small_fused_apply(M, member, C, red, stages);
+    // kind 4 (small), fused flag, the member and the matrix's index in the plan
+    ts_end(tslot, 4ull | (FUSED ? 16ull : 0ull) | (static_cast<unsigned long long>(member) << 8) |
+                      (static_cast<unsigned long long>(tl.order[k]) << 20));
 }
 
 }  // namespace thorn

@@ -170,6 +170,12 @@ struct thorn_ortho_plan {
     std::vector<char> host_table;   // host side of the table for thorn_ortho_step_noalloc
     LaunchTimer timer;
     int spin_limit = 1 << 24;   // polls of the small-matrix cluster barrier before it gives up
+    // The last filled table's step runs as one ns_small_kernel<true> launch (see ns_small.hip):
+    // every matrix on the small path, none with decouple_md, Magma or an Adam step, all applied,
+    // and the workspace the one this plan stepped on last, whose cluster barriers its previous
+    // launch left at count 0. small_fusion: thorn_ortho_set_small_fusion.
+    bool small_fusion = true;
+    bool fused_small = false;
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
     const void* filled_ws = nullptr;   // workspace of the last fill_table
@@ -767,6 +773,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     char* ws = static_cast<char*>(workspace);
     auto at = [ws](size_t o) -> void* { return o == kNone ? nullptr : ws + o; };
     bool any_exact = false, any_apply = false, any_adam_apply = false;
+    bool fuse = plan->small_fusion && n > 0 && own_workspace && workspace == plan->stepped_ws;
     auto* mats = reinterpret_cast<thorn::OrthoMat*>(host + plan->mats_off);
     for (int i = 0; i < n; ++i) {
         const MatLayout& L = plan->mats[i];
@@ -845,6 +852,8 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
             flags |= thorn::kFlagMagma;
         }
         M.flags = flags;
+        fuse = fuse && L.is_small && !(flags & (thorn::kFlagMD | thorn::kFlagMDScalar | thorn::kFlagMagma)) &&
+               (flags & thorn::kFlagApply);
         if (L.adam) any_adam_apply = any_adam_apply || (flags & thorn::kFlagApply);
         else any_apply = any_apply || (flags & thorn::kFlagApply);
         M.eta = S.eta; M.wd = S.weight_decay; M.beta1 = S.beta1;
@@ -886,6 +895,7 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     applied_only(plan->small_order, plan->small, small_blocks, plan->small_live);
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
+    plan->fused_small = fuse;
     plan->any_exact = any_exact;
     plan->any_apply = any_apply;
     plan->any_adam_apply = any_adam_apply;
@@ -923,6 +933,37 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
     hipLaunchKernelGGL(__VA_ARGS__);                       \
     tm.end(slot, st);                                      \
     if ((rc = check_launch(name))) return rc;
+
+    // ns_small_kernel over small_live: the schedule of each small matrix (fused: the whole step)
+    auto launch_small = [&](bool fused, const NsSchedule* sched) -> int {
+        thorn::SmallSchedule ss{};
+        for (int q = 0; q < 2; ++q) {
+            if (!small_encode(sched[q], ss.op[q], ss.n[q]))
+                return fail(THORN_ERR_UNSUPPORTED, "thorn_ortho_step: more than " +
+                                                       std::to_string(thorn::kSmallMaxOps) +
+                                                       " Newton-Schulz operations for the small-matrix path");
+        }
+        if (fused) {
+            THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel<true>,
+                         dim3(plan->small_live.total), dim3(thorn::kSmallThreads), 0, st, mats,
+                         task_list(dev, plan->small_live), ss, status, plan->spin_limit);
+        } else {
+            THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel<false>,
+                         dim3(plan->small_live.total), dim3(thorn::kSmallThreads), 0, st, mats,
+                         task_list(dev, plan->small_live), ss, status, plan->spin_limit);
+        }
+        return THORN_OK;
+    };
+    if (plan->fused_small && iters > 0) {   // the whole step in one launch (ns_small.hip)
+        const NsSchedule sched[2] = {plain_schedule(iters, coeffs), gram_schedule(iters, restart_mask, coeffs)};
+        if (sched[0].ops.overflow() || sched[1].ops.overflow())
+            return fail(THORN_ERR_INVALID, "thorn_ortho_step: too many Newton-Schulz operations");
+        if ((rc = signal())) return rc;
+        if ((rc = launch_small(true, sched))) return rc;
+        plan->stepped_ws = plan->filled_ws;
+        note_step(plan);
+        return THORN_OK;
+    }
 
     THORN_LAUNCH(THORN_KIND_PRE, "ortho_pre_kernel", thorn::ortho_pre_kernel, dim3(plan->pre.total), dim3(256), 0,
                  st, mats, task_list(dev, plan->pre));
@@ -986,16 +1027,7 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
                      mats, tl[1], op[1], tl[0], op[0], square_first);
     }
     if (plan->small_live.n > 0) {   // every small matrix's whole schedule in one launch
-        thorn::SmallSchedule ss{};
-        for (int q = 0; q < 2; ++q) {
-            if (!small_encode(sched[q], ss.op[q], ss.n[q]))
-                return fail(THORN_ERR_UNSUPPORTED, "thorn_ortho_step: more than " +
-                                                       std::to_string(thorn::kSmallMaxOps) +
-                                                       " Newton-Schulz operations for the small-matrix path");
-        }
-        THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel, dim3(plan->small_live.total),
-                     dim3(thorn::kSmallThreads), 0, st, mats, task_list(dev, plan->small_live), ss, status,
-                     plan->spin_limit);
+        if ((rc = launch_small(false, sched))) return rc;
     }
     if (plan->rs_live.n > 0) {
         const thorn::TaskList rs = task_list(dev, plan->rs_live);
@@ -1071,6 +1103,12 @@ int thorn_ortho_step_noalloc(thorn_ortho_plan_t plan, const ThornOrthoMatStep* s
 int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls) {
     if (!plan || polls < 0) return fail(THORN_ERR_INVALID, "thorn_ortho_set_spin_limit: null plan or negative limit");
     plan->spin_limit = polls;
+    return THORN_OK;
+}
+
+int thorn_ortho_set_small_fusion(thorn_ortho_plan_t plan, int enable) {
+    if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_set_small_fusion: null plan");
+    plan->small_fusion = enable != 0;
     return THORN_OK;
 }
 

@@ -5,6 +5,7 @@
 // lane l owns columns 4l..4l+3 (float4 path) or l, l+64, l+128, l+192 (scalar path). Partial sums
 // are written per tile and reduced later in a fixed order, so every result is bitwise
 // reproducible run to run (no float atomics).
+#pragma once
 #include "thorn_kernels.hpp"
 
 namespace thorn {
@@ -197,37 +198,50 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
 // runs over rows / 16 partials, the long part).
 constexpr int kNormSlices = 8;
 
+// ||u||_F^2 of one matrix from its tile partials, summed by threads 0..255 in turn and then across
+// their waves; a larger block gets the same sum (its other waves add zeros). Every thread returns it.
+__device__ __forceinline__ float norm_partials(const OrthoMat& M, float* scratch) {
+    const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
+    float s = 0.f;
+    if (threadIdx.x < 256)
+        for (int t = threadIdx.x; t < ntiles; t += 256) s += M.normpart[t];
+    return block_sum(s, scratch);
+}
+
+// ||u||_F + 1e-8 from ||u||_F^2 (thorn.py:633)
+__device__ __forceinline__ float norm_denom(float s) { return sqrtf(s) + 1e-8f; }
+
+// sigma = 1 / (||u||_F + 1e-8) and the first-iterate scales of one matrix from ||u||_F^2 (one
+// thread writes them).
+__device__ __forceinline__ void norm_write_scales(const OrthoMat& M, float s) {
+    const float denom = norm_denom(s);
+    const float sigma = 1.f / denom;
+    float x0scale = 1.f, repair = 0.f;
+    if (M.flags & kFlagPrescaled) {
+        // the stored iterate is u * 2^k; it matches the exact f16(sigma * u) range while 2^k is
+        // within a factor 16 of sigma, otherwise ortho_cast_kernel rebuilds it exactly
+        const float ratio = M.scal[kScalPrescale] / sigma;
+        if (ratio > 16.f || ratio < 0.0625f || !(ratio == ratio)) repair = 1.f;
+        else x0scale = sigma / M.scal[kScalPrescale];
+    }
+    M.scal[kScalSigma] = sigma;
+    M.scal[kScalDenom] = denom;
+    M.scal[kScalX0Scale] = x0scale;
+    M.scal[kScalRepair] = repair;
+    // next step's prescale: the power of two nearest sigma (kept when sigma is not finite)
+    if (sigma > 0.f && sigma < 3.0e38f) {
+        const int e = (int)rintf(log2f(sigma));
+        M.scal[kScalPrescale] = ldexpf(1.f, e < -120 ? -120 : (e > 120 ? 120 : e));
+    } else if (!(M.scal[kScalPrescale] > 0.f)) {
+        M.scal[kScalPrescale] = 1.f;
+    }
+}
+
 // sigma = 1 / (||u||_F + 1e-8), the first-iterate scales and Magma's s of one matrix.
 __device__ __forceinline__ void norm_sigma_magma(const OrthoMat* __restrict__ mats, int n_mats, const OrthoMat& M,
                                                  float* scratch) {
-    const int ntiles = M.mom_tiles_r * M.mom_tiles_c;
-    float s = 0.f;
-    for (int t = threadIdx.x; t < ntiles; t += 256) s += M.normpart[t];
-    s = block_sum(s, scratch);
-    if (threadIdx.x == 0) {
-        const float nrm = sqrtf(s);
-        const float denom = nrm + 1e-8f;
-        const float sigma = 1.f / denom;
-        float x0scale = 1.f, repair = 0.f;
-        if (M.flags & kFlagPrescaled) {
-            // the stored iterate is u * 2^k; it matches the exact f16(sigma * u) range while 2^k
-            // is within a factor 16 of sigma, otherwise ortho_cast_kernel rebuilds it exactly
-            const float ratio = M.scal[kScalPrescale] / sigma;
-            if (ratio > 16.f || ratio < 0.0625f || !(ratio == ratio)) repair = 1.f;
-            else x0scale = sigma / M.scal[kScalPrescale];
-        }
-        M.scal[kScalSigma] = sigma;
-        M.scal[kScalDenom] = denom;
-        M.scal[kScalX0Scale] = x0scale;
-        M.scal[kScalRepair] = repair;
-        // next step's prescale: the power of two nearest sigma (kept when sigma is not finite)
-        if (sigma > 0.f && sigma < 3.0e38f) {
-            const int e = (int)rintf(log2f(sigma));
-            M.scal[kScalPrescale] = ldexpf(1.f, e < -120 ? -120 : (e > 120 ? 120 : e));
-        } else if (!(M.scal[kScalPrescale] > 0.f)) {
-            M.scal[kScalPrescale] = 1.f;
-        }
-    }
+    const float s = norm_partials(M, scratch);
+    if (threadIdx.x == 0) norm_write_scales(M, s);
 
     // Magma (thorn.py:822-830): the first matrix of a parameter reduces the tile sums of all of
     // the parameter's matrices and moves s, which the apply kernels read later in the stream
@@ -309,45 +323,56 @@ __device__ __forceinline__ const _Float16* uout_of(const OrthoMat& M, const Uout
     return u.sel[M.s == M.l ? 0 : 1] == kXA ? M.xa : M.xb;
 }
 
+// sum_j u'_ij^2 of row i from its partial sums
+__device__ __forceinline__ float pnn_row_sum(const OrthoMat& M, int i) {
+    float rs = 0.f;
+    for (int t = 0; t < M.rowsq_tiles; ++t) rs += M.rowsqpart[(int64_t)t * M.rows + i];
+    return rs;
+}
+
+// s_i from the row's sum of squares (eps = torch.finfo(p.dtype).eps)
+__device__ __forceinline__ float pnn_row_scale(const OrthoMat& M, float rs) {
+    const float mean = rs / (float)M.cols;
+    return 1.f / sqrtf(fmaxf(mean, M.pnn_eps));
+}
+
+// gamma of one matrix, rows taken by threads 0..255 in turn (a larger block gets the same value:
+// its other waves add zeros); s_i into out[i] unless out is null (global or LDS memory). Every
+// thread returns gamma.
+__device__ __forceinline__ float pnn_gamma(const OrthoMat& M, float* scratch, float* out) {
+    float tot = 0.f, nw = 0.f;
+    if (threadIdx.x < 256)
+        for (int i = threadIdx.x; i < M.rows; i += 256) {
+            const float rs = pnn_row_sum(M, i);
+            const float s = pnn_row_scale(M, rs);
+            if (out) out[i] = s;
+            tot += rs;
+            nw += s * s * rs;
+        }
+    tot = block_sum(tot, scratch);
+    nw = block_sum(nw, scratch);
+    return sqrtf(tot) / fmaxf(sqrtf(nw), M.pnn_eps);
+}
+
 __global__ __launch_bounds__(256) void ortho_rowstats_kernel(const OrthoMat* __restrict__ mats,
                                                              const int32_t* __restrict__ idx) {
     __shared__ float scratch[4];
     const OrthoMat& M = mats[idx[blockIdx.x]];
-    const float eps = M.pnn_eps;   // torch.finfo(p.dtype).eps
-    float tot = 0.f, nw = 0.f;
-    for (int i = threadIdx.x; i < M.rows; i += 256) {
-        float rs = 0.f;
-        for (int t = 0; t < M.rowsq_tiles; ++t) rs += M.rowsqpart[(int64_t)t * M.rows + i];
-        const float mean = rs / (float)M.cols;
-        const float s = 1.f / sqrtf(fmaxf(mean, eps));
-        M.rowscale[i] = s;
-        tot += rs;
-        nw += s * s * rs;
-    }
-    tot = block_sum(tot, scratch);
-    nw = block_sum(nw, scratch);
-    if (threadIdx.x == 0) M.scal[kScalGamma] = sqrtf(tot) / fmaxf(sqrtf(nw), eps);
+    const float gamma = pnn_gamma(M, scratch, M.rowscale);
+    if (threadIdx.x == 0) M.scal[kScalGamma] = gamma;
 }
 
-// p <- p - eta * cwd((u' * s_i) * gamma) over per-row-normalized matrices, p <- p - eta * cwd(u')
-// over the other small-path matrices (whose u' ns_small_kernel leaves in xa), plus p^2 partials
-// for md.
-__global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
-                                                              UoutSel usel) {
-    __shared__ float scratch[4];
-    const int b = blockIdx.x;
-    const int k = find_task(tl.starts, tl.n, b);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int local = b - tl.starts[k];
+// p <- p - eta * cwd((u' * s_i) * gamma) on elementwise tile `local` of a matrix (per-row
+// normalized) or p <- p - eta * cwd(u') (another small-path matrix), by 256 threads t256 = 0..255
+// in the tile layout; returns this thread's sum of p^2 after the update. scale(row) gives s_i.
+template <class RowScale>
+__device__ __forceinline__ float pnn_apply_tile(const OrthoMat& M, int local, int t256, const _Float16* uout,
+                                                float gamma, RowScale scale) {
     const int tr = local / M.mom_tiles_c, tc = local % M.mom_tiles_c;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = t256 & 63, wave = t256 >> 6;
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
-    if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
     const bool pnn = M.flags & kFlagPNN;
-    const float gamma = pnn ? M.scal[kScalGamma] : 1.f;
     const float eta = (M.flags & kFlagMagma) ? M.eta * ldg<float>(M.magma_s) : M.eta;   // thorn.py:1405
-    const _Float16* const uout = (M.flags & kFlagSmall) ? M.xa : uout_of(M, usel);
-    const bool md = M.flags & (kFlagMD | kFlagMDScalar);
     const bool vec = M.flags & kFlagVec4;
     const int nrows = M.rows - r0;
     float psq = 0.f;
@@ -367,7 +392,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             const int row = r0 + rr;
             pv[rr] = ldg_nt<float4>(M.p + (int64_t)row * M.cols + c);
             uv[rr] = ldg_nt<half4>(uout + (int64_t)row * M.ldx + c);
-            sv[rr] = pnn ? ldg<float>(M.rowscale + row) : 1.f;
+            sv[rr] = pnn ? scale(row) : 1.f;
         }
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -385,7 +410,7 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
         for (int rr = 0; rr < 4; ++rr) {
             const int row = r0 + rr;
             if (row >= M.rows) break;
-            const float s = pnn ? M.rowscale[row] : 1.f;
+            const float s = pnn ? scale(row) : 1.f;
             const int64_t rbase = (int64_t)row * M.cols;
             const _Float16* urow = uout + (int64_t)row * M.ldx;
 #pragma unroll
@@ -399,7 +424,25 @@ __global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __
             }
         }
     }
-    if (md) {
+    return psq;
+}
+
+// pnn_apply_tile over per-row-normalized matrices and the other small-path matrices (whose u'
+// ns_small_kernel leaves in xa), s_i and gamma from ortho_rowstats_kernel, plus p^2 partials for
+// md.
+__global__ __launch_bounds__(256) void ortho_pnn_apply_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
+                                                              UoutSel usel) {
+    __shared__ float scratch[4];
+    const int b = blockIdx.x;
+    const int k = find_task(tl.starts, tl.n, b);
+    const OrthoMat& M = mats[tl.order[k]];
+    const int local = b - tl.starts[k];
+    if (!(M.flags & kFlagApply)) return;   // not due this step: p is left as it is
+    const float gamma = (M.flags & kFlagPNN) ? M.scal[kScalGamma] : 1.f;
+    const _Float16* const uout = (M.flags & kFlagSmall) ? M.xa : uout_of(M, usel);
+    const float psq = pnn_apply_tile(M, local, threadIdx.x, uout, gamma,
+                                     [&](int row) { return ldg<float>(M.rowscale + row); });
+    if (M.flags & (kFlagMD | kFlagMDScalar)) {
         const float t = block_sum(psq, scratch);
         if (threadIdx.x == 0) M.psqpart[local] = t;
     }
