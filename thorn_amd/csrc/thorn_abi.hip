@@ -841,8 +841,9 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
             flags |= thorn::kFlagVec4;
         // The first iterate of a large matrix is written directly in f16 with the previous step's
         // power-of-two scale (one pass less over u); small matrices, whose Newton-Schulz rounding
-        // is not averaged out, and decouple_md ones take the exact form of thorn.py:632-635.
-        if (workspace == plan->stepped_ws && own_workspace && !md && !mds &&
+        // is not averaged out, take the exact form of thorn.py:632-635 (and Adam-step tensors
+        // have no iterate).
+        if (!L.adam && workspace == plan->stepped_ws && own_workspace &&
             int64_t(L.rows) * L.cols >= kPrescaleMinElems)
             flags |= thorn::kFlagPrescaled;
         else if (!L.adam) any_exact = true;

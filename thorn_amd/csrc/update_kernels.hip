@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void ortho_pre_kernel(const OrthoMat* __restri
     const int r0 = tr * kTileR + wave * 4, c0 = tc * kTileC;
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
     const bool vec = M.flags & kFlagVec4;
-    const bool presc = M.flags & kFlagPrescaled;   // never combined with md
+    const bool presc = M.flags & kFlagPrescaled;   // never with kFlagAdam (no iterate)
     const bool magma = M.flags & kFlagMagma;
     const float prescale = presc ? M.scal[kScalPrescale] : 1.f;
     const float beta1 = M.beta1;
