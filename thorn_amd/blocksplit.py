@@ -54,6 +54,8 @@ def main(argv=None) -> int:
     fetch = lib.thorn_block_timestamps
     fetch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     fetch.restype = ctypes.c_int
+    lib.thorn_small_op_timestamps.argtypes = [ctypes.c_void_p]
+    lib.thorn_small_op_timestamps.restype = ctypes.c_int
     slots = 262144
     buf = np.zeros(12 * slots, dtype=np.uint64)
     n = np.zeros(1, dtype=np.uint32)
@@ -110,6 +112,23 @@ def main(argv=None) -> int:
             print(f'| {shape} | {m.sum()} | {(rs[m].min() - s0) / 100:.1f} | {((rp[m] - rs[m]) / 100).max():.1f} | '
                   f'{((rl[m] - rp[m]) / 100).max():.1f} | {((re[m] - rl[m]) / 100).max():.1f} | '
                   f'{(re[m].max() - s0) / 100:.1f} |')
+        # the last cluster to finish: per operation, from the first member's start to the last
+        # member's products, its stores, and the barrier until the last member starts the next one
+        sop = np.zeros(4096 * 64 * 3, dtype=np.uint64)
+        if lib.thorn_small_op_timestamps(sop.ctypes.data) == 0:
+            sop = sop.reshape(4096, 64, 3).astype(np.int64)
+            crit = int(mat[small][np.argmax(re[small])])
+            rows_ = [i for i in np.nonzero(small & (mat == crit))[0] if i < 4096]
+            ops = sop[rows_]                      # members x 64 x 3
+            nops = int(((ops[:, :, 0] >= rs[rows_, None]) & (ops[:, :, 0] <= re[rows_, None])).all(axis=0).sum())
+            print(f'\n{shapes[crit] if crit < len(shapes) else crit}, per operation (us): products | stores | '
+                  'barrier to the next operation')
+            line = []
+            for q in range(nops):
+                st, pr, sd = ops[:, q, 0].min(), ops[:, q, 1].max(), ops[:, q, 2].max()
+                nxt = ops[:, q + 1, 0].max() if q + 1 < nops else rl[rows_].max()
+                line.append(f'{q}: {(pr - st) / 100:.1f} | {(sd - pr) / 100:.1f} | {(nxt - sd) / 100:.1f}')
+            print('; '.join(line))
         keep = ~small
         if not keep.any():
             return 0

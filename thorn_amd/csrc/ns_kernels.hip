@@ -75,12 +75,20 @@ __device__ __forceinline__ void ts_point(unsigned slot, int k) {
         g_ts[12 * slot + 4 + k] = __builtin_amdgcn_s_memtime();
     }
 }
+// ... and per operation q < 64 of its schedule (workgroup slots below kSopSlots): the operation's
+// start [0], its products done [1], its stores issued [2] (the barrier follows)
+constexpr unsigned kSopSlots = 4096;
+__device__ unsigned long long g_sop[kSopSlots * 64 * 3];
+__device__ __forceinline__ void ts_op(unsigned slot, int q, int k) {
+    if (threadIdx.x == 0 && slot < kSopSlots && q < 64) g_sop[(slot * 64 + q) * 3 + k] = __builtin_amdgcn_s_memrealtime();
+}
 #else
 __device__ __forceinline__ void ts_loop_start() {}
 __device__ __forceinline__ void ts_mark(unsigned, int) {}
 __device__ __forceinline__ unsigned ts_begin() { return 0; }
 __device__ __forceinline__ void ts_end(unsigned, unsigned long long) {}
 __device__ __forceinline__ void ts_point(unsigned, int) {}
+__device__ __forceinline__ void ts_op(unsigned, int, int) {}
 #endif
 
 __device__ __forceinline__ Operand iterate_operand(const OrthoMat& M, int xsel) {

@@ -90,20 +90,28 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int s
 // r * 64 + (c ^ ((r >> 2) & 3)) * 16: 16 lanes reading rows r..r+15 at one chunk cover all banks).
 // A ring of kSmallStages stages is filled by direct global-to-LDS loads, one 1 KB load per wave
 // per chunk (its 64 lanes fill 64 consecutive 16-byte slots: lane slot s holds the chunk whose
-// swizzled position is s), kSmallStages - 1 chunks ahead of the MFMAs: the products here are too
-// short to cover a load's latency, so three chunks (a K of 96) are in flight. Between products the
-// ring holds the waves' epilogue staging tiles.
-constexpr int kSmallStages = 4;
+// swizzled position is s), kSmallStages - 1 chunks ahead of the MFMAs. Two chunks in flight are
+// as fast as three (5.4 against 5.5 us per 256 x 256 x 256 product), and seven are slower (6.7 us):
+// the loop's time per chunk follows the LDS traffic of its 16 waves' fragment reads (64 KB per
+// chunk for a 128 x 128 super-tile) more than the loads' latency. Between products the ring holds
+// the waves' epilogue staging tiles (and, in the fused step, the first iterate's transposes).
+constexpr int kSmallStages = 3;
 constexpr int kSmallStageBytes = 2 * 128 * 64;   // A rows [0, 128), then BT rows [0, 128)
 
 // This wave's direct loads except the newest n (0 <= n <= kSmallStages - 2, wave-uniform) are
 // complete, then the block barrier.
 __device__ __forceinline__ void wait_loads_barrier(int n) {
-    if (n >= 2) asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory"); break;
+        case 5: asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory"); break;
+    }
 }
-static_assert(kSmallStages - 2 == 2, "wait_loads_barrier covers 0 .. kSmallStages - 2");
+static_assert(kSmallStages - 2 <= 6, "wait_loads_barrier covers 0 .. kSmallStages - 2");
 
 // acc (this wave's tile of the super-tile, if it has one) = A[M0.., 0:K] * B[0:K, N0..] with A
 // row-major (lda) and B given by its transpose BT row-major (ldb), K a multiple of 32, every
@@ -424,6 +432,8 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
     const int nops = sc.n[set];
     for (int q = 0; q < nops; ++q) {
         const SmallOp op = sc.op[set][q];
+        ts_op(tslot, q, 0);
+        ts_op(tslot, q, 1);   // kept by a workgroup with no super-tile in this operation
         // output rows x cols and the operands of this operation
         const int orows = V.sp, ocols = op.kind == kOpUpdate ? V.lp : V.sp;
         const _Float16 *A, *BT, *CT = nullptr;
@@ -460,6 +470,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             if (mine && CT) small_load_c(cv, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
             const floatx16 acc = small_block(stages, M.zero, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine,
                                              ti, tj);
+            ts_op(tslot, q, 1);
             if (!mine) continue;
             const float alpha = op.kind == kOpSym ? op.alpha : 1.f;
             if (CT) small_stage<true>(acc, stage, alpha, op.beta, cv, lane);
@@ -484,6 +495,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
                 small_store(stage, V.xw(xo), V.lp, V.xwt(xo), V.sp, m0, n0, lane);
             }
         }
+        ts_op(tslot, q, 2);
         cluster_barrier(bar, C, err, spin);
     }
     ts_point(tslot, 2);
