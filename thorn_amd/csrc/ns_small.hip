@@ -84,6 +84,76 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int s
     __syncthreads();
 }
 
+// The same barrier for a cluster whose workgroups all run on one XCD, so that they share its L2:
+// the protocol of a workgroup split over CUs (LLVM's gfx942 memory model, workgroup scope in
+// threadgroup-split mode). Each wave's stores are complete in the L2 before the arrival (vmcnt(0)),
+// and after the departure the CU's L1 is invalidated (buffer_inv sc0), so the loads that follow
+// read the L2; the L2 is neither written back nor invalidated, as the agent-scope barrier does it.
+// The count and generation are accessed exactly as there (the same atomics and polling loads).
+__device__ __forceinline__ void cluster_barrier_xcd(int* bar, int C, int* err, int spin) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (C > 1 && threadIdx.x == 0) {
+        int* cnt = bar;
+        int* gen = bar + 1;
+        const int g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the generation is read before arriving
+        const int a = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a == C - 1) {
+            __hip_atomic_fetch_add(cnt, -C, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the count is reset before the release
+            __hip_atomic_fetch_add(gen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            int it = 0;
+            while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
+                if (it++ >= spin) {
+                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+}
+
+// The XCD (XCC) this workgroup runs on.
+__device__ __forceinline__ int xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return static_cast<int>(x & 0xF);
+}
+
+// A cluster's barriers. At the start each member stores its XCC id in the barrier's words and
+// meets the others at an agent-scope barrier (before the kernel has written anything, so it has
+// little to write back); then each member reads all the ids, and when they are equal (the launch
+// placed the cluster on one XCD: block b runs on XCD b mod 8, and the block map gives a cluster's
+// members one residue) every later barrier is the XCD-local one. The placement is a dispatch
+// order, not a guarantee, so the ids decide: with members on two XCDs every barrier stays agent
+// scope.
+struct SmallSync {
+    int* bar;   // count, generation, then one XCC id per member
+    int* err;
+    int C, spin;
+    bool local;
+    __device__ __forceinline__ SmallSync(int* bar_, int member, int C_, int* err_, int spin_)
+        : bar(bar_), err(err_), C(C_), spin(spin_), local(false) {
+        if (C > 1) {
+            if (threadIdx.x == 0) bar[2 + member] = xcc_id();
+            cluster_barrier(bar, C, err, spin);
+            bool same = true;
+            for (int i = 1; i < C; ++i) same = same && bar[2 + i] == bar[2];
+            local = __builtin_amdgcn_readfirstlane(same ? 1 : 0) != 0;
+        }
+    }
+    __device__ __forceinline__ void wait() {
+        if (local) cluster_barrier_xcd(bar, C, err, spin);
+        else cluster_barrier(bar, C, err, spin);
+    }
+};
+constexpr int kSmallBarWords = 2 + 16;   // the largest cluster has 16 members
+
 // Operand panels in LDS: a super-tile of up to 128 x 128 outputs (up to 16 tiles of 32 x 32, one
 // per wave) is computed from K chunks of 32: rows [M0, M0+SM) of A and [N0, N0+SN) of BT, 64
 // bytes each, in the K-major stage layout of the large-matrix GEMM (chunk c of row r at
@@ -353,7 +423,7 @@ __device__ __forceinline__ void small_x0_tile(const OrthoMat& M, const SmallView
 // threads as block_sum adds them), a cluster barrier, the norm and, in member 0, the matrix's
 // scalars, the first iterate f16(u / (||u|| + 1e-8)) and its padding, a cluster barrier.
 __device__ __forceinline__ void small_fused_prologue(const OrthoMat& M, const SmallView& V, int member, int C,
-                                                     float* red, char* stages, int* bar, int* err, int spin) {
+                                                     float* red, char* stages, SmallSync& sync) {
     const int q = threadIdx.x / kQuarter, t256 = threadIdx.x % kQuarter;
     const int ntiles = M.mom_tiles_r * M.mom_tiles_c, per = 4 * C;
     for (int t0 = 0; t0 < ntiles; t0 += per) {   // the same trip count in every quarter (barriers)
@@ -370,7 +440,7 @@ __device__ __forceinline__ void small_fused_prologue(const OrthoMat& M, const Sm
             M.normpart[t] = sum;
         }
     }
-    cluster_barrier(bar, C, err, spin);
+    sync.wait();
     const float s = norm_partials(M, red);
     if (member == 0 && threadIdx.x == 0) norm_write_scales(M, s);
     const float denom = norm_denom(s);
@@ -380,7 +450,7 @@ __device__ __forceinline__ void small_fused_prologue(const OrthoMat& M, const Sm
         const int t = t0 + 4 * member + q;
         small_x0_tile(M, V, t < ntiles ? t : 0, t256, t < ntiles, denom, tt);
     }
-    cluster_barrier(bar, C, err, spin);
+    sync.wait();
 }
 
 // After the schedule (its last barrier has made every member's u' and row sums visible): gamma and
@@ -405,8 +475,9 @@ __device__ __forceinline__ void small_fused_apply(const OrthoMat& M, int member,
     }
 }
 
-// One launch: the schedule of every small matrix in the task list (blocks starts[k] ..
-// starts[k+1]-1 are the cluster of matrix order[k]). err: set when a cluster barrier times out.
+// One launch: the schedule of every small matrix in the task list, whose block map gives each block
+// its matrix and its place in the matrix's cluster (thorn_ortho_fill_table gives a cluster's blocks
+// one residue mod 8, so that they run on one XCD). err: set when a cluster barrier times out.
 // Each operation's output is cut into super-tiles of up to 128 x 128 dealt to the cluster's
 // workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
 // FUSED: the plan's whole step (small_fused_prologue, the schedule, small_fused_apply).
@@ -416,17 +487,19 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
     __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
     __shared__ float red[kSmallWaves];
     static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
-    const int k = find_task(tl.starts, tl.n, blockIdx.x);
-    const OrthoMat& M = mats[tl.order[k]];
-    const int member = blockIdx.x - tl.starts[k];
-    const int C = tl.starts[k + 1] - tl.starts[k];
+    // the block map: (matrix, member | C << 8), or matrix -1 for a block that has no work
+    const int mat = tl.map[2 * blockIdx.x];
+    if (mat < 0) return;
+    const int mc = tl.map[2 * blockIdx.x + 1];
+    const OrthoMat& M = mats[mat];
+    const int member = mc & 255, C = mc >> 8;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     _Float16* const stage = reinterpret_cast<_Float16*>(stages) + wave * 32 * kStageLd;
     const SmallView V = small_view(M);
-    int* const bar = M.small_bar;
+    SmallSync sync(M.small_bar, member, C, err, spin);
     const int set = M.rows == M.cols ? 0 : 1;
     const unsigned tslot = ts_begin();
-    if constexpr (FUSED) small_fused_prologue(M, V, member, C, red, stages, bar, err, spin);
+    if constexpr (FUSED) small_fused_prologue(M, V, member, C, red, stages, sync);
     ts_point(tslot, 1);
 
     const int nops = sc.n[set];
@@ -496,13 +569,13 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             }
         }
         ts_op(tslot, q, 2);
-        cluster_barrier(bar, C, err, spin);
+        sync.wait();
     }
     ts_point(tslot, 2);
     if constexpr (FUSED) small_fused_apply(M, member, C, red, stages);
     // kind 4 (small), fused flag, the member and the matrix's index in the plan
     ts_end(tslot, 4ull | (FUSED ? 16ull : 0ull) | (static_cast<unsigned long long>(member) << 8) |
-                      (static_cast<unsigned long long>(tl.order[k]) << 20));
+                      (static_cast<unsigned long long>(mat) << 20));
 }
 
 }  // namespace thorn

@@ -167,6 +167,10 @@ struct thorn_ortho_plan {
     // every step and allocates nothing
     std::vector<int64_t> mom_blocks, sym_blocks, g3_blocks, small_blocks, one_block;
     std::vector<int32_t> kept;
+    // ns_small_kernel's block map (room for 8 blocks per cluster member) and its clusters sorted by
+    // size (filled every step, capacity reserved at plan creation)
+    size_t small_map = 0;
+    std::vector<int32_t> small_sorted;
     std::vector<char> host_table;   // host side of the table for thorn_ortho_step_noalloc
     LaunchTimer timer;
     int spin_limit = 1 << 24;   // polls of the small-matrix cluster barrier before it gives up
@@ -629,7 +633,7 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         if (L.is_small) {
             const size_t sp = align_up(L.s, 32), lp = align_up(L.l, 32);
             L.small = take((8 * sp * sp + 4 * sp * lp) * 2);
-            L.small_bar = take(2 * sizeof(int));
+            L.small_bar = take(thorn::kSmallBarWords * sizeof(int));
         } else {
             L.small = L.small_bar = kNone;
         }
@@ -736,6 +740,9 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
     plan->md = add_tasks(off, plan->md_order, mom_blocks);
     plan->adam = add_tasks(off, plan->adam_order, mom_blocks);
     plan->small = add_tasks(off, plan->small_order, small_blocks);
+    plan->small_map = off;
+    off = align_up(off + 2 * sizeof(int32_t) * std::max<int64_t>(1, 8 * int64_t(plan->small.total)), 16);
+    plan->small_sorted.reserve(plan->small_order.size());
     plan->table_bytes = off;
     plan->host_table.assign(plan->table_bytes, 0);
     if (int64_t(plan->sym[0].total) + plan->sym[1].total + plan->g3[0].total + plan->g3[1].total >=
@@ -899,6 +906,41 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     applied_only(plan->rs_order, plan->rs, one_block, plan->rs_live);
     applied_only(plan->adam_order, plan->adam, mom_blocks, plan->adam_live);
     applied_only(plan->small_order, plan->small, small_blocks, plan->small_live);
+    {
+        // ns_small_kernel's block map: block b runs on XCD b mod 8, so each cluster takes blocks of
+        // one residue x (x + 8 j for consecutive j), the clusters dealt largest first to the XCD
+        // with the fewest blocks; blocks past an XCD's share get matrix -1 and exit. A cluster on
+        // one XCD shares its L2, and its barriers can then skip the L2 maintenance (ns_small.hip).
+        std::vector<int32_t>& srt = plan->small_sorted;
+        srt.clear();
+        for (int32_t i : plan->small_order)
+            if (mats[i].flags & thorn::kFlagApply) srt.push_back(i);
+        for (size_t a = 1; a < srt.size(); ++a)   // insertion sort by cluster size, stable
+            for (size_t b = a; b > 0 && small_blocks[srt[b]] > small_blocks[srt[b - 1]]; --b) std::swap(srt[b], srt[b - 1]);
+        int32_t fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int32_t* smap = reinterpret_cast<int32_t*>(host + plan->small_map);
+        for (int32_t i : srt) {
+            int x = 0;
+            for (int y = 1; y < 8; ++y)
+                if (fill[y] < fill[x]) x = y;
+            const int32_t C = static_cast<int32_t>(small_blocks[i]);
+            for (int32_t m = 0; m < C; ++m) {
+                const int64_t b = x + 8 * int64_t(fill[x] + m);
+                smap[2 * b] = i;
+                smap[2 * b + 1] = m | (C << 8);
+            }
+            fill[x] += C;
+        }
+        int32_t most = 0;
+        for (int x = 0; x < 8; ++x) most = std::max(most, fill[x]);
+        for (int x = 0; x < 8; ++x)
+            for (int32_t j = fill[x]; j < most; ++j) {
+                smap[2 * (x + 8 * int64_t(j))] = -1;
+                smap[2 * (x + 8 * int64_t(j)) + 1] = 0;
+            }
+        plan->small_live.total = 8 * most;
+        plan->small_live.map = plan->small_map;
+    }
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
     plan->filled_ws = workspace;
     plan->fused_small = fuse;
