@@ -403,12 +403,14 @@ class _TableUpload:
     def __init__(self, nbytes: int):
         self.nbytes = nbytes
         self.bufs = [torch.empty(max(1, nbytes), dtype=torch.uint8, pin_memory=True) for _ in range(self.RING)]
+        self.views = [b.numpy()[:nbytes] for b in self.bufs]   # the same pinned bytes, for numpy
         self.events: list = [None] * self.RING
         self.i = 0
         # what the device table holds (its last upload): a table equal to it is not copied again
         # (the kernels only read the table; with fixed gradient buffers and hyperparameters a
-        # plan's table repeats from step to step)
-        self.last = torch.empty(max(1, nbytes), dtype=torch.uint8)
+        # plan's table repeats from step to step). numpy compares and copies these few KB in
+        # about a microsecond, a tenth of what the torch calls took.
+        self.last = np.empty(max(1, nbytes), dtype=np.uint8)[:nbytes]
         self.last_dst = None
 
     def host(self) -> torch.Tensor:
@@ -422,11 +424,11 @@ class _TableUpload:
     def upload(self, dst: torch.Tensor) -> None:
         """Copies the buffer of host() into dst on the current stream (unless dst holds it)."""
         i = self.i
-        src = self.bufs[i][:self.nbytes]
+        view = self.views[i]
         key = (dst.data_ptr(), dst.device)
-        if self.last_dst != key or not torch.equal(src, self.last[:self.nbytes]):
-            dst[:self.nbytes].copy_(src, non_blocking=True)
-            self.last[:self.nbytes].copy_(src)
+        if self.last_dst != key or not np.array_equal(view, self.last):
+            dst[:self.nbytes].copy_(self.bufs[i][:self.nbytes], non_blocking=True)
+            self.last[:] = view
             self.last_dst = key
         if self.events[i] is None:
             self.events[i] = torch.cuda.Event()
@@ -553,6 +555,9 @@ class _OrthoRunner:
         self.small = ((np.minimum(self.rows, self.cols) <= SMALL_MAX_S)
                       & (self.rows * self.cols < SMALL_MAX_ELEMS))
         self.status = _StatusWatch(self) if self.small.any() and not adam else None
+        # per-step constants computed again only when what they depend on changes
+        self._scale_key = self._eps_key = self._coeffs_key = None
+        self._scale = self._eps = self._coeffs = None
 
     @property
     def workspace(self) -> torch.Tensor:
@@ -592,13 +597,19 @@ class _OrthoRunner:
             steps['adam_degenerate'] = (rect == 0.0).astype(np.int32)[own]
         else:
             # the group is rebuilt every step, so scaling_mode and target_rms edits take effect as
-            # in the reference (thorn.py:1405)
-            scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)
-            steps['eta'] = (group.lr * scale)[own]
+            # in the reference (thorn.py:1405); the scales depend on them and the (fixed) shapes
+            skey = (group.scaling_mode_, group.target_rms)
+            if self._scale_key != skey:
+                self._scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)[own]
+                self._scale_key = skey
+            steps['eta'] = group.lr * self._scale
         steps['weight_decay'] = group.weight_decay
         steps['beta1'] = group.betas[0]
-        steps['pnn_eps'] = np.asarray([torch.finfo(getattr(p, '_thorn_dtype', p.dtype)).eps
-                                       for p in params], dtype=np.float32)[own]
+        dts = tuple(getattr(p, '_thorn_dtype', p.dtype) for p in params)
+        if self._eps_key != dts:
+            self._eps = np.asarray([torch.finfo(d).eps for d in dts], dtype=np.float32)[own]
+            self._eps_key = dts
+        steps['pnn_eps'] = self._eps
         # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
         # momentum (and the decouple_md round trip) runs every step
         due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 and (unmasked is None or unmasked[id(p)])
@@ -648,7 +659,11 @@ class _OrthoRunner:
         host = self.upload.host()
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
         self.upload.upload(self.table)
-        coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
+        ckey = (tuple(group.coeffs[:group.iters]), group.iters)
+        if self._coeffs_key != ckey:
+            self._coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
+            self._coeffs_key = ckey
+        coeffs = self._coeffs
         if self.adam or not due.any():   # no polar factor this step: momentum (gains, Magma s) only
             coeffs = coeffs[:0]
         stream = torch.cuda.current_stream(self.device)
@@ -1046,7 +1061,8 @@ class THORN(Optimizer):
             # the reference's momentum step g + beta1 * m (thorn.py:1381) fails the same way
             raise RuntimeError('add(sparse, dense) is not supported: an orthogonalized parameter needs a '
                                'dense gradient')
-        if type(p.data).__name__ == 'DTensor' or type(g).__name__ == 'DTensor':
+        if ((type(p) is not torch.nn.Parameter and type(p) is not torch.Tensor and type(p.data).__name__ == 'DTensor')
+                or type(g).__name__ == 'DTensor'):
             raise NotImplementedError('DTensor / FSDP2 parameters are not implemented on the MI355X path')
         if g.shape != p.shape:
             raise AssertionError(f'gradient shape {tuple(g.shape)} != parameter shape {tuple(p.shape)}')
