@@ -26,7 +26,9 @@ def layout(tmp_path_factory):
     src = d / 'l.cpp'
     src.write_text(f'#include "{HDR}"\n'
                    'extern "C" int write_map(int32_t* m, const int32_t* o, int n, const int64_t* b) {\n'
-                   '    return thorn_layout::write_block_map(m, o, n, b) ? 1 : 0;\n}\n')
+                   '    return thorn_layout::write_block_map(m, o, n, b) ? 1 : 0;\n}\n'
+                   'extern "C" long cluster_map(int32_t* m, const int32_t* l, int n, const int64_t* c, int32_t* s) {\n'
+                   '    return static_cast<long>(thorn_layout::write_cluster_map(m, l, n, c, s));\n}\n')
     so = d / 'l.so'
     res = subprocess.run([gxx, '-O2', '-std=c++17', '-shared', '-fPIC', str(src), '-o', str(so)],
                          capture_output=True, text=True)
@@ -34,6 +36,8 @@ def layout(tmp_path_factory):
     lib = ctypes.CDLL(str(so))
     lib.write_map.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int, ctypes.c_void_p]
     lib.write_map.restype = ctypes.c_int
+    lib.cluster_map.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] + [ctypes.c_void_p] * 2
+    lib.cluster_map.restype = ctypes.c_long
 
     def run(order, blocks):
         order = np.asarray(order, dtype=np.int32)
@@ -42,6 +46,18 @@ def layout(tmp_path_factory):
         m = np.full(2 * max(total, 1), -1, dtype=np.int32)
         assert lib.write_map(m.ctypes.data, order.ctypes.data, len(order), blocks.ctypes.data) == 1
         return m[:2 * total].reshape(total, 2)
+
+    def clusters(live, cluster_of):
+        live = np.asarray(live, dtype=np.int32)
+        cluster_of = np.asarray(cluster_of, dtype=np.int64)
+        cap = 8 * int(cluster_of[live].sum()) if len(live) else 8
+        m = np.full(2 * max(cap, 1), -7, dtype=np.int32)
+        srt = np.zeros(max(len(live), 1), dtype=np.int32)
+        grid = lib.cluster_map(m.ctypes.data, live.ctypes.data, len(live), cluster_of.ctypes.data, srt.ctypes.data)
+        assert 0 <= grid <= cap and grid % 8 == 0
+        assert (m[2 * grid:] == -7).all()   # nothing written past the grid
+        return grid, m[:2 * grid].reshape(grid, 2)
+    run.clusters = clusters
     return run
 
 
@@ -96,3 +112,38 @@ def test_config5_big_matrix_spread(layout):
     m = layout(np.arange(28), blocks)
     for lo, hi in chunks(int(blocks.sum())):
         assert (m[lo:lo + 128, 0] == 0).all() and (m[lo + 128:hi, 0] != 0).all()
+
+
+def test_small_cluster_map(layout):
+    """ns_small_kernel's block map (write_cluster_map): every (matrix, member) of the live list on
+    exactly one block, a cluster's members on consecutive blocks of one residue mod 8 (block b runs
+    on XCD b mod 8), the clusters dealt largest first to the XCD with the fewest blocks, blocks past
+    an XCD's share idle (-1), and the grid 8 times the largest share."""
+    rng = np.random.default_rng(11)
+    # config 4's seven matrices: clusters 1, 1, 1, 1, 1, 10, 1
+    grid, m = layout.clusters(list(range(7)), [1, 1, 1, 1, 1, 10, 1])
+    assert grid == 80
+    assert [int(b) for b in np.nonzero(m[:, 0] == 5)[0]] == [8 * j for j in range(10)]
+    for case in range(300):
+        n = int(rng.integers(1, 30))
+        cluster_of = rng.choice([1, 1, 1, 4, 6, 10, 16], size=n)
+        live = sorted(rng.choice(n, size=int(rng.integers(1, n + 1)), replace=False).tolist())
+        grid, m = layout.clusters(live, cluster_of)
+        share = [0] * 8
+        seen = {}
+        for b, (mat, mc) in enumerate(m):
+            if mat == -1:
+                assert mc == 0
+                continue
+            member, c = int(mc) & 255, int(mc) >> 8
+            assert c == cluster_of[mat] and (int(mat), member) not in seen, (case, b)
+            seen[(int(mat), member)] = b
+            share[b % 8] += 1
+        assert set(seen) == {(i, j) for i in live for j in range(int(cluster_of[i]))}, case
+        for i in live:
+            blocks = [seen[(i, j)] for j in range(int(cluster_of[i]))]
+            assert len({b % 8 for b in blocks}) == 1, (case, i, blocks)
+            assert [b // 8 for b in blocks] == list(range(blocks[0] // 8, blocks[0] // 8 + len(blocks)))
+        assert grid == 8 * max(share)
+        # greedy by size: the shares differ by at most the largest cluster
+        assert max(share) - min(share) <= max(int(cluster_of[i]) for i in live), (case, share)

@@ -15,6 +15,7 @@
 #pragma once
 #include <algorithm>
 #include <stdint.h>
+#include <utility>
 
 namespace thorn_layout {
 
@@ -72,6 +73,40 @@ inline bool write_block_map(int32_t* m, const int32_t* order, int n, const int64
         }
     }
     return true;
+}
+
+// Block map of ns_small_kernel: each matrix's cluster of workgroups (cluster_of[i] of them) on
+// one XCD. Block b runs on XCD b mod 8, so a cluster takes blocks of one residue x, x + 8 j for
+// consecutive j; clusters are dealt largest first (stable) to the XCD with the fewest blocks (the
+// lowest x on a tie). m[2b] = matrix, m[2b + 1] = member | C << 8, or m[2b] = -1 for a block past
+// its XCD's share. sorted: room for n entries (no allocation: fill_table runs every step). Returns
+// the launch's block count, 8 times the largest share; m needs 2 * 8 * sum(cluster_of) entries.
+inline int64_t write_cluster_map(int32_t* m, const int32_t* list, int n, const int64_t* cluster_of, int32_t* sorted) {
+    for (int k = 0; k < n; ++k) sorted[k] = list[k];
+    for (int a = 1; a < n; ++a)   // insertion sort by cluster size, stable
+        for (int b = a; b > 0 && cluster_of[sorted[b]] > cluster_of[sorted[b - 1]]; --b) std::swap(sorted[b], sorted[b - 1]);
+    int64_t fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < n; ++k) {
+        const int32_t i = sorted[k];
+        int x = 0;
+        for (int y = 1; y < 8; ++y)
+            if (fill[y] < fill[x]) x = y;
+        const int64_t C = cluster_of[i];
+        for (int64_t j = 0; j < C; ++j) {
+            const int64_t b = x + 8 * (fill[x] + j);
+            m[2 * b] = i;
+            m[2 * b + 1] = static_cast<int32_t>(j | (C << 8));
+        }
+        fill[x] += C;
+    }
+    int64_t most = 0;
+    for (int x = 0; x < 8; ++x) most = std::max(most, fill[x]);
+    for (int x = 0; x < 8; ++x)
+        for (int64_t j = fill[x]; j < most; ++j) {
+            m[2 * (x + 8 * j)] = -1;
+            m[2 * (x + 8 * j) + 1] = 0;
+        }
+    return 8 * most;
 }
 
 }  // namespace thorn_layout

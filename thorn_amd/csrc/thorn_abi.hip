@@ -907,38 +907,17 @@ int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* ste
     applied_only(plan->adam_order, plan->adam, mom_blocks, plan->adam_live);
     applied_only(plan->small_order, plan->small, small_blocks, plan->small_live);
     {
-        // ns_small_kernel's block map: block b runs on XCD b mod 8, so each cluster takes blocks of
-        // one residue x (x + 8 j for consecutive j), the clusters dealt largest first to the XCD
-        // with the fewest blocks; blocks past an XCD's share get matrix -1 and exit. A cluster on
-        // one XCD shares its L2, and its barriers can then skip the L2 maintenance (ns_small.hip).
-        std::vector<int32_t>& srt = plan->small_sorted;
-        srt.clear();
+        // ns_small_kernel's block map: each cluster on one XCD, whose L2 its workgroups then share
+        // (their barriers can skip the L2 maintenance, ns_small.hip)
+        std::vector<int32_t>& live = plan->small_sorted;   // capacity n since plan creation
+        live.clear();
         for (int32_t i : plan->small_order)
-            if (mats[i].flags & thorn::kFlagApply) srt.push_back(i);
-        for (size_t a = 1; a < srt.size(); ++a)   // insertion sort by cluster size, stable
-            for (size_t b = a; b > 0 && small_blocks[srt[b]] > small_blocks[srt[b - 1]]; --b) std::swap(srt[b], srt[b - 1]);
-        int32_t fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        int32_t* smap = reinterpret_cast<int32_t*>(host + plan->small_map);
-        for (int32_t i : srt) {
-            int x = 0;
-            for (int y = 1; y < 8; ++y)
-                if (fill[y] < fill[x]) x = y;
-            const int32_t C = static_cast<int32_t>(small_blocks[i]);
-            for (int32_t m = 0; m < C; ++m) {
-                const int64_t b = x + 8 * int64_t(fill[x] + m);
-                smap[2 * b] = i;
-                smap[2 * b + 1] = m | (C << 8);
-            }
-            fill[x] += C;
-        }
-        int32_t most = 0;
-        for (int x = 0; x < 8; ++x) most = std::max(most, fill[x]);
-        for (int x = 0; x < 8; ++x)
-            for (int32_t j = fill[x]; j < most; ++j) {
-                smap[2 * (x + 8 * int64_t(j))] = -1;
-                smap[2 * (x + 8 * int64_t(j)) + 1] = 0;
-            }
-        plan->small_live.total = 8 * most;
+            if (mats[i].flags & thorn::kFlagApply) live.push_back(i);
+        std::vector<int32_t>& srt = plan->kept;   // capacity n, free again after applied_only
+        srt.resize(live.size());
+        plan->small_live.total = static_cast<int32_t>(thorn_layout::write_cluster_map(
+            reinterpret_cast<int32_t*>(host + plan->small_map), live.data(), static_cast<int>(live.size()),
+            small_blocks.data(), srt.data()));
         plan->small_live.map = plan->small_map;
     }
     write_tasks(host, plan->md, plan->md_order, mom_blocks);
