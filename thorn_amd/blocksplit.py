@@ -114,20 +114,25 @@ def main(argv=None) -> int:
                   f'{(re[m].max() - s0) / 100:.1f} |')
         # the last cluster to finish: per operation, from the first member's start to the last
         # member's products, its stores, and the barrier until the last member starts the next one
-        sop = np.zeros(4096 * 64 * 3, dtype=np.uint64)
+        sop = np.zeros(4096 * 64 * 5, dtype=np.uint64)
         if lib.thorn_small_op_timestamps(sop.ctypes.data) == 0:
-            sop = sop.reshape(4096, 64, 3).astype(np.int64)
+            sop = sop.reshape(4096, 64, 5).astype(np.int64)
             crit = int(mat[small][np.argmax(re[small])])
             rows_ = [i for i in np.nonzero(small & (mat == crit))[0] if i < 4096]
             ops = sop[rows_]                      # members x 64 x 3
             nops = int(((ops[:, :, 0] >= rs[rows_, None]) & (ops[:, :, 0] <= re[rows_, None])).all(axis=0).sum())
-            print(f'\n{shapes[crit] if crit < len(shapes) else crit}, per operation (us): products | stores | '
-                  'barrier to the next operation')
+            print(f'\n{shapes[crit] if crit < len(shapes) else crit}, per operation (us): products (first K chunk '
+                  'landed + K loop + end) | stores | barrier to the next operation')
             line = []
             for q in range(nops):
                 st, pr, sd = ops[:, q, 0].min(), ops[:, q, 1].max(), ops[:, q, 2].max()
+                # members with a super-tile in this operation (the others keep older stamps)
+                w = (ops[:, q, 3] >= ops[:, q, 0]) & (ops[:, q, 3] <= ops[:, q, 2])
+                f0 = (ops[w, q, 3] - ops[w, q, 0]).mean() / 100 if w.any() else 0.0
+                lp = (ops[w, q, 4] - ops[w, q, 3]).mean() / 100 if w.any() else 0.0
                 nxt = ops[:, q + 1, 0].max() if q + 1 < nops else rl[rows_].max()
-                line.append(f'{q}: {(pr - st) / 100:.1f} | {(sd - pr) / 100:.1f} | {(nxt - sd) / 100:.1f}')
+                line.append(f'{q}: {(pr - st) / 100:.1f} ({f0:.1f} + {lp:.1f} + {(pr - st) / 100 - f0 - lp:.1f}) | '
+                            f'{(sd - pr) / 100:.1f} | {(nxt - sd) / 100:.1f}')
             print('; '.join(line))
         keep = ~small
         if not keep.any():

@@ -76,11 +76,14 @@ __device__ __forceinline__ void ts_point(unsigned slot, int k) {
     }
 }
 // ... and per operation q < 64 of its schedule (workgroup slots below kSopSlots): the operation's
-// start [0], its products done [1], its stores issued [2] (the barrier follows)
+// start [0], its products done [1], its stores issued [2] (the barrier follows), and inside the
+// product's K loop the first chunk landed in every wave [3] and the loop's end [4]
 constexpr unsigned kSopSlots = 4096;
-__device__ unsigned long long g_sop[kSopSlots * 64 * 3];
+constexpr int kSopWords = 5;
+__device__ unsigned long long g_sop[kSopSlots * 64 * kSopWords];
 __device__ __forceinline__ void ts_op(unsigned slot, int q, int k) {
-    if (threadIdx.x == 0 && slot < kSopSlots && q < 64) g_sop[(slot * 64 + q) * 3 + k] = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0 && slot < kSopSlots && q < 64)
+        g_sop[(slot * 64 + q) * kSopWords + k] = __builtin_amdgcn_s_memrealtime();
 }
 #else
 __device__ __forceinline__ void ts_loop_start() {}

@@ -190,7 +190,8 @@ static_assert(kSmallStages - 2 <= 6, "wait_loads_barrier covers 0 .. kSmallStage
 // in the ring); on return every load has landed and the stages are free.
 __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, const _Float16* A, int64_t lda,
                                                 const _Float16* BT, int64_t ldb, int M0, int N0, int sm, int sn,
-                                                int K, int wave, int lane, bool has_tile, int ti, int tj) {
+                                                int K, int wave, int lane, bool has_tile, int ti, int tj,
+                                                unsigned tslot = 0, int q = 0) {
     floatx16 acc = {};
     const int nk = K / 32;
     const int slot = wave * 64 + lane, part = slot >> 9, r = (slot >> 2) & 127;
@@ -214,6 +215,7 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
         // more, which then receives chunk kc + S - 1
         const int ahead = nk - 1 - kc < kSmallStages - 2 ? nk - 1 - kc : kSmallStages - 2;
         wait_loads_barrier(ahead);
+        if (kc == 0) ts_op(tslot, q, 3);
         if (kc + kSmallStages - 1 < nk) issue(kc + kSmallStages - 1);
         if (has_tile) {
             const char* st = stages + (kc % kSmallStages) * kSmallStageBytes;
@@ -225,6 +227,7 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
             }
         }
     }
+    ts_op(tslot, q, 4);
     __syncthreads();   // every wave is done with the stages
     return acc;
 }
@@ -542,7 +545,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             half4 cv[4] = {};
             if (mine && CT) small_load_c(cv, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
             const floatx16 acc = small_block(stages, M.zero, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine,
-                                             ti, tj);
+                                             ti, tj, tslot, q);
             ts_op(tslot, q, 1);
             if (!mine) continue;
             const float alpha = op.kind == kOpSym ? op.alpha : 1.f;

@@ -525,7 +525,8 @@ int thorn_block_timestamps(unsigned long long* host, unsigned* n) {
     if (hipMemcpyToSymbol(HIP_SYMBOL(thorn::g_ts_n), &z, sizeof(unsigned)) != hipSuccess) return THORN_ERR_HIP;
     return THORN_OK;
 }
-// ... and ns_small_kernel's per-operation timestamps (kSopSlots x 64 x 3 words, see ns_kernels.hip)
+// ... and ns_small_kernel's per-operation timestamps (kSopSlots x 64 x kSopWords words, see
+// ns_kernels.hip)
 int thorn_small_op_timestamps(unsigned long long* host) {
     if (hipMemcpyFromSymbol(host, HIP_SYMBOL(thorn::g_sop), sizeof(thorn::g_sop)) != hipSuccess) return THORN_ERR_HIP;
     return THORN_OK;
