@@ -613,7 +613,7 @@ def main() -> int:
         return vendor_gemm()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: this build has no multi-GPU path (each matrix\'s step '
-              'is independent; the sharding design is in DESIGN.md). Run with --gpus 1.', file=sys.stderr)
+              'is independent, so a group would shard by whole matrices). Run with --gpus 1.', file=sys.stderr)
         return 2
 
     import torch
