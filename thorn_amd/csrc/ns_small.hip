@@ -3,8 +3,9 @@
 //
 // The grouped 256 x 256-tile launches of ns_kernels.hip give a small matrix one tile per phase, so
 // its 18 phases cost 18 launch latencies. Here each small matrix gets a cluster of 1024-thread
-// workgroups (one for s <= 128, four for s <= 256) that runs every operation of the schedule in
-// turn, 32 x 32 output tiles dealt to its 16 * C waves, with a barrier between operations. The
+// workgroups (one for s <= 128; above, one per 128 x 128 super-tile of its largest output, 4 to
+// 16), placed on one XCD, that runs every operation of the schedule in turn, 32 x 32 output tiles
+// dealt to its 16 * C waves, with a barrier between operations (SmallSync). The
 // operands stay in the L2-resident workspace, each s x s result and each iterate also stored
 // transposed, so that every MFMA fragment, of A or of B, is one 16-byte load of a K-contiguous row.
 // Products are computed whole (no mirroring of a symmetric result), and every output is rounded to
