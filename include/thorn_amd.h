@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define THORN_ABI_VERSION 9
+#define THORN_ABI_VERSION 10
 
 enum {
     THORN_OK = 0,
@@ -138,6 +138,12 @@ int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls);
  * each matrix by its cluster of workgroups) instead of six; its results are bit for bit those of
  * the separate launches. On by default; enable = 0 keeps the separate launches (for comparison). */
 int thorn_ortho_set_small_fusion(thorn_ortho_plan_t plan, int enable);
+/* No counterpart in the reference. The small-matrix launch places each matrix's cluster of
+ * workgroups on one XCD and, when the workgroups find that they share one (their XCC ids agree),
+ * synchronizes them through that XCD's L2 instead of writing back and invalidating it at every
+ * barrier; results are bit for bit the same. On by default; enable = 0 keeps agent-scope barriers
+ * throughout (for comparison). */
+int thorn_ortho_set_small_xcd_barriers(thorn_ortho_plan_t plan, int enable);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,
                            void* table_dev, void* table_host);

@@ -1217,6 +1217,53 @@ def test_small_plan_fused_launch_equals_separate_launches():
     _log(f'[gpu]   launches of step 2: fused {counts["fused"]}, separate {counts["sep"]}')
 
 
+def test_small_xcd_barriers_equal_agent_barriers():
+    """The small-matrix launch's clusters sit on one XCD each and, their XCC ids agreeing,
+    synchronize through that XCD's L2 (stores complete before the arrival, the CU's L1 invalidated
+    after the departure) instead of writing back and invalidating the L2 at every barrier. Against
+    the same steps with agent-scope barriers throughout (thorn_ortho_set_small_xcd_barriers(plan,
+    0)), every parameter and state tensor is equal bit for bit after each of eight steps: config 4's
+    matrices and (640, 256), (512, 256), (200, 300), (130, 129) (clusters of 10, 8, 6 and 4), fused
+    from the second step on; a stale operand read would show as a difference."""
+    import bench
+    thorn_amd = _thorn()
+    lib = _lib()
+    _log('[gpu] small-matrix plans: XCD-local cluster barriers against agent-scope ones, bit for bit')
+    params_cpu, _, groups_cpu, _ = bench.build_workload(4, 'cpu')
+    g = torch.Generator().manual_seed(23)
+    extra = [torch.randn(r, c, generator=g) * 0.02 for r, c in ((640, 256), (512, 256), (200, 300), (130, 129))]
+
+    def make():
+        ps = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params_cpu]
+        xs = [torch.nn.Parameter(x.clone().to(DEV)) for x in extra]
+        groups = _clone_groups(groups_cpu, ps) + [dict(orthogonalize=True, params=xs, lr=2e-3, weight_decay=0.1)]
+        return ps + xs, thorn_amd.THORN(groups)
+
+    pa, local = make()
+    pb, agent = make()
+    for step in range(1, 9):
+        grads = [torch.randn(p.shape, generator=g) * 1e-2 for p in pa]
+        for p, q, gr in zip(pa, pb, grads):
+            p.grad = gr.to(DEV)
+            q.grad = gr.to(DEV)
+        local.step()
+        agent.step()
+        torch.cuda.synchronize()
+        if step == 1:   # the plans exist after the first step: agent-scope barriers from step 2 on
+            for r in agent._runners.values():
+                for pl in r.plans:
+                    if isinstance(pl, lib.OrthoPlan):
+                        pl.set_small_xcd_barriers(False)
+        for i, (p, q) in enumerate(zip(pa, pb)):
+            assert torch.equal(p, q), (step, i, tuple(p.shape), (p - q).abs().max().item())
+            for k, v in local.state[p].items():
+                if torch.is_tensor(v):
+                    assert torch.equal(v, agent.state[q][k]), (step, i, k)
+    local.check_status()
+    agent.check_status()
+    _log('[gpu]   ok')
+
+
 SYM_CASES = [
     # (batch dims, M, K, C kind, alpha, beta, B as a transposed view of A)
     ((), 300, 700, None, 1.0, 1.0, True),        # Gram R = X X^T, two tile rows

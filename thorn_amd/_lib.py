@@ -94,6 +94,7 @@ SIGNATURES = {
     'thorn_ortho_timing_enable': (_i, [_vp, _i]),
     'thorn_ortho_set_spin_limit': (_i, [_vp, _i]),
     'thorn_ortho_set_small_fusion': (_i, [_vp, _i]),
+    'thorn_ortho_set_small_xcd_barriers': (_i, [_vp, _i]),
     'thorn_ortho_timing_read': (_i, [_vp, _vp, _vp, _i]),
     'thorn_ortho_timing_intervals': (_i, [_vp, _vp, _vp, _vp, _vp, _i, ctypes.POINTER(_i)]),
     'thorn_adam_timing_enable': (_i, [_vp, _i]),
@@ -103,7 +104,7 @@ KINDS = ['pre', 'norm', 'gram', 'poly', 'update', 'rowstats', 'pnn_apply', 'md_f
          'symprod', 'magma', 'small']
 WS_STATUS_OFFSET = 256
 NOALLOC_SCRATCH_BYTES = 32 << 20
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 
@@ -199,6 +200,10 @@ class OrthoPlan:
 
     def set_small_fusion(self, enable: bool) -> None:
         check(self._lib.thorn_ortho_set_small_fusion(self.handle, int(bool(enable))), 'thorn_ortho_set_small_fusion')
+
+    def set_small_xcd_barriers(self, enable: bool) -> None:
+        check(self._lib.thorn_ortho_set_small_xcd_barriers(self.handle, int(bool(enable))),
+              'thorn_ortho_set_small_xcd_barriers')
 
     def timing_read(self) -> dict:
         return _timing_read(self._lib.thorn_ortho_timing_read, self.handle)

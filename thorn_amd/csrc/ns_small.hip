@@ -138,9 +138,11 @@ struct SmallSync {
     int* err;
     int C, spin;
     bool local;
-    __device__ __forceinline__ SmallSync(int* bar_, int member, int C_, int* err_, int spin_)
+    // xcd: XCD-local barriers allowed (thorn_ortho_set_small_xcd_barriers; with 0 every barrier is
+    // agent scope)
+    __device__ __forceinline__ SmallSync(int* bar_, int member, int C_, int* err_, int spin_, bool xcd)
         : bar(bar_), err(err_), C(C_), spin(spin_), local(false) {
-        if (C > 1) {
+        if (C > 1 && xcd) {
             if (threadIdx.x == 0) bar[2 + member] = xcc_id();
             cluster_barrier(bar, C, err, spin);
             bool same = true;
@@ -487,7 +489,8 @@ __device__ __forceinline__ void small_fused_apply(const OrthoMat& M, int member,
 // FUSED: the plan's whole step (small_fused_prologue, the schedule, small_fused_apply).
 template <bool FUSED>
 __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
-                                                                 SmallSchedule sc, int* err, int spin) {
+                                                                 SmallSchedule sc, int* err, int spin,
+                                                                 int xcd_barriers) {
     __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
     __shared__ float red[kSmallWaves];
     static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     _Float16* const stage = reinterpret_cast<_Float16*>(stages) + wave * 32 * kStageLd;
     const SmallView V = small_view(M);
-    SmallSync sync(M.small_bar, member, C, err, spin);
+    SmallSync sync(M.small_bar, member, C, err, spin, xcd_barriers != 0);
     const int set = M.rows == M.cols ? 0 : 1;
     const unsigned tslot = ts_begin();
     if constexpr (FUSED) small_fused_prologue(M, V, member, C, red, stages, sync);

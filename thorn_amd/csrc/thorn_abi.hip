@@ -180,6 +180,7 @@ struct thorn_ortho_plan {
     // launch left at count 0. small_fusion: thorn_ortho_set_small_fusion.
     bool small_fusion = true;
     bool fused_small = false;
+    bool small_xcd = true;   // XCD-local cluster barriers allowed: thorn_ortho_set_small_xcd_barriers
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
     const void* filled_ws = nullptr;   // workspace of the last fill_table
@@ -974,11 +975,13 @@ int ortho_step(thorn_ortho_plan_t plan, const void* table_dev, const float* coef
         if (fused) {
             THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel<true>,
                          dim3(plan->small_live.total), dim3(thorn::kSmallThreads), 0, st, mats,
-                         task_list(dev, plan->small_live), ss, status, plan->spin_limit);
+                         task_list(dev, plan->small_live), ss, status, plan->spin_limit,
+                         plan->small_xcd ? 1 : 0);
         } else {
             THORN_LAUNCH(THORN_KIND_SMALL, "ns_small_kernel", thorn::ns_small_kernel<false>,
                          dim3(plan->small_live.total), dim3(thorn::kSmallThreads), 0, st, mats,
-                         task_list(dev, plan->small_live), ss, status, plan->spin_limit);
+                         task_list(dev, plan->small_live), ss, status, plan->spin_limit,
+                         plan->small_xcd ? 1 : 0);
         }
         return THORN_OK;
     };
@@ -1137,6 +1140,12 @@ int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls) {
 int thorn_ortho_set_small_fusion(thorn_ortho_plan_t plan, int enable) {
     if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_set_small_fusion: null plan");
     plan->small_fusion = enable != 0;
+    return THORN_OK;
+}
+
+int thorn_ortho_set_small_xcd_barriers(thorn_ortho_plan_t plan, int enable) {
+    if (!plan) return fail(THORN_ERR_INVALID, "thorn_ortho_set_small_xcd_barriers: null plan");
+    plan->small_xcd = enable != 0;
     return THORN_OK;
 }
 
