@@ -966,6 +966,59 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
     _log('[gpu]   overlapped gradient release equals the in-order steps bit for bit')
 
 
+def test_gradient_release_small_matrices_in_windows():
+    """Gradient release puts small orthogonalized matrices (the library's small-matrix path) and
+    the tensors of non-orthogonalized groups in their group's window too: five Linear layers of
+    32..256 wide (clusters of 1 to 4 workgroups) step as one plan when backward ends, which from
+    the second backward pass on is one fused launch, and their biases (an Adam group) as one
+    multi-tensor Adam launch. Three passes must match the same training with every step in order
+    on the caller's stream (each parameter its own plan or launch), bit for bit."""
+    _log('[gpu] gradient release: small matrices in one window against in-order steps')
+    thorn_amd = _thorn()
+    from thorn_amd import optim as OPT
+    dims = [32, 64, 96, 128, 200, 256]
+    gen = torch.Generator().manual_seed(78)
+    init = [torch.randn(dims[i + 1], dims[i], generator=gen) * 0.05 for i in range(5)]
+    xs = [torch.randn(16, 32, generator=gen) for _ in range(3)]
+
+    def run(overlap: bool):
+        mods = []
+        for i in range(5):
+            mods += [torch.nn.Linear(dims[i], dims[i + 1]), torch.nn.Tanh()]
+        model = torch.nn.Sequential(*mods).to(DEV)
+        lins = [m for m in model if isinstance(m, torch.nn.Linear)]
+        with torch.no_grad():
+            for lin, w in zip(lins, init):
+                lin.weight.copy_(w.to(DEV))
+                lin.bias.copy_(w[:, 0].to(DEV))
+        keep = OPT.RELEASE_OVERLAP
+        OPT.RELEASE_OVERLAP = overlap
+        try:
+            opt = thorn_amd.THORN([{'params': [m.weight for m in lins], 'orthogonalize': True, 'lr': 1e-2,
+                                    'weight_decay': 0.1},
+                                   {'params': [m.bias for m in lins], 'orthogonalize': False, 'lr': 1e-2,
+                                    'weight_decay': 0.0}])
+            opt.setup_gradient_release(model)
+            for x in xs:
+                model(x.to(DEV)).square().mean().backward()
+            torch.cuda.synchronize()
+            assert opt._release_queued is False and not opt._release_pending and not opt._release_windows
+        finally:
+            OPT.RELEASE_OVERLAP = keep
+        return model, opt
+
+    ma, oa = run(True)
+    assert sorted(len(k[3]) for k in oa._runners if k[0] == 'release') == [5]
+    assert sorted(len(k[3]) for k in oa._runners if k[0] == 'adam') == [5]   # the biases' one launch
+    mb, ob = run(False)
+    for i, (pa, pb) in enumerate(zip(ma.parameters(), mb.parameters())):
+        assert torch.equal(pa.detach(), pb.detach()), i
+        for k, v in oa.state[pa].items():
+            assert (torch.equal(v, ob.state[pb][k]) if torch.is_tensor(v) else v == ob.state[pb][k]), (i, k)
+    oa.check_status()
+    _log('[gpu]   ok')
+
+
 @pytest.mark.parametrize('rate', [1, 2])
 def test_sparse_gradients(rate):
     """Row-sparse gradients (thorn.py:1667-1700) against the oracle over six steps: an embedding

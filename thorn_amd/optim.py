@@ -759,9 +759,9 @@ CHAIN_MAX_COST = 1e12
 # device's 4 hardware queues of a process (4 of them measured 54.8 ms on config 2's hooks, 3 41.2).
 RELEASE_STREAMS = 3
 RELEASE_OVERLAP = True   # False: every released step on the caller's stream, in order
-# Gradient release keeps the gradients of large orthogonalized parameters until this many bytes of
-# them are there (or backward ends) and steps them as one plan: one parameter's Newton-Schulz
-# launches fill only 10-48 of the device's 256 CUs. This bounds the gradient memory held back
+# Gradient release keeps the dense gradients of a group's parameters until this many bytes of them
+# are there (or backward ends) and steps them as one plan or one Adam launch: one parameter's
+# Newton-Schulz launches fill only 10-48 of the device's 256 CUs. This bounds the gradient memory held back
 # beyond the reference's (which drops each gradient in its hook); 0 steps each parameter alone.
 RELEASE_WINDOW_BYTES = 256 << 20
 # step() runs the non-orthogonalized groups on a stream of their own beside an orthogonalized group
@@ -1429,14 +1429,17 @@ class THORN(Optimizer):
         p.grad afterwards (a window keeps the tensor).
 
         The Newton-Schulz launches of one matrix fill only a few of the device's CUs, and the
-        parameters' steps are independent, so a large orthogonalized parameter joins its group's
-        window with its gradient: once the window holds RELEASE_WINDOW_BYTES of gradients it steps
-        as one plan on the next of RELEASE_STREAMS streams (_release_flush), and the caller's
-        stream waits for it in _release_join, which also steps what the windows still hold.
-        join_later=False steps and joins at once. Other parameters step on the caller's stream."""
+        parameters' steps are independent, so an orthogonalized parameter joins its group's window
+        with its gradient: once the window holds RELEASE_WINDOW_BYTES of gradients it steps as one
+        plan on the next of RELEASE_STREAMS streams (_release_flush), and the caller's stream waits
+        for it in _release_join, which also steps what the windows still hold. Small matrices (the
+        library's small-matrix path) and the tensors of non-orthogonalized groups join their
+        group's window too: a window of them is one launch (the small-matrix step, or one
+        multi-tensor Adam launch), where each would otherwise be a launch and a host round of its
+        own. join_later=False steps and joins at once. A sparse gradient steps on the caller's
+        stream at once."""
         group = self._param_to_group[id(p)]
-        if (not RELEASE_OVERLAP or not p.is_cuda or not group['orthogonalize'] or p.grad is None
-                or p.grad.is_sparse or _large_matrices([p]) == 0):
+        if not RELEASE_OVERLAP or not p.is_cuda or p.grad is None or p.grad.is_sparse:
             self.step(param=p)
             return
         gi = next(i for i, g in enumerate(self.param_groups) if g is group)
