@@ -53,32 +53,37 @@ struct SmallSchedule {
     int32_t n[2];
 };
 
-// Barrier of the C workgroups of one matrix: sense-reversing (count, generation) in the
-// workspace, agent-scope release on arrival and acquire on departure. The wait is bounded: a
-// cluster whose members are not all resident cannot hang the GPU; after `spin` polls (each a
-// 64-cycle sleep) it sets *err and goes on.
+// Barrier of the C workgroups of one matrix, on one word of the workspace: the arrival count in
+// bits 0-15 and the generation in bits 16-31. A member arrives by adding 1 and learns the
+// generation from the value it gets back; the last one to arrive (count C - 1 before its add) adds
+// 2^16 - C, which clears the count and advances the generation in one atomic, and the others poll
+// the word until the generation moves. Agent-scope release on arrival and acquire on departure.
+// The wait is bounded: a cluster whose members are not all resident cannot hang the GPU; after
+// `spin` polls (each a 64-cycle sleep) it sets *err and goes on. Should a member that gave up
+// waiting arrive at the next barrier first, its arrival stays in the count (the last arrival
+// subtracts C, it does not store 0), so every launch, whose members each arrive once at every
+// barrier, leaves the count at 0.
+__device__ __forceinline__ bool cluster_last(unsigned old, int C) { return (old & 0xFFFFu) == unsigned(C - 1); }
+__device__ __forceinline__ void cluster_poll(unsigned* w, unsigned old, int* err, int spin) {
+    int it = 0;
+    while ((__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 16) == (old >> 16)) {
+        if (it++ >= spin) {
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int spin) {
     __syncthreads();
     if (C > 1 && threadIdx.x == 0) {
-        int* cnt = bar;
-        int* gen = bar + 1;
-        const int g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int a = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (a == C - 1) {
-            // a subtraction, not a store of 0: should a member that gave up waiting arrive at the
-            // next barrier first, its arrival is kept, and every launch, whose members each arrive
-            // once at every barrier, leaves the count at 0
-            __hip_atomic_fetch_add(cnt, -C, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(gen, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned* w = reinterpret_cast<unsigned*>(bar);
+        const unsigned old = __hip_atomic_fetch_add(w, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (cluster_last(old, C)) {
+            __hip_atomic_fetch_add(w, (1u << 16) - unsigned(C), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         } else {
-            int it = 0;
-            while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
-                if (it++ >= spin) {
-                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
+            cluster_poll(w, old, err, spin);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
     }
@@ -90,30 +95,17 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int s
 // threadgroup-split mode). Each wave's stores are complete in the L2 before the arrival (vmcnt(0)),
 // and after the departure the CU's L1 is invalidated (buffer_inv sc0), so the loads that follow
 // read the L2; the L2 is neither written back nor invalidated, as the agent-scope barrier does it.
-// The count and generation are accessed exactly as there (the same atomics and polling loads).
+// The word is accessed exactly as there (the same atomics and polling loads).
 __device__ __forceinline__ void cluster_barrier_xcd(int* bar, int C, int* err, int spin) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (C > 1 && threadIdx.x == 0) {
-        int* cnt = bar;
-        int* gen = bar + 1;
-        const int g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the generation is read before arriving
-        const int a = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (a == C - 1) {
-            __hip_atomic_fetch_add(cnt, -C, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the count is reset before the release
-            __hip_atomic_fetch_add(gen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            int it = 0;
-            while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
-                if (it++ >= spin) {
-                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
+        unsigned* w = reinterpret_cast<unsigned*>(bar);
+        const unsigned old = __hip_atomic_fetch_add(w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (cluster_last(old, C))
+            __hip_atomic_fetch_add(w, (1u << 16) - unsigned(C), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            cluster_poll(w, old, err, spin);
         asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
@@ -134,7 +126,7 @@ __device__ __forceinline__ int xcc_id() {
 // order, not a guarantee, so the ids decide: with members on two XCDs every barrier stays agent
 // scope.
 struct SmallSync {
-    int* bar;   // count, generation, then one XCC id per member
+    int* bar;   // the barrier word, an unused word, then one XCC id per member
     int* err;
     int C, spin;
     bool local;

@@ -262,8 +262,8 @@ __global__ __launch_bounds__(256) void ortho_norm_kernel(const OrthoMat* __restr
     const OrthoMat& M = mats[blockIdx.x];
     const int slice = blockIdx.y;
     if (slice == 0) norm_sigma_magma(mats, n_mats, M, scratch);
-    // the small-matrix launch's cluster barrier starts from count 0 (its generation may be any
-    // value): the workspace may hold another plan's data
+    // the small-matrix launch's cluster barrier word starts with count 0 (its generation bits may
+    // hold any value; this clears them too): the workspace may hold another plan's data
     if (slice == 0 && threadIdx.x == 0 && (M.flags & kFlagSmall)) M.small_bar[0] = 0;
 
     const bool md = M.flags & kFlagMD, mds = M.flags & kFlagMDScalar;
