@@ -178,14 +178,44 @@ __device__ __forceinline__ void wait_loads_barrier(int n) {
 }
 static_assert(kSmallStages - 2 <= 6, "wait_loads_barrier covers 0 .. kSmallStages - 2");
 
+// The C term of a wave's tile in LDS (kCTileBytes per wave): its 32 rows of C^T (rows n0..,
+// columns m0..m0+31), 64 bytes each, chunk c of row r at r * 64 + (c ^ ((r >> 2) & 3)) * 16,
+// filled by two direct loads (the 64 lanes of each fill 64 consecutive 16-byte slots); `ok` false
+// loads `zero` instead. Requested after the product's first chunks, so that the first chunk's wait
+// does not cover them (the eight-byte loads of the C^T rows, 32 rows per instruction, took ~0.7 us
+// more than the chunk alone).
+constexpr int kCTileBytes = 32 * 64;
+__device__ __forceinline__ void small_issue_c(uint32_t lds, const _Float16* CT, int64_t ldc, int m0, int n0, bool ok,
+                                              const void* zero, int lane) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int r = 16 * h + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+        const void* p = ok ? static_cast<const void*>(CT + int64_t(n0 + r) * ldc + m0 + 8 * c) : zero;
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p),
+                     "{m0}"(lds + h * 1024)
+                     : "memory");
+    }
+}
+
+// This lane's C values of its tile from the LDS copy, in the accumulator layout: cv[g][e] is
+// C[m0 + 8g + 4(lane / 32) + e][n0 + lane % 32].
+__device__ __forceinline__ void small_read_c(half4 (&cv)[4], const char* ctile, int lane) {
+    const int j = lane & 31;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+        cv[g] = *reinterpret_cast<const half4*>(ctile + j * 64 + ((g ^ ((j >> 2) & 3)) << 4) + 8 * (lane >> 5));
+}
+
 // acc (this wave's tile of the super-tile, if it has one) = A[M0.., 0:K] * B[0:K, N0..] with A
 // row-major (lda) and B given by its transpose BT row-major (ldb), K a multiple of 32, every
-// operand row inside the padded buffers (rows past sm / sn read `zero`). The whole workgroup
-// calls it (barriers inside; the first one orders it after every wave's use of the staging tiles
-// in the ring); on return every load has landed and the stages are free.
+// operand row inside the padded buffers (rows past sm / sn read `zero`). With CT, the wave's C
+// tile (CT at m0, n0) is also loaded into `ctile` (small_issue_c). The whole workgroup calls it
+// (barriers inside; the first one orders it after every wave's use of the staging tiles in the
+// ring); on return every load has landed and the stages are free.
 __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, const _Float16* A, int64_t lda,
                                                 const _Float16* BT, int64_t ldb, int M0, int N0, int sm, int sn,
                                                 int K, int wave, int lane, bool has_tile, int ti, int tj,
+                                                uint32_t ctile, const _Float16* CT, int64_t ldc, int m0, int n0,
                                                 unsigned tslot = 0, int q = 0) {
     floatx16 acc = {};
     const int nk = K / 32;
@@ -204,12 +234,14 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
     __syncthreads();
     const int pre = nk < kSmallStages - 1 ? nk : kSmallStages - 1;
     for (int t = 0; t < pre; ++t) issue(t);
+    const int nc = CT ? 2 : 0;   // the C loads, issued after the first pre chunks
+    if (CT) small_issue_c(ctile, CT, ldc, m0, n0, has_tile, zero, lane);
     for (int kc = 0; kc < nk; ++kc) {
         // this wave's loads of chunk kc have landed (the ones issued after it may still be in
-        // flight); after the barrier every wave's have, and nobody reads stage (kc - 1) % S any
-        // more, which then receives chunk kc + S - 1
+        // flight: later chunks, and while kc < pre the C loads); after the barrier every wave's
+        // have, and nobody reads stage (kc - 1) % S any more, which then receives chunk kc + S - 1
         const int ahead = nk - 1 - kc < kSmallStages - 2 ? nk - 1 - kc : kSmallStages - 2;
-        wait_loads_barrier(ahead);
+        wait_loads_barrier(ahead + (kc < pre ? nc : 0));
         if (kc == 0) ts_op(tslot, q, 3);
         if (kc + kSmallStages - 1 < nk) issue(kc + kSmallStages - 1);
         if (has_tile) {
@@ -223,6 +255,7 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
         }
     }
     ts_op(tslot, q, 4);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the C loads too (after the last chunk when nk <= 2)
     __syncthreads();   // every wave is done with the stages
     return acc;
 }
@@ -236,17 +269,7 @@ constexpr int kStageLd = 34;
 // write by another lane is not visible to a single thread's program order.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// This lane's C values of tile (m0, n0), read through C's transpose CT (4 contiguous halves per
-// load), in the accumulator layout: cv[g][e] is C[m0 + 8g + 4(lane / 32) + e][n0 + lane % 32].
-// Requested before the tile's product, so that their latency overlaps it.
-__device__ __forceinline__ void small_load_c(half4 (&cv)[4], const _Float16* CT, int64_t ldc, int m0, int n0,
-                                             int lane) {
-    const int j = lane & 31;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) cv[g] = ldg<half4>(CT + int64_t(n0 + j) * ldc + m0 + 8 * g + 4 * (lane >> 5));
-}
-
-// Stages f16(alpha * acc + beta * C) of tile (m0, n0), C from small_load_c (HAS_C).
+// Stages f16(alpha * acc + beta * C) of tile (m0, n0), C from small_read_c (HAS_C).
 template <bool HAS_C>
 __device__ __forceinline__ void small_stage(const floatx16& acc, _Float16* stage, float alpha, float beta,
                                             const half4 (&cv)[4], int lane) {
@@ -485,6 +508,7 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
                                                                  int xcd_barriers) {
     __shared__ __attribute__((aligned(1024))) char stages[kSmallStages * kSmallStageBytes];
     __shared__ float red[kSmallWaves];
+    __shared__ __attribute__((aligned(1024))) char cbuf[kSmallWaves * kCTileBytes];   // C tiles (small_issue_c)
     static_assert(kSmallWaves * 32 * kStageLd * 2 <= kSmallStages * kSmallStageBytes, "staging tiles in the ring");
     // the block map: (matrix, member | C << 8), or matrix -1 for a block that has no work
     const int mat = tl.map[2 * blockIdx.x];
@@ -494,6 +518,8 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
     const int member = mc & 255, C = mc >> 8;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     _Float16* const stage = reinterpret_cast<_Float16*>(stages) + wave * 32 * kStageLd;
+    const char* const ctile = cbuf + wave * kCTileBytes;
+    const uint32_t ctile_lds = __builtin_amdgcn_readfirstlane(lds_address(ctile));
     const SmallView V = small_view(M);
     SmallSync sync(M.small_bar, member, C, err, spin, xcd_barriers != 0);
     const int set = M.rows == M.cols ? 0 : 1;
@@ -538,12 +564,13 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             const int sm = min(SM, orows - M0), sn = min(SN, ocols - N0);
             const bool mine = has_tile && 32 * ti < sm && 32 * tj < sn;
             const int m0 = M0 + 32 * ti, n0 = N0 + 32 * tj;
-            half4 cv[4] = {};
-            if (mine && CT) small_load_c(cv, CT, V.sp, m0, n0, lane);   // every C^T has s_p columns
+            // every C^T has s_p columns
             const floatx16 acc = small_block(stages, M.zero, A, lda, BT, ldb, M0, N0, sm, sn, K, wave, lane, mine,
-                                             ti, tj, tslot, q);
+                                             ti, tj, ctile_lds, CT, V.sp, m0, n0, tslot, q);
             ts_op(tslot, q, 1);
             if (!mine) continue;
+            half4 cv[4] = {};
+            if (CT) small_read_c(cv, ctile, lane);
             const float alpha = op.kind == kOpSym ? op.alpha : 1.f;
             if (CT) small_stage<true>(acc, stage, alpha, op.beta, cv, lane);
             else small_stage<false>(acc, stage, alpha, op.beta, cv, lane);
