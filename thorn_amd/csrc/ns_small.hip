@@ -118,33 +118,36 @@ __device__ __forceinline__ int xcc_id() {
     return static_cast<int>(x & 0xF);
 }
 
-// A cluster's barriers. At the start each member stores its XCC id in the barrier's words and
-// meets the others at an agent-scope barrier (before the kernel has written anything, so it has
-// little to write back); then each member reads all the ids, and when they are equal (the launch
-// placed the cluster on one XCD: block b runs on XCD b mod 8, and the block map gives a cluster's
-// members one residue) every later barrier is the XCD-local one. The placement is a dispatch
-// order, not a guarantee, so the ids decide: with members on two XCDs every barrier stays agent
-// scope.
+// A cluster's barriers. At the start each member stores its XCC id in the barrier's words; the
+// first barrier is agent scope, after which each member reads all the ids, and when they are equal
+// (the launch placed the cluster on one XCD: block b runs on XCD b mod 8, and the block map gives a
+// cluster's members one residue) every later barrier is the XCD-local one. The placement is a
+// dispatch order, not a guarantee, so the ids decide: with members on two XCDs every barrier stays
+// agent scope. (The ids ride on the first barrier the kernel needs anyway; a barrier of their own
+// at the start cost one more agent-scope round.)
 struct SmallSync {
     int* bar;   // the barrier word, an unused word, then one XCC id per member
     int* err;
     int C, spin;
-    bool local;
+    bool local, ids;   // ids: the XCC ids are read after the next (agent-scope) barrier
     // xcd: XCD-local barriers allowed (thorn_ortho_set_small_xcd_barriers; with 0 every barrier is
     // agent scope)
     __device__ __forceinline__ SmallSync(int* bar_, int member, int C_, int* err_, int spin_, bool xcd)
-        : bar(bar_), err(err_), C(C_), spin(spin_), local(false) {
-        if (C > 1 && xcd) {
-            if (threadIdx.x == 0) bar[2 + member] = xcc_id();
-            cluster_barrier(bar, C, err, spin);
+        : bar(bar_), err(err_), C(C_), spin(spin_), local(false), ids(C_ > 1 && xcd) {
+        if (ids && threadIdx.x == 0) bar[2 + member] = xcc_id();
+    }
+    __device__ __forceinline__ void wait() {
+        if (local) {
+            cluster_barrier_xcd(bar, C, err, spin);
+            return;
+        }
+        cluster_barrier(bar, C, err, spin);
+        if (ids) {
             bool same = true;
             for (int i = 1; i < C; ++i) same = same && bar[2 + i] == bar[2];
             local = __builtin_amdgcn_readfirstlane(same ? 1 : 0) != 0;
+            ids = false;
         }
-    }
-    __device__ __forceinline__ void wait() {
-        if (local) cluster_barrier_xcd(bar, C, err, spin);
-        else cluster_barrier(bar, C, err, spin);
     }
 };
 constexpr int kSmallBarWords = 2 + 16;   // the largest cluster has 16 members
