@@ -225,10 +225,14 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
     const int slot = wave * 64 + lane, part = slot >> 9, r = (slot >> 2) & 127;
     const int c = (slot & 3) ^ ((r >> 2) & 3);
     const bool ok = part == 0 ? r < sm : r < sn;
+    // a wave whose 16 rows all lie past sm / sn (an edge super-tile) loads nothing: its waits then
+    // pass at once
+    const bool loads = 16 * (wave & 7) < (part == 0 ? sm : sn);
     const char* src = reinterpret_cast<const char*>(part == 0 ? A + int64_t(M0 + r) * lda : BT + int64_t(N0 + r) * ldb) +
                       16 * c;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(stages)) + wave * 1024;
     auto issue = [&](int t) {
+        if (!loads) return;
         const void* p = ok ? static_cast<const void*>(src + int64_t(t) * 64) : zero;
         asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"((const THORN_GLOBAL void*)p),
                      "{m0}"(lds0 + (t % kSmallStages) * kSmallStageBytes)
