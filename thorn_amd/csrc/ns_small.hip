@@ -4,7 +4,7 @@
 // The grouped 256 x 256-tile launches of ns_kernels.hip give a small matrix one tile per phase, so
 // its 18 phases cost 18 launch latencies. Here each small matrix gets a cluster of 1024-thread
 // workgroups (one for s <= 128; above, one per 128 x 128 super-tile of its largest output, 4 to
-// 16), placed on one XCD, that runs every operation of the schedule in turn, 32 x 32 output tiles
+// 16), placed on one XCD (block map), that runs every operation of the schedule in turn, 32 x 32 output tiles
 // dealt to its 16 * C waves, with a barrier between operations (SmallSync). The
 // operands stay in the L2-resident workspace, each s x s result and each iterate also stored
 // transposed, so that every MFMA fragment, of A or of B, is one 16-byte load of a K-contiguous row.
@@ -118,13 +118,17 @@ __device__ __forceinline__ int xcc_id() {
     return static_cast<int>(x & 0xF);
 }
 
-// A cluster's barriers. At the start each member stores its XCC id in the barrier's words; the
-// first barrier is agent scope, after which each member reads all the ids, and when they are equal
-// (the launch placed the cluster on one XCD: block b runs on XCD b mod 8, and the block map gives a
-// cluster's members one residue) every later barrier is the XCD-local one. The placement is a
-// dispatch order, not a guarantee, so the ids decide: with members on two XCDs every barrier stays
-// agent scope. (The ids ride on the first barrier the kernel needs anyway; a barrier of their own
-// at the start cost one more agent-scope round.)
+// A cluster's barriers: agent scope, unless the plan allows XCD-local ones (off by default: in one
+// sequence, plans of one matrix each stepped in turn on a shared workspace between other kernels,
+// operands read after an XCD-local barrier were stale although written on the same XCD, for a
+// reason not found; an L2 invalidate at each departure, as the agent-scope barrier does, removed
+// it). When allowed, each member stores its XCC id in the barrier's words at the start; the first
+// barrier is agent scope, after which each member reads all the ids, and when they are equal (the
+// launch placed the cluster on one XCD: block b runs on XCD b mod 8 up to a fixed offset, and the
+// block map gives a cluster's members one residue) every later barrier is the XCD-local one. The
+// placement is a dispatch order, not a guarantee, so the ids decide: with members on two XCDs
+// every barrier stays agent scope. (The ids ride on the first barrier the kernel needs anyway; a
+// barrier of their own at the start cost one more agent-scope round.)
 struct SmallSync {
     int* bar;   // the barrier word, an unused word, then one XCC id per member
     int* err;
