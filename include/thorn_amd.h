@@ -139,11 +139,11 @@ int thorn_ortho_set_spin_limit(thorn_ortho_plan_t plan, int polls);
  * the separate launches. On by default; enable = 0 keeps the separate launches (for comparison). */
 int thorn_ortho_set_small_fusion(thorn_ortho_plan_t plan, int enable);
 /* No counterpart in the reference. The small-matrix launch places each matrix's cluster of
- * workgroups on one XCD; with enable = 1, when the workgroups find that they share one (their XCC
- * ids agree), they synchronize through that XCD's L2 instead of writing back and invalidating it at
- * every barrier. Off by default (agent-scope barriers throughout): in one sequence, plans of one
- * matrix each stepped in turn on a shared workspace between autograd's kernels, results differed
- * from those of agent-scope barriers, for a reason not found; for measurement only. */
+ * workgroups on one XCD and, when the workgroups find that they share one (their XCC ids agree),
+ * synchronizes them through that XCD's L2: no L2 write-back at the barriers, which the agent-scope
+ * barrier needs for other XCDs, and an invalidate of the caches up to the L2 after each; results
+ * are bit for bit the same. On by default; enable = 0 keeps agent-scope barriers throughout (for
+ * comparison). */
 int thorn_ortho_set_small_xcd_barriers(thorn_ortho_plan_t plan, int enable);
 size_t thorn_ortho_table_bytes(thorn_ortho_plan_t plan);
 int thorn_ortho_fill_table(thorn_ortho_plan_t plan, const ThornOrthoMatStep* steps, void* workspace,

@@ -1271,15 +1271,13 @@ def test_small_plan_fused_launch_equals_separate_launches():
 
 
 def test_small_xcd_barriers_equal_agent_barriers():
-    """With thorn_ortho_set_small_xcd_barriers(plan, 1) the small-matrix launch's clusters, on one
-    XCD each, synchronize through that XCD's L2 (stores complete before the arrival, the CU's L1
-    invalidated after the departure) instead of writing back and invalidating the L2 at every
-    barrier. (Off by default: plans of one matrix each, stepped in turn on a shared workspace
-    between autograd's kernels, gave other results than agent-scope barriers.) Here, grouped
-    plans on their own workspaces, against the same steps with agent-scope barriers (the default),
+    """The small-matrix launch's clusters sit on one XCD each and, their XCC ids agreeing,
+    synchronize through that XCD's L2 (stores complete before the arrival; after the departure the
+    caches up to the L2 invalidated, without the agent-scope barrier's L2 write-back). Against the
+    same steps with agent-scope barriers throughout (thorn_ortho_set_small_xcd_barriers(plan, 0)),
     every parameter and state tensor is equal bit for bit after each of eight steps: config 4's
-    matrices and (640, 256), (512, 256), (200, 300), (130, 129) (clusters of 10, 8, 6 and 4),
-    fused from the second step on."""
+    matrices and (640, 256), (512, 256), (200, 300), (130, 129) (clusters of 10, 8, 6 and 4), fused
+    from the second step on; a stale operand read would show as a difference."""
     import bench
     thorn_amd = _thorn()
     lib = _lib()
@@ -1304,11 +1302,11 @@ def test_small_xcd_barriers_equal_agent_barriers():
         local.step()
         agent.step()
         torch.cuda.synchronize()
-        if step == 1:   # the plans exist after the first step: XCD-local barriers from step 2 on
-            for r in local._runners.values():
+        if step == 1:   # the plans exist after the first step: agent-scope barriers from step 2 on
+            for r in agent._runners.values():
                 for pl in r.plans:
                     if isinstance(pl, lib.OrthoPlan):
-                        pl.set_small_xcd_barriers(True)
+                        pl.set_small_xcd_barriers(False)
         for i, (p, q) in enumerate(zip(pa, pb)):
             assert torch.equal(p, q), (step, i, tuple(p.shape), (p - q).abs().max().item())
             for k, v in local.state[p].items():

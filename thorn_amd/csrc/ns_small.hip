@@ -90,12 +90,15 @@ __device__ __forceinline__ void cluster_barrier(int* bar, int C, int* err, int s
     __syncthreads();
 }
 
-// The same barrier for a cluster whose workgroups all run on one XCD, so that they share its L2:
-// the protocol of a workgroup split over CUs (LLVM's gfx942 memory model, workgroup scope in
-// threadgroup-split mode). Each wave's stores are complete in the L2 before the arrival (vmcnt(0)),
-// and after the departure the CU's L1 is invalidated (buffer_inv sc0), so the loads that follow
-// read the L2; the L2 is neither written back nor invalidated, as the agent-scope barrier does it.
-// The word is accessed exactly as there (the same atomics and polling loads).
+// The same barrier for a cluster whose workgroups all run on one XCD, so that they share its L2,
+// which is then the point where their stores meet: each wave's stores are complete in the L2
+// before the arrival (vmcnt(0)), and after the departure the caches between the CU and the L2
+// are invalidated together with the L2's clean lines (buffer_inv sc1), so the loads that follow
+// read what the other members stored. The L2 is not written back (buffer_wbl2 sc1), as the
+// agent-scope barrier does it for other XCDs. (Invalidating the CU's L1 alone, buffer_inv sc0, as
+// LLVM's gfx942 model does for a workgroup split over CUs, left stale operands in one sequence
+// whose members shared the XCD but not a shader engine.) The word is accessed exactly as there
+// (the same atomics and polling loads).
 __device__ __forceinline__ void cluster_barrier_xcd(int* bar, int C, int* err, int spin) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -106,7 +109,7 @@ __device__ __forceinline__ void cluster_barrier_xcd(int* bar, int C, int* err, i
             __hip_atomic_fetch_add(w, (1u << 16) - unsigned(C), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
             cluster_poll(w, old, err, spin);
-        asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("buffer_inv sc1\n\ts_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
 }
@@ -118,15 +121,11 @@ __device__ __forceinline__ int xcc_id() {
     return static_cast<int>(x & 0xF);
 }
 
-// A cluster's barriers: agent scope, unless the plan allows XCD-local ones (off by default: in one
-// sequence, plans of one matrix each stepped in turn on a shared workspace between other kernels,
-// operands read after an XCD-local barrier were stale although written on the same XCD, for a
-// reason not found; an L2 invalidate at each departure, as the agent-scope barrier does, removed
-// it). When allowed, each member stores its XCC id in the barrier's words at the start; the first
-// barrier is agent scope, after which each member reads all the ids, and when they are equal (the
-// launch placed the cluster on one XCD: block b runs on XCD b mod 8 up to a fixed offset, and the
-// block map gives a cluster's members one residue) every later barrier is the XCD-local one. The
-// placement is a dispatch order, not a guarantee, so the ids decide: with members on two XCDs
+// A cluster's barriers. At the start each member stores its XCC id in the barrier's words; the
+// first barrier is agent scope, after which each member reads all the ids, and when they are equal
+// (the launch placed the cluster on one XCD: block b runs on XCD b mod 8 up to a fixed offset, and
+// the block map gives a cluster's members one residue) every later barrier is the XCD-local one.
+// The placement is a dispatch order, not a guarantee, so the ids decide: with members on two XCDs
 // every barrier stays agent scope. (The ids ride on the first barrier the kernel needs anyway; a
 // barrier of their own at the start cost one more agent-scope round.)
 struct SmallSync {

@@ -180,7 +180,7 @@ struct thorn_ortho_plan {
     // launch left at count 0. small_fusion: thorn_ortho_set_small_fusion.
     bool small_fusion = true;
     bool fused_small = false;
-    bool small_xcd = false;  // XCD-local cluster barriers allowed: thorn_ortho_set_small_xcd_barriers
+    bool small_xcd = true;   // XCD-local cluster barriers allowed: thorn_ortho_set_small_xcd_barriers
     // The first iterate of a step is written directly in f16, prescaled by the power of two the
     // previous step stored in the workspace, when the previous step ran on the same workspace.
     const void* filled_ws = nullptr;   // workspace of the last fill_table
