@@ -969,7 +969,7 @@ def test_gradient_release_overlapped_equals_in_order(window, rate, limit, extra)
 def test_gradient_release_small_matrices_in_windows():
     """Gradient release puts small orthogonalized matrices (the library's small-matrix path) and
     the tensors of non-orthogonalized groups in their group's window too: five Linear layers of
-    32..256 wide (clusters of 1 to 4 workgroups) step as one plan when backward ends, which from
+    32..256 wide (clusters of 1 to 16 workgroups) step as one plan when backward ends, which from
     the second backward pass on is one fused launch, and their biases (an Adam group) as one
     multi-tensor Adam launch. Three passes must match the same training with every step in order
     on the caller's stream (each parameter its own plan or launch), bit for bit."""
@@ -1214,7 +1214,7 @@ def test_small_plan_fused_launch_equals_separate_launches():
     (six launches per step), every parameter and state tensor is equal bit for bit after each of
     five steps: config 4's matrices (per-row normalized and not, float4 and scalar layouts, one
     workgroup per matrix) and a second group of (640, 256), (200, 300) and (130, 129) matrices
-    (clusters of 10, 6 and 4 workgroups, padded sides)."""
+    (clusters of 16, 16 and 9 workgroups, padded sides)."""
     import bench
     thorn_amd = _thorn()
     lib = _lib()
@@ -1276,7 +1276,7 @@ def test_small_xcd_barriers_equal_agent_barriers():
     caches up to the L2 invalidated, without the agent-scope barrier's L2 write-back). Against the
     same steps with agent-scope barriers throughout (thorn_ortho_set_small_xcd_barriers(plan, 0)),
     every parameter and state tensor is equal bit for bit after each of eight steps: config 4's
-    matrices and (640, 256), (512, 256), (200, 300), (130, 129) (clusters of 10, 8, 6 and 4), fused
+    matrices and (640, 256), (512, 256), (200, 300), (130, 129) (clusters of 16, 16, 16 and 9), fused
     from the second step on; a stale operand read would show as a difference."""
     import bench
     thorn_amd = _thorn()

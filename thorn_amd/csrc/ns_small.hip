@@ -3,8 +3,9 @@
 //
 // The grouped 256 x 256-tile launches of ns_kernels.hip give a small matrix one tile per phase, so
 // its 18 phases cost 18 launch latencies. Here each small matrix gets a cluster of 1024-thread
-// workgroups (one for s <= 128; above, one per 128 x 128 super-tile of its largest output, 4 to
-// 16), placed on one XCD (block map), that runs every operation of the schedule in turn, 32 x 32 output tiles
+// workgroups (one for s <= 128; above, enough for its s x s products in 64 x 64 super-tiles and
+// its s x l updates in 128 x 128 ones to take one round each, at most 16), placed on one XCD
+// (block map), that runs every operation of the schedule in turn, 32 x 32 output tiles
 // dealt to its 16 * C waves, with a barrier between operations (SmallSync). The
 // operands stay in the L2-resident workspace, each s x s result and each iterate also stored
 // transposed, so that every MFMA fragment, of A or of B, is one 16-byte load of a K-contiguous row.
@@ -509,8 +510,9 @@ __device__ __forceinline__ void small_fused_apply(const OrthoMat& M, int member,
 // One launch: the schedule of every small matrix in the task list, whose block map gives each block
 // its matrix and its place in the matrix's cluster (thorn_ortho_fill_table gives a cluster's blocks
 // one residue mod 8, so that they run on one XCD). err: set when a cluster barrier times out.
-// Each operation's output is cut into super-tiles of up to 128 x 128 dealt to the cluster's
-// workgroups; within one, wave w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
+// Each operation's output is cut into super-tiles of 64 x 64 or 128 x 128 (the size that takes
+// fewer rounds over the cluster, 64 on a tie) dealt to the cluster's workgroups; within one, wave
+// w takes the 32 x 32 tile (w % (SM/32), w / (SM/32)).
 // FUSED: the plan's whole step (small_fused_prologue, the schedule, small_fused_apply).
 template <bool FUSED>
 __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat* __restrict__ mats, TaskList tl,
@@ -564,13 +566,17 @@ __global__ __launch_bounds__(kSmallThreads) void ns_small_kernel(const OrthoMat*
             K = V.sp;
             if (op.c >= 0) CT = V.xwt(op.xsel);
         }
-        const int SM = min(orows, 128), SN = min(ocols, 128);
-        const int SR = (orows + 127) / 128, SC = (ocols + 127) / 128;
+        // super-tiles of 64 x 64 when they take no more rounds over the cluster than 128 x 128 ones
+        // (a quarter of the K-loop work per workgroup), else 128 x 128
+        const int r64 = (orows + 63) / 64 * ((ocols + 63) / 64), r128 = (orows + 127) / 128 * ((ocols + 127) / 128);
+        const int TS = (r64 + C - 1) / C <= (r128 + C - 1) / C ? 64 : 128;
+        const int SM = min(orows, TS), SN = min(ocols, TS);
+        const int SR = (orows + TS - 1) / TS, SC = (ocols + TS - 1) / TS;
         const int tm = SM / 32;
         const bool has_tile = wave < tm * (SN / 32);
         const int ti = has_tile ? wave % tm : 0, tj = has_tile ? wave / tm : 0;
         for (int st = member; st < SR * SC; st += C) {
-            const int M0 = 128 * (st % SR), N0 = 128 * (st / SR);
+            const int M0 = TS * (st % SR), N0 = TS * (st / SR);
             const int sm = min(SM, orows - M0), sn = min(SN, ocols - N0);
             const bool mine = has_tile && 32 * ti < sm && 32 * tj < sn;
             const int m0 = M0 + 32 * ti, n0 = N0 + 32 * tj;

@@ -619,10 +619,12 @@ int thorn_ortho_plan_create(const ThornOrthoMatDesc* descs, int n, thorn_ortho_p
         // ortho_pnn_apply_kernel (u' in xa); they always take the exact first iterate
         L.is_small = !L.adam && L.s <= thorn::kSmallMaxS && int64_t(L.rows) * L.cols < kPrescaleMinElems;
         // workgroups of its small-matrix cluster: one for s <= 128 (its s x s products are one
-        // 128 x 128 super-tile, so more would only add barriers); above, one per super-tile of the
-        // largest output (s x s, or the s x l update), at least 4 and at most 16, so that the
-        // update takes one round
-        L.cluster = L.s <= 128 ? 1 : static_cast<int32_t>(std::min<int64_t>(16, std::max<int64_t>(4, cdiv(L.s, 128) * cdiv(L.l, 128))));
+        // 128 x 128 super-tile, so more would only add barriers); above, enough for the s x s
+        // products in 64 x 64 super-tiles and the s x l updates in 128 x 128 ones to take one round
+        // each (ns_small_kernel picks each operation's super-tile size from the cluster), at most 16
+        L.cluster = L.s <= 128 ? 1
+                               : static_cast<int32_t>(std::min<int64_t>(
+                                     16, std::max<int64_t>(cdiv(L.s, 64) * cdiv(L.s, 64), cdiv(L.s, 128) * cdiv(L.l, 128))));
         L.rowsq_tiles = static_cast<int32_t>(L.is_small ? cdiv(L.cols, 32) : L.g3_tiles_n);
         L.n_psq = md ? static_cast<int32_t>(pnn || L.adam || L.is_small ? mom_tiles
                                                                          : int64_t(L.g3_tiles_m) * L.g3_tiles_n)
