@@ -188,9 +188,10 @@ static_assert(kSmallStages - 2 <= 6, "wait_loads_barrier covers 0 .. kSmallStage
 // The C term of a wave's tile in LDS (kCTileBytes per wave): its 32 rows of C^T (rows n0..,
 // columns m0..m0+31), 64 bytes each, chunk c of row r at r * 64 + (c ^ ((r >> 2) & 3)) * 16,
 // filled by two direct loads (the 64 lanes of each fill 64 consecutive 16-byte slots); `ok` false
-// loads `zero` instead. Requested after the product's first chunks, so that the first chunk's wait
-// does not cover them (the eight-byte loads of the C^T rows, 32 rows per instruction, took ~0.7 us
-// more than the chunk alone).
+// loads `zero` instead. Requested just before the product's first chunks (eight-byte loads of the
+// C^T rows into registers, 32 rows per instruction, had taken ~0.7 us more than the chunk alone;
+// these two cost the first chunk little, and issued after the chunks they were still in flight
+// when a short K loop ended).
 constexpr int kCTileBytes = 32 * 64;
 __device__ __forceinline__ void small_issue_c(uint32_t lds, const _Float16* CT, int64_t ldc, int m0, int n0, bool ok,
                                               const void* zero, int lane) {
@@ -243,16 +244,17 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
                      : "memory");
     };
     __syncthreads();
+    // the C loads first: they return before chunk 0 (loads return in order), so no wait covers
+    // them alone
+    if (CT) small_issue_c(ctile, CT, ldc, m0, n0, has_tile, zero, lane);
     const int pre = nk < kSmallStages - 1 ? nk : kSmallStages - 1;
     for (int t = 0; t < pre; ++t) issue(t);
-    const int nc = CT ? 2 : 0;   // the C loads, issued after the first pre chunks
-    if (CT) small_issue_c(ctile, CT, ldc, m0, n0, has_tile, zero, lane);
     for (int kc = 0; kc < nk; ++kc) {
         // this wave's loads of chunk kc have landed (the ones issued after it may still be in
-        // flight: later chunks, and while kc < pre the C loads); after the barrier every wave's
-        // have, and nobody reads stage (kc - 1) % S any more, which then receives chunk kc + S - 1
+        // flight); after the barrier every wave's have, and nobody reads stage (kc - 1) % S any
+        // more, which then receives chunk kc + S - 1
         const int ahead = nk - 1 - kc < kSmallStages - 2 ? nk - 1 - kc : kSmallStages - 2;
-        wait_loads_barrier(ahead + (kc < pre ? nc : 0));
+        wait_loads_barrier(ahead);
         if (kc == 0) ts_op(tslot, q, 3);
         if (kc + kSmallStages - 1 < nk) issue(kc + kSmallStages - 1);
         if (has_tile) {
@@ -266,8 +268,7 @@ __device__ __forceinline__ floatx16 small_block(char* stages, const void* zero, 
         }
     }
     ts_op(tslot, q, 4);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the C loads too (after the last chunk when nk <= 2)
-    __syncthreads();   // every wave is done with the stages
+    __syncthreads();   // every wave is done with the stages (the last wait was vmcnt(0): the C loads too)
     return acc;
 }
 
