@@ -421,8 +421,9 @@ class _TableUpload:
             ev.synchronize()
         return self.bufs[self.i]
 
-    def upload(self, dst: torch.Tensor) -> None:
-        """Copies the buffer of host() into dst on the current stream (unless dst holds it)."""
+    def upload(self, dst: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Copies the buffer of host() into dst on `stream`, the current stream (unless dst holds
+        it)."""
         i = self.i
         view = self.views[i]
         key = (dst.data_ptr(), dst.device)
@@ -432,7 +433,7 @@ class _TableUpload:
             self.last_dst = key
         if self.events[i] is None:
             self.events[i] = torch.cuda.Event()
-        self.events[i].record()
+        self.events[i].record(stream)
         self.i = (i + 1) % self.RING
 
 
@@ -658,7 +659,8 @@ class _OrthoRunner:
             steps['target_norm'] = tn
         host = self.upload.host()
         self.plan.fill_table(steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
-        self.upload.upload(self.table)
+        stream = torch.cuda.current_stream(self.device)
+        self.upload.upload(self.table, stream)
         ckey = (tuple(group.coeffs[:group.iters]), group.iters)
         if self._coeffs_key != ckey:
             self._coeffs = np.asarray(group.coeffs[:group.iters], dtype=np.float32).reshape(-1, 3)
@@ -666,7 +668,6 @@ class _OrthoRunner:
         coeffs = self._coeffs
         if self.adam or not due.any():   # no polar factor this step: momentum (gains, Magma s) only
             coeffs = coeffs[:0]
-        stream = torch.cuda.current_stream(self.device)
         self.plan.step(self.table.data_ptr(), coeffs, self.restart_mask(group, coeffs.shape[0]),
                        stream.cuda_stream, ns_begin.cuda_event if ns_begin is not None else 0)
         if self.status is not None and coeffs.shape[0] and (due & self.small).any():
@@ -905,6 +906,7 @@ class _AdamRunner:
         self.upload = _TableUpload(self.plan.table_bytes)
         self.workspace = torch.empty(max(256, self.plan.workspace_bytes), dtype=torch.uint8, device=device)
         self.steps = np.zeros(len(params), dtype=_lib.ADAM_TENSOR_STEP)
+        self.memo: dict = {}   # _fill_adam_steps: the hyperparameter columns of the last step
 
     @property
     def plans(self) -> list:
@@ -918,29 +920,57 @@ class _AdamRunner:
         """entries: (p, state, group, unmasked) per tensor, in plan order, from any number of
         groups. A tensor's parameter is written only when its step is due under update_rate
         (thorn.py:1706-1707) and not masked by Magma (unmasked False); m and v always are."""
-        s = self.steps
-        # one column at a time (a structured-array field per element costs a microsecond each)
-        steps = [e[1]['step'] for e in entries]
-        rect = [_compute_rect(e[2], st) for e, st in zip(entries, steps)]
-        s['p'] = [e[0].data_ptr() for e in entries]
-        s['g'] = [e[0].grad.data_ptr() for e in entries]
-        s['m'] = [e[1]['moment'].data_ptr() for e in entries]
-        s['v'] = [e[1]['variance'].data_ptr() for e in entries]
-        s['lr'] = [e[2].lr * r * 1.0 for e, r in zip(entries, rect)]
-        s['weight_decay'] = [e[2].weight_decay for e in entries]
-        s['beta2'] = [e[2].betas[1] for e in entries]
-        s['w1'] = [1 - e[2].betas[0] for e in entries]
-        s['w2'] = [1 - e[2].betas[1] for e in entries]
-        s['bc1'] = [1 / (1 - e[2].betas[0] ** st) for e, st in zip(entries, steps)]
-        s['bc2'] = [1 / (1 - e[2].betas[1] ** st) for e, st in zip(entries, steps)]
-        s['eps'] = [e[2].eps for e in entries]
-        s['apply'] = [1 if (st + 1) % update_rate == 0 and e[3] else 0 for e, st in zip(entries, steps)]
-        s['degenerate'] = [1 if r == 0.0 else 0 for r in rect]
-        s['magma_s'] = [e[1]['s'].data_ptr() if e[2].momentum_align else 0 for e in entries]
+        _fill_adam_steps(self.steps, entries, update_rate, self.memo)
         host = self.upload.host()
-        self.plan.fill_table(s, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
-        self.upload.upload(self.table)
-        self.plan.step(self.table.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
+        self.plan.fill_table(self.steps, self.workspace.data_ptr(), self.table.data_ptr(), host.data_ptr())
+        stream = torch.cuda.current_stream(self.device)
+        self.upload.upload(self.table, stream)
+        self.plan.step(self.table.data_ptr(), stream.cuda_stream)
+
+
+def _fill_adam_steps(s: np.ndarray, entries: list, update_rate: int, memo: dict) -> None:
+    """The per-step records of an Adam launch (ADAM_TENSOR_STEP) from entries (p, state, group,
+    unmasked). Entries come group by group, and within a run of entries of one group object with
+    one step count every scalar is the same: computed once and written to the run's slice (the
+    hyperparameter columns only when they differ from the last call's, kept in memo), with the
+    same Python arithmetic per value as per entry. Values are those of the per-entry form."""
+    n = len(entries)
+    s['p'] = [e[0].data_ptr() for e in entries]
+    s['g'] = [e[0].grad.data_ptr() for e in entries]
+    s['m'] = [e[1]['moment'].data_ptr() for e in entries]
+    s['v'] = [e[1]['variance'].data_ptr() for e in entries]
+    steps = [e[1]['step'] for e in entries]
+    runs = []
+    i = 0
+    while i < n:
+        grp, st = entries[i][2], steps[i]
+        j = i + 1
+        while j < n and entries[j][2] is grp and steps[j] == st:
+            j += 1
+        runs.append((i, j, grp, st))
+        i = j
+    hyper = tuple((i, j, g.weight_decay, g.betas[1], g.betas[0], g.eps) for i, j, g, _ in runs)
+    if memo.get('hyper') != hyper:
+        for i, j, g, _ in runs:
+            s['weight_decay'][i:j] = g.weight_decay
+            s['beta2'][i:j] = g.betas[1]
+            s['w1'][i:j] = 1 - g.betas[0]
+            s['w2'][i:j] = 1 - g.betas[1]
+            s['eps'][i:j] = g.eps
+        memo['hyper'] = hyper
+    for i, j, g, st in runs:
+        r = _compute_rect(g, st)
+        s['lr'][i:j] = g.lr * r * 1.0
+        s['bc1'][i:j] = 1 / (1 - g.betas[0] ** st)
+        s['bc2'][i:j] = 1 / (1 - g.betas[1] ** st)
+        s['degenerate'][i:j] = 1 if r == 0.0 else 0
+        due = (st + 1) % update_rate == 0
+        if g.momentum_align:
+            s['apply'][i:j] = [1 if due and e[3] else 0 for e in entries[i:j]]
+            s['magma_s'][i:j] = [e[1]['s'].data_ptr() for e in entries[i:j]]
+        else:
+            s['apply'][i:j] = 1 if due else 0
+            s['magma_s'][i:j] = 0
 
 
 class THORN(Optimizer):
