@@ -559,6 +559,11 @@ class _OrthoRunner:
         # per-step constants computed again only when what they depend on changes
         self._scale_key = self._eps_key = self._coeffs_key = None
         self._scale = self._eps = self._coeffs = None
+        self._const_key = self._flags_key = None   # the columns weight_decay, beta1, eta, pnn_eps; step_flags
+        # byte offset of each matrix in its parameter (a 3-D parameter holds several)
+        self._off = (self.sub * (self.rows * self.cols) * 4).astype(np.uint64)
+        # one matrix per parameter, in parameter order: the pointer columns need no gather
+        self._direct = len(owner) == len(params) and list(owner) == list(range(len(params)))
 
     @property
     def workspace(self) -> torch.Tensor:
@@ -575,13 +580,15 @@ class _OrthoRunner:
         elem = (self.rows * self.cols).astype(np.int64)
         bytes_off = self.sub * elem * 4
         own = self.owner
-        p_ptr = np.asarray([p.data_ptr() for p in params], dtype=np.uint64)[own]
-        g_ptr = np.asarray([p.grad.data_ptr() for p in params], dtype=np.uint64)[own]
         states = [opt._state_of(p) for p in params]
-        m_ptr = np.asarray([s['moment'].data_ptr() for s in states], dtype=np.uint64)[own]
-        steps['p'] = p_ptr + bytes_off.astype(np.uint64)
-        steps['g'] = g_ptr + bytes_off.astype(np.uint64)
-        steps['m'] = m_ptr + bytes_off.astype(np.uint64)
+        if self._direct:   # one matrix per parameter (offsets 0): the pointers as they are
+            steps['p'] = [p.data_ptr() for p in params]
+            steps['g'] = [p.grad.data_ptr() for p in params]
+            steps['m'] = [s['moment'].data_ptr() for s in states]
+        else:
+            steps['p'] = np.asarray([p.data_ptr() for p in params], dtype=np.uint64)[own] + self._off
+            steps['g'] = np.asarray([p.grad.data_ptr() for p in params], dtype=np.uint64)[own] + self._off
+            steps['m'] = np.asarray([s['moment'].data_ptr() for s in states], dtype=np.uint64)[own] + self._off
         if self.adam:   # thorn.py:1704-1714: lr * rect, the Adam moments' scalars
             beta1, beta2 = group.betas
             st = np.asarray([s['step'] for s in states], dtype=np.float64)
@@ -603,20 +610,32 @@ class _OrthoRunner:
             if self._scale_key != skey:
                 self._scale = np.asarray([_lr_scale_ortho(p.shape, group) for p in params], dtype=np.float64)[own]
                 self._scale_key = skey
-            steps['eta'] = group.lr * self._scale
-        steps['weight_decay'] = group.weight_decay
-        steps['beta1'] = group.betas[0]
         dts = tuple(getattr(p, '_thorn_dtype', p.dtype) for p in params)
         if self._eps_key != dts:
             self._eps = np.asarray([torch.finfo(d).eps for d in dts], dtype=np.float32)[own]
             self._eps_key = dts
-        steps['pnn_eps'] = self._eps
+        # columns that hold the same values from step to step are written when their inputs change
+        ckey = (group.weight_decay, group.betas[0], None if self.adam else (group.lr, self._scale_key), dts)
+        if self._const_key != ckey:
+            if not self.adam:
+                steps['eta'] = group.lr * self._scale
+            steps['weight_decay'] = group.weight_decay
+            steps['beta1'] = group.betas[0]
+            steps['pnn_eps'] = self._eps
+            self._const_key = ckey
         # a parameter is updated when its step is due under update_rate (thorn.py:1395); the
         # momentum (and the decouple_md round trip) runs every step
-        due = np.asarray([(s['step'] + 1) % opt._update_rate == 0 and (unmasked is None or unmasked[id(p)])
-                          for p, s in zip(params, states)], dtype=bool)[own]
+        rate = opt._update_rate
+        if rate == 1 and unmasked is None:   # every parameter due
+            due = np.ones(n, dtype=bool)
+        else:
+            due = np.asarray([(s['step'] + 1) % rate == 0 and (unmasked is None or unmasked[id(p)])
+                              for p, s in zip(params, states)], dtype=bool)[own]
         keep = 0 if group.none_grad else _lib.STEP_KEEP_GRAD
-        steps['step_flags'] = np.where(due, _lib.STEP_APPLY | keep, keep)
+        fkey = (keep, due.tobytes())
+        if self._flags_key != fkey:
+            steps['step_flags'] = np.where(due, _lib.STEP_APPLY | keep, keep)
+            self._flags_key = fkey
         # Magma: every matrix of a parameter carries the parameter's s (thorn.py:1392, 1405)
         steps['magma_s'] = (np.asarray([s['s'].data_ptr() for s in states], dtype=np.uint64)[own]
                             if group.momentum_align else 0)
