@@ -1317,6 +1317,59 @@ def test_small_xcd_barriers_equal_agent_barriers():
     _log('[gpu]   ok')
 
 
+def test_small_xcd_barriers_in_order_gradient_release():
+    """The sequence in which the first XCD-local barrier (which invalidated only the CU's L1) gave
+    other results than agent-scope barriers: gradient release in order, each matrix its own plan
+    on one shared workspace, stepped from its hook between autograd's kernels. Three Linear layers
+    whose matrices take clusters of 9 and 16 workgroups; three backward passes with XCD-local
+    barriers (the default) must leave the parameters bit for bit those of agent-scope barriers."""
+    _log('[gpu] small-matrix clusters in in-order gradient release: XCD-local against agent-scope barriers')
+    thorn_amd = _thorn()
+    lib = _lib()
+    from thorn_amd import optim as OPT
+    dims = [160, 200, 256, 200]
+    gen = torch.Generator().manual_seed(91)
+    init = [torch.randn(dims[i + 1], dims[i], generator=gen) * 0.05 for i in range(3)]
+    xs = [torch.randn(16, dims[0], generator=gen) for _ in range(3)]
+    keep_init = lib.OrthoPlan.__init__
+    keep_overlap = OPT.RELEASE_OVERLAP
+
+    def run(xcd: bool):
+        def init_plan(self, *a, **k):
+            keep_init(self, *a, **k)
+            self.set_small_xcd_barriers(xcd)
+        lib.OrthoPlan.__init__ = init_plan
+        OPT.RELEASE_OVERLAP = False
+        try:
+            mods = []
+            for i in range(3):
+                mods += [torch.nn.Linear(dims[i], dims[i + 1], bias=False), torch.nn.Tanh()]
+            model = torch.nn.Sequential(*mods).to(DEV)
+            lins = [m for m in model if isinstance(m, torch.nn.Linear)]
+            with torch.no_grad():
+                for lin, w in zip(lins, init):
+                    lin.weight.copy_(w.to(DEV))
+            opt = thorn_amd.THORN([{'params': [m.weight for m in lins], 'orthogonalize': True, 'lr': 1e-2,
+                                    'weight_decay': 0.1}])
+            opt.setup_gradient_release(model)
+            snaps = []
+            for x in xs:
+                model(x.to(DEV)).square().sum().backward()
+                torch.cuda.synchronize()
+                snaps.append([m.weight.detach().clone() for m in lins])
+            opt.check_status()
+            return snaps
+        finally:
+            lib.OrthoPlan.__init__ = keep_init
+            OPT.RELEASE_OVERLAP = keep_overlap
+
+    local, agent = run(True), run(False)
+    for k, (a, b) in enumerate(zip(local, agent)):
+        for i, (x, y) in enumerate(zip(a, b)):
+            assert torch.equal(x, y), (k, i, (x - y).abs().max().item())
+    _log('[gpu]   ok')
+
+
 SYM_CASES = [
     # (batch dims, M, K, C kind, alpha, beta, B as a transposed view of A)
     ((), 300, 700, None, 1.0, 1.0, True),        # Gram R = X X^T, two tile rows
