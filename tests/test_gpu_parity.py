@@ -717,6 +717,50 @@ def test_update_rate(name, rate):
     assert worst['md_roundtrip'] <= 1e-6, worst
 
 
+def test_hyperparameters_changed_between_steps():
+    """A scheduler edits the groups between steps (thorn.py:1405 rebuilds each group every step).
+    The host keeps the per-step record columns whose inputs did not change since the last step, so
+    an optimizer that has stepped before must give, after each edit, the bits of an optimizer built
+    afresh with the edited groups and the first one's state (load_state_dict), which has no kept
+    columns. Edits: the lr of every group on odd steps, the weight_decay on even ones, an Adam
+    group's betas and eps at step 4; orthogonalized matrices of the small path (fused from the
+    second step) and Adam tensors."""
+    _log('[gpu] hyperparameters edited between steps: kept record columns against a fresh optimizer')
+    thorn_amd = _thorn()
+    params, groups, grads = workloads.mixed_small()
+    gparams = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in params]
+    gpu = thorn_amd.THORN(_clone_groups(groups, gparams))
+    for s in range(1, 8):
+        for k, gg in enumerate(gpu.param_groups):
+            if s % 2 == 1:
+                gg['lr'] = groups[k]['lr'] * (1.0 + 0.5 * s)
+            else:
+                gg['weight_decay'] = groups[k]['weight_decay'] + 0.05 * s
+            if s == 4 and not gg['orthogonalize']:
+                gg['betas'] = (0.85, 0.97)
+                gg['eps'] = 1e-7
+        fparams = [torch.nn.Parameter(p.detach().clone()) for p in gparams]
+        where = {id(q): k for k, q in enumerate(gparams)}
+        fresh = thorn_amd.THORN([dict({a: b for a, b in gg.items() if a != 'params'},
+                                      params=[fparams[where[id(q)]] for q in gg['params']])
+                                 for gg in gpu.param_groups])
+        if s > 1:   # a copy: load_state_dict keeps the given tensors when dtype and device match
+            fresh.load_state_dict(copy.deepcopy(gpu.state_dict()))
+        for i, (pg, pf) in enumerate(zip(gparams, fparams)):
+            g = grads(s, i, params[i]).to(DEV)
+            pg.grad = g.clone()
+            pf.grad = g.clone()
+        gpu.step()
+        fresh.step()
+        torch.cuda.synchronize()
+        for i, (pg, pf) in enumerate(zip(gparams, fparams)):
+            assert torch.equal(pg, pf), (s, i, tuple(pg.shape), (pg - pf).abs().max().item())
+            for k, v in gpu.state[pg].items():
+                if torch.is_tensor(v):
+                    assert torch.equal(v, fresh.state[pf][k]), (s, i, k)
+    _log('[gpu]   ok')
+
+
 _W1_C = 0xD07EBC63274654C7
 
 
