@@ -738,7 +738,8 @@ def _chain_count(params: list) -> int:
     """How many chains a group of large matrices steps as: 2 while its Newton-Schulz work
     (sum of s^2 * l) is at most CHAIN_MAX_COST, else 1 (one plan). Measured on MI355X boxes, one
     process per config: the Qwen3-300M set (3.2e11) 6.82-6.85 ms with 2 chains against 7.06-7.11
-    with one (3: 6.87); its decouple_md variant 8.86-8.89 against 9.00-9.04; the Qwen3-1.7B set
+    with one (3: 6.87; with the present kernels 6.58 with 2, the Adam groups beside them, against
+    6.64-6.65 with 3 and 7.02 with 4); its decouple_md variant 8.86-8.89 against 9.00-9.04; the Qwen3-1.7B set
     (3.3e12) 49.9-50.1 ms with one against 50.2-52.4 with 2, 51.0-52.0 with 3 and 52.4-52.6 with 4.
     (Before the block map striped a large matrix's tiles over the XCDs, four chains filled the long
     tails its 8192 x 8192 matrix left in every launch: 53.8 against 70.2 ms.)"""
